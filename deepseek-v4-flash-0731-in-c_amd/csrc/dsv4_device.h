@@ -1,0 +1,159 @@
+// dsv4_device.h - gfx950 device helpers shared by the MoE expert-path kernels.
+//
+// Everything here reproduces a fixed numeric rule of the reference engine
+// bit-for-bit; the citation on each helper names the rule. All HIP sources are
+// compiled with -ffp-contract=off, so an fmaf()/fma() below is the only fused
+// operation, and fp32 division/sqrt are IEEE correctly rounded (hipcc default).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define DSV4_LIBM_FN __device__ __forceinline__
+#define DSV4_LIBM_TABLE static __constant__ const
+#include "dsv4_libm.h"
+
+namespace dsv4 {
+
+__device__ __forceinline__ uint32_t f2u(float f) { return __float_as_uint(f); }
+__device__ __forceinline__ float u2f(uint32_t u) { return __uint_as_float(u); }
+
+// BF16 round-to-nearest-even by integer bias, no NaN special case
+// (src/dsv4/dsv4_ops.c:35-44 with the widening of dsv4_internal.h:248-254).
+__device__ __forceinline__ float bf16_round(float f) {
+  uint32_t u = f2u(f);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return u2f(u & 0xFFFF0000u);
+}
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  return u2f((uint32_t)h << 16);
+}
+
+// E8M0 scale 2^(code-127); code 255 is NaN (src/dsv4/dsv4_ops.c:63-67).
+// Code 0 is the fp32 subnormal 2^-127, built from bits so no FTZ applies.
+__device__ __forceinline__ float e8m0(uint32_t code) {
+  if (code == 255u) return __builtin_nanf("");
+  return code == 0u ? u2f(0x00400000u) : u2f(code << 23);
+}
+
+// OCP E4M3FN decode (src/dsv4/dsv4_ops.c:47-61): exponent field 0 is
+// man*2^-9, S.1111.111 is NaN, else (8+man)*2^(exp-10).
+__device__ __forceinline__ float e4m3_decode(uint32_t code) {
+  const uint32_t e = (code >> 3) & 15u, m = code & 7u;
+  float mag;
+  if (e == 0u)
+    mag = (float)m * (1.0f / 512.0f);
+  else if (e == 15u && m == 7u)
+    mag = __builtin_nanf("");
+  else
+    mag = u2f(((e + 120u) << 23) | (m << 20));
+  return (code & 0x80u) ? -mag : mag;
+}
+
+// E2M1 nibble (src/dsv4/dsv4_model.c:971-974): bit 3 is the sign.
+__device__ __forceinline__ float e2m1_decode(uint32_t nib) {
+  const float mag[8] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f};
+  const float v = mag[nib & 7u];
+  return (nib & 8u) ? -v : v;
+}
+
+// Two FP4 nibbles of byte BYTE of w as fp32 (x = low nibble = even column).
+// Hardware MX convert with scale 1.0 is exact.
+template <int BYTE>
+__device__ __forceinline__ float2 fp4x2(uint32_t w) {
+  auto v = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, BYTE);
+  return make_float2(v[0], v[1]);
+}
+
+// Two OCP E4M3 codes (bytes 0,1 or 2,3 of w) as fp32.
+template <bool HI>
+__device__ __forceinline__ float2 fp8x2(uint32_t w) {
+  auto v = __builtin_amdgcn_cvt_pk_f32_fp8(w, HI);
+  return make_float2(v[0], v[1]);
+}
+
+// Nearest E4M3 grid value, ties to even (src/dsv4/dsv4_ops.c:81-109). rintf
+// is round-half-even, identical to the reference's floor-based helper for the
+// magnitudes used here (< 16).
+__device__ __forceinline__ float round_e4m3(float v) {
+  if (v == 0.0f) return 0.0f;
+  const float s = v < 0.0f ? -1.0f : 1.0f;
+  const float a = fabsf(v);
+  int e;
+  float m = frexpf(a, &e);
+  if (e >= -5) {
+    float mr = rintf(m * 16.0f) / 16.0f;
+    if (mr >= 1.0f) {
+      mr = 0.5f;
+      e++;
+    }
+    if (e - 1 > 8) return s * 448.0f;
+    return s * mr * ldexpf(1.0f, e);
+  }
+  return s * (rintf(a * 512.0f) / 512.0f);
+}
+
+// 2^ceil(log2(max(amax,1e-4)/448)) (src/dsv4/dsv4_model.c:5590-5596).
+__device__ __forceinline__ float act_scale(float amax) {
+  if (amax < 1e-4f) amax = 1e-4f;
+  const float r = amax * (1.0f / 448.0f);
+  int e;
+  const float m = frexpf(r, &e);
+  if (m == 0.5f) e--;
+  return ldexpf(1.0f, e);
+}
+
+// q = round_e4m3(clamp(x * inv, +-448)) (src/dsv4/dsv4_model.c:5598-5604).
+__device__ __forceinline__ float quant_e4m3(float x, float inv) {
+  float q = x * inv;
+  if (q > 448.0f) q = 448.0f;
+  else if (q < -448.0f) q = -448.0f;
+  return round_e4m3(q);
+}
+
+// E4M3 code of a grid value produced by round_e4m3 (exact).
+__device__ __forceinline__ uint32_t e4m3_code(float v) {
+  const uint32_t sign = (f2u(v) >> 24) & 0x80u;
+  const float a = fabsf(v);
+  if (a < 0.015625f) return sign | (uint32_t)(a * 512.0f);  // subnormal, incl. 0
+  const uint32_t b = f2u(a);
+  const uint32_t ef = ((b >> 23) & 0xFFu) - 120u;  // fp32 exp -> E4M3 field
+  return sign | (ef << 3) | ((b >> 20) & 7u);
+}
+
+// ---- glibc 2.35 libm, restated bit-exactly (dsv4_libm.h) ------------------
+__device__ __forceinline__ float libm_expf(float x) { return dsv4_libm_expf(x); }
+__device__ __forceinline__ float libm_log1pf_nonneg(float x) {
+  return dsv4_libm_log1pf_nonneg(x);
+}
+
+// sqrt(softplus(z)) (src/dsv4/dsv4_model.c:5827-5831).
+__device__ __forceinline__ float sqrt_softplus(float z) {
+  if (z > 20.0f) return sqrtf(z);
+  return sqrtf(libm_log1pf_nonneg(libm_expf(z)));
+}
+
+// SwiGLU element (src/dsv4/dsv4_model.c:6264-6268): up clamped to
+// [-limit, limit], gate clamped above only, t = silu(g) * u, rounded to fp32.
+__device__ __forceinline__ float swiglu_t(float g, float u, float limit) {
+  if (u > limit) u = limit;
+  else if (u < -limit) u = -limit;
+  if (g > limit) g = limit;
+  const float silu = g / (1.0f + libm_expf(-g));
+  return silu * u;
+}
+
+// Wave-wide reductions (wave64).
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+}  // namespace dsv4

@@ -1,0 +1,290 @@
+"""ctypes binding of libdsv4_gpu.so (include/dsv4_gpu.h) for Python callers.
+
+Device buffers are torch tensors on a ROCm device (torch only allocates and
+orders streams; all compute runs in the library's HIP kernels). Every wrapper
+launches on torch's current stream and raises RuntimeError with the
+library's message on failure. If the library is missing the import fails
+loudly: there is no fallback.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.dirname(HERE)
+LIB_PATH = os.path.join(PKG, "lib", "libdsv4_gpu.so")
+
+_vp = C.c_void_p
+
+
+class DSV4GLayer(C.Structure):
+    """Mirror of DSV4GLayer (include/dsv4_gpu.h)."""
+
+    _fields_ = [
+        ("hidden", C.c_int), ("inter", C.c_int), ("n_experts", C.c_int), ("topk", C.c_int),
+        ("route_scale", C.c_float), ("swiglu_limit", C.c_float),
+        ("gate_w", _vp), ("bias", _vp), ("tid2eid", _vp), ("experts", _vp),
+        ("expert_stride", C.c_size_t), ("scale_run", C.c_size_t),
+        ("sh1", _vp), ("sh1_s", _vp), ("sh3", _vp), ("sh3_s", _vp),
+        ("sh2", _vp), ("sh2_s", _vp),
+    ]
+
+
+# (name, argtypes) for the device-pointer ABI; all return int.
+_I, _F, _Z = C.c_int, C.c_float, C.c_size_t
+_SIGS = {
+    "dsv4g_quant_fp8_act": [_vp, _vp, _vp, _I, _I, _vp],
+    "dsv4g_dequant_fp4": [_vp, _vp, _vp, _I, _I, _vp],
+    "dsv4g_dequant_fp8": [_vp, _vp, _vp, _I, _I, _vp],
+    "dsv4g_probe_converts": [_vp, _vp, _vp],
+    "dsv4g_gemv_fp4_q": [_vp, _vp, _vp, _vp, _vp, _I, _I, _vp],
+    "dsv4g_gemv_fp4_pair_q": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _I, _I, _vp],
+    "dsv4g_gemv_fp4_batch_q": [_vp, _vp, _vp, _I, _vp, _vp, _I, _I, _vp],
+    "dsv4g_gemv_fp8_q": [_vp, _vp, _vp, _vp, _vp, _I, _I, _I, _vp],
+    "dsv4g_gemv_fp8_pair_q": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _I, _I, _vp],
+    "dsv4g_gemv_fp8_batch_q": [_vp, _vp, _vp, _I, _vp, _vp, _I, _I, _I, _vp],
+    "dsv4g_gemv_bf16": [_vp, _vp, _vp, _I, _I, _I, _I, _vp],
+    "dsv4g_gemv_fp8_float": [_vp, _vp, _vp, _vp, _I, _I, _I, _I, _vp],
+    "dsv4g_gemv_fp4_float": [_vp, _vp, _vp, _vp, _vp, _I, _I, _I, _vp],
+    "dsv4g_router": [_vp, _vp, _vp, C.POINTER(DSV4GLayer), _vp, _I, _vp, _vp, _vp],
+    "dsv4g_router_public": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _I, _I, _I, _I, _F, _vp, _vp,
+                            _vp],
+    "dsv4g_swiglu_quant": [_vp, _vp, _vp, _vp, _I, _I, _I, _F, _vp],
+    "dsv4g_moe_forward": [_vp, _vp, C.POINTER(DSV4GLayer), _vp, _I, _vp, _Z, _vp, _vp, _vp],
+    "dsv4g_quant_fp4_rows": [_vp, _vp, _vp, _I, _I, _vp],
+    "dsv4g_quant_fp8_blocks": [_vp, _vp, _vp, _I, _I, _I, _vp],
+}
+
+
+def _ptr(t):
+    return None if t is None else C.c_void_p(t.data_ptr())
+
+
+class GpuLib:
+    def __init__(self, path: str = LIB_PATH):
+        if not os.path.exists(path):
+            raise RuntimeError(f"{path} is missing: build it with `make -C "
+                               f"deepseek-v4-flash-0731-in-c_amd` (or __graft_entry__.build())")
+        self.path = path
+        lib = self.lib = C.CDLL(path)
+        lib.dsv4g_last_error.restype = C.c_char_p
+        lib.dsv4g_version.restype = C.c_char_p
+        lib.dsv4g_moe_workspace_bytes.restype = C.c_size_t
+        lib.dsv4g_moe_workspace_bytes.argtypes = [C.POINTER(DSV4GLayer), _I]
+        for name, args in _SIGS.items():
+            fn = getattr(lib, name)
+            fn.argtypes = args
+            fn.restype = C.c_int
+
+    # ---- plumbing
+    def _call(self, name, *args):
+        rc = getattr(self.lib, name)(*args)
+        if rc != 0:
+            raise RuntimeError(f"{name}: {self.lib.dsv4g_last_error().decode()}")
+
+    @staticmethod
+    def _stream():
+        import torch
+        return C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    # ---- kernels (torch tensors in, torch tensors out)
+    def quant_fp8_act(self, x):
+        import torch
+        n = x.shape[-1]
+        nvec = x.numel() // n
+        qx = torch.empty_like(x)
+        qs = torch.empty(x.shape[:-1] + ((n + 127) // 128,), dtype=torch.float32, device=x.device)
+        self._call("dsv4g_quant_fp8_act", _ptr(qx), _ptr(qs), _ptr(x), n, nvec, self._stream())
+        return qx, qs
+
+    def dequant_fp4(self, W, S, rows, cols):
+        import torch
+        out = torch.empty(rows, cols, dtype=torch.float32, device=W.device)
+        self._call("dsv4g_dequant_fp4", _ptr(out), _ptr(W), _ptr(S), rows, cols, self._stream())
+        return out
+
+    def dequant_fp8(self, W, S, rows, cols):
+        import torch
+        out = torch.empty(rows, cols, dtype=torch.float32, device=W.device)
+        self._call("dsv4g_dequant_fp8", _ptr(out), _ptr(W), _ptr(S), rows, cols, self._stream())
+        return out
+
+    def probe_converts(self, device):
+        import torch
+        a = torch.empty(512, dtype=torch.float32, device=device)
+        b = torch.empty(256, dtype=torch.float32, device=device)
+        self._call("dsv4g_probe_converts", _ptr(a), _ptr(b), self._stream())
+        return a, b
+
+    def gemv_fp4_q(self, qx, qs, W, S, in_, rows, y=None):
+        import torch
+        y = torch.empty(rows, dtype=torch.float32, device=qx.device) if y is None else y
+        self._call("dsv4g_gemv_fp4_q", _ptr(y), _ptr(qx), _ptr(qs), _ptr(W), _ptr(S), in_, rows,
+                   self._stream())
+        return y
+
+    def gemv_fp4_pair_q(self, qx, qs, W0, S0, W1, S1, in_, rows):
+        import torch
+        y0 = torch.empty(rows, dtype=torch.float32, device=qx.device)
+        y1 = torch.empty_like(y0)
+        self._call("dsv4g_gemv_fp4_pair_q", _ptr(y0), _ptr(y1), _ptr(qx), _ptr(qs), _ptr(W0),
+                   _ptr(S0), _ptr(W1), _ptr(S1), in_, rows, self._stream())
+        return y0, y1
+
+    def gemv_fp4_batch_q(self, qx, qs, W, S, in_, rows):
+        import torch
+        b = qx.shape[0]
+        y = torch.empty(b, rows, dtype=torch.float32, device=qx.device)
+        self._call("dsv4g_gemv_fp4_batch_q", _ptr(y), _ptr(qx), _ptr(qs), b, _ptr(W), _ptr(S),
+                   in_, rows, self._stream())
+        return y
+
+    def gemv_fp8_q(self, qx, qs, W, S, in_, out, round_out=1, y=None):
+        import torch
+        y = torch.empty(out, dtype=torch.float32, device=qx.device) if y is None else y
+        self._call("dsv4g_gemv_fp8_q", _ptr(y), _ptr(qx), _ptr(qs), _ptr(W), _ptr(S), in_, out,
+                   round_out, self._stream())
+        return y
+
+    def gemv_fp8_pair_q(self, qx, qs, W0, S0, W1, S1, in_, out):
+        import torch
+        y0 = torch.empty(out, dtype=torch.float32, device=qx.device)
+        y1 = torch.empty_like(y0)
+        self._call("dsv4g_gemv_fp8_pair_q", _ptr(y0), _ptr(y1), _ptr(qx), _ptr(qs), _ptr(W0),
+                   _ptr(S0), _ptr(W1), _ptr(S1), in_, out, self._stream())
+        return y0, y1
+
+    def gemv_fp8_batch_q(self, qx, qs, W, S, in_, out, round_out=1):
+        import torch
+        b = qx.shape[0]
+        y = torch.empty(b, out, dtype=torch.float32, device=qx.device)
+        self._call("dsv4g_gemv_fp8_batch_q", _ptr(y), _ptr(qx), _ptr(qs), b, _ptr(W), _ptr(S),
+                   in_, out, round_out, self._stream())
+        return y
+
+    def gemv_bf16(self, x, W, in_, out, round_out=0):
+        import torch
+        b = x.numel() // in_
+        y = torch.empty(b, out, dtype=torch.float32, device=x.device)
+        self._call("dsv4g_gemv_bf16", _ptr(y), _ptr(x), _ptr(W), in_, out, round_out, b,
+                   self._stream())
+        return y
+
+    def gemv_fp8_float(self, x, W, wscale, in_, rows, block=128, mode=0, y=None):
+        import torch
+        y = torch.empty(rows, dtype=torch.float32, device=x.device) if y is None else y
+        self._call("dsv4g_gemv_fp8_float", _ptr(y), _ptr(x), _ptr(W), _ptr(wscale), in_, rows,
+                   block, mode, self._stream())
+        return y
+
+    def gemv_fp4_float(self, qx, qs, W, wscale, in_, rows, group=32):
+        import torch
+        y = torch.empty(rows, dtype=torch.float32, device=qx.device)
+        self._call("dsv4g_gemv_fp4_float", _ptr(y), _ptr(qx), _ptr(qs), _ptr(W), _ptr(wscale),
+                   in_, rows, group, self._stream())
+        return y
+
+    def router(self, layer, x, token_ids=None):
+        import torch
+        L = layer.struct
+        n = x.shape[0]
+        idx = torch.empty(n, L.topk, dtype=torch.int32, device=x.device)
+        wt = torch.empty(n, L.topk, dtype=torch.float32, device=x.device)
+        ws = torch.empty(2, n, L.n_experts, dtype=torch.float32, device=x.device)
+        self._call("dsv4g_router", _ptr(idx), _ptr(wt), _ptr(x), C.byref(L), _ptr(token_ids), n,
+                   _ptr(ws[0]), _ptr(ws[1]), self._stream())
+        return idx, wt
+
+    def router_public(self, x, gate, bias, t2e_row, hidden, n_experts, topk, hash_layer,
+                      route_scale):
+        import torch
+        idx = torch.empty(topk, dtype=torch.int32, device=x.device)
+        wt = torch.empty(topk, dtype=torch.float32, device=x.device)
+        ws = torch.empty(2, n_experts, dtype=torch.float32, device=x.device)
+        tok = torch.zeros(1, dtype=torch.int32, device=x.device)
+        self._call("dsv4g_router_public", _ptr(idx), _ptr(wt), _ptr(x), _ptr(gate), _ptr(bias),
+                   _ptr(t2e_row), _ptr(tok), hidden, n_experts, topk, int(hash_layer),
+                   C.c_float(route_scale), _ptr(ws[0]), _ptr(ws[1]), self._stream())
+        return idx, wt
+
+    def swiglu_quant(self, gate_up, inter, limit, wt=None, K=0):
+        import torch
+        n_slots = gate_up.numel() // (2 * inter)
+        qy = torch.empty(n_slots, inter, dtype=torch.float32, device=gate_up.device)
+        qs = torch.empty(n_slots, inter // 128, dtype=torch.float32, device=gate_up.device)
+        self._call("dsv4g_swiglu_quant", _ptr(qy), _ptr(qs), _ptr(gate_up), _ptr(wt), K, n_slots,
+                   inter, C.c_float(limit), self._stream())
+        return qy, qs
+
+    def moe_workspace_bytes(self, layer, n_tokens):
+        return int(self.lib.dsv4g_moe_workspace_bytes(C.byref(layer.struct), n_tokens))
+
+    def moe_forward(self, layer, x, token_ids=None, workspace=None, out=None):
+        import torch
+        n = x.shape[0]
+        L = layer.struct
+        need = self.moe_workspace_bytes(layer, n)
+        if workspace is None or workspace.numel() < need:
+            workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
+        out = torch.empty_like(x) if out is None else out
+        idx = torch.empty(n, L.topk, dtype=torch.int32, device=x.device)
+        wt = torch.empty(n, L.topk, dtype=torch.float32, device=x.device)
+        self._call("dsv4g_moe_forward", _ptr(out), _ptr(x), C.byref(L), _ptr(token_ids), n,
+                   _ptr(workspace), workspace.numel(), _ptr(idx), _ptr(wt), self._stream())
+        return out, idx, wt
+
+    def quant_fp4_rows(self, w, packed, scales):
+        rows, cols = w.shape
+        self._call("dsv4g_quant_fp4_rows", _ptr(packed), _ptr(scales), _ptr(w), rows, cols,
+                   self._stream())
+
+    def quant_fp8_blocks(self, w, codes, scales, mode=0):
+        rows, cols = w.shape
+        self._call("dsv4g_quant_fp8_blocks", _ptr(codes), _ptr(scales), _ptr(w), rows, cols,
+                   mode, self._stream())
+
+
+class DeviceLayer:
+    """A DSV4GLayer whose buffers are torch tensors kept alive here."""
+
+    def __init__(self, tensors: dict, meta: dict):
+        self.tensors = tensors
+        L = DSV4GLayer()
+        L.hidden, L.inter = meta["hidden"], meta["inter"]
+        L.n_experts, L.topk = meta["n_experts"], meta["topk"]
+        L.route_scale, L.swiglu_limit = meta["route_scale"], meta["swiglu_limit"]
+        L.expert_stride, L.scale_run = meta["expert_stride"], meta["scale_run"]
+        for k in ("gate_w", "bias", "tid2eid", "experts", "sh1", "sh1_s", "sh3", "sh3_s", "sh2",
+                  "sh2_s"):
+            t = tensors.get(k)
+            setattr(L, k, None if t is None else t.data_ptr())
+        self.struct = L
+        self.meta = meta
+
+    @classmethod
+    def from_host(cls, layer: dict, device="cuda"):
+        """Upload a host (numpy) layer dict as built by tests/common.make_layer."""
+        import torch
+        t = {}
+        for k in ("gate_w", "bias", "tid2eid", "experts", "sh1", "sh1_s", "sh3", "sh3_s", "sh2",
+                  "sh2_s"):
+            v = layer.get(k)
+            if v is None:
+                continue
+            if v.dtype.name == "uint16":
+                v = v.view("int16")
+            t[k] = torch.from_numpy(v.copy()).to(device)
+        meta = {k: layer[k] for k in ("hidden", "inter", "n_experts", "topk", "route_scale",
+                                      "swiglu_limit", "expert_stride", "scale_run")}
+        return cls(t, meta)
+
+
+_LIB = None
+
+
+def lib() -> GpuLib:
+    global _LIB
+    if _LIB is None:
+        _LIB = GpuLib()
+    return _LIB

@@ -1,0 +1,204 @@
+/* dsv4_gpu.h - C ABI of the gfx950 (MI355X) quantized MoE expert path.
+ *
+ * Two layers, both plain C (extern "C", pointers and sizes only):
+ *
+ * 1. Drop-in entry points with the reference engine's exact names and
+ *    signatures (host pointers, void return, abort with a message on a GPU
+ *    error, as the reference exits on fatal conditions). They live in
+ *    libdsv4_gpu.so next to layer 2 and replace:
+ *      include/dsv4/dsv4.h:185-211, 251-254  (public kernels, router)
+ *      src/dsv4/dsv4_internal.h:256-286, 326-331 (internal GEMVs, quant)
+ *    Weights passed by host pointer are uploaded to HBM on first use and kept
+ *    resident, keyed by host address and size (weights are const in the
+ *    reference); dsv4_gpu_register_weights()/dsv4_gpu_forget_weights() manage
+ *    that cache explicitly. Activations are copied per call.
+ *
+ * 2. Device-pointer API (dsv4g_*): every pointer is device memory, every call
+ *    is asynchronous on the given HIP stream (NULL = default stream) and
+ *    returns 0 or a DSV4G_E* code; dsv4g_last_error() gives the message.
+ *    This is the layer a device-resident engine calls (the fused MoE entries
+ *    replace the static moe_forward / moe_forward_batch of
+ *    src/dsv4/dsv4_model.c:6599, 6812, which have no exported symbol).
+ *
+ * Numerics: the decode-path GEMVs, activation quantisation, SwiGLU requant,
+ * router (indices and weights) and combine are bit-identical to the
+ * reference's scalar loop order. The public float-scale GEMVs, the BF16 GEMV
+ * and the grouped-GEMM batch path agree to fp32 rounding (documented
+ * tolerance), not bit for bit.
+ */
+#ifndef DSV4_GPU_H
+#define DSV4_GPU_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DSV4G_VERSION "0.1.0"
+
+#define DSV4G_OK 0
+#define DSV4G_EINVAL 1 /* bad argument or unsupported shape */
+#define DSV4G_EHIP 2   /* HIP runtime error */
+
+/* One MoE layer resident in HBM (device pointers). Routed expert e occupies
+ * expert_stride bytes at experts + e*expert_stride: the E8M0 scale run
+ * [w1 | w2 | w3] (per row, per 32 columns) followed at +scale_run by the
+ * packed E2M1 weight run [w1 | w2 | w3] (two nibbles per byte, low nibble =
+ * even column); w1 = gate [inter][hidden], w2 = down [hidden][inter],
+ * w3 = up [inter][hidden]. This is the checkpoint's contiguous per-expert
+ * layout (src/dsv4/dsv4_internal.h:8-17, 33-37;
+ * src/dsv4/dsv4_model.c:6298-6305). The shared expert is FP8 E4M3 with
+ * per-128x128 E8M0 block scales (src/dsv4/dsv4_model.c:2029-2053). */
+typedef struct {
+    int hidden;            /* 4096 */
+    int inter;             /* moe_inter, 2048 */
+    int n_experts;         /* 256 */
+    int topk;              /* 6 */
+    float route_scale;     /* 1.5 */
+    float swiglu_limit;    /* 10.0 (used as (int)swiglu_limit, as the reference) */
+    const uint16_t *gate_w;   /* BF16 [n_experts][hidden] */
+    const float *bias;        /* F32 [n_experts] or NULL */
+    const int64_t *tid2eid;   /* I64 [vocab][topk] for hash layers, else NULL */
+    const uint8_t *experts;   /* routed experts, see above */
+    size_t expert_stride;     /* >= scale_run + weight run (13,369,344 at full size) */
+    size_t scale_run;         /* 786,432 at full size */
+    const uint8_t *sh1, *sh1_s;  /* shared gate FP8 [inter][hidden] + scales */
+    const uint8_t *sh3, *sh3_s;  /* shared up   FP8 [inter][hidden] + scales */
+    const uint8_t *sh2, *sh2_s;  /* shared down FP8 [hidden][inter] + scales */
+} DSV4GLayer;
+
+/* ------------------------------------------------------ runtime helpers */
+const char *dsv4g_last_error(void);
+const char *dsv4g_version(void);
+int dsv4g_device_count(int *count);
+int dsv4g_malloc(void **ptr, size_t bytes);
+int dsv4g_free(void *ptr);
+int dsv4g_memcpy_h2d(void *dst, const void *src, size_t bytes, void *stream);
+int dsv4g_memcpy_d2h(void *dst, const void *src, size_t bytes, void *stream); /* syncs */
+int dsv4g_stream_sync(void *stream);
+
+/* ----------------------------------------------- device-pointer kernels */
+/* dsv4_quant_fp8_codes / dsv4_quant_fp8_act over nvec rows of n
+ * (src/dsv4/dsv4_model.c:5580-5606, src/dsv4/dsv4_ops.c:122-146). */
+int dsv4g_quant_fp8_act(float *qx, float *qscale, const float *x, int n, int nvec,
+                        void *stream);
+/* Dequantised weights (value * scale), bit-exact with the reference decode. */
+int dsv4g_dequant_fp4(float *out, const uint8_t *W, const uint8_t *S, int rows, int cols,
+                      void *stream);
+int dsv4g_dequant_fp8(float *out, const uint8_t *W, const uint8_t *S, int rows, int cols,
+                      void *stream);
+/* Writes the hardware FP4 (512 floats: both nibbles of bytes 0..255) and FP8
+ * (256 floats) conversions the GEMVs use, for validation. */
+int dsv4g_probe_converts(float *fp4_out, float *fp8_out, void *stream);
+
+/* dsv4_gemv_fp4_q / _pair_q / _batch_q (src/dsv4/dsv4_internal.h:274-286).
+ * Batched arrays are contiguous: y [batch][rows], qx [batch][in],
+ * qscale [batch][in/128]. in: multiple of 32, at most 8192. */
+int dsv4g_gemv_fp4_q(float *y, const float *qx, const float *qscale, const uint8_t *W,
+                     const uint8_t *S, int in, int rows, void *stream);
+int dsv4g_gemv_fp4_pair_q(float *y0, float *y1, const float *qx, const float *qscale,
+                          const uint8_t *W0, const uint8_t *S0, const uint8_t *W1,
+                          const uint8_t *S1, int in, int rows, void *stream);
+int dsv4g_gemv_fp4_batch_q(float *y, const float *qx, const float *qscale, int batch,
+                           const uint8_t *W, const uint8_t *S, int in, int rows,
+                           void *stream);
+/* dsv4_gemv_fp8_q / _pair_q / _batch_q (src/dsv4/dsv4_internal.h:261-272).
+ * in: multiple of 16, at most 8192. */
+int dsv4g_gemv_fp8_q(float *y, const float *qx, const float *qscale, const uint8_t *W,
+                     const uint8_t *S, int in, int out, int round_out, void *stream);
+int dsv4g_gemv_fp8_pair_q(float *y0, float *y1, const float *qx, const float *qscale,
+                          const uint8_t *W0, const uint8_t *S0, const uint8_t *W1,
+                          const uint8_t *S1, int in, int out, void *stream);
+int dsv4g_gemv_fp8_batch_q(float *y, const float *qx, const float *qscale, int batch,
+                           const uint8_t *W, const uint8_t *S, int in, int out,
+                           int round_out, void *stream);
+/* dsv4_gemv_bf16 / _batch (src/dsv4/dsv4_internal.h:256-259); x [batch][in]. */
+int dsv4g_gemv_bf16(float *y, const float *x, const uint16_t *W, int in, int out,
+                    int round_out, int batch, void *stream);
+/* dsv4_gemv_fp8 (mode 0) / dsv4_gemv_fp8_tbl (mode 1) (include/dsv4/dsv4.h:200-206)
+ * and dsv4_gemv_fp4 (include/dsv4/dsv4.h:208-211), float block scales. */
+int dsv4g_gemv_fp8_float(float *y, const float *x, const uint8_t *W, const float *wscale,
+                         int in, int rows, int block, int mode, void *stream);
+int dsv4g_gemv_fp4_float(float *y, const float *qx, const float *qscale, const uint8_t *W,
+                         const float *wscale, int in, int rows, int group, void *stream);
+
+/* Router of moe_forward (src/dsv4/dsv4_model.c:6615-6676) for n_tokens
+ * rows of x: idx [n][topk] ascending, wt [n][topk]. z_ws, zabs_ws: device
+ * scratch of n_tokens*n_experts floats each. */
+int dsv4g_router(int *idx, float *wt, const float *x, const DSV4GLayer *L,
+                 const int *token_ids, int n_tokens, float *z_ws, float *zabs_ws,
+                 void *stream);
+/* routed_swiglu_quant (src/dsv4/dsv4_model.c:6239-6287) over n_slots slots;
+ * slot s reads gate at gate_up + 2*s*inter and up right after it. Weights:
+ * K > 0: slots are [token][K+1], slot (t,k<K) uses wt[t*K+k], slot K uses 1;
+ * K == 0: slot s uses wt[s]; wt == NULL: weight 1. */
+int dsv4g_swiglu_quant(float *qy, float *qys, const float *gate_up, const float *wt, int K,
+                       int n_slots, int inter, float limit, void *stream);
+
+/* Decode MoE layer: moe_forward for each of n_tokens rows of x (BF16 values
+ * in fp32), bit-exact. out [n][hidden]. idx_out/wt_out (optional, device)
+ * receive the routing. workspace: device memory of at least
+ * dsv4g_moe_workspace_bytes(L, n_tokens). */
+size_t dsv4g_moe_workspace_bytes(const DSV4GLayer *L, int n_tokens);
+int dsv4g_moe_forward(float *out, const float *x, const DSV4GLayer *L, const int *token_ids,
+                      int n_tokens, void *workspace, size_t workspace_bytes, int *idx_out,
+                      float *wt_out, void *stream);
+
+/* Synthetic-checkpoint quantisers (the reference ships none in C):
+ * FP4 rows with per-32 E8M0 scales; FP8 128x128 blocks with E8M0 codes
+ * (mode 0, scales = uint8) or fp32 absmax/448 (mode 1, scales = float). */
+int dsv4g_quant_fp4_rows(uint8_t *packed, uint8_t *scales, const float *w, int rows,
+                         int cols, void *stream);
+int dsv4g_quant_fp8_blocks(uint8_t *codes, void *scales, const float *w, int rows, int cols,
+                           int mode, void *stream);
+
+/* -------------------------------------------- drop-in (host pointers) ----
+ * Same names, argument meaning and error behaviour as the reference. */
+uint16_t dsv4_f32_to_bf16(float f);                                 /* dsv4.h:183 */
+float dsv4_fp8_e4m3(uint8_t code);                                  /* dsv4.h:186 */
+float dsv4_e8m0(uint8_t code);                                      /* dsv4.h:188 */
+float dsv4_round_e4m3(float v);                                     /* dsv4_internal.h:331 */
+void dsv4_quant_fp8_act(float *out, float *scales, const float *x, int n); /* dsv4.h:193 */
+void dsv4_quant_fp8_codes(float *qx, float *qscale, const float *x, int n); /* dsv4_internal.h:327 */
+void dsv4_gemv_fp8(float *y, const float *x, const uint8_t *W, const float *wscale,
+                   int in, int rows, int block);                    /* dsv4.h:200 */
+void dsv4_gemv_fp8_tbl(float *y, const float *x, const uint8_t *W, const float *wscale,
+                       int in, int rows, int block);                /* dsv4.h:203 */
+void dsv4_gemv_fp4(float *y, const float *qx, const float *qscale, const uint8_t *W,
+                   const float *wscale, int in, int rows, int group); /* dsv4.h:209 */
+void dsv4_gemv_bf16(float *y, const float *x, const uint16_t *W, int in, int out,
+                    int round_out);                                 /* dsv4_internal.h:256 */
+void dsv4_gemv_bf16_batch(float *const *y, const float *const *x, int batch,
+                          const uint16_t *W, int in, int out, int round_out);
+void dsv4_gemv_fp8_q(float *y, const float *qx, const float *qscale, const uint8_t *W,
+                     const uint8_t *wscale_code, int in, int out, int round_out);
+void dsv4_gemv_fp8_batch_q(float *const *y, const float *const *qx,
+                           const float *const *qscale, int batch, const uint8_t *W,
+                           const uint8_t *wscale_code, int in, int out, int round_out);
+void dsv4_gemv_fp8_pair_q(float *y0, float *y1, const float *qx, const float *qscale,
+                          const uint8_t *W0, const uint8_t *S0, const uint8_t *W1,
+                          const uint8_t *S1, int in, int out);
+void dsv4_gemv_fp4_q(float *y, const float *qx, const float *qscale, const uint8_t *W,
+                     const uint8_t *wscale_code, int in, int rows);
+void dsv4_gemv_fp4_batch_q(float *const *y, const float *const *qx,
+                           const float *const *qscale, int batch, const uint8_t *W,
+                           const uint8_t *wscale_code, int in, int rows);
+void dsv4_gemv_fp4_pair_q(float *y0, float *y1, const float *qx, const float *qscale,
+                          const uint8_t *W0, const uint8_t *S0, const uint8_t *W1,
+                          const uint8_t *S1, int in, int rows);
+void dsv4_router(int *idx, float *wt, const float *x, const float *gate, const float *bias,
+                 const int64_t *tid2eid, int token_id, int hidden, int n_experts,
+                 int topk, int hash_layer, float route_scale, float rms_eps); /* dsv4.h:251 */
+
+/* Weight residency for the drop-in entry points. */
+int dsv4_gpu_register_weights(const void *host, size_t bytes);
+void dsv4_gpu_forget_weights(const void *host);
+void dsv4_gpu_forget_all_weights(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DSV4_GPU_H */
