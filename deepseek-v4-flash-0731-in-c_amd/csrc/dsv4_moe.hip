@@ -455,27 +455,37 @@ int dsv4g_swiglu_quant(float *qy, float *qys, const float *gate_up, const float 
   return dsv4g_check_launch("swiglu_quant");
 }
 
-// Decode-path MoE layer: moe_forward per token, bit-exact. idx/wt (optional,
-// device) receive the routing.
-int dsv4g_moe_forward(float *out, const float *x, const DSV4GLayer *L, const int *token_ids,
-                      int n_tokens, void *workspace, size_t workspace_bytes, int *idx_out,
-                      float *wt_out, void *stream) {
-  DSV4G_TRY(layer_ok(L, "moe_forward"));
-  if (n_tokens <= 0) return dsv4g_fail(DSV4G_EINVAL, "moe_forward: n_tokens must be > 0");
+// One phase of the decode MoE layer (moe_forward per token, bit-exact):
+//   0 activation quant + router, 1 gate/up GEMVs (6 FP4 routed + shared FP8),
+//   2 SwiGLU + FP8 requant, 3 down GEMVs, 4 ordered combine into out.
+// Phases run in order on one stream; dsv4g_moe_forward runs all five.
+int dsv4g_moe_decode_phase(int phase, float *out, const float *x, const DSV4GLayer *L,
+                           const int *token_ids, int n_tokens, void *workspace,
+                           size_t workspace_bytes, void *stream) {
+  DSV4G_TRY(layer_ok(L, "moe_decode"));
+  if (n_tokens <= 0) return dsv4g_fail(DSV4G_EINVAL, "moe_decode: n_tokens must be > 0");
   if (workspace_bytes < dsv4g_moe_workspace_bytes(L, n_tokens))
-    return dsv4g_fail(DSV4G_EINVAL, "moe_forward: workspace too small (%zu < %zu)",
+    return dsv4g_fail(DSV4G_EINVAL, "moe_decode: workspace too small (%zu < %zu)",
                       workspace_bytes, dsv4g_moe_workspace_bytes(L, n_tokens));
   hipStream_t st = (hipStream_t)stream;
   const int n = n_tokens, K = L->topk, H = L->hidden, I = L->inter;
   const MoeWs w = moe_ws_layout(L, n, workspace);
-  float *qx = w.qx, *qxs = w.qxs, *z = w.z, *zabs = w.zabs, *wt = w.wt, *gu = w.gu;
-  float *qy = w.qy, *qys = w.qys, *ro = w.ro;
-  int *idx = w.idx;
-
-  DSV4G_TRY(dsv4g_quant_fp8_act(qx, qxs, x, H, n, stream));
-  DSV4G_TRY(dsv4g_router(idx, wt, x, L, token_ids, n, z, zabs, stream));
+  if (phase == 0) {
+    DSV4G_TRY(dsv4g_quant_fp8_act(w.qx, w.qxs, x, H, n, stream));
+    return dsv4g_router(w.idx, w.wt, x, L, token_ids, n, w.z, w.zabs, stream);
+  }
+  if (phase == 2)
+    return dsv4g_swiglu_quant(w.qy, w.qys, w.gu, w.wt, K, n * (K + 1), I,
+                              (float)(int)L->swiglu_limit, stream);
+  if (phase == 4) {
+    const size_t total = (size_t)n * H;
+    hipLaunchKernelGGL(k_combine, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, out,
+                       w.ro, n, K, H);
+    return dsv4g_check_launch("combine");
+  }
+  if (phase != 1 && phase != 3) return dsv4g_fail(DSV4G_EINVAL, "moe_decode: bad phase %d", phase);
   ExpertPass p = {};
-  p.idx = idx;
+  p.idx = w.idx;
   p.experts = L->experts;
   p.expert_stride = L->expert_stride;
   p.scale_run = L->scale_run;
@@ -485,53 +495,52 @@ int dsv4g_moe_forward(float *out, const float *x, const DSV4GLayer *L, const int
   p.sh_s[0] = L->sh1_s;
   p.sh_s[1] = L->sh3_s;
   p.sh_s[2] = L->sh2_s;
-  p.qx = qx;
-  p.qxs = qxs;
-  p.qy = qy;
-  p.qys = qys;
+  p.qx = w.qx;
+  p.qxs = w.qxs;
+  p.qy = w.qy;
+  p.qys = w.qys;
   p.n = n;
   p.K = K;
   p.H = H;
   p.I = I;
   p.E = L->n_experts;
-  // phase 0: gate/up
-  {
-    int G = H / 32, gp = 1;
-    while (gp < G) gp <<= 1;
-    int tr = FP4_LDS_ENTRIES / gp;
-    if (tr > 256) tr = 256;
-    p.phase = 0;
-    p.out = gu;
-    p.fp4_tiles = (I + tr - 1) / tr;
-    p.fp8_tiles = (I + FP8_TR - 1) / FP8_TR;
-    const int blocks = n * K * 2 * p.fp4_tiles + n * 2 * p.fp8_tiles;
-    hipLaunchKernelGGL(k_expert_pass, dim3(blocks), dim3(256), 0, st, p);
-    DSV4G_TRY(dsv4g_check_launch("expert_pass(gate/up)"));
-  }
-  DSV4G_TRY(dsv4g_swiglu_quant(qy, qys, gu, wt, K, n * (K + 1), I,
-                               (float)(int)L->swiglu_limit, stream));
-  {
-    int G = I / 32, gp = 1;
-    while (gp < G) gp <<= 1;
-    int tr = FP4_LDS_ENTRIES / gp;
-    if (tr > 256) tr = 256;
-    p.phase = 1;
-    p.out = ro;
-    p.fp4_tiles = (H + tr - 1) / tr;
-    p.fp8_tiles = (H + FP8_TR - 1) / FP8_TR;
-    const int blocks = n * K * p.fp4_tiles + n * p.fp8_tiles;
-    hipLaunchKernelGGL(k_expert_pass, dim3(blocks), dim3(256), 0, st, p);
-    DSV4G_TRY(dsv4g_check_launch("expert_pass(down)"));
-  }
-  const size_t total = (size_t)n * H;
-  hipLaunchKernelGGL(k_combine, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, out, ro,
-                     n, K, H);
-  DSV4G_TRY(dsv4g_check_launch("combine"));
-  if (idx_out) DSV4G_HIP(hipMemcpyAsync(idx_out, idx, (size_t)n * K * sizeof(int),
-                                        hipMemcpyDeviceToDevice, st));
-  if (wt_out) DSV4G_HIP(hipMemcpyAsync(wt_out, wt, (size_t)n * K * sizeof(float),
-                                       hipMemcpyDeviceToDevice, st));
+  const int in = phase == 1 ? H : I, rows = phase == 1 ? I : H, nmat = phase == 1 ? 2 : 1;
+  int G = in / 32, gp = 1;
+  while (gp < G) gp <<= 1;
+  int tr = FP4_LDS_ENTRIES / gp;
+  if (tr > 256) tr = 256;
+  p.phase = phase == 1 ? 0 : 1;
+  p.out = phase == 1 ? w.gu : w.ro;
+  p.fp4_tiles = (rows + tr - 1) / tr;
+  p.fp8_tiles = (rows + FP8_TR - 1) / FP8_TR;
+  const int blocks = n * K * nmat * p.fp4_tiles + n * nmat * p.fp8_tiles;
+  hipLaunchKernelGGL(k_expert_pass, dim3(blocks), dim3(256), 0, st, p);
+  return dsv4g_check_launch(phase == 1 ? "expert_pass(gate/up)" : "expert_pass(down)");
+}
+
+// Routing of the last decode call made with this workspace.
+int dsv4g_moe_decode_routing(int *idx_out, float *wt_out, const DSV4GLayer *L, int n_tokens,
+                             void *workspace, void *stream) {
+  const MoeWs w = moe_ws_layout(L, n_tokens, workspace);
+  hipStream_t st = (hipStream_t)stream;
+  if (idx_out)
+    DSV4G_HIP(hipMemcpyAsync(idx_out, w.idx, (size_t)n_tokens * L->topk * sizeof(int),
+                             hipMemcpyDeviceToDevice, st));
+  if (wt_out)
+    DSV4G_HIP(hipMemcpyAsync(wt_out, w.wt, (size_t)n_tokens * L->topk * sizeof(float),
+                             hipMemcpyDeviceToDevice, st));
   return 0;
+}
+
+// Decode-path MoE layer: moe_forward per token, bit-exact. idx/wt (optional,
+// device) receive the routing.
+int dsv4g_moe_forward(float *out, const float *x, const DSV4GLayer *L, const int *token_ids,
+                      int n_tokens, void *workspace, size_t workspace_bytes, int *idx_out,
+                      float *wt_out, void *stream) {
+  for (int phase = 0; phase < 5; ++phase)
+    DSV4G_TRY(dsv4g_moe_decode_phase(phase, out, x, L, token_ids, n_tokens, workspace,
+                                     workspace_bytes, stream));
+  return dsv4g_moe_decode_routing(idx_out, wt_out, L, n_tokens, workspace, stream);
 }
 
 }  // extern "C"

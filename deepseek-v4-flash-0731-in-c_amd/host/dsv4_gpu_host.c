@@ -436,11 +436,6 @@ void dsv4_gemv_fp4(float *y, const float *qx, const float *qscale, const uint8_t
 }
 
 /* -------------------------------------------------------------- router ---- */
-int dsv4g_router_public(int *idx, float *wt, const float *x, const uint16_t *gate,
-                        const float *bias, const int64_t *tid2eid, const int *token_id,
-                        int hidden, int n_experts, int topk, int hash_layer,
-                        float route_scale, float *z_ws, float *zabs_ws, void *stream);
-
 void dsv4_router(int *idx, float *wt, const float *x, const float *gate, const float *bias,
                  const int64_t *tid2eid, int token_id, int hidden, int n_experts, int topk,
                  int hash_layer, float route_scale, float rms_eps)

@@ -52,6 +52,8 @@ _SIGS = {
                             _vp],
     "dsv4g_swiglu_quant": [_vp, _vp, _vp, _vp, _I, _I, _I, _F, _vp],
     "dsv4g_moe_forward": [_vp, _vp, C.POINTER(DSV4GLayer), _vp, _I, _vp, _Z, _vp, _vp, _vp],
+    "dsv4g_moe_decode_phase": [_I, _vp, _vp, C.POINTER(DSV4GLayer), _vp, _I, _vp, _Z, _vp],
+    "dsv4g_moe_decode_routing": [_vp, _vp, C.POINTER(DSV4GLayer), _I, _vp, _vp],
     "dsv4g_quant_fp4_rows": [_vp, _vp, _vp, _I, _I, _vp],
     "dsv4g_quant_fp8_blocks": [_vp, _vp, _vp, _I, _I, _I, _vp],
 }
@@ -233,6 +235,11 @@ class GpuLib:
         self._call("dsv4g_moe_forward", _ptr(out), _ptr(x), C.byref(L), _ptr(token_ids), n,
                    _ptr(workspace), workspace.numel(), _ptr(idx), _ptr(wt), self._stream())
         return out, idx, wt
+
+    def moe_decode_phase(self, phase, layer, x, out, workspace, token_ids=None):
+        self._call("dsv4g_moe_decode_phase", phase, _ptr(out), _ptr(x), C.byref(layer.struct),
+                   _ptr(token_ids), x.shape[0], _ptr(workspace), workspace.numel(),
+                   self._stream())
 
     def quant_fp4_rows(self, w, packed, scales):
         rows, cols = w.shape

@@ -130,6 +130,13 @@ int dsv4g_gemv_fp4_float(float *y, const float *qx, const float *qscale, const u
 int dsv4g_router(int *idx, float *wt, const float *x, const DSV4GLayer *L,
                  const int *token_ids, int n_tokens, float *z_ws, float *zabs_ws,
                  void *stream);
+/* Public dsv4_router semantics (src/dsv4/dsv4_ops.c:473-545) for one token:
+ * unfused logits, weights (score * (1/sum)) * route_scale. For a hash layer
+ * tid2eid points at the token's row and token_id at a device 0. */
+int dsv4g_router_public(int *idx, float *wt, const float *x, const uint16_t *gate,
+                        const float *bias, const int64_t *tid2eid, const int *token_id,
+                        int hidden, int n_experts, int topk, int hash_layer,
+                        float route_scale, float *z_ws, float *zabs_ws, void *stream);
 /* routed_swiglu_quant (src/dsv4/dsv4_model.c:6239-6287) over n_slots slots;
  * slot s reads gate at gate_up + 2*s*inter and up right after it. Weights:
  * K > 0: slots are [token][K+1], slot (t,k<K) uses wt[t*K+k], slot K uses 1;
@@ -145,6 +152,14 @@ size_t dsv4g_moe_workspace_bytes(const DSV4GLayer *L, int n_tokens);
 int dsv4g_moe_forward(float *out, const float *x, const DSV4GLayer *L, const int *token_ids,
                       int n_tokens, void *workspace, size_t workspace_bytes, int *idx_out,
                       float *wt_out, void *stream);
+/* The same layer as five ordered phases (0 quant + router, 1 gate/up GEMVs,
+ * 2 SwiGLU + requant, 3 down GEMVs, 4 combine), for callers that interleave
+ * or time them; dsv4g_moe_decode_routing copies the routing of the last call. */
+int dsv4g_moe_decode_phase(int phase, float *out, const float *x, const DSV4GLayer *L,
+                           const int *token_ids, int n_tokens, void *workspace,
+                           size_t workspace_bytes, void *stream);
+int dsv4g_moe_decode_routing(int *idx_out, float *wt_out, const DSV4GLayer *L, int n_tokens,
+                             void *workspace, void *stream);
 
 /* Synthetic-checkpoint quantisers (the reference ships none in C):
  * FP4 rows with per-32 E8M0 scales; FP8 128x128 blocks with E8M0 codes
