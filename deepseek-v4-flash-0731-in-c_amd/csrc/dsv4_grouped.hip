@@ -1,0 +1,932 @@
+// dsv4_grouped.hip - the batched MoE layer for gfx950 (speculative verify and
+// prefill): moe_forward_batch (src/dsv4/dsv4_model.c:6812-7117) as a grouped
+// GEMM on the CDNA4 block-scaled MFMA.
+//
+// Pipeline (one stream):
+//   1. activations -> FP8 E4M3 codes + per-128 E8M0 scale codes
+//      (the reference's activation quant, exact);
+//   2. router: BF16 MFMA logits with sum|g*x| for a rigorous error bound,
+//      candidate experts per token, exact sequential fmaf chains for the
+//      candidates (packed one per lane across tokens), then the reference's
+//      selection and weights - indices and weights identical to the
+//      reference;
+//   3. dispatch: deterministic per-expert position lists (ascending token, as
+//      expert_forward_batch_routes gathers them, src/dsv4/dsv4_model.c:6498-6524)
+//      and a token-tile table; the shared expert is expert number E;
+//   4. gate/up grouped GEMM: V_MFMA_SCALE_F32_16X16X128_F8F6F4 with FP4 (routed)
+//      or FP8 (shared) weights x FP8 activations, E8M0 block scales applied by
+//      the MFMA; epilogue = BF16 round of gate/up, SwiGLU, x route weight,
+//      BF16 round, per-128 FP8 requant (one 128-row tile = one requant group);
+//   5. down grouped GEMM, BF16 outputs per (token, route);
+//   6. per-token combine in ascending expert id + shared, BF16.
+// Accumulation inside an MFMA differs from the reference's sequential fp32
+// order, so expert outputs agree to fp32 rounding (checked at 1e-3), not bit
+// for bit; routing is exact.
+#include "dsv4_device.h"
+#include "dsv4_gpu_internal.h"
+
+using namespace dsv4;
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+namespace dsv4 {
+
+#define GT_TN 64     // positions (tokens) per tile: 4 MFMA column fragments
+#define GT_TM 128    // weight rows per tile: 4 waves x 2 fragments of 16
+#define GT_BROW 144  // LDS bytes per staged activation row (128 + 16 pad)
+#define MX_FP8 0
+#define MX_FP4 4
+
+__device__ __forceinline__ v8i u4x2_to_v8i(uint4 a, uint4 b) {
+  v8i r;
+  r[0] = (int)a.x; r[1] = (int)a.y; r[2] = (int)a.z; r[3] = (int)a.w;
+  r[4] = (int)b.x; r[5] = (int)b.y; r[6] = (int)b.z; r[7] = (int)b.w;
+  return r;
+}
+
+template <int AFMT>
+__device__ __forceinline__ v4f mx_mfma(v8i a, v8i b, v4f c, int sa, int sb) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, AFMT, MX_FP8, 0, sa, 0, sb);
+}
+
+__device__ __forceinline__ uint32_t scale_code(float s) { return (f2u(s) >> 23) & 0xFFu; }
+
+__global__ void k_fill_zero_i32(int *p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
+// ------------------------------------------------------------ probes ----
+// One 16x16 MFMA tile from row-major operands, for layout validation.
+// A: [16][K] bytes (FP8) or [16][K/2] packed FP4; B: [16][K] FP8 (one row per
+// output column); scales [16][4] E8M0 codes. D: [16][16] row-major.
+__global__ void k_probe_mx(float *D, const uint8_t *A, const uint8_t *B, const uint8_t *sa,
+                           const uint8_t *sb, int afmt) {
+  const int l = threadIdx.x, i = l % 16, kb = l / 16;
+  uint4 a0, a1 = make_uint4(0, 0, 0, 0);
+  if (afmt == MX_FP4) {
+    a0 = *reinterpret_cast<const uint4 *>(A + i * 64 + kb * 16);
+  } else {
+    a0 = *reinterpret_cast<const uint4 *>(A + i * 128 + kb * 32);
+    a1 = *reinterpret_cast<const uint4 *>(A + i * 128 + kb * 32 + 16);
+  }
+  const uint4 b0 = *reinterpret_cast<const uint4 *>(B + i * 128 + kb * 32);
+  const uint4 b1 = *reinterpret_cast<const uint4 *>(B + i * 128 + kb * 32 + 16);
+  v4f acc = {0.f, 0.f, 0.f, 0.f};
+  if (afmt == MX_FP4)
+    acc = mx_mfma<MX_FP4>(u4x2_to_v8i(a0, a1), u4x2_to_v8i(b0, b1), acc, sa[i * 4 + kb],
+                          sb[i * 4 + kb]);
+  else
+    acc = mx_mfma<MX_FP8>(u4x2_to_v8i(a0, a1), u4x2_to_v8i(b0, b1), acc, sa[i * 4 + kb],
+                          sb[i * 4 + kb]);
+  for (int v = 0; v < 4; ++v) D[(4 * kb + v) * 16 + i] = acc[v];
+}
+
+// BF16 16x16x32: A [16][32], B [16][32] bf16 bits.
+__global__ void k_probe_bf16(float *D, const uint16_t *A, const uint16_t *B) {
+  const int l = threadIdx.x, i = l % 16, kb = l / 16;
+  const uint4 a = *reinterpret_cast<const uint4 *>(A + i * 32 + kb * 8);
+  const uint4 b = *reinterpret_cast<const uint4 *>(B + i * 32 + kb * 8);
+  v4f acc = {0.f, 0.f, 0.f, 0.f};
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                __builtin_bit_cast(bf16x8, b), acc, 0, 0, 0);
+  for (int v = 0; v < 4; ++v) D[(4 * kb + v) * 16 + i] = acc[v];
+}
+
+// ------------------------------------------------------- batch quant ----
+// Per (token, 128-group) wave: the reference activation quant; writes E4M3
+// codes and the E8M0 code of the power-of-two scale; flags tokens whose x is
+// not BF16-valued (the router bound then widens for them).
+__global__ __launch_bounds__(64) void k_batch_quant(uint8_t *__restrict__ x8,
+                                                    uint8_t *__restrict__ x8s,
+                                                    int *__restrict__ not_bf16,
+                                                    const float *__restrict__ x, int H) {
+  const int g = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
+  const float *xr = x + (size_t)t * H + g * 128;
+  const float a = xr[lane], b = xr[lane + 64];
+  const float amax = wave_max(fmaxf(fabsf(a), fabsf(b)));
+  const float scale = act_scale(amax);
+  const float inv = 1.0f / scale;
+  uint8_t *q = x8 + (size_t)t * H + g * 128;
+  q[lane] = (uint8_t)e4m3_code(quant_e4m3(a, inv));
+  q[lane + 64] = (uint8_t)e4m3_code(quant_e4m3(b, inv));
+  if (lane == 0) x8s[(size_t)t * (H / 128) + g] = (uint8_t)scale_code(scale);
+  const bool exact = bf16_round(a) == a && bf16_round(b) == b;
+  if (__any(!exact) && lane == 0) not_bf16[t] = 1;
+}
+
+// ---------------------------------------------------------- router ------
+// Approximate logits and sum|g*x| with BF16 MFMA. Tile: 64 tokens x 64
+// experts; wave w takes experts e0+16w..+15 against all 64 tokens.
+__global__ __launch_bounds__(256) void k_router_logits_mfma(float *__restrict__ z,
+                                                            float *__restrict__ zabs,
+                                                            const float *__restrict__ x,
+                                                            const uint16_t *__restrict__ G,
+                                                            int T, int H, int E) {
+  __shared__ __align__(16) uint16_t xs[64 * 40];  // [token][32 + 8 pad] bf16
+  const int t0 = blockIdx.x * 64, e0 = blockIdx.y * 64;
+  const int tid = threadIdx.x, wv = tid / 64, l = tid % 64;
+  const int erow = e0 + 16 * wv + l % 16;
+  v4f acc[4], aab[4];
+  for (int f = 0; f < 4; ++f) {
+    acc[f] = (v4f){0.f, 0.f, 0.f, 0.f};
+    aab[f] = (v4f){0.f, 0.f, 0.f, 0.f};
+  }
+  const int st = tid / 4, sq = tid % 4;  // staging: token st, 8 columns sq
+  for (int k0 = 0; k0 < H; k0 += 32) {
+    __syncthreads();
+    {
+      uint32_t p[4] = {0, 0, 0, 0};
+      if (t0 + st < T) {
+        const float4 u = *reinterpret_cast<const float4 *>(x + (size_t)(t0 + st) * H + k0 + 8 * sq);
+        const float4 v = *reinterpret_cast<const float4 *>(x + (size_t)(t0 + st) * H + k0 + 8 * sq + 4);
+        // BF16-valued inputs convert exactly (truncation of zero bits)
+        p[0] = (f2u(u.x) >> 16) | (f2u(u.y) & 0xFFFF0000u);
+        p[1] = (f2u(u.z) >> 16) | (f2u(u.w) & 0xFFFF0000u);
+        p[2] = (f2u(v.x) >> 16) | (f2u(v.y) & 0xFFFF0000u);
+        p[3] = (f2u(v.z) >> 16) | (f2u(v.w) & 0xFFFF0000u);
+      }
+      *reinterpret_cast<uint4 *>(xs + st * 40 + 8 * sq) = make_uint4(p[0], p[1], p[2], p[3]);
+    }
+    __syncthreads();
+    uint4 a = make_uint4(0, 0, 0, 0);
+    if (erow < E) a = *reinterpret_cast<const uint4 *>(G + (size_t)erow * H + k0 + 8 * (l / 16));
+    const uint4 aa = make_uint4(a.x & 0x7FFF7FFFu, a.y & 0x7FFF7FFFu, a.z & 0x7FFF7FFFu,
+                                a.w & 0x7FFF7FFFu);
+#pragma unroll
+    for (int f = 0; f < 4; ++f) {
+      const uint4 b = *reinterpret_cast<const uint4 *>(xs + (16 * f + l % 16) * 40 + 8 * (l / 16));
+      const uint4 bb = make_uint4(b.x & 0x7FFF7FFFu, b.y & 0x7FFF7FFFu, b.z & 0x7FFF7FFFu,
+                                  b.w & 0x7FFF7FFFu);
+      acc[f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                       __builtin_bit_cast(bf16x8, b), acc[f], 0, 0, 0);
+      aab[f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, aa),
+                                                       __builtin_bit_cast(bf16x8, bb), aab[f], 0, 0, 0);
+    }
+  }
+  for (int f = 0; f < 4; ++f) {
+    const int t = t0 + 16 * f + l % 16;
+    if (t >= T) continue;
+    for (int v = 0; v < 4; ++v) {
+      const int e = e0 + 16 * wv + 4 * (l / 16) + v;
+      if (e < E) {
+        z[(size_t)t * E + e] = acc[f][v];
+        zabs[(size_t)t * E + e] = aab[f][v];
+      }
+    }
+  }
+}
+
+// Wave argmax with the reference's tie rule (largest value, lowest index).
+__device__ __forceinline__ void wave_argmax(float &v, int &i) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(v, o, 64);
+    const int oi = __shfl_xor(i, o, 64);
+    if (ov > v || (ov == v && oi >= 0 && (i < 0 || oi < i))) {
+      v = ov;
+      i = oi;
+    }
+  }
+}
+
+__device__ __forceinline__ float gamma_n2(int n) {
+  const double nu = (double)n * 0x1p-24;
+  return (float)(nu / (1.0 - nu));
+}
+
+// One wave per token: approximate choices, the k-th best, and every expert
+// within the rigorous error margin of it -> candidate list (ascending id).
+__global__ __launch_bounds__(256) void k_router_cand(int *__restrict__ cand,
+                                                     int *__restrict__ ncand,
+                                                     const float *__restrict__ z,
+                                                     const float *__restrict__ zabs,
+                                                     const int *__restrict__ not_bf16,
+                                                     const float *__restrict__ bias,
+                                                     const int64_t *__restrict__ tid2eid,
+                                                     const int *__restrict__ token_ids, int T,
+                                                     int H, int E, int K) {
+  const int t = blockIdx.x * 4 + threadIdx.x / 64, l = threadIdx.x % 64;
+  if (t >= T) return;
+  int *ct = cand + (size_t)t * E;
+  if (tid2eid) {
+    if (l < K) ct[l] = (int)tid2eid[(size_t)token_ids[t] * K + l];
+    if (l == 0) ncand[t] = K;
+    return;
+  }
+  const float *zt = z + (size_t)t * E, *at = zabs + (size_t)t * E;
+  constexpr int PER = 16;  // E <= 1024
+  float ch[PER];
+  float amax = 0.0f;
+  for (int j = 0; j < PER; ++j) {
+    const int e = l + 64 * j;
+    ch[j] = -__builtin_inff();
+    if (e < E) {
+      const float c = sqrt_softplus(zt[e]) + (bias ? bias[e] : 0.0f);
+      ch[j] = c == c ? c : -__builtin_inff();  // NaN is never selected
+      amax = fmaxf(amax, at[e]);
+    }
+  }
+  amax = wave_max(amax) * 1.001f;
+  // any-order summation bound, twice (approximate and sequential), plus the
+  // BF16 conversion of a non-BF16 input; |d score/dz| <= 1/2; score slack
+  float bound_z = 2.0f * gamma_n2(H) * amax;
+  if (not_bf16[t]) bound_z += 0x1p-8f * amax;
+  const float delta = 2.0f * (0.5f * bound_z + 1e-5f);
+  unsigned long long used = 0ull;  // bit j: expert l+64j taken
+  float kth = -__builtin_inff();
+  for (int k = 0; k < K; ++k) {
+    float bv = -__builtin_inff();
+    int bi = -1;
+    for (int j = 0; j < PER; ++j) {
+      const int e = l + 64 * j;
+      if (e < E && !((used >> j) & 1ull) && (ch[j] > bv || (ch[j] == bv && bi < 0))) {
+        bv = ch[j];
+        bi = e;
+      }
+    }
+    wave_argmax(bv, bi);
+    if (bi >= 0 && (bi % 64) == l) used |= 1ull << (bi / 64);
+    kth = bv;
+  }
+  const float thr = kth - delta;
+  int base = 0;
+  for (int j = 0; j < PER; ++j) {
+    const int e = l + 64 * j;
+    const bool take = e < E && ch[j] >= thr;
+    const unsigned long long m = __ballot(take);
+    const int before = __popcll(m & ((1ull << l) - 1ull));
+    if (take) ct[base + before] = e;
+    base += __popcll(m);
+  }
+  // candidates were written in order e = l + 64j, i.e. j-major: re-sort
+  // ascending (small lists; one lane)
+  if (l == 0) {
+    for (int i = 1; i < base; ++i) {
+      const int v = ct[i];
+      int j = i - 1;
+      while (j >= 0 && ct[j] > v) {
+        ct[j + 1] = ct[j];
+        --j;
+      }
+      ct[j + 1] = v;
+    }
+    ncand[t] = base;
+  }
+}
+
+// Exclusive prefix sum of n[0..T) into off[0..T], one workgroup.
+__global__ __launch_bounds__(1024) void k_scan_counts(int *__restrict__ off,
+                                                      const int *__restrict__ n, int T) {
+  __shared__ int part[1024];
+  __shared__ int carry;
+  if (threadIdx.x == 0) carry = 0;
+  __syncthreads();
+  for (int b = 0; b < T; b += 1024) {
+    const int i = b + threadIdx.x;
+    int v = i < T ? n[i] : 0;
+    part[threadIdx.x] = v;
+    __syncthreads();
+    for (int o = 1; o < 1024; o <<= 1) {
+      const int add = threadIdx.x >= o ? part[threadIdx.x - o] : 0;
+      __syncthreads();
+      part[threadIdx.x] += add;
+      __syncthreads();
+    }
+    if (i < T) off[i] = carry + part[threadIdx.x] - v;
+    __syncthreads();
+    if (threadIdx.x == 1023) carry += part[1023];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) off[T] = carry;
+}
+
+// Exact logits of every candidate: the reference's column-order fmaf chain
+// (src/dsv4/dsv4_model.c:298-303), one lane per (token, candidate), packed
+// across tokens; grid-stride over all chains.
+__global__ __launch_bounds__(256) void k_router_chains(float *__restrict__ cscore,
+                                                       float *__restrict__ cchoice,
+                                                       const int *__restrict__ cand,
+                                                       const int *__restrict__ chain_off,
+                                                       const float *__restrict__ x,
+                                                       const uint16_t *__restrict__ G,
+                                                       const float *__restrict__ bias, int T,
+                                                       int H, int E) {
+  const int total = chain_off[T];
+  for (int g = blockIdx.x * blockDim.x + threadIdx.x; g < total; g += gridDim.x * blockDim.x) {
+    int lo = 0, hi = T;  // chain_off[lo] <= g < chain_off[lo+1]
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) / 2;
+      if (chain_off[mid] <= g) lo = mid;
+      else hi = mid;
+    }
+    const int t = lo, c = g - chain_off[t];
+    const int e = cand[(size_t)t * E + c];
+    float sc = 0.0f, ch = -__builtin_inff();
+    if (e >= 0 && e < E) {
+      const uint16_t *gr = G + (size_t)e * H;
+      const float *xr = x + (size_t)t * H;
+      float acc = 0.0f;
+      uint4 w0 = *reinterpret_cast<const uint4 *>(gr);
+      for (int c0 = 0; c0 < H; c0 += 8) {
+        const uint4 w = w0;
+        if (c0 + 8 < H) w0 = *reinterpret_cast<const uint4 *>(gr + c0 + 8);
+        const float4 xa = *reinterpret_cast<const float4 *>(xr + c0);
+        const float4 xb = *reinterpret_cast<const float4 *>(xr + c0 + 4);
+        acc = fmaf(u2f(w.x << 16), xa.x, acc);
+        acc = fmaf(u2f(w.x & 0xFFFF0000u), xa.y, acc);
+        acc = fmaf(u2f(w.y << 16), xa.z, acc);
+        acc = fmaf(u2f(w.y & 0xFFFF0000u), xa.w, acc);
+        acc = fmaf(u2f(w.z << 16), xb.x, acc);
+        acc = fmaf(u2f(w.z & 0xFFFF0000u), xb.y, acc);
+        acc = fmaf(u2f(w.w << 16), xb.z, acc);
+        acc = fmaf(u2f(w.w & 0xFFFF0000u), xb.w, acc);
+      }
+      sc = sqrt_softplus(acc);
+      ch = sc + (bias ? bias[e] : 0.0f);
+    }
+    cscore[(size_t)t * E + c] = sc;
+    cchoice[(size_t)t * E + c] = ch;
+  }
+}
+
+// Per token: the reference selection over the candidates (ascending id,
+// strict '>'), weights from the unbiased scores, exchange sort by id
+// (src/dsv4/dsv4_model.c:6866-6906).
+__global__ void k_router_finalize(int *__restrict__ idx, float *__restrict__ wt,
+                                  const int *__restrict__ cand, const int *__restrict__ ncand,
+                                  const float *__restrict__ cscore,
+                                  const float *__restrict__ cchoice, int hash, int T, int E,
+                                  int K, float route_scale) {
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= T) return;
+  const int nc = ncand[t];
+  const int *ct = cand + (size_t)t * E;
+  const float *cs = cscore + (size_t)t * E, *cc = cchoice + (size_t)t * E;
+  int order[32];
+  float sel[32], w[32];
+  uint32_t used[32] = {0};
+  for (int k = 0; k < K; ++k) {
+    if (hash) {
+      order[k] = ct[k];
+      sel[k] = cs[k];
+      continue;
+    }
+    int bi = -1;
+    float bv = -__builtin_inff();
+    for (int i = 0; i < nc; ++i)
+      if (!((used[i >> 5] >> (i & 31)) & 1u) && cc[i] > bv) {
+        bv = cc[i];
+        bi = i;
+      }
+    if (bi >= 0) used[bi >> 5] |= 1u << (bi & 31);
+    order[k] = bi >= 0 ? ct[bi] : -1;
+    sel[k] = bi >= 0 ? cs[bi] : 0.0f;
+  }
+  float sum = 0.0f;
+  for (int k = 0; k < K; ++k) sum += sel[k];
+  if (sum > 0.0f) {
+    const float rs = route_scale / sum;
+    for (int k = 0; k < K; ++k) w[k] = sel[k] * rs;
+  } else {
+    for (int k = 0; k < K; ++k) w[k] = 0.0f;
+  }
+  for (int i = 0; i < K; ++i)
+    for (int j = i + 1; j < K; ++j)
+      if (order[j] < order[i]) {
+        const int ti = order[i];
+        order[i] = order[j];
+        order[j] = ti;
+        const float tw = w[i];
+        w[i] = w[j];
+        w[j] = tw;
+      }
+  for (int k = 0; k < K; ++k) {
+    idx[(size_t)t * K + k] = order[k];
+    wt[(size_t)t * K + k] = w[k];
+  }
+}
+
+// -------------------------------------------------------- dispatch -------
+// counts[e] = routes to expert e (block e < E); counts[E] = T (shared).
+__global__ __launch_bounds__(256) void k_dispatch_count(int *__restrict__ counts,
+                                                        const int *__restrict__ idx, int T,
+                                                        int K, int E) {
+  __shared__ int red[4];
+  const int e = blockIdx.x;
+  if (e == E) {
+    if (threadIdx.x == 0) counts[E] = T;
+    return;
+  }
+  int c = 0;
+  for (int i = threadIdx.x; i < T * K; i += 256) c += idx[i] == e;
+  for (int o = 32; o > 0; o >>= 1) c += __shfl_xor(c, o, 64);
+  if (threadIdx.x % 64 == 0) red[threadIdx.x / 64] = c;
+  __syncthreads();
+  if (threadIdx.x == 0) counts[e] = red[0] + red[1] + red[2] + red[3];
+}
+
+// Block e: its position and tile offsets (prefix over lower experts) and its
+// position list in ascending (token, route) order.
+__global__ __launch_bounds__(256) void k_dispatch_fill(
+    int *__restrict__ pos_off, int *__restrict__ tile_off, int *__restrict__ pos_token,
+    int *__restrict__ pos_route, float *__restrict__ pos_wt, const int *__restrict__ counts,
+    const int *__restrict__ idx, const float *__restrict__ wt, int T, int K, int E) {
+  __shared__ int red[8];
+  __shared__ int run;
+  const int e = blockIdx.x, tid = threadIdx.x;
+  int po = 0, to = 0;
+  for (int i = tid; i < e; i += 256) {
+    po += counts[i];
+    to += (counts[i] + GT_TN - 1) / GT_TN;
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    po += __shfl_xor(po, o, 64);
+    to += __shfl_xor(to, o, 64);
+  }
+  if (tid % 64 == 0) {
+    red[tid / 64] = po;
+    red[4 + tid / 64] = to;
+  }
+  __syncthreads();
+  po = red[0] + red[1] + red[2] + red[3];
+  to = red[4] + red[5] + red[6] + red[7];
+  if (tid == 0) {
+    pos_off[e] = po;
+    tile_off[e] = to;
+    if (e == E) {
+      pos_off[E + 1] = po + T;
+      tile_off[E + 1] = to + (T + GT_TN - 1) / GT_TN;
+    }
+    run = 0;
+  }
+  __syncthreads();
+  if (e == E) {
+    for (int t = tid; t < T; t += 256) {
+      pos_token[po + t] = t;
+      pos_route[po + t] = K;
+      pos_wt[po + t] = 1.0f;
+    }
+    return;
+  }
+  __shared__ int wtot[4];
+  const int wv = tid / 64, l = tid % 64;
+  for (int b = 0; b < T * K; b += 256) {
+    const int i = b + tid;
+    const bool hit = i < T * K && idx[i] == e;
+    const unsigned long long m = __ballot(hit);
+    const int before = __popcll(m & ((1ull << l) - 1ull));
+    if (l == 0) wtot[wv] = __popcll(m);
+    __syncthreads();
+    int woff = 0;
+    for (int q = 0; q < wv; ++q) woff += wtot[q];
+    if (hit) {
+      const int p = po + run + woff + before;
+      pos_token[p] = i / K;
+      pos_route[p] = i % K;
+      pos_wt[p] = wt[i];
+    }
+    __syncthreads();
+    if (tid == 0) run += wtot[0] + wtot[1] + wtot[2] + wtot[3];
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------- grouped GEMMs ------
+struct GroupedArgs {
+  const uint8_t *experts;
+  size_t expert_stride, scale_run;
+  const uint8_t *shw[3], *shs[3];
+  const int *tile_off, *pos_off, *pos_token, *pos_route;
+  const float *pos_wt;
+  const uint8_t *x8, *x8s;  // [T][H] codes, [T][H/128] scale codes
+  uint8_t *y8, *y8s;        // [P][I], [P][I/128]
+  uint16_t *ro;             // [T][K+1][H] BF16 bits
+  int H, I, E, K, T, row_tiles;
+  float limit;
+};
+
+// Locate the tile: expert e with tile_off[e] <= tt < tile_off[e+1].
+__device__ __forceinline__ int tile_expert(const int *tile_off, int E, int tt) {
+  int lo = 0, hi = E + 1;
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) / 2;
+    if (tile_off[mid] <= tt) lo = mid;
+    else hi = mid;
+  }
+  return lo;
+}
+
+// Load one A fragment (16 rows x 128 K) for lane l: FP4 16 bytes, FP8 32.
+template <int AFMT>
+__device__ __forceinline__ v8i load_a(const uint8_t *W, const uint8_t *S, int row, int in,
+                                      int kw, int l, int &sc) {
+  uint4 a0, a1 = make_uint4(0, 0, 0, 0);
+  if (AFMT == MX_FP4) {
+    a0 = *reinterpret_cast<const uint4 *>(W + (size_t)row * (in / 2) + kw * 64 + (l / 16) * 16);
+    sc = S[(size_t)row * (in / 32) + kw * 4 + l / 16];
+  } else {
+    const uint8_t *p = W + (size_t)row * in + kw * 128 + (l / 16) * 32;
+    a0 = *reinterpret_cast<const uint4 *>(p);
+    a1 = *reinterpret_cast<const uint4 *>(p + 16);
+    sc = S[(size_t)(row / 128) * (in / 128) + kw];
+  }
+  if (sc == 255) {  // NaN scale: the reference skips the block
+    a0 = make_uint4(0, 0, 0, 0);
+    a1 = a0;
+    sc = 127;
+  }
+  return u4x2_to_v8i(a0, a1);
+}
+
+// Stage 64 activation rows (128 bytes of window kw) into LDS.
+__device__ __forceinline__ void stage_b(uint8_t *bt, const uint8_t *src, const int *rows,
+                                        int in, int kw) {
+  const int tid = threadIdx.x, j = tid >> 2, q = tid & 3;
+  uint4 u0 = make_uint4(0, 0, 0, 0), u1 = u0;
+  const int r = rows[j];
+  if (r >= 0) {
+    const uint8_t *p = src + (size_t)r * in + kw * 128 + q * 32;
+    u0 = *reinterpret_cast<const uint4 *>(p);
+    u1 = *reinterpret_cast<const uint4 *>(p + 16);
+  }
+  *reinterpret_cast<uint4 *>(bt + j * GT_BROW + q * 32) = u0;
+  *reinterpret_cast<uint4 *>(bt + j * GT_BROW + q * 32 + 16) = u1;
+}
+
+template <int AFMT>
+__device__ void gateup_tile(const GroupedArgs &a, int e, int rt, int p0, int np, uint8_t *bt,
+                            uint8_t *bsc, int *rows_s, float *wt_s, float (*amax_s)[GT_TN]) {
+  const int tid = threadIdx.x, wv = tid / 64, l = tid % 64;
+  const int H = a.H, I = a.I, nw = H / 128;
+  const uint8_t *Wg, *Wu, *Sg, *Su;
+  if (AFMT == MX_FP4) {
+    const uint8_t *sc = a.experts + (size_t)e * a.expert_stride;
+    const uint8_t *wt = sc + a.scale_run;
+    const size_t w1 = (size_t)I * (H / 2), w2 = (size_t)H * (I / 2);
+    const size_t s1 = (size_t)I * (H / 32), s2 = (size_t)H * (I / 32);
+    Wg = wt;
+    Wu = wt + w1 + w2;
+    Sg = sc;
+    Su = sc + s1 + s2;
+  } else {
+    Wg = a.shw[0];
+    Wu = a.shw[1];
+    Sg = a.shs[0];
+    Su = a.shs[1];
+  }
+  if (tid < GT_TN) {
+    rows_s[tid] = tid < np ? a.pos_token[p0 + tid] : -1;
+    wt_s[tid] = tid < np ? a.pos_wt[p0 + tid] : 0.0f;
+  }
+  __syncthreads();
+  for (int i = tid; i < GT_TN * nw; i += 256) {
+    const int j = i / nw, kw = i % nw;
+    bsc[j * 64 + kw] = rows_s[j] >= 0 ? a.x8s[(size_t)rows_s[j] * nw + kw] : 127;
+  }
+  const int nf = (np + 15) / 16;  // active token fragments (wave-uniform)
+  v4f ag[2][4], au[2][4];
+  for (int f = 0; f < 2; ++f)
+    for (int c = 0; c < 4; ++c) {
+      ag[f][c] = (v4f){0.f, 0.f, 0.f, 0.f};
+      au[f][c] = ag[f][c];
+    }
+  const int rbase = rt * GT_TM + 32 * wv;
+  for (int kw = 0; kw < nw; ++kw) {
+    __syncthreads();
+    stage_b(bt, a.x8, rows_s, H, kw);
+    int sg[2], su[2];
+    v8i Ag[2], Au[2];
+    for (int f = 0; f < 2; ++f) {
+      const int row = rbase + 16 * f + l % 16;
+      Ag[f] = load_a<AFMT>(Wg, Sg, row, H, kw, l, sg[f]);
+      Au[f] = load_a<AFMT>(Wu, Su, row, H, kw, l, su[f]);
+    }
+    __syncthreads();
+    for (int c = 0; c < 4; ++c) {
+      if (c >= nf) break;
+      const int j = 16 * c + l % 16;
+      const uint8_t *bp = bt + j * GT_BROW + (l / 16) * 32;
+      const v8i B = u4x2_to_v8i(*reinterpret_cast<const uint4 *>(bp),
+                                *reinterpret_cast<const uint4 *>(bp + 16));
+      const int sb = bsc[j * 64 + kw];
+      for (int f = 0; f < 2; ++f) {
+        ag[f][c] = mx_mfma<AFMT>(Ag[f], B, ag[f][c], sg[f], sb);
+        au[f][c] = mx_mfma<AFMT>(Au[f], B, au[f][c], su[f], sb);
+      }
+    }
+  }
+  // epilogue: y = bf16((silu(bf16(g)) * bf16(u)) * w), per-128 requant
+  float y[2][4][4];
+  for (int c = 0; c < 4; ++c) {
+    const int j = 16 * c + l % 16;
+    float m = 0.0f;
+    for (int f = 0; f < 2; ++f)
+      for (int v = 0; v < 4; ++v) {
+        float yy = 0.0f;
+        if (c < nf) {
+          const float g = bf16_round(ag[f][c][v]), u = bf16_round(au[f][c][v]);
+          yy = bf16_round(swiglu_t(g, u, a.limit) * wt_s[j]);
+        }
+        y[f][c][v] = yy;
+        m = fmaxf(m, fabsf(yy));
+      }
+    m = fmaxf(m, __shfl_xor(m, 16, 64));
+    m = fmaxf(m, __shfl_xor(m, 32, 64));
+    if (l < 16) amax_s[wv][j] = m;
+  }
+  __syncthreads();
+  const int ng = I / 128;
+  for (int c = 0; c < nf; ++c) {
+    const int j = 16 * c + l % 16;
+    if (j >= np) continue;
+    const float am = fmaxf(fmaxf(amax_s[0][j], amax_s[1][j]), fmaxf(amax_s[2][j], amax_s[3][j]));
+    const float scale = act_scale(am);
+    const float inv = 1.0f / scale;
+    const int pos = p0 + j;
+    for (int f = 0; f < 2; ++f) {
+      uint32_t packed = 0;
+      for (int v = 0; v < 4; ++v)
+        packed |= e4m3_code(quant_e4m3(y[f][c][v], inv)) << (8 * v);
+      const int row = rbase + 16 * f + 4 * (l / 16);
+      *reinterpret_cast<uint32_t *>(a.y8 + (size_t)pos * I + row) = packed;
+    }
+    if (wv == 0 && l < 16) a.y8s[(size_t)pos * ng + rt] = (uint8_t)scale_code(scale);
+  }
+}
+
+// grid.x = token-tile bound x row tiles (I / 128); tiles beyond the actual
+// count exit at once.
+__global__ __launch_bounds__(256) void k_grouped_gateup(GroupedArgs a) {
+  __shared__ __align__(16) uint8_t bt[GT_TN * GT_BROW];
+  __shared__ uint8_t bsc[GT_TN * 64];
+  __shared__ int rows_s[GT_TN];
+  __shared__ float wt_s[GT_TN];
+  __shared__ float amax_s[4][GT_TN];
+  const int rt = blockIdx.x % a.row_tiles, tt = blockIdx.x / a.row_tiles;
+  if (tt >= a.tile_off[a.E + 1]) return;
+  const int e = tile_expert(a.tile_off, a.E, tt);
+  const int p0 = a.pos_off[e] + (tt - a.tile_off[e]) * GT_TN;
+  const int np = min(GT_TN, a.pos_off[e + 1] - p0);
+  if (e == a.E)
+    gateup_tile<MX_FP8>(a, e, rt, p0, np, bt, bsc, rows_s, wt_s, amax_s);
+  else
+    gateup_tile<MX_FP4>(a, e, rt, p0, np, bt, bsc, rows_s, wt_s, amax_s);
+}
+
+template <int AFMT>
+__device__ void down_tile(const GroupedArgs &a, int e, int rt, int p0, int np, uint8_t *bt,
+                          uint8_t *bsc, int *rows_s) {
+  const int tid = threadIdx.x, wv = tid / 64, l = tid % 64;
+  const int H = a.H, I = a.I, nw = I / 128;
+  const uint8_t *W, *S;
+  if (AFMT == MX_FP4) {
+    const uint8_t *sc = a.experts + (size_t)e * a.expert_stride;
+    W = sc + a.scale_run + (size_t)I * (H / 2);
+    S = sc + (size_t)I * (H / 32);
+  } else {
+    W = a.shw[2];
+    S = a.shs[2];
+  }
+  if (tid < GT_TN) rows_s[tid] = tid < np ? p0 + tid : -1;  // positions are contiguous
+  __syncthreads();
+  for (int i = tid; i < GT_TN * nw; i += 256) {
+    const int j = i / nw, kw = i % nw;
+    bsc[j * 64 + kw] = rows_s[j] >= 0 ? a.y8s[(size_t)rows_s[j] * nw + kw] : 127;
+  }
+  const int nf = (np + 15) / 16;
+  v4f acc[2][4];
+  for (int f = 0; f < 2; ++f)
+    for (int c = 0; c < 4; ++c) acc[f][c] = (v4f){0.f, 0.f, 0.f, 0.f};
+  const int rbase = rt * GT_TM + 32 * wv;
+  for (int kw = 0; kw < nw; ++kw) {
+    __syncthreads();
+    stage_b(bt, a.y8, rows_s, I, kw);
+    int sa[2];
+    v8i A[2];
+    for (int f = 0; f < 2; ++f) A[f] = load_a<AFMT>(W, S, rbase + 16 * f + l % 16, I, kw, l, sa[f]);
+    __syncthreads();
+    for (int c = 0; c < 4; ++c) {
+      if (c >= nf) break;
+      const int j = 16 * c + l % 16;
+      const uint8_t *bp = bt + j * GT_BROW + (l / 16) * 32;
+      const v8i B = u4x2_to_v8i(*reinterpret_cast<const uint4 *>(bp),
+                                *reinterpret_cast<const uint4 *>(bp + 16));
+      const int sb = bsc[j * 64 + kw];
+      for (int f = 0; f < 2; ++f) acc[f][c] = mx_mfma<AFMT>(A[f], B, acc[f][c], sa[f], sb);
+    }
+  }
+  for (int c = 0; c < nf; ++c) {
+    const int j = 16 * c + l % 16;
+    if (j >= np) continue;
+    const int pos = p0 + j;
+    const int t = a.pos_token[pos], k = a.pos_route[pos];
+    uint16_t *dst = a.ro + ((size_t)t * (a.K + 1) + k) * H;
+    for (int f = 0; f < 2; ++f) {
+      const int row = rbase + 16 * f + 4 * (l / 16);
+      uint2 o;
+      o.x = (f2u(bf16_round(acc[f][c][0])) >> 16) | (f2u(bf16_round(acc[f][c][1])) & 0xFFFF0000u);
+      o.y = (f2u(bf16_round(acc[f][c][2])) >> 16) | (f2u(bf16_round(acc[f][c][3])) & 0xFFFF0000u);
+      *reinterpret_cast<uint2 *>(dst + row) = o;
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void k_grouped_down(GroupedArgs a) {
+  __shared__ __align__(16) uint8_t bt[GT_TN * GT_BROW];
+  __shared__ uint8_t bsc[GT_TN * 64];
+  __shared__ int rows_s[GT_TN];
+  const int rt = blockIdx.x % a.row_tiles, tt = blockIdx.x / a.row_tiles;
+  if (tt >= a.tile_off[a.E + 1]) return;
+  const int e = tile_expert(a.tile_off, a.E, tt);
+  const int p0 = a.pos_off[e] + (tt - a.tile_off[e]) * GT_TN;
+  const int np = min(GT_TN, a.pos_off[e + 1] - p0);
+  if (e == a.E)
+    down_tile<MX_FP8>(a, e, rt, p0, np, bt, bsc, rows_s);
+  else
+    down_tile<MX_FP4>(a, e, rt, p0, np, bt, bsc, rows_s);
+}
+
+// out[t][i] = bf16(((0 + r_0) + ... + r_{K-1}) + shared), routes in
+// ascending expert id (src/dsv4/dsv4_model.c:7096-7112).
+__global__ void k_combine_batch(float *__restrict__ out, const uint16_t *__restrict__ ro, int T,
+                                int K, int H) {
+  const size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+  if (i >= (size_t)T * H) return;
+  const size_t t = i / H, c = i % H;
+  const uint16_t *r = ro + t * (size_t)(K + 1) * H + c;
+  float acc = 0.0f;
+  for (int k = 0; k < K; ++k) acc += bf16_to_f32(r[(size_t)k * H]);
+  acc += bf16_to_f32(r[(size_t)K * H]);
+  out[i] = bf16_round(acc);
+}
+
+}  // namespace dsv4
+
+// ============================================================ C-ABI =====
+using namespace dsv4;
+
+namespace {
+struct BatchWs {
+  uint8_t *x8, *x8s, *y8, *y8s;
+  float *z, *zabs, *cscore, *cchoice, *wt, *pos_wt;
+  int *not_bf16, *cand, *ncand, *chain_off, *idx, *counts, *pos_off, *tile_off, *pos_token,
+      *pos_route;
+  uint16_t *ro;
+  size_t bytes;
+};
+
+BatchWs batch_ws_layout(const DSV4GLayer *L, int T, void *base) {
+  const size_t t = (size_t)T, K = (size_t)L->topk, E = (size_t)L->n_experts;
+  const size_t H = (size_t)L->hidden, I = (size_t)L->inter, P = t * K + t;
+  BatchWs w = {};
+  uintptr_t p = ((uintptr_t)base + 255) & ~(uintptr_t)255;
+  const uintptr_t p0 = (uintptr_t)base;
+  auto take = [&](size_t bytes) {
+    void *r = (void *)p;
+    p += (bytes + 255) & ~(size_t)255;
+    return r;
+  };
+  w.x8 = (uint8_t *)take(t * H);
+  w.x8s = (uint8_t *)take(t * (H / 128));
+  w.not_bf16 = (int *)take(t * 4);
+  w.z = (float *)take(t * E * 4);
+  w.zabs = (float *)take(t * E * 4);
+  w.cand = (int *)take(t * E * 4);
+  w.ncand = (int *)take(t * 4);
+  w.chain_off = (int *)take((t + 1) * 4);
+  w.cscore = (float *)take(t * E * 4);
+  w.cchoice = (float *)take(t * E * 4);
+  w.idx = (int *)take(t * K * 4);
+  w.wt = (float *)take(t * K * 4);
+  w.counts = (int *)take((E + 1) * 4);
+  w.pos_off = (int *)take((E + 2) * 4);
+  w.tile_off = (int *)take((E + 2) * 4);
+  w.pos_token = (int *)take(P * 4);
+  w.pos_route = (int *)take(P * 4);
+  w.pos_wt = (float *)take(P * 4);
+  w.y8 = (uint8_t *)take(P * I);
+  w.y8s = (uint8_t *)take(P * (I / 128));
+  w.ro = (uint16_t *)take(t * (K + 1) * H * 2);
+  w.bytes = (size_t)(p - p0) + 256;
+  return w;
+}
+}  // namespace
+
+extern "C" {
+
+int dsv4g_probe_mfma(int kind, float *D, const void *A, const void *B, const uint8_t *sa,
+                     const uint8_t *sb, void *stream) {
+  hipStream_t st = (hipStream_t)stream;
+  if (kind == 2)
+    hipLaunchKernelGGL(k_probe_bf16, dim3(1), dim3(64), 0, st, D, (const uint16_t *)A,
+                       (const uint16_t *)B);
+  else
+    hipLaunchKernelGGL(k_probe_mx, dim3(1), dim3(64), 0, st, D, (const uint8_t *)A,
+                       (const uint8_t *)B, sa, sb, kind == 0 ? MX_FP4 : MX_FP8);
+  return dsv4g_check_launch("probe_mfma");
+}
+
+size_t dsv4g_moe_batch_workspace_bytes(const DSV4GLayer *L, int n_tokens) {
+  return batch_ws_layout(L, n_tokens, nullptr).bytes;
+}
+
+// Batched MoE layer (moe_forward_batch semantics) for n_tokens rows of x
+// (BF16 values in fp32). out [n][hidden]; idx/wt (optional, device).
+int dsv4g_moe_forward_batch(float *out, const float *x, const DSV4GLayer *L,
+                            const int *token_ids, int n_tokens, void *workspace,
+                            size_t workspace_bytes, int *idx_out, float *wt_out,
+                            void *stream) {
+  if (!L || !L->gate_w || !L->experts || !L->sh1 || !L->sh2 || !L->sh3)
+    return dsv4g_fail(DSV4G_EINVAL, "moe_forward_batch: layer descriptor incomplete");
+  const int T = n_tokens, K = L->topk, E = L->n_experts, H = L->hidden, I = L->inter;
+  if (T <= 0 || H % 128 || I % 128 || H > 8192 || I > 8192 || E <= 0 || E > 1024 || K <= 0 ||
+      K > 32 || K > E)
+    return dsv4g_fail(DSV4G_EINVAL, "moe_forward_batch: unsupported shape");
+  if (L->tid2eid && !token_ids)
+    return dsv4g_fail(DSV4G_EINVAL, "moe_forward_batch: hash layer needs token_ids");
+  if (workspace_bytes < dsv4g_moe_batch_workspace_bytes(L, T))
+    return dsv4g_fail(DSV4G_EINVAL, "moe_forward_batch: workspace too small (%zu < %zu)",
+                      workspace_bytes, dsv4g_moe_batch_workspace_bytes(L, T));
+  hipStream_t st = (hipStream_t)stream;
+  const BatchWs w = batch_ws_layout(L, T, workspace);
+
+  // 1. activation quant (+ BF16-valued check for the router bound)
+  hipLaunchKernelGGL(k_fill_zero_i32, dim3((T + 255) / 256), dim3(256), 0, st, w.not_bf16, T);
+  hipLaunchKernelGGL(k_batch_quant, dim3(H / 128, T), dim3(64), 0, st, w.x8, w.x8s, w.not_bf16,
+                     x, H);
+  DSV4G_TRY(dsv4g_check_launch("batch_quant"));
+  // 2. router
+  hipLaunchKernelGGL(k_router_logits_mfma, dim3((T + 63) / 64, (E + 63) / 64), dim3(256), 0, st,
+                     w.z, w.zabs, x, L->gate_w, T, H, E);
+  hipLaunchKernelGGL(k_router_cand, dim3((T + 3) / 4), dim3(256), 0, st, w.cand, w.ncand, w.z,
+                     w.zabs, w.not_bf16, L->bias, L->tid2eid, token_ids, T, H, E, K);
+  hipLaunchKernelGGL(k_scan_counts, dim3(1), dim3(1024), 0, st, w.chain_off, w.ncand, T);
+  {
+    const long bound = (long)T * (K + 4);
+    const int blocks = (int)((bound + 255) / 256 < 4096 ? (bound + 255) / 256 : 4096);
+    hipLaunchKernelGGL(k_router_chains, dim3(blocks), dim3(256), 0, st, w.cscore, w.cchoice,
+                       w.cand, w.chain_off, x, L->gate_w, L->bias, T, H, E);
+  }
+  hipLaunchKernelGGL(k_router_finalize, dim3((T + 255) / 256), dim3(256), 0, st, w.idx, w.wt,
+                     w.cand, w.ncand, w.cscore, w.cchoice, L->tid2eid ? 1 : 0, T, E, K,
+                     L->route_scale);
+  DSV4G_TRY(dsv4g_check_launch("router"));
+  // 3. dispatch
+  hipLaunchKernelGGL(k_dispatch_count, dim3(E + 1), dim3(256), 0, st, w.counts, w.idx, T, K, E);
+  hipLaunchKernelGGL(k_dispatch_fill, dim3(E + 1), dim3(256), 0, st, w.pos_off, w.tile_off,
+                     w.pos_token, w.pos_route, w.pos_wt, w.counts, w.idx, w.wt, T, K, E);
+  DSV4G_TRY(dsv4g_check_launch("dispatch"));
+  // 4-5. grouped GEMMs
+  GroupedArgs g = {};
+  g.experts = L->experts;
+  g.expert_stride = L->expert_stride;
+  g.scale_run = L->scale_run;
+  g.shw[0] = L->sh1;
+  g.shw[1] = L->sh3;
+  g.shw[2] = L->sh2;
+  g.shs[0] = L->sh1_s;
+  g.shs[1] = L->sh3_s;
+  g.shs[2] = L->sh2_s;
+  g.tile_off = w.tile_off;
+  g.pos_off = w.pos_off;
+  g.pos_token = w.pos_token;
+  g.pos_route = w.pos_route;
+  g.pos_wt = w.pos_wt;
+  g.x8 = w.x8;
+  g.x8s = w.x8s;
+  g.y8 = w.y8;
+  g.y8s = w.y8s;
+  g.ro = w.ro;
+  g.H = H;
+  g.I = I;
+  g.E = E;
+  g.K = K;
+  g.T = T;
+  g.limit = (float)(int)L->swiglu_limit;
+  const long tile_bound = ((long)T * K + GT_TN - 1) / GT_TN + E + (T + GT_TN - 1) / GT_TN;
+  g.row_tiles = I / GT_TM;
+  hipLaunchKernelGGL(k_grouped_gateup, dim3((unsigned)(tile_bound * g.row_tiles)), dim3(256), 0,
+                     st, g);
+  DSV4G_TRY(dsv4g_check_launch("grouped_gateup"));
+  g.row_tiles = H / GT_TM;
+  hipLaunchKernelGGL(k_grouped_down, dim3((unsigned)(tile_bound * g.row_tiles)), dim3(256), 0,
+                     st, g);
+  DSV4G_TRY(dsv4g_check_launch("grouped_down"));
+  // 6. combine
+  const size_t total = (size_t)T * H;
+  hipLaunchKernelGGL(k_combine_batch, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st,
+                     out, w.ro, T, K, H);
+  DSV4G_TRY(dsv4g_check_launch("combine_batch"));
+  if (idx_out)
+    DSV4G_HIP(hipMemcpyAsync(idx_out, w.idx, (size_t)T * K * sizeof(int),
+                             hipMemcpyDeviceToDevice, st));
+  if (wt_out)
+    DSV4G_HIP(hipMemcpyAsync(wt_out, w.wt, (size_t)T * K * sizeof(float),
+                             hipMemcpyDeviceToDevice, st));
+  return 0;
+}
+
+}  // extern "C"

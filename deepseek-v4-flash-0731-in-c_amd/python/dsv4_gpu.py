@@ -54,6 +54,9 @@ _SIGS = {
     "dsv4g_moe_forward": [_vp, _vp, C.POINTER(DSV4GLayer), _vp, _I, _vp, _Z, _vp, _vp, _vp],
     "dsv4g_moe_decode_phase": [_I, _vp, _vp, C.POINTER(DSV4GLayer), _vp, _I, _vp, _Z, _vp],
     "dsv4g_moe_decode_routing": [_vp, _vp, C.POINTER(DSV4GLayer), _I, _vp, _vp],
+    "dsv4g_moe_forward_batch": [_vp, _vp, C.POINTER(DSV4GLayer), _vp, _I, _vp, _Z, _vp, _vp,
+                                _vp],
+    "dsv4g_probe_mfma": [_I, _vp, _vp, _vp, _vp, _vp, _vp],
     "dsv4g_quant_fp4_rows": [_vp, _vp, _vp, _I, _I, _vp],
     "dsv4g_quant_fp8_blocks": [_vp, _vp, _vp, _I, _I, _I, _vp],
 }
@@ -74,6 +77,8 @@ class GpuLib:
         lib.dsv4g_version.restype = C.c_char_p
         lib.dsv4g_moe_workspace_bytes.restype = C.c_size_t
         lib.dsv4g_moe_workspace_bytes.argtypes = [C.POINTER(DSV4GLayer), _I]
+        lib.dsv4g_moe_batch_workspace_bytes.restype = C.c_size_t
+        lib.dsv4g_moe_batch_workspace_bytes.argtypes = [C.POINTER(DSV4GLayer), _I]
         for name, args in _SIGS.items():
             fn = getattr(lib, name)
             fn.argtypes = args
@@ -235,6 +240,30 @@ class GpuLib:
         self._call("dsv4g_moe_forward", _ptr(out), _ptr(x), C.byref(L), _ptr(token_ids), n,
                    _ptr(workspace), workspace.numel(), _ptr(idx), _ptr(wt), self._stream())
         return out, idx, wt
+
+    def moe_batch_workspace_bytes(self, layer, n_tokens):
+        return int(self.lib.dsv4g_moe_batch_workspace_bytes(C.byref(layer.struct), n_tokens))
+
+    def moe_forward_batch(self, layer, x, token_ids=None, workspace=None, out=None):
+        import torch
+        n = x.shape[0]
+        L = layer.struct
+        need = self.moe_batch_workspace_bytes(layer, n)
+        if workspace is None or workspace.numel() < need:
+            workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
+        out = torch.empty_like(x) if out is None else out
+        idx = torch.empty(n, L.topk, dtype=torch.int32, device=x.device)
+        wt = torch.empty(n, L.topk, dtype=torch.float32, device=x.device)
+        self._call("dsv4g_moe_forward_batch", _ptr(out), _ptr(x), C.byref(L), _ptr(token_ids), n,
+                   _ptr(workspace), workspace.numel(), _ptr(idx), _ptr(wt), self._stream())
+        return out, idx, wt
+
+    def probe_mfma(self, kind, A, B, sa=None, sb=None):
+        import torch
+        D = torch.empty(16, 16, dtype=torch.float32, device=A.device)
+        self._call("dsv4g_probe_mfma", kind, _ptr(D), _ptr(A), _ptr(B), _ptr(sa), _ptr(sb),
+                   self._stream())
+        return D
 
     def moe_decode_phase(self, phase, layer, x, out, workspace, token_ids=None):
         self._call("dsv4g_moe_decode_phase", phase, _ptr(out), _ptr(x), C.byref(layer.struct),

