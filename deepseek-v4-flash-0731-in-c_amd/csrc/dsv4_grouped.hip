@@ -13,15 +13,21 @@
 //   3. dispatch: deterministic per-expert position lists (ascending token, as
 //      expert_forward_batch_routes gathers them, src/dsv4/dsv4_model.c:6498-6524)
 //      and a token-tile table; the shared expert is expert number E;
-//   4. gate/up grouped GEMM: V_MFMA_SCALE_F32_16X16X128_F8F6F4 with FP4 (routed)
-//      or FP8 (shared) weights x FP8 activations, E8M0 block scales applied by
-//      the MFMA; epilogue = BF16 round of gate/up, SwiGLU, x route weight,
-//      BF16 round, per-128 FP8 requant (one 128-row tile = one requant group);
+//   4. gate/up grouped GEMM on V_MFMA_F32_16X16X32_BF16: FP4 (routed) or FP8
+//      (shared) weights are converted in registers to BF16 already multiplied
+//      by their E8M0 block scale (V_CVT_SCALEF32_PK_BF16_FP4/FP8, exact: at
+//      most 4 significant bits times a power of two), activations are the
+//      exact BF16 dequantisation of their FP8 quantisation; epilogue = BF16
+//      round of gate/up, SwiGLU, x route weight, BF16 round, per-128 FP8
+//      requant (one 128-row tile = one requant group), stored dequantised;
 //   5. down grouped GEMM, BF16 outputs per (token, route);
 //   6. per-token combine in ascending expert id + shared, BF16.
-// Accumulation inside an MFMA differs from the reference's sequential fp32
-// order, so expert outputs agree to fp32 rounding (checked at 1e-3), not bit
-// for bit; routing is exact.
+// The products are exact; the MFMA sums them in fp32 in its own order, so
+// expert outputs agree with the reference to fp32 rounding, not bit for bit;
+// routing is exact. (The block-scaled FP8/FP4 MFMA was measured to sum each
+// 128-K window with only ~12 bits below its largest product - error up to
+// 2^-11 of the largest term - which moves results by ~5e-3; its FP8-rate
+// throughput is not used for that reason.)
 #include "dsv4_device.h"
 #include "dsv4_gpu_internal.h"
 
@@ -30,6 +36,7 @@ using namespace dsv4;
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 namespace dsv4 {
 
@@ -58,6 +65,13 @@ __global__ void k_fill_zero_i32(int *p, int n) {
   if (i < n) p[i] = 0;
 }
 
+// Operand layouts of V_MFMA_SCALE_F32_16X16X128_F8F6F4 (measured on gfx950 with
+// dsv4g_probe_mfma): lane l serves row/column l%16; with g = l/16,
+//   4-bit operand: nibbles 0..31 (4 VGPRs) = K 32g .. 32g+31, low nibble first;
+//   8-bit operand: bytes 0..15 = K 16g .. 16g+15, bytes 16..31 = K 64+16g ..;
+//   scale byte of lane l = E8M0 scale of K block g (K 32g .. 32g+31);
+//   result: lane l holds D[4g + v][l%16], v = 0..3.
+
 // ------------------------------------------------------------ probes ----
 // One 16x16 MFMA tile from row-major operands, for layout validation.
 // A: [16][K] bytes (FP8) or [16][K/2] packed FP4; B: [16][K] FP8 (one row per
@@ -69,11 +83,11 @@ __global__ void k_probe_mx(float *D, const uint8_t *A, const uint8_t *B, const u
   if (afmt == MX_FP4) {
     a0 = *reinterpret_cast<const uint4 *>(A + i * 64 + kb * 16);
   } else {
-    a0 = *reinterpret_cast<const uint4 *>(A + i * 128 + kb * 32);
-    a1 = *reinterpret_cast<const uint4 *>(A + i * 128 + kb * 32 + 16);
+    a0 = *reinterpret_cast<const uint4 *>(A + i * 128 + kb * 16);
+    a1 = *reinterpret_cast<const uint4 *>(A + i * 128 + 64 + kb * 16);
   }
-  const uint4 b0 = *reinterpret_cast<const uint4 *>(B + i * 128 + kb * 32);
-  const uint4 b1 = *reinterpret_cast<const uint4 *>(B + i * 128 + kb * 32 + 16);
+  const uint4 b0 = *reinterpret_cast<const uint4 *>(B + i * 128 + kb * 16);
+  const uint4 b1 = *reinterpret_cast<const uint4 *>(B + i * 128 + 64 + kb * 16);
   v4f acc = {0.f, 0.f, 0.f, 0.f};
   if (afmt == MX_FP4)
     acc = mx_mfma<MX_FP4>(u4x2_to_v8i(a0, a1), u4x2_to_v8i(b0, b1), acc, sa[i * 4 + kb],
@@ -96,11 +110,10 @@ __global__ void k_probe_bf16(float *D, const uint16_t *A, const uint16_t *B) {
 }
 
 // ------------------------------------------------------- batch quant ----
-// Per (token, 128-group) wave: the reference activation quant; writes E4M3
-// codes and the E8M0 code of the power-of-two scale; flags tokens whose x is
-// not BF16-valued (the router bound then widens for them).
-__global__ __launch_bounds__(64) void k_batch_quant(uint8_t *__restrict__ x8,
-                                                    uint8_t *__restrict__ x8s,
+// Per (token, 128-group) wave: the reference activation quant, stored as the
+// exact BF16 value of each quantised element (E4M3 grid value x scale); flags
+// tokens whose x is not BF16-valued (the router bound then widens for them).
+__global__ __launch_bounds__(64) void k_batch_quant(uint16_t *__restrict__ xb,
                                                     int *__restrict__ not_bf16,
                                                     const float *__restrict__ x, int H) {
   const int g = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
@@ -109,10 +122,10 @@ __global__ __launch_bounds__(64) void k_batch_quant(uint8_t *__restrict__ x8,
   const float amax = wave_max(fmaxf(fabsf(a), fabsf(b)));
   const float scale = act_scale(amax);
   const float inv = 1.0f / scale;
-  uint8_t *q = x8 + (size_t)t * H + g * 128;
-  q[lane] = (uint8_t)e4m3_code(quant_e4m3(a, inv));
-  q[lane + 64] = (uint8_t)e4m3_code(quant_e4m3(b, inv));
-  if (lane == 0) x8s[(size_t)t * (H / 128) + g] = (uint8_t)scale_code(scale);
+  uint16_t *q = xb + (size_t)t * H + g * 128;
+  // dequantised grid value qx * scale: <= 4 significant bits, exact in BF16
+  q[lane] = (uint16_t)(f2u(quant_e4m3(a, inv) * scale) >> 16);
+  q[lane + 64] = (uint16_t)(f2u(quant_e4m3(b, inv) * scale) >> 16);
   const bool exact = bf16_round(a) == a && bf16_round(b) == b;
   if (__any(!exact) && lane == 0) not_bf16[t] = 1;
 }
@@ -495,20 +508,26 @@ __global__ __launch_bounds__(256) void k_dispatch_fill(
 }
 
 // ---------------------------------------------------- grouped GEMMs ------
+// BF16 operands over a 128-K super-window. Lane group g = l/16 owns the 32
+// physical columns [32g, 32g+32) of the super-window; MFMA step q (0..3)
+// feeds it columns [32g+8q, 32g+8q+8). The same permutation of K is used for
+// both operands, so each step still computes exact products of matching
+// columns, and every lane reads 16-64 contiguous bytes.
+#define GT_BROW2 272  // LDS bytes per staged BF16 activation row (256 + 16 pad)
+
 struct GroupedArgs {
   const uint8_t *experts;
   size_t expert_stride, scale_run;
   const uint8_t *shw[3], *shs[3];
   const int *tile_off, *pos_off, *pos_token, *pos_route;
   const float *pos_wt;
-  const uint8_t *x8, *x8s;  // [T][H] codes, [T][H/128] scale codes
-  uint8_t *y8, *y8s;        // [P][I], [P][I/128]
-  uint16_t *ro;             // [T][K+1][H] BF16 bits
+  const uint16_t *xb;  // [T][H] BF16 activations (dequantised FP8)
+  uint16_t *yb;        // [P][I] BF16 intermediate (dequantised FP8)
+  uint16_t *ro;        // [T][K+1][H] BF16 bits
   int H, I, E, K, T, row_tiles;
   float limit;
 };
 
-// Locate the tile: expert e with tile_off[e] <= tt < tile_off[e+1].
 __device__ __forceinline__ int tile_expert(const int *tile_off, int E, int tt) {
   int lo = 0, hi = E + 1;
   while (hi - lo > 1) {
@@ -519,48 +538,86 @@ __device__ __forceinline__ int tile_expert(const int *tile_off, int E, int tt) {
   return lo;
 }
 
-// Load one A fragment (16 rows x 128 K) for lane l: FP4 16 bytes, FP8 32.
+__device__ __forceinline__ uint32_t bf2_bits(bf16x2_t v) { return __builtin_bit_cast(uint32_t, v); }
+
+// A operand of one 16-row fragment over super-window sw: the 32 weights of
+// lane group g, converted to BF16 times their block scale, as four 8-element
+// MFMA operands. A NaN scale (E8M0 255) zeroes the block, as the reference
+// skips it.
 template <int AFMT>
-__device__ __forceinline__ v8i load_a(const uint8_t *W, const uint8_t *S, int row, int in,
-                                      int kw, int l, int &sc) {
-  uint4 a0, a1 = make_uint4(0, 0, 0, 0);
+__device__ __forceinline__ void load_a_bf16(uint4 (&op)[4], const uint8_t *W, const uint8_t *S,
+                                            int row, int in, int sw, int l) {
+  const int g = l / 16;
+  uint32_t code;
+  uint4 r0, r1 = make_uint4(0, 0, 0, 0);
   if (AFMT == MX_FP4) {
-    a0 = *reinterpret_cast<const uint4 *>(W + (size_t)row * (in / 2) + kw * 64 + (l / 16) * 16);
-    sc = S[(size_t)row * (in / 32) + kw * 4 + l / 16];
+    r0 = *reinterpret_cast<const uint4 *>(W + (size_t)row * (in / 2) + sw * 64 + g * 16);
+    code = S[(size_t)row * (in / 32) + sw * 4 + g];
   } else {
-    const uint8_t *p = W + (size_t)row * in + kw * 128 + (l / 16) * 32;
-    a0 = *reinterpret_cast<const uint4 *>(p);
-    a1 = *reinterpret_cast<const uint4 *>(p + 16);
-    sc = S[(size_t)(row / 128) * (in / 128) + kw];
+    const uint8_t *p = W + (size_t)row * in + sw * 128 + g * 32;
+    r0 = *reinterpret_cast<const uint4 *>(p);
+    r1 = *reinterpret_cast<const uint4 *>(p + 16);
+    code = S[(size_t)(row / 128) * (in / 128) + sw];
   }
-  if (sc == 255) {  // NaN scale: the reference skips the block
-    a0 = make_uint4(0, 0, 0, 0);
-    a1 = a0;
-    sc = 127;
+  if (code == 255u) {
+    for (int q = 0; q < 4; ++q) op[q] = make_uint4(0, 0, 0, 0);
+    return;
   }
-  return u4x2_to_v8i(a0, a1);
+  const float s = e8m0(code);
+  if (AFMT == MX_FP4) {
+    const uint32_t d[4] = {r0.x, r0.y, r0.z, r0.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      op[q].x = bf2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d[q], s, 0));
+      op[q].y = bf2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d[q], s, 1));
+      op[q].z = bf2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d[q], s, 2));
+      op[q].w = bf2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d[q], s, 3));
+    }
+  } else {
+    const uint32_t d[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      op[q].x = bf2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d[2 * q], s, false));
+      op[q].y = bf2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d[2 * q], s, true));
+      op[q].z = bf2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d[2 * q + 1], s, false));
+      op[q].w = bf2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d[2 * q + 1], s, true));
+    }
+  }
 }
 
-// Stage 64 activation rows (128 bytes of window kw) into LDS.
-__device__ __forceinline__ void stage_b(uint8_t *bt, const uint8_t *src, const int *rows,
-                                        int in, int kw) {
+__device__ __forceinline__ v4f mfma_bf16(uint4 a, uint4 b, v4f c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                 __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+// Stage 64 BF16 activation rows (super-window sw, 256 bytes each) into LDS.
+__device__ __forceinline__ void stage_b16(uint8_t *bt, const uint16_t *src, const int *rows,
+                                          int in, int sw) {
   const int tid = threadIdx.x, j = tid >> 2, q = tid & 3;
-  uint4 u0 = make_uint4(0, 0, 0, 0), u1 = u0;
+  uint4 u[4] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0),
+                make_uint4(0, 0, 0, 0)};
   const int r = rows[j];
   if (r >= 0) {
-    const uint8_t *p = src + (size_t)r * in + kw * 128 + q * 32;
-    u0 = *reinterpret_cast<const uint4 *>(p);
-    u1 = *reinterpret_cast<const uint4 *>(p + 16);
+    const uint4 *p = reinterpret_cast<const uint4 *>(src + (size_t)r * in + sw * 128 + q * 32);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) u[i] = p[i];
   }
-  *reinterpret_cast<uint4 *>(bt + j * GT_BROW + q * 32) = u0;
-  *reinterpret_cast<uint4 *>(bt + j * GT_BROW + q * 32 + 16) = u1;
+  uint4 *d = reinterpret_cast<uint4 *>(bt + j * GT_BROW2 + q * 64);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) d[i] = u[i];
+}
+
+__device__ __forceinline__ void load_b_ops(uint4 (&op)[4], const uint8_t *bt, int j, int l) {
+  const uint4 *p = reinterpret_cast<const uint4 *>(bt + j * GT_BROW2 + (l / 16) * 64);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) op[q] = p[q];
 }
 
 template <int AFMT>
 __device__ void gateup_tile(const GroupedArgs &a, int e, int rt, int p0, int np, uint8_t *bt,
-                            uint8_t *bsc, int *rows_s, float *wt_s, float (*amax_s)[GT_TN]) {
+                            int *rows_s, float *wt_s, float (*amax_s)[GT_TN]) {
   const int tid = threadIdx.x, wv = tid / 64, l = tid % 64;
-  const int H = a.H, I = a.I, nw = H / 128;
+  const int H = a.H, I = a.I, nsw = H / 128;
   const uint8_t *Wg, *Wu, *Sg, *Su;
   if (AFMT == MX_FP4) {
     const uint8_t *sc = a.experts + (size_t)e * a.expert_stride;
@@ -581,12 +638,7 @@ __device__ void gateup_tile(const GroupedArgs &a, int e, int rt, int p0, int np,
     rows_s[tid] = tid < np ? a.pos_token[p0 + tid] : -1;
     wt_s[tid] = tid < np ? a.pos_wt[p0 + tid] : 0.0f;
   }
-  __syncthreads();
-  for (int i = tid; i < GT_TN * nw; i += 256) {
-    const int j = i / nw, kw = i % nw;
-    bsc[j * 64 + kw] = rows_s[j] >= 0 ? a.x8s[(size_t)rows_s[j] * nw + kw] : 127;
-  }
-  const int nf = (np + 15) / 16;  // active token fragments (wave-uniform)
+  const int nf = (np + 15) / 16;  // active token fragments (block-uniform)
   v4f ag[2][4], au[2][4];
   for (int f = 0; f < 2; ++f)
     for (int c = 0; c < 4; ++c) {
@@ -594,31 +646,30 @@ __device__ void gateup_tile(const GroupedArgs &a, int e, int rt, int p0, int np,
       au[f][c] = ag[f][c];
     }
   const int rbase = rt * GT_TM + 32 * wv;
-  for (int kw = 0; kw < nw; ++kw) {
+  for (int sw = 0; sw < nsw; ++sw) {
     __syncthreads();
-    stage_b(bt, a.x8, rows_s, H, kw);
-    int sg[2], su[2];
-    v8i Ag[2], Au[2];
+    stage_b16(bt, a.xb, rows_s, H, sw);
+    uint4 Ag[2][4], Au[2][4];
     for (int f = 0; f < 2; ++f) {
       const int row = rbase + 16 * f + l % 16;
-      Ag[f] = load_a<AFMT>(Wg, Sg, row, H, kw, l, sg[f]);
-      Au[f] = load_a<AFMT>(Wu, Su, row, H, kw, l, su[f]);
+      load_a_bf16<AFMT>(Ag[f], Wg, Sg, row, H, sw, l);
+      load_a_bf16<AFMT>(Au[f], Wu, Su, row, H, sw, l);
     }
     __syncthreads();
     for (int c = 0; c < 4; ++c) {
       if (c >= nf) break;
-      const int j = 16 * c + l % 16;
-      const uint8_t *bp = bt + j * GT_BROW + (l / 16) * 32;
-      const v8i B = u4x2_to_v8i(*reinterpret_cast<const uint4 *>(bp),
-                                *reinterpret_cast<const uint4 *>(bp + 16));
-      const int sb = bsc[j * 64 + kw];
-      for (int f = 0; f < 2; ++f) {
-        ag[f][c] = mx_mfma<AFMT>(Ag[f], B, ag[f][c], sg[f], sb);
-        au[f][c] = mx_mfma<AFMT>(Au[f], B, au[f][c], su[f], sb);
-      }
+      uint4 B[4];
+      load_b_ops(B, bt, 16 * c + l % 16, l);
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        for (int f = 0; f < 2; ++f) {
+          ag[f][c] = mfma_bf16(Ag[f][q], B[q], ag[f][c]);
+          au[f][c] = mfma_bf16(Au[f][q], B[q], au[f][c]);
+        }
     }
   }
-  // epilogue: y = bf16((silu(bf16(g)) * bf16(u)) * w), per-128 requant
+  // epilogue: y = bf16((silu(bf16(g)) * bf16(u)) * w), per-128 requant,
+  // stored as the exact BF16 of the dequantised FP8 value
   float y[2][4][4];
   for (int c = 0; c < 4; ++c) {
     const int j = 16 * c + l % 16;
@@ -638,7 +689,6 @@ __device__ void gateup_tile(const GroupedArgs &a, int e, int rt, int p0, int np,
     if (l < 16) amax_s[wv][j] = m;
   }
   __syncthreads();
-  const int ng = I / 128;
   for (int c = 0; c < nf; ++c) {
     const int j = 16 * c + l % 16;
     if (j >= np) continue;
@@ -647,21 +697,19 @@ __device__ void gateup_tile(const GroupedArgs &a, int e, int rt, int p0, int np,
     const float inv = 1.0f / scale;
     const int pos = p0 + j;
     for (int f = 0; f < 2; ++f) {
-      uint32_t packed = 0;
-      for (int v = 0; v < 4; ++v)
-        packed |= e4m3_code(quant_e4m3(y[f][c][v], inv)) << (8 * v);
+      uint32_t h[4];
+      for (int v = 0; v < 4; ++v) h[v] = f2u(quant_e4m3(y[f][c][v], inv) * scale) >> 16;
       const int row = rbase + 16 * f + 4 * (l / 16);
-      *reinterpret_cast<uint32_t *>(a.y8 + (size_t)pos * I + row) = packed;
+      *reinterpret_cast<uint2 *>(a.yb + (size_t)pos * I + row) =
+          make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
     }
-    if (wv == 0 && l < 16) a.y8s[(size_t)pos * ng + rt] = (uint8_t)scale_code(scale);
   }
 }
 
 // grid.x = token-tile bound x row tiles (I / 128); tiles beyond the actual
 // count exit at once.
 __global__ __launch_bounds__(256) void k_grouped_gateup(GroupedArgs a) {
-  __shared__ __align__(16) uint8_t bt[GT_TN * GT_BROW];
-  __shared__ uint8_t bsc[GT_TN * 64];
+  __shared__ __align__(16) uint8_t bt[GT_TN * GT_BROW2];
   __shared__ int rows_s[GT_TN];
   __shared__ float wt_s[GT_TN];
   __shared__ float amax_s[4][GT_TN];
@@ -671,16 +719,16 @@ __global__ __launch_bounds__(256) void k_grouped_gateup(GroupedArgs a) {
   const int p0 = a.pos_off[e] + (tt - a.tile_off[e]) * GT_TN;
   const int np = min(GT_TN, a.pos_off[e + 1] - p0);
   if (e == a.E)
-    gateup_tile<MX_FP8>(a, e, rt, p0, np, bt, bsc, rows_s, wt_s, amax_s);
+    gateup_tile<MX_FP8>(a, e, rt, p0, np, bt, rows_s, wt_s, amax_s);
   else
-    gateup_tile<MX_FP4>(a, e, rt, p0, np, bt, bsc, rows_s, wt_s, amax_s);
+    gateup_tile<MX_FP4>(a, e, rt, p0, np, bt, rows_s, wt_s, amax_s);
 }
 
 template <int AFMT>
 __device__ void down_tile(const GroupedArgs &a, int e, int rt, int p0, int np, uint8_t *bt,
-                          uint8_t *bsc, int *rows_s) {
+                          int *rows_s) {
   const int tid = threadIdx.x, wv = tid / 64, l = tid % 64;
-  const int H = a.H, I = a.I, nw = I / 128;
+  const int H = a.H, I = a.I, nsw = I / 128;
   const uint8_t *W, *S;
   if (AFMT == MX_FP4) {
     const uint8_t *sc = a.experts + (size_t)e * a.expert_stride;
@@ -691,31 +739,24 @@ __device__ void down_tile(const GroupedArgs &a, int e, int rt, int p0, int np, u
     S = a.shs[2];
   }
   if (tid < GT_TN) rows_s[tid] = tid < np ? p0 + tid : -1;  // positions are contiguous
-  __syncthreads();
-  for (int i = tid; i < GT_TN * nw; i += 256) {
-    const int j = i / nw, kw = i % nw;
-    bsc[j * 64 + kw] = rows_s[j] >= 0 ? a.y8s[(size_t)rows_s[j] * nw + kw] : 127;
-  }
   const int nf = (np + 15) / 16;
   v4f acc[2][4];
   for (int f = 0; f < 2; ++f)
     for (int c = 0; c < 4; ++c) acc[f][c] = (v4f){0.f, 0.f, 0.f, 0.f};
   const int rbase = rt * GT_TM + 32 * wv;
-  for (int kw = 0; kw < nw; ++kw) {
+  for (int sw = 0; sw < nsw; ++sw) {
     __syncthreads();
-    stage_b(bt, a.y8, rows_s, I, kw);
-    int sa[2];
-    v8i A[2];
-    for (int f = 0; f < 2; ++f) A[f] = load_a<AFMT>(W, S, rbase + 16 * f + l % 16, I, kw, l, sa[f]);
+    stage_b16(bt, a.yb, rows_s, I, sw);
+    uint4 A[2][4];
+    for (int f = 0; f < 2; ++f) load_a_bf16<AFMT>(A[f], W, S, rbase + 16 * f + l % 16, I, sw, l);
     __syncthreads();
     for (int c = 0; c < 4; ++c) {
       if (c >= nf) break;
-      const int j = 16 * c + l % 16;
-      const uint8_t *bp = bt + j * GT_BROW + (l / 16) * 32;
-      const v8i B = u4x2_to_v8i(*reinterpret_cast<const uint4 *>(bp),
-                                *reinterpret_cast<const uint4 *>(bp + 16));
-      const int sb = bsc[j * 64 + kw];
-      for (int f = 0; f < 2; ++f) acc[f][c] = mx_mfma<AFMT>(A[f], B, acc[f][c], sa[f], sb);
+      uint4 B[4];
+      load_b_ops(B, bt, 16 * c + l % 16, l);
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        for (int f = 0; f < 2; ++f) acc[f][c] = mfma_bf16(A[f][q], B[q], acc[f][c]);
     }
   }
   for (int c = 0; c < nf; ++c) {
@@ -735,8 +776,7 @@ __device__ void down_tile(const GroupedArgs &a, int e, int rt, int p0, int np, u
 }
 
 __global__ __launch_bounds__(256) void k_grouped_down(GroupedArgs a) {
-  __shared__ __align__(16) uint8_t bt[GT_TN * GT_BROW];
-  __shared__ uint8_t bsc[GT_TN * 64];
+  __shared__ __align__(16) uint8_t bt[GT_TN * GT_BROW2];
   __shared__ int rows_s[GT_TN];
   const int rt = blockIdx.x % a.row_tiles, tt = blockIdx.x / a.row_tiles;
   if (tt >= a.tile_off[a.E + 1]) return;
@@ -744,9 +784,9 @@ __global__ __launch_bounds__(256) void k_grouped_down(GroupedArgs a) {
   const int p0 = a.pos_off[e] + (tt - a.tile_off[e]) * GT_TN;
   const int np = min(GT_TN, a.pos_off[e + 1] - p0);
   if (e == a.E)
-    down_tile<MX_FP8>(a, e, rt, p0, np, bt, bsc, rows_s);
+    down_tile<MX_FP8>(a, e, rt, p0, np, bt, rows_s);
   else
-    down_tile<MX_FP4>(a, e, rt, p0, np, bt, bsc, rows_s);
+    down_tile<MX_FP4>(a, e, rt, p0, np, bt, rows_s);
 }
 
 // out[t][i] = bf16(((0 + r_0) + ... + r_{K-1}) + shared), routes in
@@ -770,7 +810,7 @@ using namespace dsv4;
 
 namespace {
 struct BatchWs {
-  uint8_t *x8, *x8s, *y8, *y8s;
+  uint16_t *xb, *yb;
   float *z, *zabs, *cscore, *cchoice, *wt, *pos_wt;
   int *not_bf16, *cand, *ncand, *chain_off, *idx, *counts, *pos_off, *tile_off, *pos_token,
       *pos_route;
@@ -789,8 +829,7 @@ BatchWs batch_ws_layout(const DSV4GLayer *L, int T, void *base) {
     p += (bytes + 255) & ~(size_t)255;
     return r;
   };
-  w.x8 = (uint8_t *)take(t * H);
-  w.x8s = (uint8_t *)take(t * (H / 128));
+  w.xb = (uint16_t *)take(t * H * 2);
   w.not_bf16 = (int *)take(t * 4);
   w.z = (float *)take(t * E * 4);
   w.zabs = (float *)take(t * E * 4);
@@ -807,8 +846,7 @@ BatchWs batch_ws_layout(const DSV4GLayer *L, int T, void *base) {
   w.pos_token = (int *)take(P * 4);
   w.pos_route = (int *)take(P * 4);
   w.pos_wt = (float *)take(P * 4);
-  w.y8 = (uint8_t *)take(P * I);
-  w.y8s = (uint8_t *)take(P * (I / 128));
+  w.yb = (uint16_t *)take(P * I * 2);
   w.ro = (uint16_t *)take(t * (K + 1) * H * 2);
   w.bytes = (size_t)(p - p0) + 256;
   return w;
@@ -855,8 +893,7 @@ int dsv4g_moe_forward_batch(float *out, const float *x, const DSV4GLayer *L,
 
   // 1. activation quant (+ BF16-valued check for the router bound)
   hipLaunchKernelGGL(k_fill_zero_i32, dim3((T + 255) / 256), dim3(256), 0, st, w.not_bf16, T);
-  hipLaunchKernelGGL(k_batch_quant, dim3(H / 128, T), dim3(64), 0, st, w.x8, w.x8s, w.not_bf16,
-                     x, H);
+  hipLaunchKernelGGL(k_batch_quant, dim3(H / 128, T), dim3(64), 0, st, w.xb, w.not_bf16, x, H);
   DSV4G_TRY(dsv4g_check_launch("batch_quant"));
   // 2. router
   hipLaunchKernelGGL(k_router_logits_mfma, dim3((T + 63) / 64, (E + 63) / 64), dim3(256), 0, st,
@@ -895,10 +932,8 @@ int dsv4g_moe_forward_batch(float *out, const float *x, const DSV4GLayer *L,
   g.pos_token = w.pos_token;
   g.pos_route = w.pos_route;
   g.pos_wt = w.pos_wt;
-  g.x8 = w.x8;
-  g.x8s = w.x8s;
-  g.y8 = w.y8;
-  g.y8s = w.y8s;
+  g.xb = w.xb;
+  g.yb = w.yb;
   g.ro = w.ro;
   g.H = H;
   g.I = I;
