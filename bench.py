@@ -14,6 +14,13 @@ roofline: the dominant kernel (the gate/up GEMV pass), timed live with HIP
 events around a graph of its launches on the launch stream. cpu_baseline: the
 reference's own moe_forward (oracle/_ref, compiled from the reference sources)
 on the same layer on the host cores.
+
+The same run also measures the batched path on layer 0 with a Zipf(1.2)
+router bias (config keys "verify_64" and "prefill_4096"): 64 tokens
+(speculative verify) and 4096 tokens (prefill) through the grouped GEMMs,
+timed with HIP events on the launch stream, FLOPs = 6 * hidden * inter per
+(token, expert) pair including the shared expert. --workload picks one part
+alone (for profiling); the JSON line then carries that part's numbers.
 """
 from __future__ import annotations
 
@@ -27,6 +34,8 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "deepseek-v4-flash-0731-in-c_amd", "python"))
 
 HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0   # dense MFMA peaks of one MI355X
+FP8_PEAK_TFLOPS = 5000.0
 METRIC = "MoE layer decode GB/s (% HBM peak); prefill grouped-GEMM TFLOPS (% MFMA)"
 
 H, I, E, K = 4096, 2048, 256, 6
@@ -51,7 +60,57 @@ def parse():
     p.add_argument("--replays", type=int, default=5)
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--workload", choices=("all", "decode", "verify", "prefill"), default="all")
+    p.add_argument("--zipf-strength", type=float, default=0.15)
     return p.parse_args()
+
+
+def zipf_bias(n_experts, seed=8, s=1.2, strength=0.15):
+    """Router bias giving Zipf(s)-skewed expert popularity over a seeded
+    permutation of the experts: strength * (log p_rank - mean), p ~ rank^-s."""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    p = np.arange(1, n_experts + 1, dtype=np.float64) ** -s
+    b = np.empty(n_experts)
+    b[rng.permutation(n_experts)] = np.log(p / p.sum())
+    return (strength * (b - b.mean())).astype(np.float32)
+
+
+def bench_batch(lib, layer, n_tokens, iters):
+    """Time moe_forward_batch on n_tokens seeded tokens (warm-up call first)."""
+    import numpy as np
+    import torch
+    import synth
+    dev = torch.device("cuda:0")
+    X = synth.bf16_tokens(n_tokens, H, seed=11 + n_tokens, device=dev)
+    ws = torch.empty(lib.moe_batch_workspace_bytes(layer, n_tokens), dtype=torch.uint8,
+                     device=dev)
+    out, idx, wt = lib.moe_forward_batch(layer, X, workspace=ws)
+    torch.cuda.synchronize()
+    counts = torch.bincount(idx.flatten().long(), minlength=E).cpu().numpy()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(iters):
+        lib.moe_forward_batch(layer, X, workspace=ws, out=out)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / iters
+    pairs = int(counts.sum()) + n_tokens              # routed + shared (token, expert) pairs
+    flops = 6 * H * I * pairs
+    hit = int((counts > 0).sum())
+    wbytes = hit * EXPERT_BYTES + SHARED_BYTES + GATE_BYTES
+    return {
+        "tokens": n_tokens, "ms_per_layer": round(ms, 4),
+        "tflops": round(flops / (ms * 1e-3) / 1e12, 2),
+        "frac_bf16_mfma_peak": round(flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+        "frac_fp8_mfma_peak": round(flops / (ms * 1e-3) / 1e12 / FP8_PEAK_TFLOPS, 4),
+        "weight_gbs": round(wbytes / (ms * 1e-3) / 1e9, 1),
+        "experts_hit": hit, "max_tokens_per_expert": int(counts.max()),
+        "median_tokens_per_expert": float(np.median(counts)),
+        "expert_flops": flops, "iters": iters,
+        "mfma": "v_mfma_f32_16x16x32_bf16 (FP4/FP8 weights converted to BF16 x block scale "
+                "in registers; exact products, fp32 accumulate)",
+    }
 
 
 def cpu_baseline(layer_dev, xs, seconds):
@@ -104,23 +163,13 @@ def ref_kernel_bench():
     return res
 
 
-def main():
-    args = parse()
-    if args.gpus != 1:
-        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              f"(the multi-GPU expert-parallel design is described, not built)", file=sys.stderr)
-        sys.exit(2)
+def bench_decode(args, lib, layers):
+    """Graph-replayed decode steps over the rotated layers; returns the
+    per-step and gate/up-pass times and the graph/eager agreement."""
     import torch
-    import dsv4_gpu
     import synth
-
     dev = torch.device("cuda:0")
-    lib = dsv4_gpu.lib()
-    nl = args.layers
-    t0 = time.perf_counter()
-    layers = [synth.device_layer(seed=100 + l, device=dev) for l in range(nl)]
-    torch.cuda.synchronize()
-    gen_s = time.perf_counter() - t0
+    nl = len(layers)
     nsteps = args.steps
     X = synth.bf16_tokens(nsteps + args.warmup, H, seed=7, device=dev)
     OUT = torch.empty_like(X)
@@ -180,7 +229,59 @@ def main():
     ev1.record()
     torch.cuda.synchronize()
     ms_gateup = ev0.elapsed_time(ev1) / (args.replays * nsteps)
+    del graph, g2
+    return ms_step, ms_gateup, eager_ok and replay_ok, X
 
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              f"(the multi-GPU expert-parallel design is described, not built)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import dsv4_gpu
+    import synth
+
+    dev = torch.device("cuda:0")
+    lib = dsv4_gpu.lib()
+    wl = args.workload
+    nl = args.layers if wl in ("all", "decode") else 1
+    t0 = time.perf_counter()
+    layers = [synth.device_layer(seed=100 + l, device=dev) for l in range(nl)]
+    torch.cuda.synchronize()
+    gen_s = time.perf_counter() - t0
+
+    batch = {}
+    if wl in ("all", "verify", "prefill"):
+        zl = layers[0].with_bias(torch.from_numpy(
+            zipf_bias(E, strength=args.zipf_strength)).to(dev))
+        if wl in ("all", "verify"):
+            batch["verify_64"] = bench_batch(lib, zl, 64, 50)
+        if wl in ("all", "prefill"):
+            batch["prefill_4096"] = bench_batch(lib, zl, 4096, 10)
+        for v in batch.values():
+            v["router"] = (f"Zipf(1.2) expert skew: bias {args.zipf_strength} * centred "
+                           f"log rank^-1.2 over a seeded expert permutation")
+
+    if wl in ("verify", "prefill"):
+        key = "verify_64" if wl == "verify" else "prefill_4096"
+        r = batch[key]
+        result = {
+            "metric": METRIC, "value": r["tflops"], "unit": "TFLOP/s", "n_gpus": 1,
+            "steps": r["iters"], "warmup": 1, "ms_per_step": r["ms_per_layer"],
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "bf16 MFMA operands (exact FP4/FP8 x E8M0 values), fp32 accumulate",
+            "data": "synthetic",
+            "config": dict(workload=f"{key}: {r['tokens']} tokens through one MoE layer (256 "
+                                    f"FP4 experts top-6 + FP8 shared), grouped GEMMs", **r),
+            "roofline": {"bound": "mfma", "achieved": r["tflops"], "peak": BF16_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": r["frac_bf16_mfma_peak"], "traffic": None},
+        }
+        print(json.dumps(result))
+        return
+
+    ms_step, ms_gateup, graph_ok, X = bench_decode(args, lib, layers)
     value = DECODE_BYTES / (ms_step * 1e-3) / 1e9
     achieved = GATEUP_BYTES / (ms_gateup * 1e-3) / 1e9
     result = {
@@ -188,7 +289,7 @@ def main():
         "value": round(value, 2),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": nsteps,
+        "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_step, 5),
         "higher_is_better": True,
@@ -204,8 +305,9 @@ def main():
             "algorithmic_bytes_per_step": DECODE_BYTES,
             "algorithmic_flops_per_step": DECODE_FLOPS,
             "layers_rotated": nl,
-            "graph_replay_matches_eager": eager_ok and replay_ok,
+            "graph_replay_matches_eager": graph_ok,
             "layer_generation_s": round(gen_s, 2),
+            **batch,
         },
         "roofline": {
             "bound": "hbm",

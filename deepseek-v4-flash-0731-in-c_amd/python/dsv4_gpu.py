@@ -298,6 +298,10 @@ class DeviceLayer:
         self.struct = L
         self.meta = meta
 
+    def with_bias(self, bias):
+        """The same weights (shared, not copied) with another router bias."""
+        return DeviceLayer(dict(self.tensors, bias=bias), self.meta)
+
     @classmethod
     def from_host(cls, layer: dict, device="cuda"):
         """Upload a host (numpy) layer dict as built by tests/common.make_layer."""
