@@ -1,0 +1,954 @@
+// dsv4_decode.hip - the decode MoE layer on gfx950: moe_forward
+// (src/dsv4/dsv4_model.c:6599-6807) for a few tokens, bit for bit, as four
+// kernels per layer.
+//
+//   k_dec_router   approximate router logits z and sum|w*x| for every
+//                  (token, expert) and the approximate choice
+//                  sqrt_softplus(z) + bias; the FP8 activation quant of x.
+//                  The last logit workgroup to finish derives each token's
+//                  candidate experts (below).
+//   k_dec_gateup   gate and up GEMVs of every candidate (FP4) and of the
+//                  shared expert (FP8), a workgroup holding the same rows of
+//                  both so that it writes t = silu(bf16 gate) * bf16 up
+//                  (src/dsv4/dsv4_model.c:6264-6268); beside them one
+//                  workgroup per candidate slot runs the reference's exact
+//                  sequential logit chain (dsv4_gemv_bf16,
+//                  src/dsv4/dsv4_model.c:298-303), and the last of those
+//                  takes the exact top-k and route weights
+//                  (src/dsv4/dsv4_model.c:6615-6676).
+//   k_dec_down     per (token, route): y = bf16(t * w), per-128 FP8 requant
+//                  into LDS (src/dsv4/dsv4_model.c:6239-6287), the down GEMV.
+//   k_dec_combine  the routes in ascending expert id, then the shared expert,
+//                  rounded to BF16 (src/dsv4/dsv4_model.c:6795-6805).
+//
+// Candidates. A parallel logit differs from the sequential fmaf chain by at
+// most gamma_{H/64+8} + gamma_H times sum|w*x|. Mapped through
+// |d score / dz| <= 1/2 plus slack for the score's own rounding, and doubled
+// for both sides, that gives delta: an expert whose approximate choice is
+// below (k-th best approximate choice) - delta has k experts surely above it
+// and cannot be selected. The others are the candidates, in ascending expert
+// id. Gate/up runs for the first `maxc` of them while the exact chains run
+// beside it, so the chains' latency (a 4096-long dependent fmaf chain, about
+// 15 us) hides under the weight stream. With more candidates than slots
+// (near-ties such as a constant gate) the chains cover every candidate and
+// the down kernel computes t for a selected expert without a slot itself:
+// slow, still exact.
+//
+// Cross-workgroup hand-offs (logits -> candidates, chains -> selection) use
+// one device-scope release fence and counter increment per workgroup; the
+// last arrival acquires, does the work and resets its counter. The counters
+// sit in the first bytes of the workspace, which must be zero before the
+// first call (dsv4g_moe_workspace_init); every call leaves them zero.
+#include "dsv4_device.h"
+#include "dsv4_gpu_internal.h"
+#include "dsv4_tiles.h"
+
+namespace dsv4 {
+
+#define DEC_CTL_BYTES 4096  // control words: [0] + one per token, so n <= 1023
+
+struct DecArgs {
+  const float *x;
+  float *out;
+  const uint16_t *gate;
+  const float *bias;
+  const int64_t *tid2eid;
+  const int *token_ids;
+  const uint8_t *experts;
+  size_t expert_stride, scale_run;
+  const uint8_t *sh[3], *sh_s[3];  // shared gate, up, down
+  unsigned *ctl;                   // [0] logit arrivals, [1 + t] chain arrivals of token t
+  uint8_t *qx8;                    // [n][H] E4M3 codes of the quantised activation
+  float *qxs;                      // [n][H/128] its scales
+  float *ch, *zabs;                // [n][E]
+  int *cand;                       // [n][E] candidate ids, ascending
+  int *ncand;                      // [n]
+  float *zx;                       // [n][E] exact logit per candidate position
+  int *sel_e;                      // [n][K] routing, ascending id (moe_forward's idx)
+  float *sel_w;                    // [n][K] route weights (moe_forward's wt)
+  int *sel_pos;                    // [n][K] candidate position of each route
+  float *sv;                       // [n][maxc + 1][I] SwiGLU t; slot maxc = shared expert
+  float *fb;                       // [n][K][I] t of selected experts without a slot
+  float *ro;                       // [n][K + 1][H] per-route outputs (BF16 values)
+  int *idx_out;                    // optional copies of the routing
+  float *wt_out;
+  int n, H, I, E, K, maxc;
+  int gu_tiles, dn_tiles;  // paired gate/up tiles (rows I, in H); down tiles (rows H, in I)
+  float route_scale, limit;
+};
+
+// Expert e's matrix m (0 gate w1, 1 up w3, 2 down w2) in the reference slot
+// layout [s1 | s2 | s3 | w1 | w2 | w3] (src/dsv4/dsv4_model.c:1584-1640).
+__device__ __forceinline__ void expert_mat(const DecArgs &a, int e, int m, const uint8_t *&W,
+                                           const uint8_t *&S) {
+  const uint8_t *sc = a.experts + (size_t)e * a.expert_stride;
+  const uint8_t *wt = sc + a.scale_run;
+  const size_t w1 = (size_t)a.I * (a.H / 2), w2 = (size_t)a.H * (a.I / 2);
+  const size_t s1 = (size_t)a.I * (a.H / 32), s2 = (size_t)a.H * (a.I / 32);
+  if (m == 0) {
+    W = wt;
+    S = sc;
+  } else if (m == 1) {
+    W = wt + w1 + w2;
+    S = sc + s1 + s2;
+  } else {
+    W = wt + w1;
+    S = sc + s1;
+  }
+}
+
+// The 4096 bytes of FP4 tile scales follow the pairs in dynamic LDS.
+__device__ __forceinline__ uint8_t *fp4_scale_lds(float *lds, const Fp4Geom &q) {
+  return reinterpret_cast<uint8_t *>(lds) + (size_t)(FP4_LDS_ENTRIES + 2 * q.tr) * 8;
+}
+
+// One arrival on *cnt by the calling workgroup, after its global writes;
+// true (workgroup-uniform) for the arrival that completes `total`, which then
+// sees every other arrival's writes.
+__device__ __forceinline__ bool dec_arrive_last(unsigned *cnt, unsigned total, int *s_flag) {
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    __threadfence();
+    const unsigned old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = old == total - 1u;
+    if (last) __threadfence();
+    *s_flag = last;
+  }
+  __syncthreads();
+  return *s_flag != 0;
+}
+
+// Candidates of token t in ascending expert id (whole calling wave) into
+// cand[0 .. count); returns the count. A hash layer's candidates are its
+// tid2eid row. NPER = experts per lane (E <= 64 * NPER).
+template <int NPER>
+__device__ int dec_candidates_t(const DecArgs &a, int t, int *cand) {
+  const int lane = threadIdx.x % 64;
+  const float *cht = a.ch + (size_t)t * a.E, *zat = a.zabs + (size_t)t * a.E;
+  const float ninf = -__builtin_inff();
+  float v[NPER];
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NPER; ++j) {
+    const int e = lane + 64 * j;
+    v[j] = ninf;
+    if (e < a.E) {
+      const float c = cht[e];
+      v[j] = c == c ? c : ninf;  // a NaN choice never wins a strict '>'
+      amax = fmaxf(amax, zat[e]);
+    }
+  }
+  // k-th best approximate choice: k times remove one instance of the maximum
+  float kth = ninf;
+  unsigned used = 0u;
+  for (int k = 0; k < a.K; ++k) {
+    float m = ninf;
+    int mj = -1;
+#pragma unroll
+    for (int j = 0; j < NPER; ++j)
+      if (!((used >> j) & 1u) && v[j] > m) {
+        m = v[j];
+        mj = j;
+      }
+    const float wm = wave_max_dpp(m);
+    const unsigned long long bal = __ballot(mj >= 0 && m == wm);
+    if (bal == 0ull) {  // fewer than k selectable experts
+      kth = ninf;
+      break;
+    }
+    if (lane == __builtin_ctzll(bal)) used |= 1u << mj;
+    kth = wm;
+  }
+  const float sum_abs = wave_max_dpp(amax);
+  const float bound_z = (gamma_n(a.H / 64 + 8) + gamma_n(a.H)) * sum_abs;
+  const float thr = kth - 2.0f * (0.5f * bound_z + 1e-5f);
+  int base = 0;
+#pragma unroll
+  for (int j = 0; j < NPER; ++j) {
+    const int e = lane + 64 * j;
+    const bool p = e < a.E && v[j] >= thr;
+    const unsigned long long bal = __ballot(p);
+    const int pos = base + __popcll(bal & ((1ull << lane) - 1ull));
+    if (p) cand[pos] = e;
+    base += __popcll(bal);
+  }
+  return base;
+}
+
+__device__ int dec_candidates(const DecArgs &a, int t, int *cand) {
+  if (a.tid2eid) {
+    const int64_t *row = a.tid2eid + (size_t)a.token_ids[t] * a.K;
+    for (int k = threadIdx.x % 64; k < a.K; k += 64) cand[k] = (int)row[k];
+    return a.K;
+  }
+  if (a.E <= 64) return dec_candidates_t<1>(a, t, cand);
+  if (a.E <= 128) return dec_candidates_t<2>(a, t, cand);
+  if (a.E <= 256) return dec_candidates_t<4>(a, t, cand);
+  if (a.E <= 512) return dec_candidates_t<8>(a, t, cand);
+  return dec_candidates_t<16>(a, t, cand);
+}
+
+__device__ void dec_select_finish(const DecArgs &a, int t, int my_e, float my_sc, int my_pos);
+
+// Exact top-k of token t from the candidates' exact logits (one whole wave):
+// routes ascending by id with weights and candidate positions, written to
+// sel_* (and idx_out / wt_out) (src/dsv4/dsv4_model.c:6615-6676). Lane k
+// carries route k in selection order.
+template <int NPER>
+__device__ void dec_select_t(const DecArgs &a, int t, const uint64_t *tab) {
+  const int lane = threadIdx.x % 64;
+  const int K = a.K;
+  const int nc = a.ncand[t];
+  const int *ct = a.cand + (size_t)t * a.E;
+  const float *zt = a.zx + (size_t)t * a.E;
+  int my_e = -1, my_pos = -1;
+  float my_sc = 0.0f;
+  if (a.tid2eid) {
+    if (lane < K) {
+      my_e = ct[lane];
+      my_pos = lane;
+      my_sc = (my_e >= 0 && my_e < a.E) ? sqrt_softplus(zt[lane], tab) : 0.0f;
+    }
+  } else {
+    const float ninf = -__builtin_inff();
+    float sc[NPER], chv[NPER];
+    int ce[NPER];
+#pragma unroll
+    for (int j = 0; j < NPER; ++j) {
+      const int pos = lane + 64 * j;
+      sc[j] = 0.0f;
+      chv[j] = ninf;
+      ce[j] = -1;
+      if (pos < nc) {
+        ce[j] = ct[pos];
+        sc[j] = sqrt_softplus(zt[pos], tab);
+        chv[j] = sc[j] + (a.bias ? a.bias[ce[j]] : 0.0f);
+      }
+    }
+    unsigned used = 0u;
+    for (int k = 0; k < K; ++k) {
+      // strict '>' in ascending id: the lowest id (position) wins a tie
+      float m = ninf;
+      int mj = -1;
+#pragma unroll
+      for (int j = 0; j < NPER; ++j)
+        if (!((used >> j) & 1u) && chv[j] > m) {
+          m = chv[j];
+          mj = j;
+        }
+      const float wm = wave_max_dpp(m);
+      const int win = wave_min_dpp((mj >= 0 && m == wm) ? lane + 64 * mj : 0x7fffffff);
+      if (win == 0x7fffffff) continue;  // nothing left: route k stays empty (-1)
+      float wsc = 0.0f;
+      int we = -1;
+#pragma unroll
+      for (int j = 0; j < NPER; ++j)
+        if (j == mj) {
+          wsc = sc[j];
+          we = ce[j];
+        }
+      const int wl = win % 64;
+      if (lane == wl) used |= 1u << mj;
+      const float bsc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wsc), wl));
+      const int be = __builtin_amdgcn_readlane(we, wl);
+      if (lane == k) {
+        my_e = be;
+        my_sc = bsc;
+        my_pos = win;
+      }
+    }
+  }
+  dec_select_finish(a, t, my_e, my_sc, my_pos);
+}
+
+// Route weights from the unbiased scores, summed in selection order, then the
+// routes sorted by id (src/dsv4/dsv4_model.c:6650-6674; equal ids carry
+// equal weights, so any order among them matches the exchange sort). Lane k
+// holds route k in selection order.
+__device__ void dec_select_finish(const DecArgs &a, int t, int my_e, float my_sc, int my_pos) {
+  const int lane = threadIdx.x % 64;
+  const int K = a.K;
+  float sum = 0.0f;
+  for (int k = 0; k < K; ++k) {
+    const int ek = __builtin_amdgcn_readlane(my_e, k);
+    const float sk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_sc), k));
+    sum += ek >= 0 ? sk : 0.0f;
+  }
+  const float rs = sum > 0.0f ? a.route_scale / sum : 0.0f;
+  const float my_w = (sum > 0.0f && my_e >= 0) ? my_sc * rs : 0.0f;
+  int rank = 0;
+  for (int k = 0; k < K; ++k) {
+    const int ek = __builtin_amdgcn_readlane(my_e, k);
+    rank += (ek < my_e || (ek == my_e && k < lane)) ? 1 : 0;
+  }
+  if (lane < K) {
+    const size_t o = (size_t)t * K + rank;
+    a.sel_e[o] = my_e;
+    a.sel_w[o] = my_w;
+    a.sel_pos[o] = my_pos;
+    if (a.idx_out) a.idx_out[o] = my_e;
+    if (a.wt_out) a.wt_out[o] = my_w;
+  }
+}
+
+// More than 256 candidates (near-ties or large expert counts): scores in
+// LDS (2 * nc floats, nc <= 1024), scanned with plain loops.
+__device__ void dec_select_big(const DecArgs &a, int t, const uint64_t *tab, float *lds) {
+  const int lane = threadIdx.x % 64;
+  const int nc = a.ncand[t];
+  const int *ct = a.cand + (size_t)t * a.E;
+  const float *zt = a.zx + (size_t)t * a.E;
+  const float ninf = -__builtin_inff();
+  float *sc = lds, *chv = lds + nc;
+  for (int pos = lane; pos < nc; pos += 64) {
+    sc[pos] = sqrt_softplus(zt[pos], tab);
+    chv[pos] = sc[pos] + (a.bias ? a.bias[ct[pos]] : 0.0f);
+  }
+  __builtin_amdgcn_wave_barrier();
+  int my_e = -1, my_pos = -1;
+  float my_sc = 0.0f;
+  for (int k = 0; k < a.K; ++k) {
+    float m = ninf;
+    int mp = 0x7fffffff;
+    for (int pos = lane; pos < nc; pos += 64)
+      if (chv[pos] > m) {  // ascending positions: the lowest wins a tie
+        m = chv[pos];
+        mp = pos;
+      }
+    const float wm = wave_max_dpp(m);
+    const int win = wave_min_dpp((mp != 0x7fffffff && m == wm) ? mp : 0x7fffffff);
+    if (win == 0x7fffffff) continue;
+    if (lane == k) {
+      my_e = ct[win];
+      my_sc = sc[win];
+      my_pos = win;
+    }
+    __builtin_amdgcn_wave_barrier();
+    if (lane == 0) chv[win] = ninf;  // taken
+    __builtin_amdgcn_wave_barrier();
+  }
+  dec_select_finish(a, t, my_e, my_sc, my_pos);
+}
+
+__device__ void dec_select(const DecArgs &a, int t, const uint64_t *tab, float *lds) {
+  const int nc = a.tid2eid ? 0 : a.ncand[t];
+  if (nc <= 64) return dec_select_t<1>(a, t, tab);
+  if (nc <= 128) return dec_select_t<2>(a, t, tab);
+  if (nc <= 256) return dec_select_t<4>(a, t, tab);
+  dec_select_big(a, t, tab, lds);
+}
+
+// ------------------------------------------------------------ router ----
+// Blocks [0, ceil(E/4)): one wave per expert, for every token (the gate row
+// stays in registers; x is staged in LDS); the last of them derives the
+// candidates. Later blocks: FP8 activation quant, one wave per (token,
+// 128-group).
+__global__ __launch_bounds__(256) void k_dec_router(DecArgs a) {
+  extern __shared__ __align__(16) float xs[];  // H floats
+  __shared__ uint64_t s_tab[32];
+  __shared__ int s_flag;
+  const int tid = threadIdx.x, wv = tid / 64, lane = tid % 64;
+  const int H = a.H;
+  const int nlog = (a.E + 3) / 4;
+  if ((int)blockIdx.x < nlog) {
+    const int e = blockIdx.x * 4 + wv;
+    const bool act = e < a.E;
+    const uint16_t *gr = a.gate + (size_t)(act ? e : 0) * H;
+    uint4 w[16];  // lane holds columns 8 lane + 512 i
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int c = 8 * lane + 512 * i;
+      w[i] = (act && c < H) ? *reinterpret_cast<const uint4 *>(gr + c) : make_uint4(0, 0, 0, 0);
+    }
+    libm_stage_table(s_tab);
+    for (int t = 0; t < a.n; ++t) {
+      __syncthreads();
+      const float *xt = a.x + (size_t)t * H;
+      for (int i = 4 * tid; i < H; i += 1024)
+        *reinterpret_cast<float4 *>(xs + i) = *reinterpret_cast<const float4 *>(xt + i);
+      __syncthreads();
+      float acc = 0.0f, aabs = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int c = 8 * lane + 512 * i;
+        if (c < H) {
+          const float4 xa = *reinterpret_cast<const float4 *>(xs + c);
+          const float4 xb = *reinterpret_cast<const float4 *>(xs + c + 4);
+          const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+          const uint32_t wd[4] = {w[i].x, w[i].y, w[i].z, w[i].w};
+#pragma unroll
+          for (int d = 0; d < 4; ++d) {
+            const float p0 = u2f(wd[d] << 16) * xv[2 * d];
+            const float p1 = u2f(wd[d] & 0xFFFF0000u) * xv[2 * d + 1];
+            acc += p0;
+            acc += p1;
+            aabs += fabsf(p0);
+            aabs += fabsf(p1);
+          }
+        }
+      }
+      acc = wave_sum(acc);
+      aabs = wave_sum(aabs);
+      if (act && lane == 0) {
+        a.ch[(size_t)t * a.E + e] = sqrt_softplus(acc, s_tab) + (a.bias ? a.bias[e] : 0.0f);
+        a.zabs[(size_t)t * a.E + e] = aabs;
+      }
+    }
+    if (!dec_arrive_last(&a.ctl[0], (unsigned)nlog, &s_flag)) return;
+    for (int t = wv; t < a.n; t += 4) {
+      const int nc = dec_candidates(a, t, a.cand + (size_t)t * a.E);
+      if (lane == 0) a.ncand[t] = nc;
+    }
+    if (tid == 0) a.ctl[0] = 0u;
+    return;
+  }
+  const int b = blockIdx.x - nlog;
+  const int gpt = H / 128, gi = b * 4 + wv;
+  if (gi >= a.n * gpt) return;
+  const int t = gi / gpt, g = gi % gpt;
+  // quant_fp8_act (src/dsv4/dsv4_ops.c:96-121) of one 128-group
+  const float *xr = a.x + (size_t)t * H + g * 128;
+  const float v0 = xr[lane], v1 = xr[lane + 64];
+  const float amax = wave_max(fmaxf(fabsf(v0), fabsf(v1)));
+  const float scale = act_scale(amax);
+  const float inv = 1.0f / scale;
+  uint8_t *q = a.qx8 + (size_t)t * H + g * 128;
+  q[lane] = (uint8_t)e4m3_code(quant_e4m3(v0, inv));
+  q[lane + 64] = (uint8_t)e4m3_code(quant_e4m3(v1, inv));
+  if (lane == 0) a.qxs[(size_t)t * gpt + g] = scale;
+}
+
+// --------------------------------------------------------- gate / up ----
+// 16 columns of the exact logit chain: acc = fmaf(g[c], x[c], acc) in order.
+__device__ __forceinline__ float chain16(const float4 (&g)[4], const float4 (&x)[4], float acc) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    acc = fmaf(g[j].x, x[j].x, acc);
+    acc = fmaf(g[j].y, x[j].y, acc);
+    acc = fmaf(g[j].z, x[j].z, acc);
+    acc = fmaf(g[j].w, x[j].w, acc);
+  }
+  return acc;
+}
+
+// Exact logits of candidate positions c, c + maxc, ... of token t: the whole
+// block stages x and the candidate's gate row (widened to fp32) into LDS in
+// one shot, then wave 0 runs the reference's fmaf chain in column order
+// (every lane the same chain; lane 0's result is kept). The chain is a pure
+// sequence of dependent fmas fed by 16-column LDS batches in two register
+// sets, the next batch's reads in flight while the current one is chained.
+// The last chain workgroup of the token selects the routes.
+__device__ void dec_chain_block(const DecArgs &a, int t, int c, float *lds, uint64_t *s_tab,
+                                int *s_flag) {
+  const int tid = threadIdx.x, wv = tid / 64;
+  const int H = a.H;
+  libm_stage_table(s_tab);
+  const int nc = a.ncand[t];
+  const float *xt = a.x + (size_t)t * H;
+  float *xs = lds, *gs = lds + H;  // H floats each
+  if (c < nc)
+    for (int i = tid; i < H / 4; i += 256)
+      reinterpret_cast<float4 *>(xs)[i] = reinterpret_cast<const float4 *>(xt)[i];
+  for (int pos = c; pos < nc; pos += a.maxc) {
+    const int e = a.cand[(size_t)t * a.E + pos];
+    float acc = 0.0f;
+    if (e >= 0 && e < a.E) {
+      const uint16_t *gr = a.gate + (size_t)e * H;
+      for (int i = tid; i < H / 8; i += 256) {
+        const uint4 w = reinterpret_cast<const uint4 *>(gr)[i];
+        float4 *gp = reinterpret_cast<float4 *>(gs) + 2 * i;
+        gp[0] = make_float4(u2f(w.x << 16), u2f(w.x & 0xFFFF0000u), u2f(w.y << 16),
+                            u2f(w.y & 0xFFFF0000u));
+        gp[1] = make_float4(u2f(w.z << 16), u2f(w.z & 0xFFFF0000u), u2f(w.w << 16),
+                            u2f(w.w & 0xFFFF0000u));
+      }
+      __syncthreads();
+      if (wv == 0) {
+        // a zero held in a VGPR: with a provably uniform address the backend
+        // splits each 16-byte LDS read into four
+        int vz;
+        asm volatile("v_mov_b32 %0, 0" : "=v"(vz));
+        const float4 *xp = reinterpret_cast<const float4 *>(xs) + vz;
+        const float4 *gp = reinterpret_cast<const float4 *>(gs) + vz;
+        // 128 columns per iteration: eight 16-column batches, fully unrolled,
+        // each batch's LDS reads issued before the previous batch is chained
+        // (no register state carried across iterations; H % 128 == 0)
+        for (int c0 = 0; c0 < H / 4; c0 += 32) {
+          float4 xa[4], ga[4], xb[4], gb[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            xa[j] = xp[c0 + j];
+            ga[j] = gp[c0 + j];
+          }
+#pragma unroll
+          for (int h = 0; h < 4; ++h) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              xb[j] = xp[c0 + 8 * h + 4 + j];
+              gb[j] = gp[c0 + 8 * h + 4 + j];
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            acc = chain16(ga, xa, acc);
+            __builtin_amdgcn_sched_barrier(0);
+            if (h < 3) {
+#pragma unroll
+              for (int j = 0; j < 4; ++j) {
+                xa[j] = xp[c0 + 8 * h + 8 + j];
+                ga[j] = gp[c0 + 8 * h + 8 + j];
+              }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            acc = chain16(gb, xb, acc);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+      }
+      __syncthreads();  // the next candidate restages the gate row
+    }
+    if (tid == 0) a.zx[(size_t)t * a.E + pos] = acc;
+  }
+  if (!dec_arrive_last(&a.ctl[1 + t], (unsigned)a.maxc, s_flag)) return;
+  if (wv == 0) dec_select(a, t, s_tab, lds);
+  if (tid == 0) a.ctl[1 + t] = 0u;
+}
+
+// Blocks: [n*maxc chain workgroups][n*(I/8) shared FP8 pairs]
+// [maxc*n*gu_tiles routed FP4 pairs, candidate-major]; routed tiles of
+// candidate slots a token does not use exit at once.
+__global__ __launch_bounds__(256) void k_dec_gateup(DecArgs a) {
+  extern __shared__ __align__(16) float lds[];
+  __shared__ uint64_t s_tab[32];
+  __shared__ float s_y[256];
+  __shared__ int s_flag;
+  const int tid = threadIdx.x;
+  const int H = a.H, I = a.I;
+  const int nchain = a.n * a.maxc;
+  const int t8 = (I + FP8_TR / 2 - 1) / (FP8_TR / 2);
+  const int nshared = a.n * t8;
+  int b = blockIdx.x;
+  if (b < nchain) {
+    dec_chain_block(a, b / a.maxc, b % a.maxc, lds, s_tab, &s_flag);
+    return;
+  }
+  b -= nchain;
+  if (b < nshared) {
+    const int tile = b % t8, t = b / t8, r0 = tile * (FP8_TR / 2);
+    // the activation (at most 8192 wide: 32 per thread) ahead of the weights
+    const uint8_t *qx8 = a.qx8 + (size_t)t * H;
+    uint32_t xr[32];
+#pragma unroll
+    for (int j = 0; j < 32; ++j) xr[j] = tid + 256 * j < H ? qx8[tid + 256 * j] : 0u;
+    Fp8Regs R;
+    fp8_pair_load(R, a.sh[0], a.sh[1], H, I, r0);
+    libm_stage_table(s_tab);
+    float *xs = lds;
+    float2 *ps = reinterpret_cast<float2 *>(lds + (H / 128) * 132);
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+      const int i = tid + 256 * j;
+      if (i < H) xs[(i / 128) * 132 + (i % 128)] = e4m3_decode(xr[j]);
+    }
+    __syncthreads();
+    fp8_pair_finish(R, s_y, xs, a.qxs + (size_t)t * (H / 128), a.sh[0], a.sh_s[0], a.sh[1],
+                    a.sh_s[1], H, I, r0, ps);
+    __syncthreads();
+    if (tid < FP8_TR / 2 && r0 + tid < I)
+      a.sv[((size_t)t * (a.maxc + 1) + a.maxc) * I + r0 + tid] =
+          swiglu_t(s_y[tid], s_y[tid + FP8_TR / 2], a.limit, s_tab);
+    return;
+  }
+  b -= nshared;
+  const int tile = b % a.gu_tiles;
+  b /= a.gu_tiles;
+  const int t = b % a.n, c = b / a.n;
+  const int nc = a.ncand[t];
+  if (c >= min(nc, a.maxc)) return;
+  const int e = a.cand[(size_t)t * a.E + c];
+  if (e < 0 || e >= a.E) return;  // malformed tid2eid entry: the route contributes zeros
+  const Fp4Geom q = fp4_geom(H);
+  const int half = q.tr / 2, r0 = tile * half;
+  const uint8_t *W0, *S0, *W1, *S1;
+  expert_mat(a, e, 0, W0, S0);
+  expert_mat(a, e, 1, W1, S1);
+  Fp4Regs R;
+  fp4_tile_x(R, a.qx8 + (size_t)t * H, a.qxs + (size_t)t * (H / 128), q);
+  fp4_pair_load(R, W0, S0, W1, S1, H, I, r0, q);
+  libm_stage_table(s_tab);
+  fp4_pair_finish(R, s_y, I, r0, q, reinterpret_cast<float2 *>(lds), fp4_scale_lds(lds, q));
+  __syncthreads();
+  if (tid < half && r0 + tid < I)
+    a.sv[((size_t)t * (a.maxc + 1) + c) * I + r0 + tid] =
+        swiglu_t(s_y[tid], s_y[tid + half], a.limit, s_tab);
+}
+
+// -------------------------------------------------------------- down ----
+// y = bf16(t * w), then per-128 E4M3 requant into LDS (all threads):
+// qy[i + pad * (i / 128)], qys[i / 128] (src/dsv4/dsv4_model.c:6268-6287).
+// Wave wv takes groups wv, wv + 4, ...; the t values of its first eight
+// groups (all of them for inter <= 4096) are loaded ahead of the weights by
+// dec_tv_load.
+struct TvRegs {
+  float v[16];
+};
+
+__device__ __forceinline__ void dec_tv_load(TvRegs &T, const float *tv, int I) {
+  const int wv = threadIdx.x / 64, lane = threadIdx.x % 64;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int g = wv + 4 * j;
+    T.v[2 * j] = g < I / 128 ? tv[g * 128 + lane] : 0.0f;
+    T.v[2 * j + 1] = g < I / 128 ? tv[g * 128 + 64 + lane] : 0.0f;
+  }
+}
+
+// CODES: qy receives E4M3 codes as bytes (the FP4 down tile), otherwise the
+// grid values as floats, padded by 4 per 128 (the FP8 tile).
+template <bool CODES>
+__device__ void dec_requant(void *qyv, float *qys, const TvRegs &T, const float *tv, float w,
+                            int I) {
+  const int wv = threadIdx.x / 64, lane = threadIdx.x % 64;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const int g = wv + 4 * j;
+    if (g >= I / 128) break;
+    const int i0 = g * 128 + lane, i1 = i0 + 64;
+    const float t0 = j < 8 ? T.v[(2 * j) & 15] : tv[i0];
+    const float t1 = j < 8 ? T.v[(2 * j + 1) & 15] : tv[i1];
+    const float y0 = bf16_round(t0 * w);
+    const float y1 = bf16_round(t1 * w);
+    const float amax = wave_max(fmaxf(fabsf(y0), fabsf(y1)));
+    const float scale = act_scale(amax);
+    const float inv = 1.0f / scale;
+    if (CODES) {
+      uint8_t *q = reinterpret_cast<uint8_t *>(qyv) + g * 128;
+      q[lane] = (uint8_t)e4m3_code(quant_e4m3(y0, inv));
+      q[lane + 64] = (uint8_t)e4m3_code(quant_e4m3(y1, inv));
+    } else {
+      float *q = reinterpret_cast<float *>(qyv) + g * 132;
+      q[lane] = quant_e4m3(y0, inv);
+      q[lane + 64] = quant_e4m3(y1, inv);
+    }
+    if (lane == 0) qys[g] = scale;
+  }
+  __syncthreads();
+}
+
+// One FP4 row in the reference's order (per-32 partials, then the group
+// chain; src/dsv4/dsv4_model.c:651-673), by a single lane, BF16-rounded.
+__device__ float dec_row_exact(const uint8_t *W, const uint8_t *S, const uint8_t *qx8,
+                               const float *qxs, int in, int row) {
+  const int G = in / 32;
+  const uint8_t *wr = W + (size_t)row * (in / 2);
+  const uint8_t *sr = S + (size_t)row * G;
+  float acc = 0.0f;
+  for (int g = 0; g < G; ++g) {
+    const uint32_t code = sr[g];
+    if (code == 255u) continue;  // NaN scale: the reference skips the group
+    float xq[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) xq[i] = e4m3_decode(qx8[32 * g + i]);
+    const float p = fp4_group_partial(*reinterpret_cast<const uint4 *>(wr + 16 * g), xq);
+    acc = fmaf(p, qxs[g / 4] * e8m0(code), acc);
+  }
+  return bf16_round(acc);
+}
+
+// t of expert e for token t into fb (route slot k), for a selected expert
+// that had no candidate slot: one row per lane, few registers (this path
+// only runs on near-ties). Every workgroup of that route computes the same
+// values and reads back only its own writes (ordered by the barrier).
+__device__ void dec_fallback_t(const DecArgs &a, int t, int k, int e, uint64_t *tab) {
+  libm_stage_table(tab);
+  __syncthreads();
+  const uint8_t *W0, *S0, *W1, *S1;
+  expert_mat(a, e, 0, W0, S0);
+  expert_mat(a, e, 1, W1, S1);
+  const uint8_t *qx = a.qx8 + (size_t)t * a.H;
+  const float *qxs = a.qxs + (size_t)t * (a.H / 128);
+  float *dst = a.fb + ((size_t)t * a.K + k) * a.I;
+  for (int r = threadIdx.x; r < a.I; r += 256) {
+    const float g = dec_row_exact(W0, S0, qx, qxs, a.H, r);
+    const float u = dec_row_exact(W1, S1, qx, qxs, a.H, r);
+    dst[r] = swiglu_t(g, u, a.limit, tab);
+  }
+  __syncthreads();
+}
+
+// Blocks: [n*K*dn_tiles routed FP4 down tiles][n*(H/16) shared FP8 tiles].
+__global__ __launch_bounds__(256) void k_dec_down(DecArgs a) {
+  extern __shared__ __align__(16) float lds[];
+  __shared__ uint64_t s_tab[32];
+  const int tid = threadIdx.x;
+  const int H = a.H, I = a.I, K = a.K;
+  const int nrouted = a.n * K * a.dn_tiles;
+  int b = blockIdx.x;
+  if (b < nrouted) {
+    const int tile = b % a.dn_tiles;
+    b /= a.dn_tiles;
+    const int k = b % K, t = b / K;
+    const size_t o = (size_t)t * K + k;
+    const int e = a.sel_e[o], pos = a.sel_pos[o];
+    const float w = a.sel_w[o];
+    const Fp4Geom q = fp4_geom(I);
+    const int r0 = tile * q.tr;
+    float *ro = a.ro + ((size_t)t * (K + 1) + k) * H;
+    if (e < 0 || e >= a.E) {  // no expert: the route adds zeros
+      for (int r = r0 + tid; r < min(H, r0 + q.tr); r += 256) ro[r] = 0.0f;
+      return;
+    }
+    if (pos >= a.maxc) dec_fallback_t(a, t, k, e, s_tab);
+    const float *tv = pos < a.maxc ? a.sv + ((size_t)t * (a.maxc + 1) + pos) * I
+                                   : a.fb + ((size_t)t * K + k) * I;
+    const uint8_t *W, *S;
+    expert_mat(a, e, 2, W, S);
+    TvRegs T;
+    dec_tv_load(T, tv, I);
+    Fp4Regs R;
+    fp4_tile_load(R, W, S, I, H, r0, q);
+    // E4M3 codes and scales of y, read into registers before the pairs
+    // overwrite them
+    uint8_t *qy8 = reinterpret_cast<uint8_t *>(lds);  // I + I/32 bytes: within the pairs
+    float *qys = lds + I / 4;
+    dec_requant<true>(qy8, qys, T, tv, w, I);
+    fp4_tile_x(R, qy8, qys, q);
+    fp4_tile_finish(R, ro, H, r0, q, reinterpret_cast<float2 *>(lds), fp4_scale_lds(lds, q));
+    return;
+  }
+  b -= nrouted;
+  const int t16 = (H + FP8_TR - 1) / FP8_TR;
+  const int tile = b % t16, t = b / t16;
+  const float *tv = a.sv + ((size_t)t * (a.maxc + 1) + a.maxc) * I;
+  TvRegs T;
+  dec_tv_load(T, tv, I);
+  Fp8Regs R;
+  fp8_tile_load(R, a.sh[2], I, H, tile * FP8_TR);
+  float *xs = lds, *qys = lds + (I / 128) * 132;
+  float2 *ps = reinterpret_cast<float2 *>(qys + ((I / 128 + 3) & ~3));
+  dec_requant<false>(xs, qys, T, tv, 1.0f, I);
+  fp8_tile_finish(R, a.ro + ((size_t)t * (K + 1) + K) * H, xs, qys, a.sh[2], a.sh_s[2], I, H,
+                  tile * FP8_TR, 1, ps);
+}
+
+// out[t][i] = bf16(((0 + ro[t][0][i]) + ... + ro[t][K-1][i]) + ro[t][K][i]):
+// routes in ascending expert id, then the shared expert
+// (src/dsv4/dsv4_model.c:6795-6805).
+__global__ __launch_bounds__(256) void k_dec_combine(DecArgs a) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= a.n * a.H) return;
+  const int t = i / a.H, c = i % a.H;
+  const float *r = a.ro + (size_t)t * (a.K + 1) * a.H + c;
+  float acc = 0.0f;
+  for (int k = 0; k < a.K; ++k) acc += r[(size_t)k * a.H];
+  acc += r[(size_t)a.K * a.H];
+  a.out[i] = bf16_round(acc);
+}
+
+__global__ void k_fill_zero_u32(unsigned *p, size_t n) {
+  const size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+}  // namespace dsv4
+
+// ============================================================ C-ABI =====
+using namespace dsv4;
+
+namespace {
+
+struct DecWs {
+  unsigned *ctl;
+  uint8_t *qx8;
+  float *qxs, *ch, *zabs, *zx, *sel_w, *sv, *fb, *ro;
+  int *cand, *ncand, *sel_e, *sel_pos;
+  size_t bytes;
+};
+
+int dec_maxc(const DSV4GLayer *L) {
+  int m = L->topk + 10;
+  if (m < 16) m = 16;
+  return m < L->n_experts ? m : L->n_experts;
+}
+
+// The control words come first (offset 0 for every layer shape), then the
+// rest, each piece 256-byte aligned.
+DecWs dec_ws_layout(const DSV4GLayer *L, int n_tokens, void *base) {
+  const size_t n = (size_t)n_tokens, K = (size_t)L->topk, E = (size_t)L->n_experts;
+  const size_t H = (size_t)L->hidden, I = (size_t)L->inter, C = (size_t)dec_maxc(L);
+  DecWs w = {};
+  uintptr_t p = (uintptr_t)base;
+  auto take = [&](size_t bytes) {
+    void *r = (void *)p;
+    p += (bytes + 255) & ~(size_t)255;
+    return r;
+  };
+  w.ctl = (unsigned *)take(DEC_CTL_BYTES);
+  w.qx8 = (uint8_t *)take(n * H);
+  w.qxs = (float *)take(n * (H / 128) * 4);
+  w.ch = (float *)take(n * E * 4);
+  w.zabs = (float *)take(n * E * 4);
+  w.cand = (int *)take(n * E * 4);
+  w.ncand = (int *)take(n * 4);
+  w.zx = (float *)take(n * E * 4);
+  w.sel_e = (int *)take(n * K * 4);
+  w.sel_w = (float *)take(n * K * 4);
+  w.sel_pos = (int *)take(n * K * 4);
+  w.sv = (float *)take(n * (C + 1) * I * 4);
+  w.fb = (float *)take(n * K * I * 4);
+  w.ro = (float *)take(n * (K + 1) * H * 4);
+  w.bytes = (size_t)(p - (uintptr_t)base);
+  return w;
+}
+
+Fp4Geom host_fp4_geom(int in) {
+  Fp4Geom q;
+  q.G = in / 32;
+  q.gp = 1;
+  while (q.gp < q.G) q.gp <<= 1;
+  q.rpp = 256 / q.gp;
+  q.tr = FP4_LDS_ENTRIES / q.gp;
+  if (q.tr > 256) q.tr = 256;
+  return q;
+}
+
+size_t max_sz(size_t a, size_t b) { return a > b ? a : b; }
+
+int dec_launch(int phase, float *out, const float *x, const DSV4GLayer *L, const int *token_ids,
+               int n_tokens, void *workspace, size_t workspace_bytes, int *idx_out,
+               float *wt_out, hipStream_t st) {
+  DSV4G_TRY(dsv4g_layer_ok(L, "moe_decode"));
+  if (n_tokens <= 0) return dsv4g_fail(DSV4G_EINVAL, "moe_decode: n_tokens must be > 0");
+  if (L->tid2eid && !token_ids)
+    return dsv4g_fail(DSV4G_EINVAL, "moe_decode: hash layer needs token_ids");
+  if (((uintptr_t)workspace & 255) || ((uintptr_t)x & 15) || ((uintptr_t)out & 15))
+    return dsv4g_fail(DSV4G_EINVAL,
+                      "moe_decode: workspace must be 256-byte aligned, x and out 16-byte aligned");
+  const DecWs w = dec_ws_layout(L, n_tokens, workspace);
+  if (!workspace || workspace_bytes < w.bytes)
+    return dsv4g_fail(DSV4G_EINVAL, "moe_decode: workspace too small (%zu < %zu)",
+                      workspace_bytes, w.bytes);
+  DecArgs a = {};
+  a.x = x;
+  a.out = out;
+  a.gate = L->gate_w;
+  a.bias = L->bias;
+  a.tid2eid = L->tid2eid;
+  a.token_ids = token_ids;
+  a.experts = L->experts;
+  a.expert_stride = L->expert_stride;
+  a.scale_run = L->scale_run;
+  a.sh[0] = L->sh1;
+  a.sh[1] = L->sh3;
+  a.sh[2] = L->sh2;
+  a.sh_s[0] = L->sh1_s;
+  a.sh_s[1] = L->sh3_s;
+  a.sh_s[2] = L->sh2_s;
+  a.ctl = w.ctl;
+  a.qx8 = w.qx8;
+  a.qxs = w.qxs;
+  a.ch = w.ch;
+  a.zabs = w.zabs;
+  a.cand = w.cand;
+  a.ncand = w.ncand;
+  a.zx = w.zx;
+  a.sel_e = w.sel_e;
+  a.sel_w = w.sel_w;
+  a.sel_pos = w.sel_pos;
+  a.sv = w.sv;
+  a.fb = w.fb;
+  a.ro = w.ro;
+  a.idx_out = idx_out;
+  a.wt_out = wt_out;
+  a.n = n_tokens;
+  a.H = L->hidden;
+  a.I = L->inter;
+  a.E = L->n_experts;
+  a.K = L->topk;
+  a.maxc = dec_maxc(L);
+  const Fp4Geom qg = host_fp4_geom(a.H), qd = host_fp4_geom(a.I);
+  a.gu_tiles = (a.I + qg.tr / 2 - 1) / (qg.tr / 2);
+  a.dn_tiles = (a.H + qd.tr - 1) / qd.tr;
+  a.route_scale = L->route_scale;
+  a.limit = (float)(int)L->swiglu_limit;  // the reference passes the limit as int
+  const int n = n_tokens, H = a.H, I = a.I;
+  if (n > DEC_CTL_BYTES / 4 - 1)
+    return dsv4g_fail(DSV4G_EINVAL, "moe_decode: at most %d tokens per call",
+                      DEC_CTL_BYTES / 4 - 1);
+  if (phase == 0) {
+    const int blocks = (a.E + 3) / 4 + (n * (H / 128) + 3) / 4;
+    hipLaunchKernelGGL(k_dec_router, dim3(blocks), dim3(256), (size_t)H * 4, st, a);
+    return dsv4g_check_launch("dec_router");
+  }
+  if (phase == 1) {
+    const size_t lds = max_sz(max_sz((size_t)(FP4_LDS_ENTRIES + 2 * qg.tr) * 8 + 4096,
+                                     (size_t)H * 8),
+                              (size_t)(H / 128) * 132 * 4 +
+                                  (size_t)FP8_TR * pair_stride(H / 128) * 8);
+    const long blocks = (long)n * a.maxc + (long)n * ((I + FP8_TR / 2 - 1) / (FP8_TR / 2)) +
+                        (long)a.maxc * n * a.gu_tiles;
+    hipLaunchKernelGGL(k_dec_gateup, dim3((unsigned)blocks), dim3(256), lds, st, a);
+    return dsv4g_check_launch("dec_gateup");
+  }
+  if (phase == 2) {
+    const size_t lds_r = (size_t)(FP4_LDS_ENTRIES + 2 * qd.tr) * 8 + 4096;
+    const size_t lds_s = (size_t)(I / 128) * 132 * 4 + (size_t)((I / 128 + 3) & ~3) * 4 +
+                         (size_t)FP8_TR * pair_stride(I / 128) * 8;
+    const long blocks = (long)n * a.K * a.dn_tiles + (long)n * ((H + FP8_TR - 1) / FP8_TR);
+    hipLaunchKernelGGL(k_dec_down, dim3((unsigned)blocks), dim3(256), max_sz(lds_r, lds_s), st,
+                       a);
+    return dsv4g_check_launch("dec_down");
+  }
+  if (phase == 3) {
+    hipLaunchKernelGGL(k_dec_combine, dim3((unsigned)((n * H + 255) / 256)), dim3(256), 0, st, a);
+    return dsv4g_check_launch("dec_combine");
+  }
+  return dsv4g_fail(DSV4G_EINVAL, "moe_decode: bad phase %d", phase);
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t dsv4g_moe_workspace_bytes(const DSV4GLayer *L, int n_tokens) {
+  return dec_ws_layout(L, n_tokens, nullptr).bytes;
+}
+
+int dsv4g_moe_workspace_init(void *workspace, size_t workspace_bytes, void *stream) {
+  if (!workspace || ((uintptr_t)workspace & 255) || workspace_bytes < DEC_CTL_BYTES)
+    return dsv4g_fail(DSV4G_EINVAL, "moe_workspace_init: bad workspace");
+  const size_t words = workspace_bytes / 4;
+  hipLaunchKernelGGL(k_fill_zero_u32, dim3((unsigned)((words + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, (unsigned *)workspace, words);
+  return dsv4g_check_launch("moe_workspace_init");
+}
+
+int dsv4g_moe_decode_phase(int phase, float *out, const float *x, const DSV4GLayer *L,
+                           const int *token_ids, int n_tokens, void *workspace,
+                           size_t workspace_bytes, void *stream) {
+  return dec_launch(phase, out, x, L, token_ids, n_tokens, workspace, workspace_bytes, nullptr,
+                    nullptr, (hipStream_t)stream);
+}
+
+int dsv4g_moe_decode_routing(int *idx_out, float *wt_out, const DSV4GLayer *L, int n_tokens,
+                             void *workspace, void *stream) {
+  const DecWs w = dec_ws_layout(L, n_tokens, workspace);
+  hipStream_t st = (hipStream_t)stream;
+  if (idx_out)
+    DSV4G_HIP(hipMemcpyAsync(idx_out, w.sel_e, (size_t)n_tokens * L->topk * sizeof(int),
+                             hipMemcpyDeviceToDevice, st));
+  if (wt_out)
+    DSV4G_HIP(hipMemcpyAsync(wt_out, w.sel_w, (size_t)n_tokens * L->topk * sizeof(float),
+                             hipMemcpyDeviceToDevice, st));
+  return 0;
+}
+
+int dsv4g_moe_forward(float *out, const float *x, const DSV4GLayer *L, const int *token_ids,
+                      int n_tokens, void *workspace, size_t workspace_bytes, int *idx_out,
+                      float *wt_out, void *stream) {
+  for (int phase = 0; phase < 4; ++phase)
+    DSV4G_TRY(dec_launch(phase, out, x, L, token_ids, n_tokens, workspace, workspace_bytes,
+                         idx_out, wt_out, (hipStream_t)stream));
+  return 0;
+}
+
+}  // extern "C"

@@ -128,20 +128,34 @@ __device__ __forceinline__ float libm_log1pf_nonneg(float x) {
   return dsv4_libm_log1pf_nonneg(x);
 }
 
+// The expf table staged in LDS by threads 0-31 (the caller synchronises):
+// kernels that evaluate expf under heavy HBM traffic read it there instead
+// of paying a global-memory round trip per call.
+__device__ __forceinline__ void libm_stage_table(uint64_t *tab) {
+  if (threadIdx.x < 32) tab[threadIdx.x] = dsv4_libm_exp2_tab[threadIdx.x];
+}
+
 // sqrt(softplus(z)) (src/dsv4/dsv4_model.c:5827-5831).
-__device__ __forceinline__ float sqrt_softplus(float z) {
+__device__ __forceinline__ float sqrt_softplus(float z, const uint64_t *tab) {
   if (z > 20.0f) return sqrtf(z);
-  return sqrtf(libm_log1pf_nonneg(libm_expf(z)));
+  return sqrtf(libm_log1pf_nonneg(dsv4_libm_expf_t(z, tab)));
+}
+__device__ __forceinline__ float sqrt_softplus(float z) {
+  return sqrt_softplus(z, dsv4_libm_exp2_tab);
 }
 
 // SwiGLU element (src/dsv4/dsv4_model.c:6264-6268): up clamped to
 // [-limit, limit], gate clamped above only, t = silu(g) * u, rounded to fp32.
-__device__ __forceinline__ float swiglu_t(float g, float u, float limit) {
+__device__ __forceinline__ float swiglu_t(float g, float u, float limit, const uint64_t *tab) {
   if (u > limit) u = limit;
   else if (u < -limit) u = -limit;
   if (g > limit) g = limit;
-  const float silu = g / (1.0f + libm_expf(-g));
+  const float silu = g / (1.0f + dsv4_libm_expf_t(-g, tab));
   return silu * u;
+}
+
+__device__ __forceinline__ float swiglu_t(float g, float u, float limit) {
+  return swiglu_t(g, u, limit, dsv4_libm_exp2_tab);
 }
 
 // Wave-wide reductions (wave64).
@@ -154,6 +168,54 @@ __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
   return v;
+}
+__device__ __forceinline__ int wave_min_i(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// The same reductions through DPP row shifts and row broadcasts (register
+// moves, no LDS round trip), for latency-critical single-wave code. The
+// windows overlap, which max/min tolerate; lane 63 ends with the result,
+// which readlane makes uniform.
+template <int CTRL, int ROW_MASK, int BANK_MASK>
+__device__ __forceinline__ float dpp_f(float v, float idv) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(idv), __float_as_int(v), CTRL,
+                                                    ROW_MASK, BANK_MASK, false));
+}
+template <int CTRL, int ROW_MASK, int BANK_MASK>
+__device__ __forceinline__ int dpp_i(int v, int idv) {
+  return __builtin_amdgcn_update_dpp(idv, v, CTRL, ROW_MASK, BANK_MASK, false);
+}
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  const float id = -__builtin_inff();
+  v = fmaxf(v, dpp_f<0x111, 0xf, 0xf>(v, id));  // row_shr:1
+  v = fmaxf(v, dpp_f<0x112, 0xf, 0xf>(v, id));  // row_shr:2
+  v = fmaxf(v, dpp_f<0x113, 0xf, 0xf>(v, id));  // row_shr:3
+  v = fmaxf(v, dpp_f<0x114, 0xf, 0xe>(v, id));  // row_shr:4
+  v = fmaxf(v, dpp_f<0x118, 0xf, 0xc>(v, id));  // row_shr:8
+  v = fmaxf(v, dpp_f<0x142, 0xa, 0xf>(v, id));  // row_bcast:15
+  v = fmaxf(v, dpp_f<0x143, 0xc, 0xf>(v, id));  // row_bcast:31
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+__device__ __forceinline__ int wave_min_dpp(int v) {
+  const int id = 0x7fffffff;
+  v = min(v, dpp_i<0x111, 0xf, 0xf>(v, id));
+  v = min(v, dpp_i<0x112, 0xf, 0xf>(v, id));
+  v = min(v, dpp_i<0x113, 0xf, 0xf>(v, id));
+  v = min(v, dpp_i<0x114, 0xf, 0xe>(v, id));
+  v = min(v, dpp_i<0x118, 0xf, 0xc>(v, id));
+  v = min(v, dpp_i<0x142, 0xa, 0xf>(v, id));
+  v = min(v, dpp_i<0x143, 0xc, 0xf>(v, id));
+  return __builtin_amdgcn_readlane(v, 63);
+}
+
+// gamma_n = n u / (1 - n u), u = 2^-24: the classic bound on the rounding
+// error of any n-term summation order.
+__device__ __forceinline__ float gamma_n(int n) {
+  const double nu = (double)n * 0x1p-24;
+  return (float)(nu / (1.0 - nu));
 }
 
 }  // namespace dsv4

@@ -27,7 +27,11 @@ struct GemvArgs {
   int in, rows, round_out;
 };
 
+// Largest expert count of the router kernels.
+#define ROUTER_MAX_EXPERTS 1024
+
 extern "C" {
+int dsv4g_layer_ok(const DSV4GLayer *L, const char *who);
 int dsv4g_fail(int code, const char *fmt, ...);
 int dsv4g_check_launch(const char *what);
 int dsv4g_launch_gemv_fp4(const GemvArgs *a, int nvec, int nmat, void *stream);

@@ -822,7 +822,9 @@ BatchWs batch_ws_layout(const DSV4GLayer *L, int T, void *base) {
   const size_t t = (size_t)T, K = (size_t)L->topk, E = (size_t)L->n_experts;
   const size_t H = (size_t)L->hidden, I = (size_t)L->inter, P = t * K + t;
   BatchWs w = {};
-  uintptr_t p = ((uintptr_t)base + 255) & ~(uintptr_t)255;
+  // the first 4096 bytes stay untouched: a workspace shared with the decode
+  // entry keeps that entry's (zero) control words there
+  uintptr_t p = (((uintptr_t)base + 255) & ~(uintptr_t)255) + 4096;
   const uintptr_t p0 = (uintptr_t)base;
   auto take = [&](size_t bytes) {
     void *r = (void *)p;

@@ -49,8 +49,9 @@ DSV4_LIBM_TABLE uint64_t dsv4_libm_exp2_tab[32] = {
 
 // expf: double-precision table method with 32 entries of 2^(i/32), a cubic
 // polynomial, and the reduction residual r formed by one fma (the form the
-// FMA-capable x86-64 libm variant computes).
-DSV4_LIBM_FN float dsv4_libm_expf(float x) {
+// FMA-capable x86-64 libm variant computes). tab: dsv4_libm_exp2_tab or a
+// copy of it (a GPU kernel keeps one in LDS).
+DSV4_LIBM_FN float dsv4_libm_expf_t(float x, const uint64_t *tab) {
   if (x != x) return x + x;
   if (x > 0x1.62e42ep6f) return dsv4_libm_inf();
   if (x < -0x1.9fe368p6f) return 0.0f;
@@ -65,7 +66,7 @@ DSV4_LIBM_FN float dsv4_libm_expf(float x) {
   const uint64_t ki = dsv4_libm_d2u(kd);
   kd -= shift;
   const double r = fma(inv_ln2_n, xd, -kd);
-  uint64_t t = dsv4_libm_exp2_tab[ki % 32];
+  uint64_t t = tab[ki % 32];
   t += ki << 47;
   const double s = dsv4_libm_u2d(t);
   const double p = fma(c0, r, c1);
@@ -75,6 +76,8 @@ DSV4_LIBM_FN float dsv4_libm_expf(float x) {
   y = y * s;
   return (float)y;
 }
+
+DSV4_LIBM_FN float dsv4_libm_expf(float x) { return dsv4_libm_expf_t(x, dsv4_libm_exp2_tab); }
 
 // log1pf: argument reduction 1+x = 2^k (1+f) with a correction term, then
 // log(1+f) = f - (hfsq - s(hfsq + R)), s = f/(2+f), R a degree-7 polynomial in

@@ -1,7 +1,8 @@
-// dsv4_moe.hip - MoE layer kernels for gfx950: router (logits, sqrt-softplus
-// scoring, biased top-k, weights), SwiGLU + FP8 requant, multi-expert GEMV
-// launches and the ordered combine. Together they reproduce moe_forward
-// (src/dsv4/dsv4_model.c:6599-6807) bit for bit.
+// dsv4_moe.hip - router entry points for gfx950 (logits, sqrt-softplus
+// scoring, biased top-k, weights; the moe_forward router of
+// src/dsv4/dsv4_model.c:6615-6676 and the public dsv4_router of
+// src/dsv4/dsv4_ops.c:473-545) and the standalone SwiGLU + FP8 requant
+// (src/dsv4/dsv4_model.c:6239-6287), all bit for bit.
 //
 // Router exactness. The reference's logit z[e] is one 4096-long fmaf chain in
 // column order (dsv4_gemv_bf16, src/dsv4/dsv4_model.c:298-303), and the route
@@ -21,12 +22,9 @@ using namespace dsv4;
 
 namespace dsv4 {
 
-#define ROUTER_MAX_EXPERTS 1024
-// LDS of one k_expert_pass workgroup: the larger of the FP4 tile (float2 pairs)
-// and the FP8 tile (padded qx plus float2 pairs).
-#define EXPERT_LDS_BYTES (FP8_MAX_IN / 128 * 132 * 4 + FP8_TR * (FP8_MAX_IN / 128 + 1) * 8)
-
 // ------------------------------------------------------------- router ----
+// (The decode MoE layer itself is in dsv4_decode.hip; these kernels serve the
+// standalone router entry points.)
 // z and sum|bf16(g)*x| per (token, expert); one wave per expert row.
 __global__ __launch_bounds__(256) void k_router_logits(float *__restrict__ z,
                                                        float *__restrict__ zabs,
@@ -59,13 +57,6 @@ __global__ __launch_bounds__(256) void k_router_logits(float *__restrict__ z,
     z[(size_t)t * E + e] = acc;
     zabs[(size_t)t * E + e] = aabs;
   }
-}
-
-// gamma_n = n u / (1 - n u), u = 2^-24: the classic bound on the rounding
-// error of any n-term summation order.
-__device__ __forceinline__ float gamma_n(int n) {
-  const double nu = (double)n * 0x1p-24;
-  return (float)(nu / (1.0 - nu));
 }
 
 // One workgroup (256 threads) per token. Writes idx[K] ascending and wt[K].
@@ -265,99 +256,12 @@ __global__ __launch_bounds__(64) void k_swiglu_quant(float *__restrict__ qy,
   if (i1 < I) q[i1] = quant_e4m3(y1, inv);
 }
 
-// ----------------------------------------------- multi-expert GEMVs ------
-// Work slots: for token t and route k < K the routed expert idx[t][k]; slot
-// K of each token is the shared FP8 expert. Phase 0 computes gate/up rows
-// (gu[slot] = [gate | up]), phase 1 the down rows (ro[slot]).
-struct ExpertPass {
-  const int *idx;  // [n][K]
-  const uint8_t *experts;
-  size_t expert_stride, scale_run;
-  const uint8_t *sh[3], *sh_s[3];  // gate, up, down
-  const float *qx, *qxs;           // phase 0: [n][H], [n][H/128]
-  const float *qy, *qys;           // phase 1: [n][K+1][I], [n][K+1][I/128]
-  float *out;                      // phase 0: gu [n][K+1][2][I]; phase 1: ro [n][K+1][H]
-  int n, K, H, I, E, phase;
-  int fp4_tiles, fp8_tiles;  // row tiles per matrix
-};
-
-__global__ __launch_bounds__(256) void k_expert_pass(ExpertPass p) {
-  __shared__ float4 lds[EXPERT_LDS_BYTES / 16];
-  float2 *ps = reinterpret_cast<float2 *>(lds);
-  const int nmat = p.phase == 0 ? 2 : 1;
-  const int in = p.phase == 0 ? p.H : p.I;
-  const int rows = p.phase == 0 ? p.I : p.H;
-  const int routed_blocks = p.n * p.K * nmat * p.fp4_tiles;
-  int b = blockIdx.x;
-  if (b < routed_blocks) {
-    const int tile = b % p.fp4_tiles;
-    b /= p.fp4_tiles;
-    const int m = b % nmat;
-    b /= nmat;
-    const int k = b % p.K, t = b / p.K;
-    const int e = p.idx[t * p.K + k];
-    const int slot = t * (p.K + 1) + k;
-    const Fp4Geom q = fp4_geom(in);
-    if (e < 0 || e >= p.E) {  // no expert selected (all choices NaN): zero rows
-      float *y = p.phase == 0 ? p.out + ((size_t)slot * 2 + m) * p.I : p.out + (size_t)slot * p.H;
-      for (int r = tile * q.tr + threadIdx.x; r < min(rows, (tile + 1) * q.tr); r += 256)
-        y[r] = 0.0f;
-      return;
-    }
-    const uint8_t *scales = p.experts + (size_t)e * p.expert_stride;
-    const uint8_t *weights = scales + p.scale_run;
-    const size_t w1 = (size_t)p.I * (p.H / 2), w2 = (size_t)p.H * (p.I / 2);
-    const size_t s1 = (size_t)p.I * (p.H / 32), s2 = (size_t)p.H * (p.I / 32);
-    const uint8_t *W, *S;
-    if (p.phase == 0) {
-      W = m == 0 ? weights : weights + w1 + w2;
-      S = m == 0 ? scales : scales + s1 + s2;
-    } else {
-      W = weights + w1;
-      S = scales + s1;
-    }
-    const float *qx = p.phase == 0 ? p.qx + (size_t)t * p.H : p.qy + (size_t)slot * p.I;
-    const float *qs =
-        p.phase == 0 ? p.qxs + (size_t)t * (p.H / 128) : p.qys + (size_t)slot * (p.I / 128);
-    float *y = p.phase == 0 ? p.out + ((size_t)slot * 2 + m) * p.I : p.out + (size_t)slot * p.H;
-    fp4_rows_exact(y, qx, qs, W, S, in, rows, tile * q.tr, ps);
-    return;
-  }
-  b -= routed_blocks;
-  const int tile = b % p.fp8_tiles;
-  b /= p.fp8_tiles;
-  const int m = b % nmat, t = b / nmat;
-  const int slot = t * (p.K + 1) + p.K;
-  const int mi = p.phase == 0 ? m : 2;
-  const float *qx = p.phase == 0 ? p.qx + (size_t)t * p.H : p.qy + (size_t)slot * p.I;
-  const float *qs =
-      p.phase == 0 ? p.qxs + (size_t)t * (p.H / 128) : p.qys + (size_t)slot * (p.I / 128);
-  float *y = p.phase == 0 ? p.out + ((size_t)slot * 2 + m) * p.I : p.out + (size_t)slot * p.H;
-  float *xs = reinterpret_cast<float *>(lds);
-  float2 *ps8 = reinterpret_cast<float2 *>(xs + FP8_MAX_IN / 128 * 132);
-  fp8_rows_exact(y, qx, qs, p.sh[mi], p.sh_s[mi], in, rows, tile * FP8_TR, 1, xs, ps8);
-}
-
-// out[t][i] = bf16(((0 + ro[t][0][i]) + ... + ro[t][K-1][i]) + ro[t][K][i])
-// (src/dsv4/dsv4_model.c:6795-6805).
-__global__ void k_combine(float *__restrict__ out, const float *__restrict__ ro, int n, int K,
-                          int H) {
-  const size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
-  if (i >= (size_t)n * H) return;
-  const size_t t = i / H, c = i % H;
-  const float *r = ro + t * (size_t)(K + 1) * H + c;
-  float acc = 0.0f;
-  for (int k = 0; k < K; ++k) acc += r[(size_t)k * H];
-  acc += r[(size_t)K * H];
-  out[i] = bf16_round(acc);
-}
-
 }  // namespace dsv4
 
 // ============================================================ C-ABI =====
 using namespace dsv4;
 
-static int layer_ok(const DSV4GLayer *L, const char *who) {
+extern "C" int dsv4g_layer_ok(const DSV4GLayer *L, const char *who) {
   if (!L || !L->gate_w || !L->experts || !L->sh1 || !L->sh3 || !L->sh2)
     return dsv4g_fail(DSV4G_EINVAL, "%s: layer descriptor incomplete", who);
   if (L->hidden <= 0 || L->hidden % 128 || L->hidden > 8192 || L->inter <= 0 ||
@@ -373,46 +277,10 @@ static int layer_ok(const DSV4GLayer *L, const char *who) {
 
 extern "C" {
 
-// Decode workspace layout: 256-byte aligned pieces, in this order.
-struct MoeWs {
-  float *qx, *qxs, *z, *zabs, *wt, *gu, *qy, *qys, *ro;
-  int *idx;
-  size_t bytes;
-};
-
-static MoeWs moe_ws_layout(const DSV4GLayer *L, int n_tokens, void *base) {
-  const size_t n = (size_t)n_tokens, K = (size_t)L->topk, E = (size_t)L->n_experts;
-  const size_t H = (size_t)L->hidden, I = (size_t)L->inter;
-  MoeWs w = {};
-  uintptr_t p = ((uintptr_t)base + 255) & ~(uintptr_t)255;
-  const uintptr_t p0 = (uintptr_t)base;
-  auto take = [&](size_t bytes) {
-    void *r = (void *)p;
-    p += (bytes + 255) & ~(size_t)255;
-    return r;
-  };
-  w.qx = (float *)take(n * H * 4);
-  w.qxs = (float *)take(n * (H / 128) * 4);
-  w.z = (float *)take(n * E * 4);
-  w.zabs = (float *)take(n * E * 4);
-  w.wt = (float *)take(n * K * 4);
-  w.gu = (float *)take(n * (K + 1) * 2 * I * 4);
-  w.qy = (float *)take(n * (K + 1) * I * 4);
-  w.qys = (float *)take(n * (K + 1) * (I / 128) * 4);
-  w.ro = (float *)take(n * (K + 1) * H * 4);
-  w.idx = (int *)take(n * K * 4);
-  w.bytes = (size_t)(p - p0) + 256;
-  return w;
-}
-
-extern "C" size_t dsv4g_moe_workspace_bytes(const DSV4GLayer *L, int n_tokens) {
-  return moe_ws_layout(L, n_tokens, nullptr).bytes;
-}
-
 int dsv4g_router(int *idx, float *wt, const float *x, const DSV4GLayer *L,
                  const int *token_ids, int n_tokens, float *z_ws, float *zabs_ws,
                  void *stream) {
-  DSV4G_TRY(layer_ok(L, "router"));
+  DSV4G_TRY(dsv4g_layer_ok(L, "router"));
   if (L->tid2eid && !token_ids)
     return dsv4g_fail(DSV4G_EINVAL, "router: hash layer needs token_ids");
   hipStream_t st = (hipStream_t)stream;
@@ -453,94 +321,6 @@ int dsv4g_swiglu_quant(float *qy, float *qys, const float *gate_up, const float 
   hipLaunchKernelGGL(k_swiglu_quant, dim3(inter / 128, n_slots), dim3(64), 0,
                      (hipStream_t)stream, qy, qys, gate_up, wt, K, inter, limit);
   return dsv4g_check_launch("swiglu_quant");
-}
-
-// One phase of the decode MoE layer (moe_forward per token, bit-exact):
-//   0 activation quant + router, 1 gate/up GEMVs (6 FP4 routed + shared FP8),
-//   2 SwiGLU + FP8 requant, 3 down GEMVs, 4 ordered combine into out.
-// Phases run in order on one stream; dsv4g_moe_forward runs all five.
-int dsv4g_moe_decode_phase(int phase, float *out, const float *x, const DSV4GLayer *L,
-                           const int *token_ids, int n_tokens, void *workspace,
-                           size_t workspace_bytes, void *stream) {
-  DSV4G_TRY(layer_ok(L, "moe_decode"));
-  if (n_tokens <= 0) return dsv4g_fail(DSV4G_EINVAL, "moe_decode: n_tokens must be > 0");
-  if (workspace_bytes < dsv4g_moe_workspace_bytes(L, n_tokens))
-    return dsv4g_fail(DSV4G_EINVAL, "moe_decode: workspace too small (%zu < %zu)",
-                      workspace_bytes, dsv4g_moe_workspace_bytes(L, n_tokens));
-  hipStream_t st = (hipStream_t)stream;
-  const int n = n_tokens, K = L->topk, H = L->hidden, I = L->inter;
-  const MoeWs w = moe_ws_layout(L, n, workspace);
-  if (phase == 0) {
-    DSV4G_TRY(dsv4g_quant_fp8_act(w.qx, w.qxs, x, H, n, stream));
-    return dsv4g_router(w.idx, w.wt, x, L, token_ids, n, w.z, w.zabs, stream);
-  }
-  if (phase == 2)
-    return dsv4g_swiglu_quant(w.qy, w.qys, w.gu, w.wt, K, n * (K + 1), I,
-                              (float)(int)L->swiglu_limit, stream);
-  if (phase == 4) {
-    const size_t total = (size_t)n * H;
-    hipLaunchKernelGGL(k_combine, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, out,
-                       w.ro, n, K, H);
-    return dsv4g_check_launch("combine");
-  }
-  if (phase != 1 && phase != 3) return dsv4g_fail(DSV4G_EINVAL, "moe_decode: bad phase %d", phase);
-  ExpertPass p = {};
-  p.idx = w.idx;
-  p.experts = L->experts;
-  p.expert_stride = L->expert_stride;
-  p.scale_run = L->scale_run;
-  p.sh[0] = L->sh1;
-  p.sh[1] = L->sh3;
-  p.sh[2] = L->sh2;
-  p.sh_s[0] = L->sh1_s;
-  p.sh_s[1] = L->sh3_s;
-  p.sh_s[2] = L->sh2_s;
-  p.qx = w.qx;
-  p.qxs = w.qxs;
-  p.qy = w.qy;
-  p.qys = w.qys;
-  p.n = n;
-  p.K = K;
-  p.H = H;
-  p.I = I;
-  p.E = L->n_experts;
-  const int in = phase == 1 ? H : I, rows = phase == 1 ? I : H, nmat = phase == 1 ? 2 : 1;
-  int G = in / 32, gp = 1;
-  while (gp < G) gp <<= 1;
-  int tr = FP4_LDS_ENTRIES / gp;
-  if (tr > 256) tr = 256;
-  p.phase = phase == 1 ? 0 : 1;
-  p.out = phase == 1 ? w.gu : w.ro;
-  p.fp4_tiles = (rows + tr - 1) / tr;
-  p.fp8_tiles = (rows + FP8_TR - 1) / FP8_TR;
-  const int blocks = n * K * nmat * p.fp4_tiles + n * nmat * p.fp8_tiles;
-  hipLaunchKernelGGL(k_expert_pass, dim3(blocks), dim3(256), 0, st, p);
-  return dsv4g_check_launch(phase == 1 ? "expert_pass(gate/up)" : "expert_pass(down)");
-}
-
-// Routing of the last decode call made with this workspace.
-int dsv4g_moe_decode_routing(int *idx_out, float *wt_out, const DSV4GLayer *L, int n_tokens,
-                             void *workspace, void *stream) {
-  const MoeWs w = moe_ws_layout(L, n_tokens, workspace);
-  hipStream_t st = (hipStream_t)stream;
-  if (idx_out)
-    DSV4G_HIP(hipMemcpyAsync(idx_out, w.idx, (size_t)n_tokens * L->topk * sizeof(int),
-                             hipMemcpyDeviceToDevice, st));
-  if (wt_out)
-    DSV4G_HIP(hipMemcpyAsync(wt_out, w.wt, (size_t)n_tokens * L->topk * sizeof(float),
-                             hipMemcpyDeviceToDevice, st));
-  return 0;
-}
-
-// Decode-path MoE layer: moe_forward per token, bit-exact. idx/wt (optional,
-// device) receive the routing.
-int dsv4g_moe_forward(float *out, const float *x, const DSV4GLayer *L, const int *token_ids,
-                      int n_tokens, void *workspace, size_t workspace_bytes, int *idx_out,
-                      float *wt_out, void *stream) {
-  for (int phase = 0; phase < 5; ++phase)
-    DSV4G_TRY(dsv4g_moe_decode_phase(phase, out, x, L, token_ids, n_tokens, workspace,
-                                     workspace_bytes, stream));
-  return dsv4g_moe_decode_routing(idx_out, wt_out, L, n_tokens, workspace, stream);
 }
 
 }  // extern "C"

@@ -60,6 +60,41 @@ __device__ __forceinline__ float fp4_group_partial(const uint4 w, const float *x
   return p;
 }
 
+// acc = fmaf(p, s, acc) over n (p, s) pairs in order (the group chain of
+// one output row). The LDS reads of the next 16 pairs are in flight while the
+// current 16 are chained, so the loop runs at the fma dependency latency.
+// pr: 16-byte aligned.
+__device__ __forceinline__ float pair_chain(const float2 *pr, int n) {
+  const float4 *p4 = reinterpret_cast<const float4 *>(pr);
+  const int nb = n / 16;
+  float acc = 0.0f;
+  float4 cur[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) cur[j] = nb > 0 ? p4[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int b = 0; b < nb; ++b) {
+    const int nx = (b + 1 < nb ? b + 1 : b) * 8;
+    float4 nxt[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) nxt[j] = p4[nx + j];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      acc = fmaf(cur[j].x, cur[j].y, acc);
+      acc = fmaf(cur[j].z, cur[j].w, acc);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) cur[j] = nxt[j];
+  }
+  for (int i = nb * 16; i < n; ++i) {
+    const float2 v = pr[i];
+    acc = fmaf(v.x, v.y, acc);
+  }
+  return acc;
+}
+
+// Even LDS row stride (in float2) for n pairs: 16-byte aligned rows whose
+// 16-byte reads by consecutive lanes fall in distinct banks.
+__device__ __host__ __forceinline__ int pair_stride(int n) { return (n | 1) + 1; }
+
 // Rows [r0, r0 + tr) of y = bf16(W . qx) (FP4, per-32 E8M0 scales).
 // ps: LDS scratch of FP4_LDS_ENTRIES + tr float2.
 __device__ inline void fp4_rows_exact(float *__restrict__ y, const float *__restrict__ qx,
@@ -190,5 +225,368 @@ __device__ inline void fp8_rows_exact(float *__restrict__ y, const float *__rest
   }
 }
 
+
+// ============================================ two-step tiles (decode) ====
+// The same exact schemes, split so that a kernel issues every weight load
+// of its tile before it has the activation vector: *_load fills registers,
+// *_finish computes. Register indices are compile-time constants throughout.
+// LDS: the pairs take tr * pair_stride(G) float2 (FP4; at most
+// FP4_LDS_ENTRIES + 2 * tr), plus 4096 bytes of FP4 scales, or
+// FP8_TR * pair_stride(CB) float2 (FP8).
+
+// FP4: all passes of the tile in flight (npass = tr / rpp <= 16 for every
+// supported width). The lane's activation slice (group g: 32 E4M3 codes and
+// the per-128 scale) is loaded first (fp4_tile_x), so that the first passes
+// can start while later weights still stream in; holding codes rather than
+// floats keeps the tile within 128 VGPRs (four waves per SIMD).
+struct Fp4Regs {
+  uint4 w[16];
+  uint4 sc;        // this thread's 16 bytes of the tile's E8M0 scales
+  uint32_t x8[8];  // E4M3 codes of the activation group, 4 per word
+  float as;
+};
+
+// qx8: E4M3 codes of the quantised activation (their values are the grid
+// values quant_fp8_act produces, exactly); qscale: per-128 scales.
+__device__ __forceinline__ void fp4_tile_x(Fp4Regs &R, const uint8_t *qx8, const float *qscale,
+                                           const Fp4Geom &q) {
+  const int g = threadIdx.x % q.gp;
+  if (g < q.G) {
+    const uint4 a = *reinterpret_cast<const uint4 *>(qx8 + 32 * g);
+    const uint4 b = *reinterpret_cast<const uint4 *>(qx8 + 32 * g + 16);
+    R.x8[0] = a.x;
+    R.x8[1] = a.y;
+    R.x8[2] = a.z;
+    R.x8[3] = a.w;
+    R.x8[4] = b.x;
+    R.x8[5] = b.y;
+    R.x8[6] = b.z;
+    R.x8[7] = b.w;
+    R.as = qscale[g / 4];
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) R.x8[i] = 0u;
+    R.as = 0.0f;
+  }
+}
+
+__device__ __forceinline__ uint32_t u4_word(const uint4 &v, int d) {
+  return d == 0 ? v.x : d == 1 ? v.y : d == 2 ? v.z : v.w;
+}
+
+// One nibble pair (byte B of each word) of four independent group chains.
+template <int B>
+__device__ __forceinline__ void fp4_step4(const uint32_t (&wd)[4], float x0, float x1,
+                                          float (&p)[4]) {
+  float2 v[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = fp4x2<B>(wd[i]);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) p[i] = fmaf(v[i].x, x0, p[i]);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) p[i] = fmaf(v[i].y, x1, p[i]);
+}
+
+// Partials of passes u0 .. u0 + 3: four 32-long fmaf chains, each in the
+// reference's column order, interleaved so the fma latency is hidden.
+__device__ __forceinline__ void fp4_partials4(const Fp4Regs &R, int u0, float (&p)[4]) {
+  // converted per call on purpose: the scheduling barrier keeps the compiler
+  // from hoisting 32 converted floats of every call to the top (registers)
+  __builtin_amdgcn_sched_barrier(0);
+  const uint32_t *x8 = R.x8;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) p[i] = 0.0f;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const uint32_t wd[4] = {u4_word(R.w[u0], d), u4_word(R.w[u0 + 1], d),
+                            u4_word(R.w[u0 + 2], d), u4_word(R.w[u0 + 3], d)};
+    // columns 8d .. 8d + 7: codes in bytes of x8[2d] and x8[2d + 1]
+    const float2 x01 = fp8x2<false>(x8[2 * d]), x23 = fp8x2<true>(x8[2 * d]);
+    const float2 x45 = fp8x2<false>(x8[2 * d + 1]), x67 = fp8x2<true>(x8[2 * d + 1]);
+    fp4_step4<0>(wd, x01.x, x01.y, p);
+    fp4_step4<1>(wd, x23.x, x23.y, p);
+    fp4_step4<2>(wd, x45.x, x45.y, p);
+    fp4_step4<3>(wd, x67.x, x67.y, p);
+  }
+}
+
+// Weights of rows [r0, r0 + tr) (single matrix) or, paired, of rows
+// [r0, r0 + tr/2) of W0 then the same rows of W1 (row lr < half is W0 row
+// r0 + lr, lr >= half is W1 row r0 + lr - half; half is npass / 2 whole
+// passes, so the matrix of a pass is uniform). The tile's scales (tr * G <= 4096 bytes, row
+// lr at lr * G) are fetched first, 16 bytes per thread, for LDS. Offsets are
+// 32-bit (a matrix is below 4 GB): each load takes a scalar base and one
+// VGPR of offset.
+__device__ __forceinline__ void fp4_load_w(Fp4Regs &R, const uint8_t *__restrict__ W0,
+                                           const uint8_t *__restrict__ S0,
+                                           const uint8_t *__restrict__ W1,
+                                           const uint8_t *__restrict__ S1, int in, int rows,
+                                           int r0, const Fp4Geom &q, bool pair) {
+  const int t = threadIdx.x, g = t % q.gp, rsub = t / q.gp;
+  const int npass = q.tr / q.rpp, half = q.tr / 2;
+  const uint32_t pcols = (uint32_t)in / 2, G = (uint32_t)q.G;
+  {
+    // scales: [W0 rows][W1 rows] when paired, else tr rows of W0
+    const uint32_t seg = (uint32_t)(pair ? half : q.tr) * G;
+    const uint32_t o = 16u * (uint32_t)t;
+    const bool m1 = pair && o >= seg;
+    const uint32_t oo = m1 ? o - seg : o;
+    const uint32_t lim = (uint32_t)(rows > r0 ? rows - r0 : 0) * G;  // rows that exist
+    R.sc = (o < (pair ? 2 * seg : seg) && oo + 16u <= lim)
+               ? *reinterpret_cast<const uint4 *>((m1 ? S1 : S0) + ((uint32_t)r0 * G + oo))
+               : make_uint4(0x7f7f7f7fu, 0x7f7f7f7fu, 0x7f7f7f7fu, 0x7f7f7f7fu);
+  }
+#pragma unroll
+  for (int u = 0; u < 16; ++u) {
+    const bool m1 = pair && u >= npass / 2;  // == (lr >= half): half = npass / 2 passes
+    const int lr = u * q.rpp + rsub;
+    const int row = r0 + (m1 ? lr - half : lr);
+    const uint8_t *W = m1 ? W1 : W0;
+    R.w[u] = (g < q.G && u < npass && row < rows)
+                 ? *reinterpret_cast<const uint4 *>(W + ((uint32_t)row * pcols + 16u * g))
+                 : make_uint4(0, 0, 0, 0);
+  }
+}
+
+// Partials into ps, then one lane per tile row runs the group chain; returns
+// bf16(acc) for lane t < tr (row lr = t), garbage otherwise. cl: 4096 bytes
+// of LDS for the scales, apart from ps. Starts with a barrier: the activation
+// may have been read from LDS that ps overlaps.
+__device__ __forceinline__ float fp4_tile_rows(const Fp4Regs &R, int rows, int r0,
+                                               const Fp4Geom &q, float2 *ps, uint8_t *cl,
+                                               bool pair) {
+  const int t = threadIdx.x, g = t % q.gp, rsub = t / q.gp;
+  const bool gact = g < q.G;
+  const int npass = q.tr / q.rpp, half = q.tr / 2;
+  const int stride = pair_stride(q.G);
+  reinterpret_cast<uint4 *>(cl)[t] = R.sc;
+  __syncthreads();
+#pragma unroll
+  for (int u0 = 0; u0 < 16; u0 += 4) {
+    if (u0 < npass) {
+      float p[4];
+      fp4_partials4(R, u0, p);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int u = u0 + i;
+        const int lr = u * q.rpp + rsub;
+        const int row = r0 + ((pair && lr >= half) ? lr - half : lr);
+        if (gact && u < npass && row < rows) {
+          const uint32_t code = cl[lr * q.G + g];
+          float part = p[i];
+          float s = R.as * e8m0(code);
+          if (code == 255u) {  // NaN scale: the reference skips the group
+            part = 0.0f;
+            s = 0.0f;
+          }
+          ps[lr * stride + g] = make_float2(part, s);
+        }
+      }
+    }
+  }
+  __syncthreads();
+  float acc = 0.0f;
+  if (t < q.tr) acc = pair_chain(ps + t * stride, q.G);
+  return bf16_round(acc);
+}
+
+// Single matrix: y[r0 + t] for the tile's rows.
+__device__ __forceinline__ void fp4_tile_load(Fp4Regs &R, const uint8_t *__restrict__ W,
+                                              const uint8_t *__restrict__ S, int in, int rows,
+                                              int r0, const Fp4Geom &q) {
+  fp4_load_w(R, W, S, W, S, in, rows, r0, q, false);
+}
+__device__ __forceinline__ void fp4_tile_finish(const Fp4Regs &R, float *y, int rows, int r0,
+                                                const Fp4Geom &q, float2 *ps, uint8_t *cl) {
+  const float v = fp4_tile_rows(R, rows, r0, q, ps, cl, false);
+  if (threadIdx.x < q.tr && r0 + (int)threadIdx.x < rows) y[r0 + threadIdx.x] = v;
+}
+
+// Paired: yl[lr] (LDS) for lr < tr.
+__device__ __forceinline__ void fp4_pair_load(Fp4Regs &R, const uint8_t *__restrict__ W0,
+                                              const uint8_t *__restrict__ S0,
+                                              const uint8_t *__restrict__ W1,
+                                              const uint8_t *__restrict__ S1, int in, int rows,
+                                              int r0, const Fp4Geom &q) {
+  fp4_load_w(R, W0, S0, W1, S1, in, rows, r0, q, true);
+}
+__device__ __forceinline__ void fp4_pair_finish(const Fp4Regs &R, float *yl, int rows, int r0,
+                                                const Fp4Geom &q, float2 *ps, uint8_t *cl) {
+  const float v = fp4_tile_rows(R, rows, r0, q, ps, cl, true);
+  if (threadIdx.x < q.tr) yl[threadIdx.x] = v;
+}
+
+// FP8: lane t = (row r0 + t / 16, block slot t % 16), blocks slot, slot + 16,
+// ...; the first two blocks of each lane (inputs up to 4096 wide) are loaded
+// ahead, wider inputs load the rest in finish.
+struct Fp8Regs {
+  uint4 w[16];
+};
+
+__device__ __forceinline__ void fp8_tile_load(Fp8Regs &R, const uint8_t *__restrict__ W, int in,
+                                              int rows, int r0) {
+  const int t = threadIdx.x, slot = t % 16, row = r0 + t / 16;
+  const int CB = (in + 127) / 128;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int cb = slot + 16 * j;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int c = cb * 128 + 16 * i;
+      R.w[8 * j + i] = (row < rows && cb < CB && c < in)
+                           ? *reinterpret_cast<const uint4 *>(W + (size_t)row * in + c)
+                           : make_uint4(0, 0, 0, 0);
+    }
+  }
+}
+
+// Sequential partial of one 16-column piece.
+__device__ __forceinline__ float fp8_piece(const uint4 w, const float *xb, float part) {
+  const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const float4 xv = *reinterpret_cast<const float4 *>(xb + 4 * d);
+    float2 v = fp8x2<false>(wd[d]);
+    part = fmaf(v.x, xv.x, part);
+    part = fmaf(v.y, xv.y, part);
+    v = fp8x2<true>(wd[d]);
+    part = fmaf(v.x, xv.z, part);
+    part = fmaf(v.y, xv.w, part);
+  }
+  return part;
+}
+
+// xs: the activation in LDS, padded to 132 floats per 128-block; qscale may
+// be LDS or global. Rows [r0, r0 + FP8_TR) of y (BF16-rounded if round_out).
+__device__ __forceinline__ void fp8_tile_finish(const Fp8Regs &R, float *y, const float *xs,
+                                                const float *qscale,
+                                                const uint8_t *__restrict__ W,
+                                                const uint8_t *__restrict__ S, int in, int rows,
+                                                int r0, int round_out, float2 *ps) {
+  const int t = threadIdx.x, lr = t / 16, slot = t % 16, row = r0 + lr;
+  const int CB = (in + 127) / 128, stride = pair_stride(CB);
+  if (row < rows) {
+    const uint8_t *sr = S + (size_t)(row / 128) * CB;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int cb = slot + 16 * j;
+      if (cb < CB) {
+        const int len = min(128, in - cb * 128);
+        const float *xb = xs + cb * 132;
+        float part = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          if (16 * i < len) part = fp8_piece(R.w[8 * j + i], xb + 16 * i, part);
+        const uint32_t code = sr[cb];
+        float s = qscale[cb] * e8m0(code);
+        if (code == 255u) {
+          part = 0.0f;
+          s = 0.0f;
+        }
+        ps[lr * stride + cb] = make_float2(part, s);
+      }
+    }
+    for (int cb = slot + 32; cb < CB; cb += 16) {
+      const int len = min(128, in - cb * 128);
+      const uint8_t *wr = W + (size_t)row * in + cb * 128;
+      const float *xb = xs + cb * 132;
+      float part = 0.0f;
+      for (int c = 0; c < len; c += 16)
+        part = fp8_piece(*reinterpret_cast<const uint4 *>(wr + c), xb + c, part);
+      const uint32_t code = sr[cb];
+      float s = qscale[cb] * e8m0(code);
+      if (code == 255u) {
+        part = 0.0f;
+        s = 0.0f;
+      }
+      ps[lr * stride + cb] = make_float2(part, s);
+    }
+  }
+  __syncthreads();
+  if (t < FP8_TR && r0 + t < rows) {
+    const float acc = pair_chain(ps + t * stride, CB);
+    y[r0 + t] = round_out ? bf16_round(acc) : acc;
+  }
+}
+
+// ---- paired FP8 tiles: the first half of a tile's rows from matrix 0
+// (gate), the second half the same rows of matrix 1 (up), so one workgroup
+// holds both operands of SwiGLU; yl[lr] receives bf16(acc).
+// FP8 pairs: lanes t / 16 < 8 take W0 rows r0 + t / 16, the others W1 rows
+// r0 + t / 16 - 8 (FP8_TR / 2 = 8 rows of each).
+__device__ __forceinline__ void fp8_pair_load(Fp8Regs &R, const uint8_t *__restrict__ W0,
+                                              const uint8_t *__restrict__ W1, int in, int rows,
+                                              int r0) {
+  const int t = threadIdx.x, slot = t % 16, lr = t / 16;
+  const int row = r0 + (lr & 7);
+  const uint8_t *W = lr < 8 ? W0 : W1;
+  const int CB = (in + 127) / 128;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int cb = slot + 16 * j;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int c = cb * 128 + 16 * i;
+      R.w[8 * j + i] = (row < rows && cb < CB && c < in)
+                           ? *reinterpret_cast<const uint4 *>(W + (size_t)row * in + c)
+                           : make_uint4(0, 0, 0, 0);
+    }
+  }
+}
+
+__device__ __forceinline__ void fp8_pair_finish(const Fp8Regs &R, float *yl, const float *xs,
+                                                const float *qscale,
+                                                const uint8_t *__restrict__ W0,
+                                                const uint8_t *__restrict__ S0,
+                                                const uint8_t *__restrict__ W1,
+                                                const uint8_t *__restrict__ S1, int in, int rows,
+                                                int r0, float2 *ps) {
+  const int t = threadIdx.x, lr = t / 16, slot = t % 16, row = r0 + (lr & 7);
+  const uint8_t *W = lr < 8 ? W0 : W1;
+  const uint8_t *S = lr < 8 ? S0 : S1;
+  const int CB = (in + 127) / 128, stride = pair_stride(CB);
+  if (row < rows) {
+    const uint8_t *sr = S + (size_t)(row / 128) * CB;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int cb = slot + 16 * j;
+      if (cb < CB) {
+        const int len = min(128, in - cb * 128);
+        const float *xb = xs + cb * 132;
+        float part = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          if (16 * i < len) part = fp8_piece(R.w[8 * j + i], xb + 16 * i, part);
+        const uint32_t code = sr[cb];
+        float s = qscale[cb] * e8m0(code);
+        if (code == 255u) {
+          part = 0.0f;
+          s = 0.0f;
+        }
+        ps[lr * stride + cb] = make_float2(part, s);
+      }
+    }
+    for (int cb = slot + 32; cb < CB; cb += 16) {
+      const int len = min(128, in - cb * 128);
+      const uint8_t *wr = W + (size_t)row * in + cb * 128;
+      const float *xb = xs + cb * 132;
+      float part = 0.0f;
+      for (int c = 0; c < len; c += 16)
+        part = fp8_piece(*reinterpret_cast<const uint4 *>(wr + c), xb + c, part);
+      const uint32_t code = sr[cb];
+      float s = qscale[cb] * e8m0(code);
+      if (code == 255u) {
+        part = 0.0f;
+        s = 0.0f;
+      }
+      ps[lr * stride + cb] = make_float2(part, s);
+    }
+  }
+  __syncthreads();
+  if (t < FP8_TR && r0 + (t & 7) < rows) {
+    const float acc = pair_chain(ps + t * stride, CB);
+    yl[t] = bf16_round(acc);
+  }
+}
 
 }  // namespace dsv4

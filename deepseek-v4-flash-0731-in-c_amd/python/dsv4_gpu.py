@@ -54,6 +54,7 @@ _SIGS = {
     "dsv4g_moe_forward": [_vp, _vp, C.POINTER(DSV4GLayer), _vp, _I, _vp, _Z, _vp, _vp, _vp],
     "dsv4g_moe_decode_phase": [_I, _vp, _vp, C.POINTER(DSV4GLayer), _vp, _I, _vp, _Z, _vp],
     "dsv4g_moe_decode_routing": [_vp, _vp, C.POINTER(DSV4GLayer), _I, _vp, _vp],
+    "dsv4g_moe_workspace_init": [_vp, _Z, _vp],
     "dsv4g_moe_forward_batch": [_vp, _vp, C.POINTER(DSV4GLayer), _vp, _I, _vp, _Z, _vp, _vp,
                                 _vp],
     "dsv4g_probe_mfma": [_I, _vp, _vp, _vp, _vp, _vp, _vp],
@@ -233,13 +234,22 @@ class GpuLib:
         L = layer.struct
         need = self.moe_workspace_bytes(layer, n)
         if workspace is None or workspace.numel() < need:
-            workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
+            workspace = self.new_moe_workspace(layer, n, x.device)
         out = torch.empty_like(x) if out is None else out
         idx = torch.empty(n, L.topk, dtype=torch.int32, device=x.device)
         wt = torch.empty(n, L.topk, dtype=torch.float32, device=x.device)
         self._call("dsv4g_moe_forward", _ptr(out), _ptr(x), C.byref(L), _ptr(token_ids), n,
                    _ptr(workspace), workspace.numel(), _ptr(idx), _ptr(wt), self._stream())
         return out, idx, wt
+
+    def new_moe_workspace(self, layer, n_tokens, device):
+        """A decode workspace, zeroed as dsv4g_moe_forward requires before its
+        first use (every call leaves it reusable)."""
+        import torch
+        ws = torch.empty(self.moe_workspace_bytes(layer, n_tokens), dtype=torch.uint8,
+                         device=device)
+        self._call("dsv4g_moe_workspace_init", _ptr(ws), ws.numel(), self._stream())
+        return ws
 
     def moe_batch_workspace_bytes(self, layer, n_tokens):
         return int(self.lib.dsv4g_moe_batch_workspace_bytes(C.byref(layer.struct), n_tokens))

@@ -144,17 +144,24 @@ int dsv4g_router_public(int *idx, float *wt, const float *x, const uint16_t *gat
 int dsv4g_swiglu_quant(float *qy, float *qys, const float *gate_up, const float *wt, int K,
                        int n_slots, int inter, float limit, void *stream);
 
-/* Decode MoE layer: moe_forward for each of n_tokens rows of x (BF16 values
- * in fp32), bit-exact. out [n][hidden]. idx_out/wt_out (optional, device)
- * receive the routing. workspace: device memory of at least
- * dsv4g_moe_workspace_bytes(L, n_tokens). */
+/* Decode MoE layer: moe_forward for each of n_tokens (at most 1023) rows of
+ * x (BF16 values in fp32), bit-exact. out [n][hidden]. idx_out/wt_out
+ * (optional, device) receive the routing. workspace: 256-byte aligned device
+ * memory of at least dsv4g_moe_workspace_bytes(L, n_tokens), zeroed once
+ * before its first use (dsv4g_moe_workspace_init, or any zero fill); every
+ * call leaves it ready for the next. Calls sharing one workspace must not
+ * overlap. */
 size_t dsv4g_moe_workspace_bytes(const DSV4GLayer *L, int n_tokens);
+int dsv4g_moe_workspace_init(void *workspace, size_t workspace_bytes, void *stream);
 int dsv4g_moe_forward(float *out, const float *x, const DSV4GLayer *L, const int *token_ids,
                       int n_tokens, void *workspace, size_t workspace_bytes, int *idx_out,
                       float *wt_out, void *stream);
-/* The same layer as five ordered phases (0 quant + router, 1 gate/up GEMVs,
- * 2 SwiGLU + requant, 3 down GEMVs, 4 combine), for callers that interleave
- * or time them; dsv4g_moe_decode_routing copies the routing of the last call. */
+/* The same layer as four ordered phases, for callers that interleave or
+ * time them: 0 router logits + activation quant, 1 gate/up GEMVs of the
+ * candidate experts and the shared expert with the exact router chains
+ * beside them, 2 exact top-k, SwiGLU + requant and down GEMVs, 3 the ordered
+ * combine. dsv4g_moe_decode_routing copies the routing of the last call.
+ * x and out: 16-byte aligned. */
 int dsv4g_moe_decode_phase(int phase, float *out, const float *x, const DSV4GLayer *L,
                            const int *token_ids, int n_tokens, void *workspace,
                            size_t workspace_bytes, void *stream);

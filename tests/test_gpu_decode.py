@@ -236,3 +236,82 @@ def test_moe_forward_full_size_bit_exact(env):
         o, i, w = orc.moe_forward(L, X[t])
         assert np.array_equal(idx[t], i) and same_bits(wt[t], w)
         assert same_bits(out[t], o), max_rel_err(out[t], o)
+
+
+@pytest.mark.parametrize("kw", [dict(), dict(bias=True), dict(hash_vocab=11)])
+def test_moe_forward_256_experts_bit_exact(env, kw):
+    """The decode layer with all 256 experts (hidden 4096, inter 128 to keep
+    the oracle quick) for 5 tokens at once: candidates, exact chains, final
+    top-k, weights and outputs bit-identical to the oracle."""
+    orc, lib, dg = env["orc"], env["lib"], env["dsv4_gpu"]
+    L = make_layer(orc, 4096, 128, 256, 6, seed=8, **kw)
+    DL = dg.DeviceLayer.from_host(L, env["dev"])
+    X = bf16_input(np.random.default_rng(13), (5, 4096))
+    tok = (np.arange(5, dtype=np.int32) * 3) % 11
+    out, idx, wt = lib.moe_forward(DL, T(env, X), T(env, tok))
+    out, idx, wt = H(out), H(idx), H(wt)
+    for t in range(5):
+        o, i, w = orc.moe_forward(L, X[t], int(tok[t]))
+        assert np.array_equal(idx[t], i), t
+        assert same_bits(wt[t], w), t
+        assert same_bits(out[t], o), (t, max_rel_err(out[t], o))
+
+
+def tie_layer(orc, n_experts, winners, hidden=4096):
+    """Identical gate rows except one element, raised by k BF16 ulps (k = 1,
+    2, ...) for the experts in `winners`: every expert stays within the
+    parallel-sum bound of the k-th best, so all are candidates, and the exact
+    logits rank the winners first."""
+    L = make_layer(orc, hidden, 128, n_experts, 6, seed=17)
+    base = L["gate_w"][0].copy()
+    base[7] = 0x3A80  # 2^-10 (BF16 ulp there: 2^-17)
+    G = np.tile(base, (n_experts, 1))
+    for k, e in enumerate(winners):
+        G[e, 7] = base[7] + k + 1
+    L["gate_w"] = np.ascontiguousarray(G)
+    return L
+
+
+@pytest.mark.parametrize("winners", [[], [26, 27, 28, 29, 30, 31], [2, 20, 5, 30, 17, 9]])
+def test_moe_forward_ties_and_overflow_candidates(env, winners):
+    """More candidates than gate/up slots (32 experts, 16 slots): with a
+    constant gate the lowest ids win; with winners beyond the slots the down
+    kernel computes their gate/up itself. Bit-exact either way."""
+    orc, lib, dg = env["orc"], env["lib"], env["dsv4_gpu"]
+    L = tie_layer(orc, 32, winners)
+    DL = dg.DeviceLayer.from_host(L, env["dev"])
+    X = bf16_input(np.random.default_rng(23), (2, 4096))
+    X[:, 7] = 1.0
+    out, idx, wt = lib.moe_forward(DL, T(env, X))
+    out, idx, wt = H(out), H(idx), H(wt)
+    for t in range(2):
+        o, i, w = orc.moe_forward(L, X[t])
+        if winners:
+            assert sorted(i) == sorted(winners)  # the construction's premise
+        else:
+            assert list(i) == [0, 1, 2, 3, 4, 5]
+        assert np.array_equal(idx[t], i), t
+        assert same_bits(wt[t], w), t
+        assert same_bits(out[t], o), (t, max_rel_err(out[t], o))
+
+
+@pytest.mark.parametrize("winners", [[], [300, 17, 260, 5, 299, 111]])
+def test_moe_forward_more_than_256_candidates(env, winners):
+    """320 experts all within the bound (constant gate): more than 256
+    candidates per token, the long selection path, bit-exact."""
+    orc, lib, dg = env["orc"], env["lib"], env["dsv4_gpu"]
+    L = tie_layer(orc, 320, winners, hidden=512)
+    DL = dg.DeviceLayer.from_host(L, env["dev"])
+    X = bf16_input(np.random.default_rng(29), (2, 512))
+    X[:, 7] = 1.0
+    out, idx, wt = lib.moe_forward(DL, T(env, X))
+    out, idx, wt = H(out), H(idx), H(wt)
+    for t in range(2):
+        o, i, w = orc.moe_forward(L, X[t])
+        if winners:
+            assert sorted(i) == sorted(winners)
+        else:
+            assert list(i) == [0, 1, 2, 3, 4, 5]
+        assert np.array_equal(idx[t], i), t
+        assert same_bits(wt[t], w), t
+        assert same_bits(out[t], o), (t, max_rel_err(out[t], o))
