@@ -65,8 +65,8 @@ struct DecArgs {
   int *ncand;                      // [n]
   float *zx;                       // [n][E] exact logit per candidate position
   int *sel_e;                      // [n][K] routing, ascending id (moe_forward's idx)
-  float *sel_w;                    // [n][K] route weights (moe_forward's wt)
   int *sel_pos;                    // [n][K] candidate position of each route
+  float *sel_w;                    // [n][K] route weights (moe_forward's wt)
   float *sv;                       // [n][maxc + 1][I] SwiGLU t; slot maxc = shared expert
   float *fb;                       // [n][K][I] t of selected experts without a slot
   float *ro;                       // [n][K + 1][H] per-route outputs (BF16 values)
@@ -352,21 +352,24 @@ __global__ __launch_bounds__(256) void k_dec_router(DecArgs a) {
   const int H = a.H;
   const int nlog = (a.E + 3) / 4;
   if ((int)blockIdx.x < nlog) {
-    const int e = blockIdx.x * 4 + wv;
+    const int e = __builtin_amdgcn_readfirstlane((int)blockIdx.x * 4 + wv);
     const bool act = e < a.E;
-    const uint16_t *gr = a.gate + (size_t)(act ? e : 0) * H;
-    uint4 w[16];  // lane holds columns 8 lane + 512 i
+    // lane holds columns 8 lane + 512 i; an inactive wave reads zeros
+    const BufRsrc rg = buf_rsrc(a.gate + (size_t)(act ? e : 0) * H, act ? 2u * H : 0u);
+    uint4 w[16];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int c = 8 * lane + 512 * i;
-      w[i] = (act && c < H) ? *reinterpret_cast<const uint4 *>(gr + c) : make_uint4(0, 0, 0, 0);
-    }
+    for (int i = 0; i < 16; ++i) w[i] = buf_load16(rg, 16u * (lane + 64 * i));
     libm_stage_table(s_tab);
     for (int t = 0; t < a.n; ++t) {
       __syncthreads();
-      const float *xt = a.x + (size_t)t * H;
-      for (int i = 4 * tid; i < H; i += 1024)
-        *reinterpret_cast<float4 *>(xs + i) = *reinterpret_cast<const float4 *>(xt + i);
+      const BufRsrc rx = buf_rsrc(a.x + (size_t)t * H, 4u * H);
+      uint4 xv4[8];  // H <= 8192
+#pragma unroll
+      for (int j = 0; j < 8; ++j) xv4[j] = buf_load16(rx, 16u * (tid + 256 * j));
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (4 * (tid + 256 * j) < H)
+          *reinterpret_cast<uint4 *>(xs + 4 * (tid + 256 * j)) = xv4[j];
       __syncthreads();
       float acc = 0.0f, aabs = 0.0f;
 #pragma unroll
@@ -419,90 +422,103 @@ __global__ __launch_bounds__(256) void k_dec_router(DecArgs a) {
   if (lane == 0) a.qxs[(size_t)t * gpt + g] = scale;
 }
 
-// --------------------------------------------------------- gate / up ----
-// 16 columns of the exact logit chain: acc = fmaf(g[c], x[c], acc) in order.
-__device__ __forceinline__ float chain16(const float4 (&g)[4], const float4 (&x)[4], float acc) {
+// ------------------------------------------------------------ chains ----
+// One 8-column batch of the exact chain acc = fmaf(g[c], x[c], acc), in
+// column order.
+__device__ __forceinline__ float chain8(const float4 &ga, const float4 &gb, const float4 &xa,
+                                        const float4 &xb, float acc) {
+  acc = fmaf(ga.x, xa.x, acc);
+  acc = fmaf(ga.y, xa.y, acc);
+  acc = fmaf(ga.z, xa.z, acc);
+  acc = fmaf(ga.w, xa.w, acc);
+  acc = fmaf(gb.x, xb.x, acc);
+  acc = fmaf(gb.y, xb.y, acc);
+  acc = fmaf(gb.z, xb.z, acc);
+  acc = fmaf(gb.w, xb.w, acc);
+  return acc;
+}
+
+// Chain 8 * NB columns from LDS: g, x at the first column (fp32). The reads
+// of the batch two ahead are in flight while a batch is chained; nothing is
+// carried across calls (a loop-carried prefetch costs a full LDS drain per
+// iteration), so the chain runs at the fma dependency latency.
+template <int NB>
+__device__ __forceinline__ float chain_cols(const float4 *g, const float4 *x, float acc) {
+  float4 g0[4], g1[4], x0[4], x1[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    acc = fmaf(g[j].x, x[j].x, acc);
-    acc = fmaf(g[j].y, x[j].y, acc);
-    acc = fmaf(g[j].z, x[j].z, acc);
-    acc = fmaf(g[j].w, x[j].w, acc);
+  for (int j = 0; j < 2; ++j) {
+    g0[j] = g[2 * j];
+    g1[j] = g[2 * j + 1];
+    x0[j] = x[2 * j];
+    x1[j] = x[2 * j + 1];
+  }
+#pragma unroll
+  for (int j = 0; j < NB; ++j) {
+    if (j + 2 < NB) {
+      g0[(j + 2) % 4] = g[2 * (j + 2)];
+      g1[(j + 2) % 4] = g[2 * (j + 2) + 1];
+      x0[(j + 2) % 4] = x[2 * (j + 2)];
+      x1[(j + 2) % 4] = x[2 * (j + 2) + 1];
+    }
+    acc = chain8(g0[j % 4], g1[j % 4], x0[j % 4], x1[j % 4], acc);
+    // pins the batch in place: its fmas before this point, the next reads
+    // after it (otherwise every read is hoisted to the top and the fmas sink)
+    asm volatile("" : "+v"(acc)::"memory");
   }
   return acc;
 }
 
 // Exact logits of candidate positions c, c + maxc, ... of token t: the whole
 // block stages x and the candidate's gate row (widened to fp32) into LDS in
-// one shot, then wave 0 runs the reference's fmaf chain in column order
-// (every lane the same chain; lane 0's result is kept). The chain is a pure
-// sequence of dependent fmas fed by 16-column LDS batches in two register
-// sets, the next batch's reads in flight while the current one is chained.
+// one shot, then lane 0 of wave 0 runs the reference's fmaf chain in column
+// order (dsv4_gemv_bf16, src/dsv4/dsv4_model.c:298-303) from LDS alone.
 // The last chain workgroup of the token selects the routes.
 __device__ void dec_chain_block(const DecArgs &a, int t, int c, float *lds, uint64_t *s_tab,
                                 int *s_flag) {
-  const int tid = threadIdx.x, wv = tid / 64;
+  const int tid = threadIdx.x, wv = tid / 64, lane = tid % 64;
   const int H = a.H;
-  libm_stage_table(s_tab);
   const int nc = a.ncand[t];
-  const float *xt = a.x + (size_t)t * H;
   float *xs = lds, *gs = lds + H;  // H floats each
-  if (c < nc)
-    for (int i = tid; i < H / 4; i += 256)
-      reinterpret_cast<float4 *>(xs)[i] = reinterpret_cast<const float4 *>(xt)[i];
+  const uint64_t tabv = libm_table_load();
+  if (c < nc) {
+    const BufRsrc rx = buf_rsrc(a.x + (size_t)t * H, 4u * (uint32_t)H);
+    uint4 xv[8];  // H <= 8192: 8 pieces per thread
+#pragma unroll
+    for (int j = 0; j < 8; ++j) xv[j] = buf_load16(rx, 16u * (uint32_t)(tid + 256 * j));
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (4 * (tid + 256 * j) < H) reinterpret_cast<uint4 *>(xs)[tid + 256 * j] = xv[j];
+  }
+  libm_table_store(s_tab, tabv);
   for (int pos = c; pos < nc; pos += a.maxc) {
     const int e = a.cand[(size_t)t * a.E + pos];
     float acc = 0.0f;
     if (e >= 0 && e < a.E) {
-      const uint16_t *gr = a.gate + (size_t)e * H;
-      for (int i = tid; i < H / 8; i += 256) {
-        const uint4 w = reinterpret_cast<const uint4 *>(gr)[i];
-        float4 *gp = reinterpret_cast<float4 *>(gs) + 2 * i;
-        gp[0] = make_float4(u2f(w.x << 16), u2f(w.x & 0xFFFF0000u), u2f(w.y << 16),
-                            u2f(w.y & 0xFFFF0000u));
-        gp[1] = make_float4(u2f(w.z << 16), u2f(w.z & 0xFFFF0000u), u2f(w.w << 16),
-                            u2f(w.w & 0xFFFF0000u));
+      const BufRsrc rg = buf_rsrc(a.gate + (size_t)e * H, 2u * (uint32_t)H);
+      uint4 gv[4];  // H / 8 <= 1024 pieces: 4 per thread
+#pragma unroll
+      for (int j = 0; j < 4; ++j) gv[j] = buf_load16(rg, 16u * (uint32_t)(tid + 256 * j));
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int i = tid + 256 * j;
+        if (8 * i < H) {
+          float4 *gp = reinterpret_cast<float4 *>(gs) + 2 * i;
+          gp[0] = make_float4(u2f(gv[j].x << 16), u2f(gv[j].x & 0xFFFF0000u),
+                              u2f(gv[j].y << 16), u2f(gv[j].y & 0xFFFF0000u));
+          gp[1] = make_float4(u2f(gv[j].z << 16), u2f(gv[j].z & 0xFFFF0000u),
+                              u2f(gv[j].w << 16), u2f(gv[j].w & 0xFFFF0000u));
+        }
       }
       __syncthreads();
-      if (wv == 0) {
-        // a zero held in a VGPR: with a provably uniform address the backend
-        // splits each 16-byte LDS read into four
-        int vz;
-        asm volatile("v_mov_b32 %0, 0" : "=v"(vz));
-        const float4 *xp = reinterpret_cast<const float4 *>(xs) + vz;
-        const float4 *gp = reinterpret_cast<const float4 *>(gs) + vz;
-        // 128 columns per iteration: eight 16-column batches, fully unrolled,
-        // each batch's LDS reads issued before the previous batch is chained
-        // (no register state carried across iterations; H % 128 == 0)
-        for (int c0 = 0; c0 < H / 4; c0 += 32) {
-          float4 xa[4], ga[4], xb[4], gb[4];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            xa[j] = xp[c0 + j];
-            ga[j] = gp[c0 + j];
-          }
-#pragma unroll
-          for (int h = 0; h < 4; ++h) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              xb[j] = xp[c0 + 8 * h + 4 + j];
-              gb[j] = gp[c0 + 8 * h + 4 + j];
-            }
-            __builtin_amdgcn_sched_barrier(0);
-            acc = chain16(ga, xa, acc);
-            __builtin_amdgcn_sched_barrier(0);
-            if (h < 3) {
-#pragma unroll
-              for (int j = 0; j < 4; ++j) {
-                xa[j] = xp[c0 + 8 * h + 8 + j];
-                ga[j] = gp[c0 + 8 * h + 8 + j];
-              }
-            }
-            __builtin_amdgcn_sched_barrier(0);
-            acc = chain16(gb, xb, acc);
-            __builtin_amdgcn_sched_barrier(0);
-          }
-        }
+      if (wv == 0 && lane == 0) {
+        __builtin_amdgcn_s_setprio(3);
+        const float4 *g = reinterpret_cast<const float4 *>(gs);
+        const float4 *x = reinterpret_cast<const float4 *>(xs);
+        if (H % 256 == 0)
+          for (int cc = 0; cc < H / 4; cc += 64) acc = chain_cols<32>(g + cc, x + cc, acc);
+        else
+          for (int cc = 0; cc < H / 4; cc += 32) acc = chain_cols<16>(g + cc, x + cc, acc);
+        __builtin_amdgcn_s_setprio(0);
       }
       __syncthreads();  // the next candidate restages the gate row
     }
@@ -513,6 +529,7 @@ __device__ void dec_chain_block(const DecArgs &a, int t, int c, float *lds, uint
   if (tid == 0) a.ctl[1 + t] = 0u;
 }
 
+// --------------------------------------------------------- gate / up ----
 // Blocks: [n*maxc chain workgroups][n*(I/8) shared FP8 pairs]
 // [maxc*n*gu_tiles routed FP4 pairs, candidate-major]; routed tiles of
 // candidate slots a token does not use exit at once.
@@ -534,24 +551,33 @@ __global__ __launch_bounds__(256) void k_dec_gateup(DecArgs a) {
   b -= nchain;
   if (b < nshared) {
     const int tile = b % t8, t = b / t8, r0 = tile * (FP8_TR / 2);
-    // the activation (at most 8192 wide: 32 per thread) ahead of the weights
-    const uint8_t *qx8 = a.qx8 + (size_t)t * H;
-    uint32_t xr[32];
+    // the activation codes (at most 8192: 8 words per thread) and its
+    // per-128 scales ahead of the weights
+    const BufRsrc rq = buf_rsrc(a.qx8 + (size_t)t * H, (uint32_t)H);
+    const BufRsrc rqs = buf_rsrc(a.qxs + (size_t)t * (H / 128), (uint32_t)(H / 128) * 4u);
+    uint32_t xr[8];
 #pragma unroll
-    for (int j = 0; j < 32; ++j) xr[j] = tid + 256 * j < H ? qx8[tid + 256 * j] : 0u;
+    for (int j = 0; j < 8; ++j) xr[j] = buf_load4(rq, 4u * (tid + 256 * j));
+    const float qsv = buf_loadf(rqs, 4u * tid);
+    __builtin_amdgcn_sched_barrier(0);  // issued before the weights
     Fp8Regs R;
-    fp8_pair_load(R, a.sh[0], a.sh[1], H, I, r0);
-    libm_stage_table(s_tab);
-    float *xs = lds;
-    float2 *ps = reinterpret_cast<float2 *>(lds + (H / 128) * 132);
+    fp8_pair_load(R, a.sh[0], a.sh_s[0], a.sh[1], a.sh_s[1], H, I, r0);
+    const uint64_t tabv = libm_table_load();
+    float *xs = lds, *qs = lds + (H / 128) * 132;
+    float2 *ps = reinterpret_cast<float2 *>(qs + ((H / 128 + 3) & ~3));
 #pragma unroll
-    for (int j = 0; j < 32; ++j) {
-      const int i = tid + 256 * j;
-      if (i < H) xs[(i / 128) * 132 + (i % 128)] = e4m3_decode(xr[j]);
+    for (int j = 0; j < 8; ++j) {
+      const int i = 4 * (tid + 256 * j);
+      if (i < H) {
+        const float2 lo = fp8x2<false>(xr[j]), hi = fp8x2<true>(xr[j]);
+        *reinterpret_cast<float4 *>(xs + (i / 128) * 132 + (i % 128)) =
+            make_float4(lo.x, lo.y, hi.x, hi.y);
+      }
     }
+    if (tid < H / 128) qs[tid] = qsv;
     __syncthreads();
-    fp8_pair_finish(R, s_y, xs, a.qxs + (size_t)t * (H / 128), a.sh[0], a.sh_s[0], a.sh[1],
-                    a.sh_s[1], H, I, r0, ps);
+    fp8_pair_finish(R, s_y, xs, qs, a.sh[0], a.sh_s[0], a.sh[1], a.sh_s[1], H, I, r0, ps);
+    libm_table_store(s_tab, tabv);
     __syncthreads();
     if (tid < FP8_TR / 2 && r0 + tid < I)
       a.sv[((size_t)t * (a.maxc + 1) + a.maxc) * I + r0 + tid] =
@@ -574,8 +600,9 @@ __global__ __launch_bounds__(256) void k_dec_gateup(DecArgs a) {
   Fp4Regs R;
   fp4_tile_x(R, a.qx8 + (size_t)t * H, a.qxs + (size_t)t * (H / 128), q);
   fp4_pair_load(R, W0, S0, W1, S1, H, I, r0, q);
-  libm_stage_table(s_tab);
+  const uint64_t tabv = libm_table_load();
   fp4_pair_finish(R, s_y, I, r0, q, reinterpret_cast<float2 *>(lds), fp4_scale_lds(lds, q));
+  libm_table_store(s_tab, tabv);
   __syncthreads();
   if (tid < half && r0 + tid < I)
     a.sv[((size_t)t * (a.maxc + 1) + c) * I + r0 + tid] =
@@ -593,13 +620,15 @@ struct TvRegs {
 };
 
 __device__ __forceinline__ void dec_tv_load(TvRegs &T, const float *tv, int I) {
-  const int wv = threadIdx.x / 64, lane = threadIdx.x % 64;
+  const uint32_t wv = threadIdx.x / 64, lane = threadIdx.x % 64;
+  const BufRsrc r = buf_rsrc(tv, 4u * (uint32_t)I);  // groups past I / 128 read zeros
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    const int g = wv + 4 * j;
-    T.v[2 * j] = g < I / 128 ? tv[g * 128 + lane] : 0.0f;
-    T.v[2 * j + 1] = g < I / 128 ? tv[g * 128 + 64 + lane] : 0.0f;
+    const uint32_t g = wv + 4u * j;
+    T.v[2 * j] = buf_loadf(r, 4u * (g * 128u + lane));
+    T.v[2 * j + 1] = buf_loadf(r, 4u * (g * 128u + 64u + lane));
   }
+  __builtin_amdgcn_sched_barrier(0);  // issued before the weights that follow
 }
 
 // CODES: qy receives E4M3 codes as bytes (the FP4 down tile), otherwise the
@@ -711,7 +740,7 @@ __global__ __launch_bounds__(256) void k_dec_down(DecArgs a) {
     uint8_t *qy8 = reinterpret_cast<uint8_t *>(lds);  // I + I/32 bytes: within the pairs
     float *qys = lds + I / 4;
     dec_requant<true>(qy8, qys, T, tv, w, I);
-    fp4_tile_x(R, qy8, qys, q);
+    fp4_tile_x_lds(R, qy8, qys, q);
     fp4_tile_finish(R, ro, H, r0, q, reinterpret_cast<float2 *>(lds), fp4_scale_lds(lds, q));
     return;
   }
@@ -722,7 +751,7 @@ __global__ __launch_bounds__(256) void k_dec_down(DecArgs a) {
   TvRegs T;
   dec_tv_load(T, tv, I);
   Fp8Regs R;
-  fp8_tile_load(R, a.sh[2], I, H, tile * FP8_TR);
+  fp8_tile_load(R, a.sh[2], a.sh_s[2], I, H, tile * FP8_TR);
   float *xs = lds, *qys = lds + (I / 128) * 132;
   float2 *ps = reinterpret_cast<float2 *>(qys + ((I / 128 + 3) & ~3));
   dec_requant<false>(xs, qys, T, tv, 1.0f, I);
@@ -882,7 +911,7 @@ int dec_launch(int phase, float *out, const float *x, const DSV4GLayer *L, const
   if (phase == 1) {
     const size_t lds = max_sz(max_sz((size_t)(FP4_LDS_ENTRIES + 2 * qg.tr) * 8 + 4096,
                                      (size_t)H * 8),
-                              (size_t)(H / 128) * 132 * 4 +
+                              (size_t)(H / 128) * 132 * 4 + (size_t)((H / 128 + 3) & ~3) * 4 +
                                   (size_t)FP8_TR * pair_stride(H / 128) * 8);
     const long blocks = (long)n * a.maxc + (long)n * ((I + FP8_TR / 2 - 1) / (FP8_TR / 2)) +
                         (long)a.maxc * n * a.gu_tiles;

@@ -18,6 +18,27 @@ namespace dsv4 {
 __device__ __forceinline__ uint32_t f2u(float f) { return __float_as_uint(f); }
 __device__ __forceinline__ float u2f(uint32_t u) { return __uint_as_float(u); }
 
+// Raw buffer over [p, p + bytes) (gfx9 descriptor word 3). A load at or past
+// `bytes` returns zeros without a memory access, so a tile's edge needs no
+// branch around its loads: branch-free loads keep the compiler's vmcnt waits
+// progressive (the first result is consumed while later loads stream in).
+// The base must be wave-uniform.
+typedef __amdgpu_buffer_rsrc_t BufRsrc;
+__device__ __forceinline__ BufRsrc buf_rsrc(const void *p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes,
+                                           0x00020000);
+}
+__device__ __forceinline__ uint4 buf_load16(BufRsrc r, uint32_t off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ uint32_t buf_load4(BufRsrc r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+__device__ __forceinline__ float buf_loadf(BufRsrc r, uint32_t off) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+
 // BF16 round-to-nearest-even by integer bias, no NaN special case
 // (src/dsv4/dsv4_ops.c:35-44 with the widening of dsv4_internal.h:248-254).
 __device__ __forceinline__ float bf16_round(float f) {
@@ -133,6 +154,15 @@ __device__ __forceinline__ float libm_log1pf_nonneg(float x) {
 // of paying a global-memory round trip per call.
 __device__ __forceinline__ void libm_stage_table(uint64_t *tab) {
   if (threadIdx.x < 32) tab[threadIdx.x] = dsv4_libm_exp2_tab[threadIdx.x];
+}
+// The same in two steps, for kernels with weight loads in flight: an
+// unconditional load into a register (a branch around it would make the
+// compiler wait for every earlier load), stored once the weights are used.
+__device__ __forceinline__ uint64_t libm_table_load() {
+  return dsv4_libm_exp2_tab[threadIdx.x % 32];
+}
+__device__ __forceinline__ void libm_table_store(uint64_t *tab, uint64_t v) {
+  if (threadIdx.x < 32) tab[threadIdx.x] = v;
 }
 
 // sqrt(softplus(z)) (src/dsv4/dsv4_model.c:5827-5831).

@@ -234,40 +234,61 @@ __device__ inline void fp8_rows_exact(float *__restrict__ y, const float *__rest
 // FP4_LDS_ENTRIES + 2 * tr), plus 4096 bytes of FP4 scales, or
 // FP8_TR * pair_stride(CB) float2 (FP8).
 
-// FP4: all passes of the tile in flight (npass = tr / rpp <= 16 for every
-// supported width). The lane's activation slice (group g: 32 E4M3 codes and
+// FP4: all passes of the tile in flight (npass = tr / rpp <= NP; the full
+// geometry of fp4_geom has npass <= 16 for every supported width, a caller
+// may pass a geometry with fewer rows per tile). The lane's activation slice (group g: 32 E4M3 codes and
 // the per-128 scale) is loaded first (fp4_tile_x), so that the first passes
 // can start while later weights still stream in; holding codes rather than
 // floats keeps the tile within 128 VGPRs (four waves per SIMD).
-struct Fp4Regs {
-  uint4 w[16];
+template <int NP = 16>
+struct Fp4RegsT {
+  uint4 w[NP];
   uint4 sc;        // this thread's 16 bytes of the tile's E8M0 scales
   uint32_t x8[8];  // E4M3 codes of the activation group, 4 per word
   float as;
 };
+using Fp4Regs = Fp4RegsT<16>;
 
 // qx8: E4M3 codes of the quantised activation (their values are the grid
-// values quant_fp8_act produces, exactly); qscale: per-128 scales.
-__device__ __forceinline__ void fp4_tile_x(Fp4Regs &R, const uint8_t *qx8, const float *qscale,
+// values quant_fp8_act produces, exactly); qscale: per-128 scales. Both in
+// global memory (buffer loads); fp4_tile_x_lds reads them from LDS.
+template <int NP>
+__device__ __forceinline__ void fp4_tile_x(Fp4RegsT<NP> &R, const uint8_t *qx8, const float *qscale,
                                            const Fp4Geom &q) {
-  const int g = threadIdx.x % q.gp;
-  if (g < q.G) {
-    const uint4 a = *reinterpret_cast<const uint4 *>(qx8 + 32 * g);
-    const uint4 b = *reinterpret_cast<const uint4 *>(qx8 + 32 * g + 16);
-    R.x8[0] = a.x;
-    R.x8[1] = a.y;
-    R.x8[2] = a.z;
-    R.x8[3] = a.w;
-    R.x8[4] = b.x;
-    R.x8[5] = b.y;
-    R.x8[6] = b.z;
-    R.x8[7] = b.w;
-    R.as = qscale[g / 4];
-  } else {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) R.x8[i] = 0u;
-    R.as = 0.0f;
-  }
+  // lanes g >= G read past both buffers: zeros
+  const uint32_t g = threadIdx.x % q.gp;
+  const BufRsrc rx = buf_rsrc(qx8, 32u * q.G), rs = buf_rsrc(qscale, (uint32_t)q.G);
+  const uint4 a = buf_load16(rx, 32u * g);
+  const uint4 b = buf_load16(rx, 32u * g + 16u);
+  R.x8[0] = a.x;
+  R.x8[1] = a.y;
+  R.x8[2] = a.z;
+  R.x8[3] = a.w;
+  R.x8[4] = b.x;
+  R.x8[5] = b.y;
+  R.x8[6] = b.z;
+  R.x8[7] = b.w;
+  R.as = buf_loadf(rs, 4u * (g / 4));
+  __builtin_amdgcn_sched_barrier(0);  // issued before the weights that follow
+}
+
+// The same from LDS (after the weights are issued: no wait on them). Lanes
+// g >= G read group G - 1; their partials are never stored.
+template <int NP>
+__device__ __forceinline__ void fp4_tile_x_lds(Fp4RegsT<NP> &R, const uint8_t *qx8,
+                                               const float *qscale, const Fp4Geom &q) {
+  const int g = min((int)threadIdx.x % q.gp, q.G - 1);
+  const uint4 a = *reinterpret_cast<const uint4 *>(qx8 + 32 * g);
+  const uint4 b = *reinterpret_cast<const uint4 *>(qx8 + 32 * g + 16);
+  R.x8[0] = a.x;
+  R.x8[1] = a.y;
+  R.x8[2] = a.z;
+  R.x8[3] = a.w;
+  R.x8[4] = b.x;
+  R.x8[5] = b.y;
+  R.x8[6] = b.z;
+  R.x8[7] = b.w;
+  R.as = qscale[g / 4];
 }
 
 __device__ __forceinline__ uint32_t u4_word(const uint4 &v, int d) {
@@ -289,7 +310,8 @@ __device__ __forceinline__ void fp4_step4(const uint32_t (&wd)[4], float x0, flo
 
 // Partials of passes u0 .. u0 + 3: four 32-long fmaf chains, each in the
 // reference's column order, interleaved so the fma latency is hidden.
-__device__ __forceinline__ void fp4_partials4(const Fp4Regs &R, int u0, float (&p)[4]) {
+template <int NP>
+__device__ __forceinline__ void fp4_partials4(const Fp4RegsT<NP> &R, int u0, float (&p)[4]) {
   // converted per call on purpose: the scheduling barrier keeps the compiler
   // from hoisting 32 converted floats of every call to the top (registers)
   __builtin_amdgcn_sched_barrier(0);
@@ -314,10 +336,12 @@ __device__ __forceinline__ void fp4_partials4(const Fp4Regs &R, int u0, float (&
 // [r0, r0 + tr/2) of W0 then the same rows of W1 (row lr < half is W0 row
 // r0 + lr, lr >= half is W1 row r0 + lr - half; half is npass / 2 whole
 // passes, so the matrix of a pass is uniform). The tile's scales (tr * G <= 4096 bytes, row
-// lr at lr * G) are fetched first, 16 bytes per thread, for LDS. Offsets are
-// 32-bit (a matrix is below 4 GB): each load takes a scalar base and one
-// VGPR of offset.
-__device__ __forceinline__ void fp4_load_w(Fp4Regs &R, const uint8_t *__restrict__ W0,
+// lr at lr * G) are fetched first, 16 bytes per thread, for LDS. Every load
+// is a buffer load over the tile's existing rows of one matrix (at most 64 KB,
+// 32-bit offsets): rows past the matrix, passes past npass and lanes g >= G
+// read zeros without touching memory.
+template <int NP>
+__device__ __forceinline__ void fp4_load_w(Fp4RegsT<NP> &R, const uint8_t *__restrict__ W0,
                                            const uint8_t *__restrict__ S0,
                                            const uint8_t *__restrict__ W1,
                                            const uint8_t *__restrict__ S1, int in, int rows,
@@ -325,26 +349,34 @@ __device__ __forceinline__ void fp4_load_w(Fp4Regs &R, const uint8_t *__restrict
   const int t = threadIdx.x, g = t % q.gp, rsub = t / q.gp;
   const int npass = q.tr / q.rpp, half = q.tr / 2;
   const uint32_t pcols = (uint32_t)in / 2, G = (uint32_t)q.G;
+  const int span = pair ? half : q.tr;  // tile rows of each matrix
+  const uint32_t nrow = (uint32_t)max(0, min(span, rows - r0));
+  const BufRsrc rs0 = buf_rsrc(S0 + (size_t)r0 * G, nrow * G);
+  const BufRsrc rw0 = buf_rsrc(W0 + (size_t)r0 * pcols, nrow * pcols);
+  const BufRsrc rs1 = pair ? buf_rsrc(S1 + (size_t)r0 * G, nrow * G) : rs0;
+  const BufRsrc rw1 = pair ? buf_rsrc(W1 + (size_t)r0 * pcols, nrow * pcols) : rw0;
   {
-    // scales: [W0 rows][W1 rows] when paired, else tr rows of W0
-    const uint32_t seg = (uint32_t)(pair ? half : q.tr) * G;
+    // scales: [W0 rows][W1 rows] when paired (seg bytes each), else the tile's
+    // rows of W0; a lane's offset is in range of at most one of the two.
+    // Dword loads: the ranges are multiples of 4 bytes, not always of 16.
     const uint32_t o = 16u * (uint32_t)t;
-    const bool m1 = pair && o >= seg;
-    const uint32_t oo = m1 ? o - seg : o;
-    const uint32_t lim = (uint32_t)(rows > r0 ? rows - r0 : 0) * G;  // rows that exist
-    R.sc = (o < (pair ? 2 * seg : seg) && oo + 16u <= lim)
-               ? *reinterpret_cast<const uint4 *>((m1 ? S1 : S0) + ((uint32_t)r0 * G + oo))
-               : make_uint4(0x7f7f7f7fu, 0x7f7f7f7fu, 0x7f7f7f7fu, 0x7f7f7f7fu);
-  }
+    uint32_t v[4];
 #pragma unroll
-  for (int u = 0; u < 16; ++u) {
+    for (int d = 0; d < 4; ++d) v[d] = buf_load4(rs0, o + 4u * d);
+    if (pair) {
+      const uint32_t seg = (uint32_t)half * G;
+#pragma unroll
+      for (int d = 0; d < 4; ++d) v[d] |= buf_load4(rs1, o + 4u * d - seg);  // o < seg wraps
+    }
+    R.sc = make_uint4(v[0], v[1], v[2], v[3]);
+  }
+  const uint32_t gcol = g < q.G ? 16u * (uint32_t)g : 0xFFFFFFF0u;  // g >= G: out of range
+#pragma unroll
+  for (int u = 0; u < NP; ++u) {
     const bool m1 = pair && u >= npass / 2;  // == (lr >= half): half = npass / 2 passes
-    const int lr = u * q.rpp + rsub;
-    const int row = r0 + (m1 ? lr - half : lr);
-    const uint8_t *W = m1 ? W1 : W0;
-    R.w[u] = (g < q.G && u < npass && row < rows)
-                 ? *reinterpret_cast<const uint4 *>(W + ((uint32_t)row * pcols + 16u * g))
-                 : make_uint4(0, 0, 0, 0);
+    const uint32_t lr = (uint32_t)(u * q.rpp + rsub);
+    const uint32_t lrow = m1 ? lr - (uint32_t)half : lr;
+    R.w[u] = buf_load16(m1 ? rw1 : rw0, gcol == 0xFFFFFFF0u ? gcol : lrow * pcols + gcol);
   }
 }
 
@@ -352,7 +384,8 @@ __device__ __forceinline__ void fp4_load_w(Fp4Regs &R, const uint8_t *__restrict
 // bf16(acc) for lane t < tr (row lr = t), garbage otherwise. cl: 4096 bytes
 // of LDS for the scales, apart from ps. Starts with a barrier: the activation
 // may have been read from LDS that ps overlaps.
-__device__ __forceinline__ float fp4_tile_rows(const Fp4Regs &R, int rows, int r0,
+template <int NP>
+__device__ __forceinline__ float fp4_tile_rows(const Fp4RegsT<NP> &R, int rows, int r0,
                                                const Fp4Geom &q, float2 *ps, uint8_t *cl,
                                                bool pair) {
   const int t = threadIdx.x, g = t % q.gp, rsub = t / q.gp;
@@ -362,7 +395,7 @@ __device__ __forceinline__ float fp4_tile_rows(const Fp4Regs &R, int rows, int r
   reinterpret_cast<uint4 *>(cl)[t] = R.sc;
   __syncthreads();
 #pragma unroll
-  for (int u0 = 0; u0 < 16; u0 += 4) {
+  for (int u0 = 0; u0 < NP; u0 += 4) {
     if (u0 < npass) {
       float p[4];
       fp4_partials4(R, u0, p);
@@ -391,26 +424,30 @@ __device__ __forceinline__ float fp4_tile_rows(const Fp4Regs &R, int rows, int r
 }
 
 // Single matrix: y[r0 + t] for the tile's rows.
-__device__ __forceinline__ void fp4_tile_load(Fp4Regs &R, const uint8_t *__restrict__ W,
+template <int NP>
+__device__ __forceinline__ void fp4_tile_load(Fp4RegsT<NP> &R, const uint8_t *__restrict__ W,
                                               const uint8_t *__restrict__ S, int in, int rows,
                                               int r0, const Fp4Geom &q) {
   fp4_load_w(R, W, S, W, S, in, rows, r0, q, false);
 }
-__device__ __forceinline__ void fp4_tile_finish(const Fp4Regs &R, float *y, int rows, int r0,
+template <int NP>
+__device__ __forceinline__ void fp4_tile_finish(const Fp4RegsT<NP> &R, float *y, int rows, int r0,
                                                 const Fp4Geom &q, float2 *ps, uint8_t *cl) {
   const float v = fp4_tile_rows(R, rows, r0, q, ps, cl, false);
   if (threadIdx.x < q.tr && r0 + (int)threadIdx.x < rows) y[r0 + threadIdx.x] = v;
 }
 
 // Paired: yl[lr] (LDS) for lr < tr.
-__device__ __forceinline__ void fp4_pair_load(Fp4Regs &R, const uint8_t *__restrict__ W0,
+template <int NP>
+__device__ __forceinline__ void fp4_pair_load(Fp4RegsT<NP> &R, const uint8_t *__restrict__ W0,
                                               const uint8_t *__restrict__ S0,
                                               const uint8_t *__restrict__ W1,
                                               const uint8_t *__restrict__ S1, int in, int rows,
                                               int r0, const Fp4Geom &q) {
   fp4_load_w(R, W0, S0, W1, S1, in, rows, r0, q, true);
 }
-__device__ __forceinline__ void fp4_pair_finish(const Fp4Regs &R, float *yl, int rows, int r0,
+template <int NP>
+__device__ __forceinline__ void fp4_pair_finish(const Fp4RegsT<NP> &R, float *yl, int rows, int r0,
                                                 const Fp4Geom &q, float2 *ps, uint8_t *cl) {
   const float v = fp4_tile_rows(R, rows, r0, q, ps, cl, true);
   if (threadIdx.x < q.tr) yl[threadIdx.x] = v;
@@ -421,23 +458,40 @@ __device__ __forceinline__ void fp4_pair_finish(const Fp4Regs &R, float *yl, int
 // ahead, wider inputs load the rest in finish.
 struct Fp8Regs {
   uint4 w[16];
+  uint32_t sc[2];  // E8M0 codes of the lane's two 128-blocks
 };
 
-__device__ __forceinline__ void fp8_tile_load(Fp8Regs &R, const uint8_t *__restrict__ W, int in,
-                                              int rows, int r0) {
-  const int t = threadIdx.x, slot = t % 16, row = r0 + t / 16;
-  const int CB = (in + 127) / 128;
+// Weights (two 128-blocks per lane) and block-scale codes of rows
+// [r0, r0 + nr) of W for lane row lr = lr0 + t / 16, as buffer loads: rows
+// past the matrix and blocks past the width read zeros.
+__device__ __forceinline__ void fp8_load_rows(Fp8Regs &R, const uint8_t *__restrict__ W,
+                                              const uint8_t *__restrict__ S, int in, int rows,
+                                              int r0, int nr, int lr) {
+  const int slot = threadIdx.x % 16;
+  const uint32_t CB = (uint32_t)(in + 127) / 128;
+  const uint32_t nrow = (uint32_t)max(0, min(nr, rows - r0));
+  const BufRsrc rw = buf_rsrc(W + (size_t)r0 * in, nrow * (uint32_t)in);
+  const BufRsrc rs = buf_rsrc(S, (uint32_t)((rows + 127) / 128) * CB);
+  const uint32_t srow = (uint32_t)((r0 + lr) / 128) * CB;
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    const int cb = slot + 16 * j;
+    const uint32_t cb = (uint32_t)(slot + 16 * j);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const int c = cb * 128 + 16 * i;
-      R.w[8 * j + i] = (row < rows && cb < CB && c < in)
-                           ? *reinterpret_cast<const uint4 *>(W + (size_t)row * in + c)
-                           : make_uint4(0, 0, 0, 0);
+      const uint32_t c = cb * 128u + 16u * i;
+      R.w[8 * j + i] = buf_load16(rw, cb < CB && c < (uint32_t)in
+                                          ? (uint32_t)lr * (uint32_t)in + c
+                                          : 0xFFFFFFF0u);
     }
+    R.sc[j] = __builtin_amdgcn_raw_buffer_load_b8(
+        rs, cb < CB && (uint32_t)lr < nrow ? srow + cb : 0xFFFFFFF0u, 0, 0);
   }
+}
+
+__device__ __forceinline__ void fp8_tile_load(Fp8Regs &R, const uint8_t *__restrict__ W,
+                                              const uint8_t *__restrict__ S, int in, int rows,
+                                              int r0) {
+  fp8_load_rows(R, W, S, in, rows, r0, FP8_TR, threadIdx.x / 16);
 }
 
 // Sequential partial of one 16-column piece.
@@ -456,52 +510,62 @@ __device__ __forceinline__ float fp8_piece(const uint4 w, const float *xb, float
   return part;
 }
 
-// xs: the activation in LDS, padded to 132 floats per 128-block; qscale may
-// be LDS or global. Rows [r0, r0 + FP8_TR) of y (BF16-rounded if round_out).
-__device__ __forceinline__ void fp8_tile_finish(const Fp8Regs &R, float *y, const float *xs,
-                                                const float *qscale,
-                                                const uint8_t *__restrict__ W,
-                                                const uint8_t *__restrict__ S, int in, int rows,
-                                                int r0, int round_out, float2 *ps) {
-  const int t = threadIdx.x, lr = t / 16, slot = t % 16, row = r0 + lr;
+// Block partials of the lane's row (row < rows) into ps[lr * stride + cb]:
+// the two blocks held in R, then, for inputs wider than 4096, the rest
+// streamed here. xs: the activation in LDS, padded to 132 floats per
+// 128-block; qscale may be LDS or global.
+__device__ __forceinline__ void fp8_partials(const Fp8Regs &R, const float *xs,
+                                             const float *qscale, const uint8_t *__restrict__ W,
+                                             const uint8_t *__restrict__ S, int in, int row,
+                                             int lr, float2 *ps) {
+  const int slot = threadIdx.x % 16;
   const int CB = (in + 127) / 128, stride = pair_stride(CB);
-  if (row < rows) {
-    const uint8_t *sr = S + (size_t)(row / 128) * CB;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int cb = slot + 16 * j;
-      if (cb < CB) {
-        const int len = min(128, in - cb * 128);
-        const float *xb = xs + cb * 132;
-        float part = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-          if (16 * i < len) part = fp8_piece(R.w[8 * j + i], xb + 16 * i, part);
-        const uint32_t code = sr[cb];
-        float s = qscale[cb] * e8m0(code);
-        if (code == 255u) {
-          part = 0.0f;
-          s = 0.0f;
-        }
-        ps[lr * stride + cb] = make_float2(part, s);
-      }
-    }
-    for (int cb = slot + 32; cb < CB; cb += 16) {
+  for (int j = 0; j < 2; ++j) {
+    const int cb = slot + 16 * j;
+    if (cb < CB) {
       const int len = min(128, in - cb * 128);
-      const uint8_t *wr = W + (size_t)row * in + cb * 128;
       const float *xb = xs + cb * 132;
       float part = 0.0f;
-      for (int c = 0; c < len; c += 16)
-        part = fp8_piece(*reinterpret_cast<const uint4 *>(wr + c), xb + c, part);
-      const uint32_t code = sr[cb];
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        if (16 * i < len) part = fp8_piece(R.w[8 * j + i], xb + 16 * i, part);
+      const uint32_t code = R.sc[j];
       float s = qscale[cb] * e8m0(code);
-      if (code == 255u) {
+      if (code == 255u) {  // NaN scale: the reference skips the block
         part = 0.0f;
         s = 0.0f;
       }
       ps[lr * stride + cb] = make_float2(part, s);
     }
   }
+  const uint8_t *sr = S + (size_t)(row / 128) * CB;
+  for (int cb = slot + 32; cb < CB; cb += 16) {
+    const int len = min(128, in - cb * 128);
+    const uint8_t *wr = W + (size_t)row * in + cb * 128;
+    const float *xb = xs + cb * 132;
+    float part = 0.0f;
+    for (int c = 0; c < len; c += 16)
+      part = fp8_piece(*reinterpret_cast<const uint4 *>(wr + c), xb + c, part);
+    const uint32_t code = sr[cb];
+    float s = qscale[cb] * e8m0(code);
+    if (code == 255u) {
+      part = 0.0f;
+      s = 0.0f;
+    }
+    ps[lr * stride + cb] = make_float2(part, s);
+  }
+}
+
+// Rows [r0, r0 + FP8_TR) of y (BF16-rounded if round_out).
+__device__ __forceinline__ void fp8_tile_finish(const Fp8Regs &R, float *y, const float *xs,
+                                                const float *qscale,
+                                                const uint8_t *__restrict__ W,
+                                                const uint8_t *__restrict__ S, int in, int rows,
+                                                int r0, int round_out, float2 *ps) {
+  const int t = threadIdx.x, lr = t / 16, row = r0 + lr;
+  const int CB = (in + 127) / 128, stride = pair_stride(CB);
+  if (row < rows) fp8_partials(R, xs, qscale, W, S, in, row, lr, ps);
   __syncthreads();
   if (t < FP8_TR && r0 + t < rows) {
     const float acc = pair_chain(ps + t * stride, CB);
@@ -512,26 +576,17 @@ __device__ __forceinline__ void fp8_tile_finish(const Fp8Regs &R, float *y, cons
 // ---- paired FP8 tiles: the first half of a tile's rows from matrix 0
 // (gate), the second half the same rows of matrix 1 (up), so one workgroup
 // holds both operands of SwiGLU; yl[lr] receives bf16(acc).
-// FP8 pairs: lanes t / 16 < 8 take W0 rows r0 + t / 16, the others W1 rows
-// r0 + t / 16 - 8 (FP8_TR / 2 = 8 rows of each).
+// Lanes t / 16 < 8 (waves 0 and 1) take W0 rows r0 + t / 16, the others W1
+// rows r0 + t / 16 - 8 (FP8_TR / 2 = 8 rows of each): the matrix is
+// wave-uniform.
 __device__ __forceinline__ void fp8_pair_load(Fp8Regs &R, const uint8_t *__restrict__ W0,
-                                              const uint8_t *__restrict__ W1, int in, int rows,
+                                              const uint8_t *__restrict__ S0,
+                                              const uint8_t *__restrict__ W1,
+                                              const uint8_t *__restrict__ S1, int in, int rows,
                                               int r0) {
-  const int t = threadIdx.x, slot = t % 16, lr = t / 16;
-  const int row = r0 + (lr & 7);
-  const uint8_t *W = lr < 8 ? W0 : W1;
-  const int CB = (in + 127) / 128;
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int cb = slot + 16 * j;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int c = cb * 128 + 16 * i;
-      R.w[8 * j + i] = (row < rows && cb < CB && c < in)
-                           ? *reinterpret_cast<const uint4 *>(W + (size_t)row * in + c)
-                           : make_uint4(0, 0, 0, 0);
-    }
-  }
+  const bool m1 = __builtin_amdgcn_readfirstlane((int)threadIdx.x / 64) >= 2;
+  fp8_load_rows(R, m1 ? W1 : W0, m1 ? S1 : S0, in, rows, r0, FP8_TR / 2,
+                (threadIdx.x / 16) & 7);
 }
 
 __device__ __forceinline__ void fp8_pair_finish(const Fp8Regs &R, float *yl, const float *xs,
@@ -541,47 +596,9 @@ __device__ __forceinline__ void fp8_pair_finish(const Fp8Regs &R, float *yl, con
                                                 const uint8_t *__restrict__ W1,
                                                 const uint8_t *__restrict__ S1, int in, int rows,
                                                 int r0, float2 *ps) {
-  const int t = threadIdx.x, lr = t / 16, slot = t % 16, row = r0 + (lr & 7);
-  const uint8_t *W = lr < 8 ? W0 : W1;
-  const uint8_t *S = lr < 8 ? S0 : S1;
+  const int t = threadIdx.x, lr = t / 16, row = r0 + (lr & 7);
   const int CB = (in + 127) / 128, stride = pair_stride(CB);
-  if (row < rows) {
-    const uint8_t *sr = S + (size_t)(row / 128) * CB;
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int cb = slot + 16 * j;
-      if (cb < CB) {
-        const int len = min(128, in - cb * 128);
-        const float *xb = xs + cb * 132;
-        float part = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-          if (16 * i < len) part = fp8_piece(R.w[8 * j + i], xb + 16 * i, part);
-        const uint32_t code = sr[cb];
-        float s = qscale[cb] * e8m0(code);
-        if (code == 255u) {
-          part = 0.0f;
-          s = 0.0f;
-        }
-        ps[lr * stride + cb] = make_float2(part, s);
-      }
-    }
-    for (int cb = slot + 32; cb < CB; cb += 16) {
-      const int len = min(128, in - cb * 128);
-      const uint8_t *wr = W + (size_t)row * in + cb * 128;
-      const float *xb = xs + cb * 132;
-      float part = 0.0f;
-      for (int c = 0; c < len; c += 16)
-        part = fp8_piece(*reinterpret_cast<const uint4 *>(wr + c), xb + c, part);
-      const uint32_t code = sr[cb];
-      float s = qscale[cb] * e8m0(code);
-      if (code == 255u) {
-        part = 0.0f;
-        s = 0.0f;
-      }
-      ps[lr * stride + cb] = make_float2(part, s);
-    }
-  }
+  if (row < rows) fp8_partials(R, xs, qscale, lr < 8 ? W0 : W1, lr < 8 ? S0 : S1, in, row, lr, ps);
   __syncthreads();
   if (t < FP8_TR && r0 + (t & 7) < rows) {
     const float acc = pair_chain(ps + t * stride, CB);

@@ -242,6 +242,17 @@ class GpuLib:
                    _ptr(workspace), workspace.numel(), _ptr(idx), _ptr(wt), self._stream())
         return out, idx, wt
 
+    def moe_workspace_init(self, workspace):
+        """Zero a decode workspace, once, before its first dsv4g_moe_forward."""
+        self._call("dsv4g_moe_workspace_init", _ptr(workspace), workspace.numel(), self._stream())
+
+    def moe_forward_into(self, layer, x, out, workspace, token_ids=None):
+        """dsv4g_moe_forward into out with a prepared workspace, routing not
+        copied out: the form a captured decode loop uses."""
+        self._call("dsv4g_moe_forward", _ptr(out), _ptr(x), C.byref(layer.struct),
+                   _ptr(token_ids), x.shape[0], _ptr(workspace), workspace.numel(), None, None,
+                   self._stream())
+
     def new_moe_workspace(self, layer, n_tokens, device):
         """A decode workspace, zeroed as dsv4g_moe_forward requires before its
         first use (every call leaves it reusable)."""

@@ -157,10 +157,11 @@ int dsv4g_moe_forward(float *out, const float *x, const DSV4GLayer *L, const int
                       int n_tokens, void *workspace, size_t workspace_bytes, int *idx_out,
                       float *wt_out, void *stream);
 /* The same layer as four ordered phases, for callers that interleave or
- * time them: 0 router logits + activation quant, 1 gate/up GEMVs of the
- * candidate experts and the shared expert with the exact router chains
- * beside them, 2 exact top-k, SwiGLU + requant and down GEMVs, 3 the ordered
- * combine. dsv4g_moe_decode_routing copies the routing of the last call.
+ * time them: 0 router logits, candidate experts and activation quant; 1
+ * gate/up GEMVs of the candidates and the shared expert, with the exact
+ * router chains of the candidates and the exact top-k beside them; 2 SwiGLU
+ * requant and down GEMVs; 3 the ordered combine.
+ * dsv4g_moe_decode_routing copies the routing of the last call.
  * x and out: 16-byte aligned. */
 int dsv4g_moe_decode_phase(int phase, float *out, const float *x, const DSV4GLayer *L,
                            const int *token_ids, int n_tokens, void *workspace,

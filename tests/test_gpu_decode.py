@@ -315,3 +315,63 @@ def test_moe_forward_more_than_256_candidates(env, winners):
         assert np.array_equal(idx[t], i), t
         assert same_bits(wt[t], w), t
         assert same_bits(out[t], o), (t, max_rel_err(out[t], o))
+
+
+def test_moe_phases_and_graph_replay_match_fused(env):
+    """The four phases in order on one stream, and a captured graph of the
+    fused entry replayed several times with eager calls on the same
+    workspace between the replays: every result has the fused call's bits,
+    which match the oracle."""
+    torch, orc, lib, dg = env["torch"], env["orc"], env["lib"], env["dsv4_gpu"]
+    L = make_layer(orc, 4096, 128, 64, 6, seed=31, bias=True)
+    DL = dg.DeviceLayer.from_host(L, env["dev"])
+    Xh = bf16_input(np.random.default_rng(37), (3, 4096))
+    X = T(env, Xh)
+    ref, idx, wt = lib.moe_forward(DL, X)
+    torch.cuda.synchronize()
+    for t in range(3):
+        o, i, w = orc.moe_forward(L, Xh[t])
+        assert np.array_equal(H(idx)[t], i) and same_bits(H(wt)[t], w)
+        assert same_bits(H(ref)[t], o), t
+    ws = lib.new_moe_workspace(DL, 3, env["dev"])
+    out = torch.zeros_like(X)
+    for ph in range(4):
+        lib.moe_decode_phase(ph, DL, X, out, ws)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    out2 = torch.zeros_like(X)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        lib.moe_forward_into(DL, X, out2, ws)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        lib.moe_forward_into(DL, X, out2, ws)
+    for r in range(4):
+        out2.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out2, ref), r
+        e, _, _ = lib.moe_forward(DL, X, workspace=ws)
+        torch.cuda.synchronize()
+        assert torch.equal(e, ref), r
+
+
+@pytest.mark.parametrize("hidden,experts", [(384, 24), (1280, 40)])
+def test_moe_forward_odd_widths_bit_exact(env, hidden, experts):
+    """Hidden sizes whose exact-chain slices are 128 columns (384: three
+    slices) or 256 (1280: five), with expert counts that leave a partial
+    chain block: outputs, indices and weights bit-identical to the oracle."""
+    orc, lib, dg = env["orc"], env["lib"], env["dsv4_gpu"]
+    L = make_layer(orc, hidden, 256, experts, 6, seed=41, bias=True)
+    DL = dg.DeviceLayer.from_host(L, env["dev"])
+    X = bf16_input(np.random.default_rng(43), (2, hidden))
+    out, idx, wt = lib.moe_forward(DL, T(env, X))
+    out, idx, wt = H(out), H(idx), H(wt)
+    for t in range(2):
+        o, i, w = orc.moe_forward(L, X[t])
+        assert np.array_equal(idx[t], i), t
+        assert same_bits(wt[t], w), t
+        assert same_bits(out[t], o), (t, max_rel_err(out[t], o))
