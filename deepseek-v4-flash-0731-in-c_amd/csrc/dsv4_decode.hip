@@ -46,6 +46,7 @@
 namespace dsv4 {
 
 #define DEC_CTL_BYTES 4096  // control words: [0] + one per token, so n <= 1023
+#define DEC_NP 8            // passes per FP4 tile (gate/up pairs and down)
 
 struct DecArgs {
   const float *x;
@@ -60,7 +61,7 @@ struct DecArgs {
   unsigned *ctl;                   // [0] logit arrivals, [1 + t] chain arrivals of token t
   uint8_t *qx8;                    // [n][H] E4M3 codes of the quantised activation
   float *qxs;                      // [n][H/128] its scales
-  float *ch, *zabs;                // [n][E]
+  float *ch, *zabs, *za;           // [n][E]: approximate choice, sum|w*x|, logit
   int *cand;                       // [n][E] candidate ids, ascending
   int *ncand;                      // [n]
   float *zx;                       // [n][E] exact logit per candidate position
@@ -75,6 +76,7 @@ struct DecArgs {
   int n, H, I, E, K, maxc;
   int gu_tiles, dn_tiles;  // paired gate/up tiles (rows I, in H); down tiles (rows H, in I)
   float route_scale, limit;
+  int fast;  // routing from the parallel logits when the candidates are exactly top-k
 };
 
 // Expert e's matrix m (0 gate w1, 1 up w3, 2 down w2) in the reference slot
@@ -97,9 +99,9 @@ __device__ __forceinline__ void expert_mat(const DecArgs &a, int e, int m, const
   }
 }
 
-// The 4096 bytes of FP4 tile scales follow the pairs in dynamic LDS.
+// The 4096 bytes of FP4 tile scales follow the tile's pairs in dynamic LDS.
 __device__ __forceinline__ uint8_t *fp4_scale_lds(float *lds, const Fp4Geom &q) {
-  return reinterpret_cast<uint8_t *>(lds) + (size_t)(FP4_LDS_ENTRIES + 2 * q.tr) * 8;
+  return reinterpret_cast<uint8_t *>(lds) + (size_t)q.tr * pair_stride(q.G) * 8;
 }
 
 // One arrival on *cnt by the calling workgroup, after its global writes;
@@ -119,36 +121,48 @@ __device__ __forceinline__ bool dec_arrive_last(unsigned *cnt, unsigned total, i
   return *s_flag != 0;
 }
 
+__device__ __forceinline__ void dec_select_finish(const DecArgs &a, int t, int my_e, float my_sc,
+                                                  int my_pos);
+
 // Candidates of token t in ascending expert id (whole calling wave) into
 // cand[0 .. count); returns the count. A hash layer's candidates are its
 // tid2eid row. NPER = experts per lane (E <= 64 * NPER).
+// In fast mode, when the candidates are exactly the top-k, the routing is
+// taken here from the approximate choices (selection order) and the parallel
+// logits (scores), with no further memory round trip.
 template <int NPER>
-__device__ int dec_candidates_t(const DecArgs &a, int t, int *cand) {
+__device__ __forceinline__ int dec_candidates_t(const DecArgs &a, int t, int *cand,
+                                                const uint64_t *tab) {
   const int lane = threadIdx.x % 64;
-  const float *cht = a.ch + (size_t)t * a.E, *zat = a.zabs + (size_t)t * a.E;
+  const size_t row = (size_t)t * a.E;
   const float ninf = -__builtin_inff();
-  float v[NPER];
+  float v[NPER], z[NPER];
   float amax = 0.0f;
 #pragma unroll
   for (int j = 0; j < NPER; ++j) {
     const int e = lane + 64 * j;
     v[j] = ninf;
+    z[j] = 0.0f;
     if (e < a.E) {
-      const float c = cht[e];
+      const float c = a.ch[row + e];
       v[j] = c == c ? c : ninf;  // a NaN choice never wins a strict '>'
-      amax = fmaxf(amax, zat[e]);
+      amax = fmaxf(amax, a.zabs[row + e]);
+      if (a.fast) z[j] = a.za[row + e];
     }
   }
-  // k-th best approximate choice: k times remove one instance of the maximum
-  float kth = ninf;
+  // k-th best approximate choice: k times remove one instance of the
+  // maximum; lane k keeps the expert and logit of the k-th removal
+  float kth = ninf, my_z = 0.0f;
+  int my_e = -1;
   unsigned used = 0u;
   for (int k = 0; k < a.K; ++k) {
-    float m = ninf;
+    float m = ninf, mz = 0.0f;
     int mj = -1;
 #pragma unroll
     for (int j = 0; j < NPER; ++j)
       if (!((used >> j) & 1u) && v[j] > m) {
         m = v[j];
+        mz = z[j];
         mj = j;
       }
     const float wm = wave_max_dpp(m);
@@ -157,7 +171,14 @@ __device__ int dec_candidates_t(const DecArgs &a, int t, int *cand) {
       kth = ninf;
       break;
     }
-    if (lane == __builtin_ctzll(bal)) used |= 1u << mj;
+    const int wl = __builtin_ctzll(bal);
+    if (lane == wl) used |= 1u << mj;
+    const int we = wl + 64 * __builtin_amdgcn_readlane(mj, wl);
+    const float wz = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mz), wl));
+    if (lane == k) {
+      my_e = we;
+      my_z = wz;
+    }
     kth = wm;
   }
   const float sum_abs = wave_max_dpp(amax);
@@ -173,30 +194,38 @@ __device__ int dec_candidates_t(const DecArgs &a, int t, int *cand) {
     if (p) cand[pos] = e;
     base += __popcll(bal);
   }
+  if (a.fast && base == a.K) {  // the same test as dec_chain_block's early exit
+    // candidates == top-k: sel_pos is the rank by id (dec_select_finish)
+    dec_select_finish(a, t, my_e, lane < a.K ? sqrt_softplus(my_z, tab) : 0.0f, -1);
+  }
   return base;
 }
 
-__device__ int dec_candidates(const DecArgs &a, int t, int *cand) {
+__device__ __forceinline__ int dec_candidates(const DecArgs &a, int t, int *cand,
+                                              const uint64_t *tab) {
   if (a.tid2eid) {
     const int64_t *row = a.tid2eid + (size_t)a.token_ids[t] * a.K;
-    for (int k = threadIdx.x % 64; k < a.K; k += 64) cand[k] = (int)row[k];
+    for (int k = threadIdx.x % 64; k < a.K; k += 64) {
+      const int e = (int)row[k];
+      cand[k] = e;
+      if (a.fast) a.zx[(size_t)t * a.E + k] = (e >= 0 && e < a.E) ? a.za[(size_t)t * a.E + e] : 0.0f;
+    }
     return a.K;
   }
-  if (a.E <= 64) return dec_candidates_t<1>(a, t, cand);
-  if (a.E <= 128) return dec_candidates_t<2>(a, t, cand);
-  if (a.E <= 256) return dec_candidates_t<4>(a, t, cand);
-  if (a.E <= 512) return dec_candidates_t<8>(a, t, cand);
-  return dec_candidates_t<16>(a, t, cand);
+  if (a.E <= 64) return dec_candidates_t<1>(a, t, cand, tab);
+  if (a.E <= 128) return dec_candidates_t<2>(a, t, cand, tab);
+  if (a.E <= 256) return dec_candidates_t<4>(a, t, cand, tab);
+  if (a.E <= 512) return dec_candidates_t<8>(a, t, cand, tab);
+  return dec_candidates_t<16>(a, t, cand, tab);
 }
 
-__device__ void dec_select_finish(const DecArgs &a, int t, int my_e, float my_sc, int my_pos);
 
 // Exact top-k of token t from the candidates' exact logits (one whole wave):
 // routes ascending by id with weights and candidate positions, written to
 // sel_* (and idx_out / wt_out) (src/dsv4/dsv4_model.c:6615-6676). Lane k
 // carries route k in selection order.
 template <int NPER>
-__device__ void dec_select_t(const DecArgs &a, int t, const uint64_t *tab) {
+__device__ __forceinline__ void dec_select_t(const DecArgs &a, int t, const uint64_t *tab) {
   const int lane = threadIdx.x % 64;
   const int K = a.K;
   const int nc = a.ncand[t];
@@ -266,7 +295,7 @@ __device__ void dec_select_t(const DecArgs &a, int t, const uint64_t *tab) {
 // routes sorted by id (src/dsv4/dsv4_model.c:6650-6674; equal ids carry
 // equal weights, so any order among them matches the exchange sort). Lane k
 // holds route k in selection order.
-__device__ void dec_select_finish(const DecArgs &a, int t, int my_e, float my_sc, int my_pos) {
+__device__ __forceinline__ void dec_select_finish(const DecArgs &a, int t, int my_e, float my_sc, int my_pos) {
   const int lane = threadIdx.x % 64;
   const int K = a.K;
   float sum = 0.0f;
@@ -286,7 +315,7 @@ __device__ void dec_select_finish(const DecArgs &a, int t, int my_e, float my_sc
     const size_t o = (size_t)t * K + rank;
     a.sel_e[o] = my_e;
     a.sel_w[o] = my_w;
-    a.sel_pos[o] = my_pos;
+    a.sel_pos[o] = my_pos >= 0 ? my_pos : rank;  // fast path: candidates == routes
     if (a.idx_out) a.idx_out[o] = my_e;
     if (a.wt_out) a.wt_out[o] = my_w;
   }
@@ -294,7 +323,7 @@ __device__ void dec_select_finish(const DecArgs &a, int t, int my_e, float my_sc
 
 // More than 256 candidates (near-ties or large expert counts): scores in
 // LDS (2 * nc floats, nc <= 1024), scanned with plain loops.
-__device__ void dec_select_big(const DecArgs &a, int t, const uint64_t *tab, float *lds) {
+__device__ __forceinline__ void dec_select_big(const DecArgs &a, int t, const uint64_t *tab, float *lds) {
   const int lane = threadIdx.x % 64;
   const int nc = a.ncand[t];
   const int *ct = a.cand + (size_t)t * a.E;
@@ -331,7 +360,7 @@ __device__ void dec_select_big(const DecArgs &a, int t, const uint64_t *tab, flo
   dec_select_finish(a, t, my_e, my_sc, my_pos);
 }
 
-__device__ void dec_select(const DecArgs &a, int t, const uint64_t *tab, float *lds) {
+__device__ __forceinline__ void dec_select(const DecArgs &a, int t, const uint64_t *tab, float *lds) {
   const int nc = a.tid2eid ? 0 : a.ncand[t];
   if (nc <= 64) return dec_select_t<1>(a, t, tab);
   if (nc <= 128) return dec_select_t<2>(a, t, tab);
@@ -340,77 +369,85 @@ __device__ void dec_select(const DecArgs &a, int t, const uint64_t *tab, float *
 }
 
 // ------------------------------------------------------------ router ----
-// Blocks [0, ceil(E/4)): one wave per expert, for every token (the gate row
-// stays in registers; x is staged in LDS); the last of them derives the
-// candidates. Later blocks: FP8 activation quant, one wave per (token,
-// 128-group).
-__global__ __launch_bounds__(256) void k_dec_router(DecArgs a) {
-  extern __shared__ __align__(16) float xs[];  // H floats
-  __shared__ uint64_t s_tab[32];
-  __shared__ int s_flag;
+// Router logits of experts 4 b .. 4 b + 3 (one wave each, for every token;
+// the gate row stays in registers, x is staged in LDS): approximate choice
+// sqrt_softplus(z) + bias, sum|w*x| and z. The last of these blocks derives
+// the candidates and, in fast mode, the routing of every token whose
+// candidates are exactly its top-k.
+__device__ __forceinline__ void dec_router_block(const DecArgs &a, int b, float *xs, uint64_t *s_tab,
+                                 int *s_flag) {
   const int tid = threadIdx.x, wv = tid / 64, lane = tid % 64;
   const int H = a.H;
   const int nlog = (a.E + 3) / 4;
-  if ((int)blockIdx.x < nlog) {
-    const int e = __builtin_amdgcn_readfirstlane((int)blockIdx.x * 4 + wv);
-    const bool act = e < a.E;
-    // lane holds columns 8 lane + 512 i; an inactive wave reads zeros
-    const BufRsrc rg = buf_rsrc(a.gate + (size_t)(act ? e : 0) * H, act ? 2u * H : 0u);
-    uint4 w[16];
+  const int e = __builtin_amdgcn_readfirstlane(b * 4 + wv);
+  const bool act = e < a.E;
+  // lane holds columns 8 lane + 512 i; an inactive wave reads zeros
+  const BufRsrc rg = buf_rsrc(a.gate + (size_t)(act ? e : 0) * H, act ? 2u * H : 0u);
+  uint4 w[16];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) w[i] = buf_load16(rg, 16u * (lane + 64 * i));
-    libm_stage_table(s_tab);
-    for (int t = 0; t < a.n; ++t) {
-      __syncthreads();
-      const BufRsrc rx = buf_rsrc(a.x + (size_t)t * H, 4u * H);
-      uint4 xv4[8];  // H <= 8192
+  for (int i = 0; i < 16; ++i) w[i] = buf_load16(rg, 16u * (lane + 64 * i));
+  const uint64_t tabv = libm_table_load();
+  for (int t = 0; t < a.n; ++t) {
+    __syncthreads();
+    const BufRsrc rx = buf_rsrc(a.x + (size_t)t * H, 4u * H);
+    uint4 xv4[8];  // H <= 8192
 #pragma unroll
-      for (int j = 0; j < 8; ++j) xv4[j] = buf_load16(rx, 16u * (tid + 256 * j));
+    for (int j = 0; j < 8; ++j) xv4[j] = buf_load16(rx, 16u * (tid + 256 * j));
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-        if (4 * (tid + 256 * j) < H)
-          *reinterpret_cast<uint4 *>(xs + 4 * (tid + 256 * j)) = xv4[j];
-      __syncthreads();
-      float acc = 0.0f, aabs = 0.0f;
+    for (int j = 0; j < 8; ++j)
+      if (4 * (tid + 256 * j) < H) *reinterpret_cast<uint4 *>(xs + 4 * (tid + 256 * j)) = xv4[j];
+    if (t == 0) libm_table_store(s_tab, tabv);
+    __syncthreads();
+    float acc = 0.0f, aabs = 0.0f;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int c = 8 * lane + 512 * i;
-        if (c < H) {
-          const float4 xa = *reinterpret_cast<const float4 *>(xs + c);
-          const float4 xb = *reinterpret_cast<const float4 *>(xs + c + 4);
-          const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
-          const uint32_t wd[4] = {w[i].x, w[i].y, w[i].z, w[i].w};
+    for (int i = 0; i < 16; ++i) {
+      const int c = 8 * lane + 512 * i;
+      if (c < H) {
+        const float4 xa = *reinterpret_cast<const float4 *>(xs + c);
+        const float4 xb = *reinterpret_cast<const float4 *>(xs + c + 4);
+        const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+        const uint32_t wd[4] = {w[i].x, w[i].y, w[i].z, w[i].w};
 #pragma unroll
-          for (int d = 0; d < 4; ++d) {
-            const float p0 = u2f(wd[d] << 16) * xv[2 * d];
-            const float p1 = u2f(wd[d] & 0xFFFF0000u) * xv[2 * d + 1];
-            acc += p0;
-            acc += p1;
-            aabs += fabsf(p0);
-            aabs += fabsf(p1);
-          }
+        for (int d = 0; d < 4; ++d) {
+          const float p0 = u2f(wd[d] << 16) * xv[2 * d];
+          const float p1 = u2f(wd[d] & 0xFFFF0000u) * xv[2 * d + 1];
+          acc += p0;
+          acc += p1;
+          aabs += fabsf(p0);
+          aabs += fabsf(p1);
         }
       }
-      acc = wave_sum(acc);
-      aabs = wave_sum(aabs);
-      if (act && lane == 0) {
-        a.ch[(size_t)t * a.E + e] = sqrt_softplus(acc, s_tab) + (a.bias ? a.bias[e] : 0.0f);
-        a.zabs[(size_t)t * a.E + e] = aabs;
-      }
     }
-    if (!dec_arrive_last(&a.ctl[0], (unsigned)nlog, &s_flag)) return;
-    for (int t = wv; t < a.n; t += 4) {
-      const int nc = dec_candidates(a, t, a.cand + (size_t)t * a.E);
-      if (lane == 0) a.ncand[t] = nc;
+    acc = wave_sum(acc);
+    aabs = wave_sum(aabs);
+    if (act && lane == 0) {
+      const size_t o = (size_t)t * a.E + e;
+      a.ch[o] = sqrt_softplus(acc, s_tab) + (a.bias ? a.bias[e] : 0.0f);
+      a.zabs[o] = aabs;
+      a.za[o] = acc;
     }
-    if (tid == 0) a.ctl[0] = 0u;
-    return;
   }
-  const int b = blockIdx.x - nlog;
-  const int gpt = H / 128, gi = b * 4 + wv;
+  if (!dec_arrive_last(&a.ctl[0], (unsigned)nlog, s_flag)) return;
+  for (int t = wv; t < a.n; t += 4) {
+    const int nc = dec_candidates(a, t, a.cand + (size_t)t * a.E, s_tab);
+    if (lane == 0) a.ncand[t] = nc;
+    if (a.fast && a.tid2eid) {
+      // hash layer: its tid2eid row routes; weights from the parallel logits
+      // copied to zx by dec_candidates (this wave's writes)
+      __threadfence_block();
+      dec_select(a, t, s_tab, xs);
+    }
+  }
+  if (tid == 0) a.ctl[0] = 0u;
+}
+
+// quant_fp8_act (src/dsv4/dsv4_ops.c:96-121) of one 128-group per wave, for
+// the routed experts' gate/up tiles.
+__device__ __forceinline__ void dec_quant_block(const DecArgs &a, int b) {
+  const int wv = threadIdx.x / 64, lane = threadIdx.x % 64;
+  const int H = a.H, gpt = H / 128, gi = b * 4 + wv;
   if (gi >= a.n * gpt) return;
   const int t = gi / gpt, g = gi % gpt;
-  // quant_fp8_act (src/dsv4/dsv4_ops.c:96-121) of one 128-group
   const float *xr = a.x + (size_t)t * H + g * 128;
   const float v0 = xr[lane], v1 = xr[lane + 64];
   const float amax = wave_max(fmaxf(fabsf(v0), fabsf(v1)));
@@ -420,6 +457,57 @@ __global__ __launch_bounds__(256) void k_dec_router(DecArgs a) {
   q[lane] = (uint8_t)e4m3_code(quant_e4m3(v0, inv));
   q[lane + 64] = (uint8_t)e4m3_code(quant_e4m3(v1, inv));
   if (lane == 0) a.qxs[(size_t)t * gpt + g] = scale;
+}
+
+// Shared expert gate/up, rows [r0, r0 + 8) of both, from the quantised x
+// (E4M3 codes and per-128 scales, loaded ahead of the weights, decoded into
+// LDS padded to 132 per group): t = silu(bf16 gate) * bf16 up for the 8 rows
+// (src/dsv4/dsv4_model.c:6264-6268) into the shared slot of sv.
+__device__ __forceinline__ void dec_shared_gateup(const DecArgs &a, int t, int tile, float *lds,
+                                                  float *s_y, uint64_t *s_tab) {
+  const int tid = threadIdx.x;
+  const int H = a.H, I = a.I, r0 = tile * (FP8_TR / 2);
+  // the activation codes (at most 8192: 8 words per thread) and its
+  // per-128 scales ahead of the weights
+  const BufRsrc rq = buf_rsrc(a.qx8 + (size_t)t * H, (uint32_t)H);
+  const BufRsrc rqs = buf_rsrc(a.qxs + (size_t)t * (H / 128), (uint32_t)(H / 128) * 4u);
+  uint32_t xr[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) xr[j] = buf_load4(rq, 4u * (tid + 256 * j));
+  const float qsv = buf_loadf(rqs, 4u * tid);
+  __builtin_amdgcn_sched_barrier(0);  // issued before the weights
+  Fp8Regs R;
+  fp8_pair_load(R, a.sh[0], a.sh_s[0], a.sh[1], a.sh_s[1], H, I, r0);
+  const uint64_t tabv = libm_table_load();
+  float *xs = lds, *qs = lds + (H / 128) * 132;
+  float2 *ps = reinterpret_cast<float2 *>(qs + ((H / 128 + 3) & ~3));
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int i = 4 * (tid + 256 * j);
+    if (i < H) {
+      const float2 lo = fp8x2<false>(xr[j]), hi = fp8x2<true>(xr[j]);
+      *reinterpret_cast<float4 *>(xs + (i / 128) * 132 + (i % 128)) =
+          make_float4(lo.x, lo.y, hi.x, hi.y);
+    }
+  }
+  if (tid < H / 128) qs[tid] = qsv;
+  __syncthreads();
+  fp8_pair_finish(R, s_y, xs, qs, a.sh[0], a.sh_s[0], a.sh[1], a.sh_s[1], H, I, r0, ps);
+  libm_table_store(s_tab, tabv);
+  __syncthreads();
+  if (tid < FP8_TR / 2 && r0 + tid < I)
+    a.sv[((size_t)t * (a.maxc + 1) + a.maxc) * I + r0 + tid] =
+        swiglu_t(s_y[tid], s_y[tid + FP8_TR / 2], a.limit, s_tab);
+}
+
+// Blocks: [ceil(E/4) router logits][quant of x].
+__global__ __launch_bounds__(256) void k_dec_router(DecArgs a) {
+  extern __shared__ __align__(16) float lds[];  // H floats
+  __shared__ uint64_t s_tab[32];
+  __shared__ int s_flag;
+  const int nlog = (a.E + 3) / 4;
+  if ((int)blockIdx.x < nlog) return dec_router_block(a, blockIdx.x, lds, s_tab, &s_flag);
+  dec_quant_block(a, blockIdx.x - nlog);
 }
 
 // ------------------------------------------------------------ chains ----
@@ -473,11 +561,12 @@ __device__ __forceinline__ float chain_cols(const float4 *g, const float4 *x, fl
 // one shot, then lane 0 of wave 0 runs the reference's fmaf chain in column
 // order (dsv4_gemv_bf16, src/dsv4/dsv4_model.c:298-303) from LDS alone.
 // The last chain workgroup of the token selects the routes.
-__device__ void dec_chain_block(const DecArgs &a, int t, int c, float *lds, uint64_t *s_tab,
+__device__ __forceinline__ void dec_chain_block(const DecArgs &a, int t, int c, float *lds, uint64_t *s_tab,
                                 int *s_flag) {
   const int tid = threadIdx.x, wv = tid / 64, lane = tid % 64;
   const int H = a.H;
   const int nc = a.ncand[t];
+  if (a.fast && nc == a.K) return;  // routed by the router kernel already
   float *xs = lds, *gs = lds + H;  // H floats each
   const uint64_t tabv = libm_table_load();
   if (c < nc) {
@@ -530,7 +619,7 @@ __device__ void dec_chain_block(const DecArgs &a, int t, int c, float *lds, uint
 }
 
 // --------------------------------------------------------- gate / up ----
-// Blocks: [n*maxc chain workgroups][n*(I/8) shared FP8 pairs]
+// Blocks: [n*maxc chain workgroups][n*(I/8) shared FP8 gate/up pairs]
 // [maxc*n*gu_tiles routed FP4 pairs, candidate-major]; routed tiles of
 // candidate slots a token does not use exit at once.
 __global__ __launch_bounds__(256) void k_dec_gateup(DecArgs a) {
@@ -549,41 +638,7 @@ __global__ __launch_bounds__(256) void k_dec_gateup(DecArgs a) {
     return;
   }
   b -= nchain;
-  if (b < nshared) {
-    const int tile = b % t8, t = b / t8, r0 = tile * (FP8_TR / 2);
-    // the activation codes (at most 8192: 8 words per thread) and its
-    // per-128 scales ahead of the weights
-    const BufRsrc rq = buf_rsrc(a.qx8 + (size_t)t * H, (uint32_t)H);
-    const BufRsrc rqs = buf_rsrc(a.qxs + (size_t)t * (H / 128), (uint32_t)(H / 128) * 4u);
-    uint32_t xr[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) xr[j] = buf_load4(rq, 4u * (tid + 256 * j));
-    const float qsv = buf_loadf(rqs, 4u * tid);
-    __builtin_amdgcn_sched_barrier(0);  // issued before the weights
-    Fp8Regs R;
-    fp8_pair_load(R, a.sh[0], a.sh_s[0], a.sh[1], a.sh_s[1], H, I, r0);
-    const uint64_t tabv = libm_table_load();
-    float *xs = lds, *qs = lds + (H / 128) * 132;
-    float2 *ps = reinterpret_cast<float2 *>(qs + ((H / 128 + 3) & ~3));
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int i = 4 * (tid + 256 * j);
-      if (i < H) {
-        const float2 lo = fp8x2<false>(xr[j]), hi = fp8x2<true>(xr[j]);
-        *reinterpret_cast<float4 *>(xs + (i / 128) * 132 + (i % 128)) =
-            make_float4(lo.x, lo.y, hi.x, hi.y);
-      }
-    }
-    if (tid < H / 128) qs[tid] = qsv;
-    __syncthreads();
-    fp8_pair_finish(R, s_y, xs, qs, a.sh[0], a.sh_s[0], a.sh[1], a.sh_s[1], H, I, r0, ps);
-    libm_table_store(s_tab, tabv);
-    __syncthreads();
-    if (tid < FP8_TR / 2 && r0 + tid < I)
-      a.sv[((size_t)t * (a.maxc + 1) + a.maxc) * I + r0 + tid] =
-          swiglu_t(s_y[tid], s_y[tid + FP8_TR / 2], a.limit, s_tab);
-    return;
-  }
+  if (b < nshared) return dec_shared_gateup(a, b / t8, b % t8, lds, s_y, s_tab);
   b -= nshared;
   const int tile = b % a.gu_tiles;
   b /= a.gu_tiles;
@@ -592,12 +647,12 @@ __global__ __launch_bounds__(256) void k_dec_gateup(DecArgs a) {
   if (c >= min(nc, a.maxc)) return;
   const int e = a.cand[(size_t)t * a.E + c];
   if (e < 0 || e >= a.E) return;  // malformed tid2eid entry: the route contributes zeros
-  const Fp4Geom q = fp4_geom(H);
+  const Fp4Geom q = fp4_geom_np(H, DEC_NP);
   const int half = q.tr / 2, r0 = tile * half;
   const uint8_t *W0, *S0, *W1, *S1;
   expert_mat(a, e, 0, W0, S0);
   expert_mat(a, e, 1, W1, S1);
-  Fp4Regs R;
+  Fp4RegsT<DEC_NP> R;
   fp4_tile_x(R, a.qx8 + (size_t)t * H, a.qxs + (size_t)t * (H / 128), q);
   fp4_pair_load(R, W0, S0, W1, S1, H, I, r0, q);
   const uint64_t tabv = libm_table_load();
@@ -687,7 +742,7 @@ __device__ float dec_row_exact(const uint8_t *W, const uint8_t *S, const uint8_t
 // that had no candidate slot: one row per lane, few registers (this path
 // only runs on near-ties). Every workgroup of that route computes the same
 // values and reads back only its own writes (ordered by the barrier).
-__device__ void dec_fallback_t(const DecArgs &a, int t, int k, int e, uint64_t *tab) {
+__device__ __forceinline__ void dec_fallback_t(const DecArgs &a, int t, int k, int e, uint64_t *tab) {
   libm_stage_table(tab);
   __syncthreads();
   const uint8_t *W0, *S0, *W1, *S1;
@@ -704,7 +759,23 @@ __device__ void dec_fallback_t(const DecArgs &a, int t, int k, int e, uint64_t *
   __syncthreads();
 }
 
-// Blocks: [n*K*dn_tiles routed FP4 down tiles][n*(H/16) shared FP8 tiles].
+// Shared expert down, rows [16 tile, 16 tile + 16): its t (weight 1)
+// requantised into LDS, then the FP8 tile into route slot K of ro.
+__device__ __forceinline__ void dec_shared_down(const DecArgs &a, int t, int tile, float *lds) {
+  const int H = a.H, I = a.I, K = a.K;
+  const float *tv = a.sv + ((size_t)t * (a.maxc + 1) + a.maxc) * I;
+  TvRegs T;
+  dec_tv_load(T, tv, I);
+  Fp8Regs R;
+  fp8_tile_load(R, a.sh[2], a.sh_s[2], I, H, tile * FP8_TR);
+  float *xs = lds, *qys = lds + (I / 128) * 132;
+  float2 *ps = reinterpret_cast<float2 *>(qys + ((I / 128 + 3) & ~3));
+  dec_requant<false>(xs, qys, T, tv, 1.0f, I);
+  fp8_tile_finish(R, a.ro + ((size_t)t * (K + 1) + K) * H, xs, qys, a.sh[2], a.sh_s[2], I, H,
+                  tile * FP8_TR, 1, ps);
+}
+
+// Blocks: [n*K*dn_tiles routed FP4 down tiles][n*(H/16) shared FP8 down].
 __global__ __launch_bounds__(256) void k_dec_down(DecArgs a) {
   extern __shared__ __align__(16) float lds[];
   __shared__ uint64_t s_tab[32];
@@ -719,7 +790,7 @@ __global__ __launch_bounds__(256) void k_dec_down(DecArgs a) {
     const size_t o = (size_t)t * K + k;
     const int e = a.sel_e[o], pos = a.sel_pos[o];
     const float w = a.sel_w[o];
-    const Fp4Geom q = fp4_geom(I);
+    const Fp4Geom q = fp4_geom_np(I, DEC_NP);
     const int r0 = tile * q.tr;
     float *ro = a.ro + ((size_t)t * (K + 1) + k) * H;
     if (e < 0 || e >= a.E) {  // no expert: the route adds zeros
@@ -733,7 +804,7 @@ __global__ __launch_bounds__(256) void k_dec_down(DecArgs a) {
     expert_mat(a, e, 2, W, S);
     TvRegs T;
     dec_tv_load(T, tv, I);
-    Fp4Regs R;
+    Fp4RegsT<DEC_NP> R;
     fp4_tile_load(R, W, S, I, H, r0, q);
     // E4M3 codes and scales of y, read into registers before the pairs
     // overwrite them
@@ -746,17 +817,7 @@ __global__ __launch_bounds__(256) void k_dec_down(DecArgs a) {
   }
   b -= nrouted;
   const int t16 = (H + FP8_TR - 1) / FP8_TR;
-  const int tile = b % t16, t = b / t16;
-  const float *tv = a.sv + ((size_t)t * (a.maxc + 1) + a.maxc) * I;
-  TvRegs T;
-  dec_tv_load(T, tv, I);
-  Fp8Regs R;
-  fp8_tile_load(R, a.sh[2], a.sh_s[2], I, H, tile * FP8_TR);
-  float *xs = lds, *qys = lds + (I / 128) * 132;
-  float2 *ps = reinterpret_cast<float2 *>(qys + ((I / 128 + 3) & ~3));
-  dec_requant<false>(xs, qys, T, tv, 1.0f, I);
-  fp8_tile_finish(R, a.ro + ((size_t)t * (K + 1) + K) * H, xs, qys, a.sh[2], a.sh_s[2], I, H,
-                  tile * FP8_TR, 1, ps);
+  dec_shared_down(a, b / t16, b % t16, lds);
 }
 
 // out[t][i] = bf16(((0 + ro[t][0][i]) + ... + ro[t][K-1][i]) + ro[t][K][i]):
@@ -788,7 +849,7 @@ namespace {
 struct DecWs {
   unsigned *ctl;
   uint8_t *qx8;
-  float *qxs, *ch, *zabs, *zx, *sel_w, *sv, *fb, *ro;
+  float *qxs, *ch, *zabs, *za, *zx, *sel_w, *sv, *fb, *ro;
   int *cand, *ncand, *sel_e, *sel_pos;
   size_t bytes;
 };
@@ -816,6 +877,7 @@ DecWs dec_ws_layout(const DSV4GLayer *L, int n_tokens, void *base) {
   w.qxs = (float *)take(n * (H / 128) * 4);
   w.ch = (float *)take(n * E * 4);
   w.zabs = (float *)take(n * E * 4);
+  w.za = (float *)take(n * E * 4);
   w.cand = (int *)take(n * E * 4);
   w.ncand = (int *)take(n * 4);
   w.zx = (float *)take(n * E * 4);
@@ -829,22 +891,11 @@ DecWs dec_ws_layout(const DSV4GLayer *L, int n_tokens, void *base) {
   return w;
 }
 
-Fp4Geom host_fp4_geom(int in) {
-  Fp4Geom q;
-  q.G = in / 32;
-  q.gp = 1;
-  while (q.gp < q.G) q.gp <<= 1;
-  q.rpp = 256 / q.gp;
-  q.tr = FP4_LDS_ENTRIES / q.gp;
-  if (q.tr > 256) q.tr = 256;
-  return q;
-}
-
 size_t max_sz(size_t a, size_t b) { return a > b ? a : b; }
 
 int dec_launch(int phase, float *out, const float *x, const DSV4GLayer *L, const int *token_ids,
                int n_tokens, void *workspace, size_t workspace_bytes, int *idx_out,
-               float *wt_out, hipStream_t st) {
+               float *wt_out, hipStream_t st, int fast) {
   DSV4G_TRY(dsv4g_layer_ok(L, "moe_decode"));
   if (n_tokens <= 0) return dsv4g_fail(DSV4G_EINVAL, "moe_decode: n_tokens must be > 0");
   if (L->tid2eid && !token_ids)
@@ -877,6 +928,7 @@ int dec_launch(int phase, float *out, const float *x, const DSV4GLayer *L, const
   a.qxs = w.qxs;
   a.ch = w.ch;
   a.zabs = w.zabs;
+  a.za = w.za;
   a.cand = w.cand;
   a.ncand = w.ncand;
   a.zx = w.zx;
@@ -894,37 +946,40 @@ int dec_launch(int phase, float *out, const float *x, const DSV4GLayer *L, const
   a.E = L->n_experts;
   a.K = L->topk;
   a.maxc = dec_maxc(L);
-  const Fp4Geom qg = host_fp4_geom(a.H), qd = host_fp4_geom(a.I);
+  const Fp4Geom qg = fp4_geom_np(a.H, DEC_NP), qd = fp4_geom_np(a.I, DEC_NP);
   a.gu_tiles = (a.I + qg.tr / 2 - 1) / (qg.tr / 2);
   a.dn_tiles = (a.H + qd.tr - 1) / qd.tr;
   a.route_scale = L->route_scale;
   a.limit = (float)(int)L->swiglu_limit;  // the reference passes the limit as int
+  a.fast = fast;
   const int n = n_tokens, H = a.H, I = a.I;
   if (n > DEC_CTL_BYTES / 4 - 1)
     return dsv4g_fail(DSV4G_EINVAL, "moe_decode: at most %d tokens per call",
                       DEC_CTL_BYTES / 4 - 1);
+  const size_t lds_fp8_gu = (size_t)(H / 128) * 132 * 4 + (size_t)((H / 128 + 3) & ~3) * 4 +
+                            (size_t)FP8_TR * pair_stride(H / 128) * 8;
+  const size_t lds_fp8_dn = (size_t)(I / 128) * 132 * 4 + (size_t)((I / 128 + 3) & ~3) * 4 +
+                            (size_t)FP8_TR * pair_stride(I / 128) * 8;
   if (phase == 0) {
     const int blocks = (a.E + 3) / 4 + (n * (H / 128) + 3) / 4;
     hipLaunchKernelGGL(k_dec_router, dim3(blocks), dim3(256), (size_t)H * 4, st, a);
     return dsv4g_check_launch("dec_router");
   }
   if (phase == 1) {
-    const size_t lds = max_sz(max_sz((size_t)(FP4_LDS_ENTRIES + 2 * qg.tr) * 8 + 4096,
-                                     (size_t)H * 8),
-                              (size_t)(H / 128) * 132 * 4 + (size_t)((H / 128 + 3) & ~3) * 4 +
-                                  (size_t)FP8_TR * pair_stride(H / 128) * 8);
+    // routed pairs: the tile's pairs and scales; chains: x and a gate row
+    const size_t lds_fp4 = (size_t)qg.tr * pair_stride(qg.G) * 8 + 4096;
+    const size_t lds = max_sz(max_sz(lds_fp4, (size_t)H * 8), lds_fp8_gu);
     const long blocks = (long)n * a.maxc + (long)n * ((I + FP8_TR / 2 - 1) / (FP8_TR / 2)) +
                         (long)a.maxc * n * a.gu_tiles;
     hipLaunchKernelGGL(k_dec_gateup, dim3((unsigned)blocks), dim3(256), lds, st, a);
     return dsv4g_check_launch("dec_gateup");
   }
   if (phase == 2) {
-    const size_t lds_r = (size_t)(FP4_LDS_ENTRIES + 2 * qd.tr) * 8 + 4096;
-    const size_t lds_s = (size_t)(I / 128) * 132 * 4 + (size_t)((I / 128 + 3) & ~3) * 4 +
-                         (size_t)FP8_TR * pair_stride(I / 128) * 8;
+    const size_t lds = max_sz(max_sz((size_t)qd.tr * pair_stride(qd.G) * 8 + 4096,
+                                     (size_t)I + (size_t)I / 32 + 64),
+                              lds_fp8_dn);
     const long blocks = (long)n * a.K * a.dn_tiles + (long)n * ((H + FP8_TR - 1) / FP8_TR);
-    hipLaunchKernelGGL(k_dec_down, dim3((unsigned)blocks), dim3(256), max_sz(lds_r, lds_s), st,
-                       a);
+    hipLaunchKernelGGL(k_dec_down, dim3((unsigned)blocks), dim3(256), lds, st, a);
     return dsv4g_check_launch("dec_down");
   }
   if (phase == 3) {
@@ -954,8 +1009,9 @@ int dsv4g_moe_workspace_init(void *workspace, size_t workspace_bytes, void *stre
 int dsv4g_moe_decode_phase(int phase, float *out, const float *x, const DSV4GLayer *L,
                            const int *token_ids, int n_tokens, void *workspace,
                            size_t workspace_bytes, void *stream) {
-  return dec_launch(phase, out, x, L, token_ids, n_tokens, workspace, workspace_bytes, nullptr,
-                    nullptr, (hipStream_t)stream);
+  const int fast = (phase & DSV4G_DECODE_FAST) != 0;
+  return dec_launch(phase & ~DSV4G_DECODE_FAST, out, x, L, token_ids, n_tokens, workspace,
+                    workspace_bytes, nullptr, nullptr, (hipStream_t)stream, fast);
 }
 
 int dsv4g_moe_decode_routing(int *idx_out, float *wt_out, const DSV4GLayer *L, int n_tokens,
@@ -976,7 +1032,16 @@ int dsv4g_moe_forward(float *out, const float *x, const DSV4GLayer *L, const int
                       float *wt_out, void *stream) {
   for (int phase = 0; phase < 4; ++phase)
     DSV4G_TRY(dec_launch(phase, out, x, L, token_ids, n_tokens, workspace, workspace_bytes,
-                         idx_out, wt_out, (hipStream_t)stream));
+                         idx_out, wt_out, (hipStream_t)stream, 0));
+  return 0;
+}
+
+int dsv4g_moe_forward_fast(float *out, const float *x, const DSV4GLayer *L,
+                           const int *token_ids, int n_tokens, void *workspace,
+                           size_t workspace_bytes, int *idx_out, float *wt_out, void *stream) {
+  for (int phase = 0; phase < 4; ++phase)
+    DSV4G_TRY(dec_launch(phase, out, x, L, token_ids, n_tokens, workspace, workspace_bytes,
+                         idx_out, wt_out, (hipStream_t)stream, 1));
   return 0;
 }
 

@@ -26,7 +26,7 @@ struct Fp4Geom {
   int G, gp, rpp, tr;
 };
 
-__device__ __forceinline__ Fp4Geom fp4_geom(int in) {
+__device__ __host__ __forceinline__ Fp4Geom fp4_geom(int in) {
   Fp4Geom q;
   q.G = in / 32;
   q.gp = 1;
@@ -34,6 +34,14 @@ __device__ __forceinline__ Fp4Geom fp4_geom(int in) {
   q.rpp = 256 / q.gp;
   q.tr = FP4_LDS_ENTRIES / q.gp;
   if (q.tr > 256) q.tr = 256;
+  return q;
+}
+
+// The same with at most np passes per tile (np even: a paired tile holds
+// np / 2 passes of each matrix), for tiles held in Fp4RegsT<np>.
+__device__ __host__ __forceinline__ Fp4Geom fp4_geom_np(int in, int np) {
+  Fp4Geom q = fp4_geom(in);
+  if (q.tr > np * q.rpp) q.tr = np * q.rpp;
   return q;
 }
 

@@ -52,6 +52,7 @@ _SIGS = {
                             _vp],
     "dsv4g_swiglu_quant": [_vp, _vp, _vp, _vp, _I, _I, _I, _F, _vp],
     "dsv4g_moe_forward": [_vp, _vp, C.POINTER(DSV4GLayer), _vp, _I, _vp, _Z, _vp, _vp, _vp],
+    "dsv4g_moe_forward_fast": [_vp, _vp, C.POINTER(DSV4GLayer), _vp, _I, _vp, _Z, _vp, _vp, _vp],
     "dsv4g_moe_decode_phase": [_I, _vp, _vp, C.POINTER(DSV4GLayer), _vp, _I, _vp, _Z, _vp],
     "dsv4g_moe_decode_routing": [_vp, _vp, C.POINTER(DSV4GLayer), _I, _vp, _vp],
     "dsv4g_moe_workspace_init": [_vp, _Z, _vp],
@@ -228,7 +229,7 @@ class GpuLib:
     def moe_workspace_bytes(self, layer, n_tokens):
         return int(self.lib.dsv4g_moe_workspace_bytes(C.byref(layer.struct), n_tokens))
 
-    def moe_forward(self, layer, x, token_ids=None, workspace=None, out=None):
+    def moe_forward(self, layer, x, token_ids=None, workspace=None, out=None, fast=False):
         import torch
         n = x.shape[0]
         L = layer.struct
@@ -238,18 +239,20 @@ class GpuLib:
         out = torch.empty_like(x) if out is None else out
         idx = torch.empty(n, L.topk, dtype=torch.int32, device=x.device)
         wt = torch.empty(n, L.topk, dtype=torch.float32, device=x.device)
-        self._call("dsv4g_moe_forward", _ptr(out), _ptr(x), C.byref(L), _ptr(token_ids), n,
-                   _ptr(workspace), workspace.numel(), _ptr(idx), _ptr(wt), self._stream())
+        self._call("dsv4g_moe_forward_fast" if fast else "dsv4g_moe_forward", _ptr(out), _ptr(x),
+                   C.byref(L), _ptr(token_ids), n, _ptr(workspace), workspace.numel(), _ptr(idx),
+                   _ptr(wt), self._stream())
         return out, idx, wt
 
     def moe_workspace_init(self, workspace):
         """Zero a decode workspace, once, before its first dsv4g_moe_forward."""
         self._call("dsv4g_moe_workspace_init", _ptr(workspace), workspace.numel(), self._stream())
 
-    def moe_forward_into(self, layer, x, out, workspace, token_ids=None):
-        """dsv4g_moe_forward into out with a prepared workspace, routing not
-        copied out: the form a captured decode loop uses."""
-        self._call("dsv4g_moe_forward", _ptr(out), _ptr(x), C.byref(layer.struct),
+    def moe_forward_into(self, layer, x, out, workspace, token_ids=None, fast=False):
+        """dsv4g_moe_forward(_fast) into out with a prepared workspace, routing
+        not copied out: the form a captured decode loop uses."""
+        self._call("dsv4g_moe_forward_fast" if fast else "dsv4g_moe_forward", _ptr(out), _ptr(x),
+                   C.byref(layer.struct),
                    _ptr(token_ids), x.shape[0], _ptr(workspace), workspace.numel(), None, None,
                    self._stream())
 

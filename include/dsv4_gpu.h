@@ -156,13 +156,26 @@ int dsv4g_moe_workspace_init(void *workspace, size_t workspace_bytes, void *stre
 int dsv4g_moe_forward(float *out, const float *x, const DSV4GLayer *L, const int *token_ids,
                       int n_tokens, void *workspace, size_t workspace_bytes, int *idx_out,
                       float *wt_out, void *stream);
+/* The same layer with the tolerance of the north-star contract instead of
+ * bit-exactness: top-k indices identical to the reference's always; when a
+ * token's candidate experts are exactly its top-k (the rigorous bound of the
+ * parallel router logits separates the k-th from the (k+1)-th), the route
+ * weights come from the parallel logits (within a few fp32 ulps of the
+ * reference's) and the exact sequential chains are skipped; otherwise the
+ * token is routed exactly as by dsv4g_moe_forward. Expert outputs agree to
+ * fp32 rounding, so a BF16 output element may differ by one BF16 ulp. No
+ * counterpart in the reference: for decode loops that accept that tolerance. */
+int dsv4g_moe_forward_fast(float *out, const float *x, const DSV4GLayer *L,
+                           const int *token_ids, int n_tokens, void *workspace,
+                           size_t workspace_bytes, int *idx_out, float *wt_out, void *stream);
 /* The same layer as four ordered phases, for callers that interleave or
  * time them: 0 router logits, candidate experts and activation quant; 1
  * gate/up GEMVs of the candidates and the shared expert, with the exact
  * router chains of the candidates and the exact top-k beside them; 2 SwiGLU
- * requant and down GEMVs; 3 the ordered combine.
- * dsv4g_moe_decode_routing copies the routing of the last call.
- * x and out: 16-byte aligned. */
+ * requant and down GEMVs; 3 the ordered combine. phase | DSV4G_DECODE_FAST runs the phases of
+ * dsv4g_moe_forward_fast. dsv4g_moe_decode_routing copies the routing of
+ * the last call. x and out: 16-byte aligned. */
+#define DSV4G_DECODE_FAST 256
 int dsv4g_moe_decode_phase(int phase, float *out, const float *x, const DSV4GLayer *L,
                            const int *token_ids, int n_tokens, void *workspace,
                            size_t workspace_bytes, void *stream);

@@ -272,17 +272,19 @@ def tie_layer(orc, n_experts, winners, hidden=4096):
     return L
 
 
+@pytest.mark.parametrize("fast", [False, True])
 @pytest.mark.parametrize("winners", [[], [26, 27, 28, 29, 30, 31], [2, 20, 5, 30, 17, 9]])
-def test_moe_forward_ties_and_overflow_candidates(env, winners):
+def test_moe_forward_ties_and_overflow_candidates(env, winners, fast):
     """More candidates than gate/up slots (32 experts, 16 slots): with a
     constant gate the lowest ids win; with winners beyond the slots the down
-    kernel computes their gate/up itself. Bit-exact either way."""
+    kernel computes their gate/up itself. Bit-exact either way, in fast mode
+    too (more candidates than routes: the exact chains decide)."""
     orc, lib, dg = env["orc"], env["lib"], env["dsv4_gpu"]
     L = tie_layer(orc, 32, winners)
     DL = dg.DeviceLayer.from_host(L, env["dev"])
     X = bf16_input(np.random.default_rng(23), (2, 4096))
     X[:, 7] = 1.0
-    out, idx, wt = lib.moe_forward(DL, T(env, X))
+    out, idx, wt = lib.moe_forward(DL, T(env, X), fast=fast)
     out, idx, wt = H(out), H(idx), H(wt)
     for t in range(2):
         o, i, w = orc.moe_forward(L, X[t])
@@ -375,3 +377,40 @@ def test_moe_forward_odd_widths_bit_exact(env, hidden, experts):
         assert np.array_equal(idx[t], i), t
         assert same_bits(wt[t], w), t
         assert same_bits(out[t], o), (t, max_rel_err(out[t], o))
+
+
+def bf16_ulp(v):
+    """Spacing of BF16 values at |v| (normal range)."""
+    e = np.floor(np.log2(np.maximum(np.abs(v), 2.0 ** -126)))
+    return np.ldexp(1.0, (e - 7).astype(int))
+
+
+@pytest.mark.parametrize("shape,kw", [((4096, 128, 256), dict()),
+                                      ((4096, 128, 256), dict(bias=True)),
+                                      ((4096, 128, 256), dict(hash_vocab=11)),
+                                      ((4096, 2048, 16), dict(bias=True))])
+def test_moe_forward_fast_tolerance(env, shape, kw):
+    """dsv4g_moe_forward_fast: top-k indices identical to the oracle; route
+    weights from the parallel logits within 1e-5 relative; outputs within
+    1e-3 norm-wise and, elementwise, one BF16 ulp plus 1e-3 of the largest
+    element (the rounding of the final BF16 output may flip)."""
+    orc, lib, dg = env["orc"], env["lib"], env["dsv4_gpu"]
+    hidden, inter, experts = shape
+    L = make_layer(orc, hidden, inter, experts, 6, seed=8, **kw)
+    DL = dg.DeviceLayer.from_host(L, env["dev"])
+    X = bf16_input(np.random.default_rng(13), (5, hidden))
+    tok = (np.arange(5, dtype=np.int32) * 3) % 11
+    out, idx, wt = lib.moe_forward(DL, T(env, X), T(env, tok), fast=True)
+    out, idx, wt = H(out), H(idx), H(wt)
+    worst = 0.0
+    for t in range(5):
+        o, i, w = orc.moe_forward(L, X[t], int(tok[t]))
+        assert np.array_equal(idx[t], i), t
+        assert np.max(np.abs(wt[t] - w) / np.maximum(np.abs(w), 1e-30)) <= 1e-5, t
+        d = out[t].astype(np.float64) - o
+        r = float(np.linalg.norm(d) / max(np.linalg.norm(o), 1e-30))
+        worst = max(worst, r)
+        assert r <= 1e-3, (t, r)
+        bound = bf16_ulp(o) + 1e-3 * np.max(np.abs(o))
+        assert np.all(np.abs(d) <= bound), (t, float(np.max(np.abs(d) / bound)))
+    print(f"\n  fast decode: max norm-relative error {worst:.2e}")
