@@ -524,9 +524,28 @@ struct GroupedArgs {
   const uint16_t *xb;  // [T][H] BF16 activations (dequantised FP8)
   uint16_t *yb;        // [P][I] BF16 intermediate (dequantised FP8)
   uint16_t *ro;        // [T][K+1][H] BF16 bits
+  uint32_t xb_bytes, yb_bytes;
   int H, I, E, K, T, row_tiles;
   float limit;
 };
+
+// (token tile, row tile) of this workgroup. Workgroups go to the 8 XCDs
+// round-robin by index and each XCD has its own L2: when the row tiles split
+// evenly, XCD x takes row tiles [x RT/8, (x+1) RT/8) for every token tile,
+// token tile by token tile, so a row tile's weights are read into that L2
+// once and reused by every token tile, and a token tile's activations by
+// the XCD's row tiles. Otherwise row tiles vary fastest.
+__device__ __forceinline__ void tile_coords(int rt_n, int &tt, int &rt) {
+  const int b = blockIdx.x, nb = gridDim.x;
+  if (rt_n % 8 == 0 && nb % 8 == 0) {
+    const int per = rt_n / 8, k = b / 8;
+    tt = k / per;
+    rt = (b % 8) * per + k % per;
+  } else {
+    tt = b / rt_n;
+    rt = b % rt_n;
+  }
+}
 
 __device__ __forceinline__ int tile_expert(const int *tile_off, int E, int tt) {
   int lo = 0, hi = E + 1;
@@ -540,71 +559,9 @@ __device__ __forceinline__ int tile_expert(const int *tile_off, int E, int tt) {
 
 __device__ __forceinline__ uint32_t bf2_bits(bf16x2_t v) { return __builtin_bit_cast(uint32_t, v); }
 
-// A operand of one 16-row fragment over super-window sw: the 32 weights of
-// lane group g, converted to BF16 times their block scale, as four 8-element
-// MFMA operands. A NaN scale (E8M0 255) zeroes the block, as the reference
-// skips it.
-template <int AFMT>
-__device__ __forceinline__ void load_a_bf16(uint4 (&op)[4], const uint8_t *W, const uint8_t *S,
-                                            int row, int in, int sw, int l) {
-  const int g = l / 16;
-  uint32_t code;
-  uint4 r0, r1 = make_uint4(0, 0, 0, 0);
-  if (AFMT == MX_FP4) {
-    r0 = *reinterpret_cast<const uint4 *>(W + (size_t)row * (in / 2) + sw * 64 + g * 16);
-    code = S[(size_t)row * (in / 32) + sw * 4 + g];
-  } else {
-    const uint8_t *p = W + (size_t)row * in + sw * 128 + g * 32;
-    r0 = *reinterpret_cast<const uint4 *>(p);
-    r1 = *reinterpret_cast<const uint4 *>(p + 16);
-    code = S[(size_t)(row / 128) * (in / 128) + sw];
-  }
-  if (code == 255u) {
-    for (int q = 0; q < 4; ++q) op[q] = make_uint4(0, 0, 0, 0);
-    return;
-  }
-  const float s = e8m0(code);
-  if (AFMT == MX_FP4) {
-    const uint32_t d[4] = {r0.x, r0.y, r0.z, r0.w};
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      op[q].x = bf2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d[q], s, 0));
-      op[q].y = bf2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d[q], s, 1));
-      op[q].z = bf2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d[q], s, 2));
-      op[q].w = bf2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d[q], s, 3));
-    }
-  } else {
-    const uint32_t d[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      op[q].x = bf2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d[2 * q], s, false));
-      op[q].y = bf2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d[2 * q], s, true));
-      op[q].z = bf2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d[2 * q + 1], s, false));
-      op[q].w = bf2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d[2 * q + 1], s, true));
-    }
-  }
-}
-
 __device__ __forceinline__ v4f mfma_bf16(uint4 a, uint4 b, v4f c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
                                                  __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-}
-
-// Stage 64 BF16 activation rows (super-window sw, 256 bytes each) into LDS.
-__device__ __forceinline__ void stage_b16(uint8_t *bt, const uint16_t *src, const int *rows,
-                                          int in, int sw) {
-  const int tid = threadIdx.x, j = tid >> 2, q = tid & 3;
-  uint4 u[4] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0),
-                make_uint4(0, 0, 0, 0)};
-  const int r = rows[j];
-  if (r >= 0) {
-    const uint4 *p = reinterpret_cast<const uint4 *>(src + (size_t)r * in + sw * 128 + q * 32);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) u[i] = p[i];
-  }
-  uint4 *d = reinterpret_cast<uint4 *>(bt + j * GT_BROW2 + q * 64);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) d[i] = u[i];
 }
 
 __device__ __forceinline__ void load_b_ops(uint4 (&op)[4], const uint8_t *bt, int j, int l) {
@@ -613,12 +570,188 @@ __device__ __forceinline__ void load_b_ops(uint4 (&op)[4], const uint8_t *bt, in
   for (int q = 0; q < 4; ++q) op[q] = p[q];
 }
 
+// ---- software-pipelined K loop. Per 128-K window a wave needs, for each of
+// its NM x 2 weight fragments (NM matrices, two 16-row fragments), the lane's
+// 16 (FP4) or 32 (FP8) weight bytes and one scale code, and each thread
+// stages 64 bytes of one activation row into LDS. Those raw operands are
+// buffer-loaded GT_DEPTH windows ahead, window by window in consumption
+// order (loads complete in order, so a window's wait never waits on a later
+// window); the activation tile is double-buffered in LDS, one barrier per
+// window. A operands are converted one MFMA step (q) at a time to keep
+// registers for the ring. Windows run in chunks of GT_CHUNK, fully unrolled
+// (a loop-carried prefetch would be drained at every iteration); windows
+// past the end read zeros and skip their MFMAs.
+#define GT_CHUNK 12
+#define GT_DEPTH 3
+#define GT_BT_BYTES (GT_TN * GT_BROW2)
+#define GT_BAD 0x80000000u  // an offset past every range (and its +48)
+
+template <int AFMT, int NM>
+struct WinRaw {
+  uint4 a0[NM][2], a1[NM][2];  // a1: the second 16 bytes of an FP8 fragment
+  uint32_t code[NM][2];
+  uint4 b[4];
+};
+
+// W[m], S[m]: buffers of matrix m and its scales; in: K width; rbase: the
+// wave's first row; brow: this thread's activation row (-1: none); bsrc:
+// buffer over the activation matrix (row stride in BF16 elements). The loads
+// of a window come in four parts (matrix 0, matrix 1, two halves of the
+// activation row), issued between MFMA steps so that the vector memory path
+// works while the matrix cores do; every part of a window is issued before
+// any part of the next (waits are in-order).
+template <int AFMT, int NM>
+__device__ __forceinline__ void win_load_part(WinRaw<AFMT, NM> &R, int part,
+                                              const BufRsrc (&W)[NM], const BufRsrc (&S)[NM],
+                                              BufRsrc bsrc, int in, int rbase, int brow, int sw,
+                                              int nsw) {
+  const int l = threadIdx.x % 64, g = l / 16, q = threadIdx.x & 3;
+  const bool ok = sw < nsw;
+  if (part < 2) {
+    const int m = part;
+    if (m < NM) {
+#pragma unroll
+      for (int f = 0; f < 2; ++f) {
+        const uint32_t row = (uint32_t)(rbase + 16 * f + l % 16);
+        if (AFMT == MX_FP4) {
+          R.a0[m][f] = buf_load16(W[m], ok ? row * (uint32_t)(in / 2) + sw * 64u + g * 16u : GT_BAD);
+          R.code[m][f] = __builtin_amdgcn_raw_buffer_load_b8(
+              S[m], ok ? row * (uint32_t)(in / 32) + sw * 4u + g : GT_BAD, 0, 0);
+        } else {
+          const uint32_t o = ok ? row * (uint32_t)in + sw * 128u + g * 32u : GT_BAD;
+          R.a0[m][f] = buf_load16(W[m], o);
+          R.a1[m][f] = buf_load16(W[m], o + 16u);
+          R.code[m][f] = __builtin_amdgcn_raw_buffer_load_b8(
+              S[m], ok ? (row / 128u) * (uint32_t)(in / 128) + sw : GT_BAD, 0, 0);
+        }
+      }
+    }
+  } else {
+    const uint32_t bo =
+        (ok && brow >= 0) ? 2u * ((uint32_t)brow * (uint32_t)in + sw * 128u + q * 32u) : GT_BAD;
+    const int i0 = (part - 2) * 2;
+    R.b[i0] = buf_load16(bsrc, bo + 16u * i0);
+    R.b[i0 + 1] = buf_load16(bsrc, bo + 16u * (i0 + 1));
+  }
+  __builtin_amdgcn_sched_barrier(0);  // keep the parts in order
+}
+
+template <int AFMT, int NM>
+__device__ __forceinline__ void win_load(WinRaw<AFMT, NM> &R, const BufRsrc (&W)[NM],
+                                         const BufRsrc (&S)[NM], BufRsrc bsrc, int in, int rbase,
+                                         int brow, int sw, int nsw) {
+#pragma unroll
+  for (int part = 0; part < 4; ++part)
+    win_load_part<AFMT, NM>(R, part, W, S, bsrc, in, rbase, brow, sw, nsw);
+}
+
+// MFMA step q's A operand (8 K values) from the raw bytes: BF16 weight times
+// its block scale (exact); a NaN scale zeroes the block, as the reference
+// skips it (zero bytes at scale 1, selected without a branch).
 template <int AFMT>
-__device__ void gateup_tile(const GroupedArgs &a, int e, int rt, int p0, int np, uint8_t *bt,
-                            int *rows_s, float *wt_s, float (*amax_s)[GT_TN]) {
+__device__ __forceinline__ uint4 win_op(uint4 r0, uint4 r1, uint32_t code, int q) {
+  const bool nan = code == 255u;
+  const float s = nan ? 1.0f : e8m0(code);
+  uint4 o;
+  if (AFMT == MX_FP4) {
+    const uint32_t d = nan ? 0u : (q == 0 ? r0.x : q == 1 ? r0.y : q == 2 ? r0.z : r0.w);
+    o.x = bf2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, s, 0));
+    o.y = bf2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, s, 1));
+    o.z = bf2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, s, 2));
+    o.w = bf2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, s, 3));
+  } else {
+    const uint32_t d0 = nan ? 0u : (q == 0 ? r0.x : q == 1 ? r0.z : q == 2 ? r1.x : r1.z);
+    const uint32_t d1 = nan ? 0u : (q == 0 ? r0.y : q == 1 ? r0.w : q == 2 ? r1.y : r1.w);
+    o.x = bf2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d0, s, false));
+    o.y = bf2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d0, s, true));
+    o.z = bf2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d1, s, false));
+    o.w = bf2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d1, s, true));
+  }
+  return o;
+}
+
+// The K loop of one tile: acc[m][f][c] += A_m rows (rbase + 16 f ..) x the
+// staged activation rows of fragment c < nf. brow: this thread's activation
+// row; the caller has published rows before (barrier).
+template <int AFMT, int NM>
+__device__ __forceinline__ void gemm_k_loop(v4f (&acc)[NM][2][4], const BufRsrc (&W)[NM],
+                                            const BufRsrc (&S)[NM], BufRsrc bsrc, int in,
+                                            int rbase, int brow, int nf, uint8_t *bt) {
+  const int tid = threadIdx.x, l = tid % 64;
+  const int nsw = in / 128;
+  for (int c0 = 0; c0 < nsw; c0 += GT_CHUNK) {
+    WinRaw<AFMT, NM> R[GT_DEPTH];
+#pragma unroll
+    for (int d = 0; d < GT_DEPTH; ++d)
+      win_load<AFMT, NM>(R[d], W, S, bsrc, in, rbase, brow, c0 + d, nsw);
+#pragma unroll
+    for (int i = 0; i < GT_CHUNK; ++i) {
+      const int sw = c0 + i;
+      WinRaw<AFMT, NM> &Rc = R[i % GT_DEPTH];
+      uint8_t *bb = bt + (sw & 1) * GT_BT_BYTES;
+      {
+        uint4 *d = reinterpret_cast<uint4 *>(bb + (tid >> 2) * GT_BROW2 + (tid & 3) * 64);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) d[k] = Rc.b[k];
+      }
+      // this window's A bytes, kept while the ring slot is refilled
+      uint4 A0[NM][2], A1[NM][2];
+      uint32_t Ac[NM][2];
+#pragma unroll
+      for (int m = 0; m < NM; ++m)
+#pragma unroll
+        for (int f = 0; f < 2; ++f) {
+          A0[m][f] = Rc.a0[m][f];
+          A1[m][f] = Rc.a1[m][f];
+          Ac[m][f] = Rc.code[m][f];
+        }
+      const bool pre = i + GT_DEPTH < GT_CHUNK;  // refill this ring slot, window sw + DEPTH
+      __syncthreads();
+      if (sw >= nsw && pre) win_load<AFMT, NM>(Rc, W, S, bsrc, in, rbase, brow, sw + GT_DEPTH, nsw);
+      if (sw < nsw) {
+        // every fragment, whatever nf: rows past the tile are staged as
+        // zeros, and branches here would serialise the LDS reads. The
+        // activation operands of step q + 1 are read during step q's MFMAs.
+        const uint8_t *brow_p = bb + (l % 16) * GT_BROW2 + (l / 16) * 64;
+        uint4 Bq[2][4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          Bq[0][c] = *reinterpret_cast<const uint4 *>(brow_p + 16 * c * GT_BROW2);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          if (pre) win_load_part<AFMT, NM>(Rc, q, W, S, bsrc, in, rbase, brow, sw + GT_DEPTH, nsw);
+          if (q + 1 < 4) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+              Bq[(q + 1) & 1][c] =
+                  *reinterpret_cast<const uint4 *>(brow_p + 16 * c * GT_BROW2 + 16 * (q + 1));
+          }
+          uint4 A[NM][2];
+#pragma unroll
+          for (int m = 0; m < NM; ++m)
+#pragma unroll
+            for (int f = 0; f < 2; ++f) A[m][f] = win_op<AFMT>(A0[m][f], A1[m][f], Ac[m][f], q);
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int m = 0; m < NM; ++m)
+#pragma unroll
+              for (int f = 0; f < 2; ++f)
+                acc[m][f][c] = mfma_bf16(A[m][f], Bq[q & 1][c], acc[m][f][c]);
+        }
+      }
+    }
+  }
+}
+
+template <int AFMT>
+__device__ __forceinline__ void gateup_tile(const GroupedArgs &a, int e, int rt, int p0, int np,
+                                            uint8_t *bt, int *rows_s, float *wt_s,
+                                            float (*amax_s)[GT_TN]) {
   const int tid = threadIdx.x, wv = tid / 64, l = tid % 64;
-  const int H = a.H, I = a.I, nsw = H / 128;
+  const int H = a.H, I = a.I;
   const uint8_t *Wg, *Wu, *Sg, *Su;
+  uint32_t wbytes, sbytes;
   if (AFMT == MX_FP4) {
     const uint8_t *sc = a.experts + (size_t)e * a.expert_stride;
     const uint8_t *wt = sc + a.scale_run;
@@ -628,57 +761,44 @@ __device__ void gateup_tile(const GroupedArgs &a, int e, int rt, int p0, int np,
     Wu = wt + w1 + w2;
     Sg = sc;
     Su = sc + s1 + s2;
+    wbytes = (uint32_t)w1;
+    sbytes = (uint32_t)s1;
   } else {
     Wg = a.shw[0];
     Wu = a.shw[1];
     Sg = a.shs[0];
     Su = a.shs[1];
+    wbytes = (uint32_t)I * (uint32_t)H;
+    sbytes = (uint32_t)((I + 127) / 128) * (uint32_t)(H / 128);
   }
   if (tid < GT_TN) {
     rows_s[tid] = tid < np ? a.pos_token[p0 + tid] : -1;
     wt_s[tid] = tid < np ? a.pos_wt[p0 + tid] : 0.0f;
   }
+  __syncthreads();
   const int nf = (np + 15) / 16;  // active token fragments (block-uniform)
-  v4f ag[2][4], au[2][4];
-  for (int f = 0; f < 2; ++f)
-    for (int c = 0; c < 4; ++c) {
-      ag[f][c] = (v4f){0.f, 0.f, 0.f, 0.f};
-      au[f][c] = ag[f][c];
-    }
+  v4f acc[2][2][4];
+  for (int m = 0; m < 2; ++m)
+    for (int f = 0; f < 2; ++f)
+      for (int c = 0; c < 4; ++c) acc[m][f][c] = (v4f){0.f, 0.f, 0.f, 0.f};
   const int rbase = rt * GT_TM + 32 * wv;
-  for (int sw = 0; sw < nsw; ++sw) {
-    __syncthreads();
-    stage_b16(bt, a.xb, rows_s, H, sw);
-    uint4 Ag[2][4], Au[2][4];
-    for (int f = 0; f < 2; ++f) {
-      const int row = rbase + 16 * f + l % 16;
-      load_a_bf16<AFMT>(Ag[f], Wg, Sg, row, H, sw, l);
-      load_a_bf16<AFMT>(Au[f], Wu, Su, row, H, sw, l);
-    }
-    __syncthreads();
-    for (int c = 0; c < 4; ++c) {
-      if (c >= nf) break;
-      uint4 B[4];
-      load_b_ops(B, bt, 16 * c + l % 16, l);
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        for (int f = 0; f < 2; ++f) {
-          ag[f][c] = mfma_bf16(Ag[f][q], B[q], ag[f][c]);
-          au[f][c] = mfma_bf16(Au[f][q], B[q], au[f][c]);
-        }
-    }
-  }
+  const BufRsrc W[2] = {buf_rsrc(Wg, wbytes), buf_rsrc(Wu, wbytes)};
+  const BufRsrc S[2] = {buf_rsrc(Sg, sbytes), buf_rsrc(Su, sbytes)};
+  gemm_k_loop<AFMT, 2>(acc, W, S, buf_rsrc(a.xb, a.xb_bytes), H, rbase, rows_s[tid >> 2], nf, bt);
   // epilogue: y = bf16((silu(bf16(g)) * bf16(u)) * w), per-128 requant,
   // stored as the exact BF16 of the dequantised FP8 value
   float y[2][4][4];
+#pragma unroll
   for (int c = 0; c < 4; ++c) {
     const int j = 16 * c + l % 16;
     float m = 0.0f;
+#pragma unroll
     for (int f = 0; f < 2; ++f)
+#pragma unroll
       for (int v = 0; v < 4; ++v) {
         float yy = 0.0f;
         if (c < nf) {
-          const float g = bf16_round(ag[f][c][v]), u = bf16_round(au[f][c][v]);
+          const float g = bf16_round(acc[0][f][c][v]), u = bf16_round(acc[1][f][c][v]);
           yy = bf16_round(swiglu_t(g, u, a.limit) * wt_s[j]);
         }
         y[f][c][v] = yy;
@@ -689,15 +809,18 @@ __device__ void gateup_tile(const GroupedArgs &a, int e, int rt, int p0, int np,
     if (l < 16) amax_s[wv][j] = m;
   }
   __syncthreads();
-  for (int c = 0; c < nf; ++c) {
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
     const int j = 16 * c + l % 16;
-    if (j >= np) continue;
+    if (c >= nf || j >= np) continue;
     const float am = fmaxf(fmaxf(amax_s[0][j], amax_s[1][j]), fmaxf(amax_s[2][j], amax_s[3][j]));
     const float scale = act_scale(am);
     const float inv = 1.0f / scale;
     const int pos = p0 + j;
+#pragma unroll
     for (int f = 0; f < 2; ++f) {
       uint32_t h[4];
+#pragma unroll
       for (int v = 0; v < 4; ++v) h[v] = f2u(quant_e4m3(y[f][c][v], inv) * scale) >> 16;
       const int row = rbase + 16 * f + 4 * (l / 16);
       *reinterpret_cast<uint2 *>(a.yb + (size_t)pos * I + row) =
@@ -706,87 +829,87 @@ __device__ void gateup_tile(const GroupedArgs &a, int e, int rt, int p0, int np,
   }
 }
 
-// grid.x = token-tile bound x row tiles (I / 128); tiles beyond the actual
-// count exit at once.
+// Routed experts (FP4) and the shared expert (FP8) are separate launches,
+// each with the registers of its own format. grid.x = token-tile bound x row
+// tiles (I / 128); FP4: tiles [0, tile_off[E]) (beyond the actual count exit
+// at once); FP8: the shared expert's tiles from tile_off[E].
+template <int AFMT>
 __global__ __launch_bounds__(256) void k_grouped_gateup(GroupedArgs a) {
-  __shared__ __align__(16) uint8_t bt[GT_TN * GT_BROW2];
+  __shared__ __align__(16) uint8_t bt[2 * GT_BT_BYTES];
   __shared__ int rows_s[GT_TN];
   __shared__ float wt_s[GT_TN];
   __shared__ float amax_s[4][GT_TN];
-  const int rt = blockIdx.x % a.row_tiles, tt = blockIdx.x / a.row_tiles;
-  if (tt >= a.tile_off[a.E + 1]) return;
-  const int e = tile_expert(a.tile_off, a.E, tt);
+  int tt, rt;
+  tile_coords(a.row_tiles, tt, rt);
+  if (AFMT == MX_FP8) tt += a.tile_off[a.E];
+  if (tt >= a.tile_off[AFMT == MX_FP8 ? a.E + 1 : a.E]) return;
+  const int e = AFMT == MX_FP8 ? a.E : tile_expert(a.tile_off, a.E, tt);
   const int p0 = a.pos_off[e] + (tt - a.tile_off[e]) * GT_TN;
   const int np = min(GT_TN, a.pos_off[e + 1] - p0);
-  if (e == a.E)
-    gateup_tile<MX_FP8>(a, e, rt, p0, np, bt, rows_s, wt_s, amax_s);
-  else
-    gateup_tile<MX_FP4>(a, e, rt, p0, np, bt, rows_s, wt_s, amax_s);
+  gateup_tile<AFMT>(a, e, rt, p0, np, bt, rows_s, wt_s, amax_s);
 }
 
 template <int AFMT>
-__device__ void down_tile(const GroupedArgs &a, int e, int rt, int p0, int np, uint8_t *bt,
-                          int *rows_s) {
+__device__ __forceinline__ void down_tile(const GroupedArgs &a, int e, int rt, int p0, int np,
+                                          uint8_t *bt, int *rows_s) {
   const int tid = threadIdx.x, wv = tid / 64, l = tid % 64;
-  const int H = a.H, I = a.I, nsw = I / 128;
-  const uint8_t *W, *S;
+  const int H = a.H, I = a.I;
+  const uint8_t *Wp, *Sp;
+  uint32_t wbytes, sbytes;
   if (AFMT == MX_FP4) {
     const uint8_t *sc = a.experts + (size_t)e * a.expert_stride;
-    W = sc + a.scale_run + (size_t)I * (H / 2);
-    S = sc + (size_t)I * (H / 32);
+    Wp = sc + a.scale_run + (size_t)I * (H / 2);
+    Sp = sc + (size_t)I * (H / 32);
+    wbytes = (uint32_t)((size_t)H * (I / 2));
+    sbytes = (uint32_t)((size_t)H * (I / 32));
   } else {
-    W = a.shw[2];
-    S = a.shs[2];
+    Wp = a.shw[2];
+    Sp = a.shs[2];
+    wbytes = (uint32_t)H * (uint32_t)I;
+    sbytes = (uint32_t)((H + 127) / 128) * (uint32_t)(I / 128);
   }
   if (tid < GT_TN) rows_s[tid] = tid < np ? p0 + tid : -1;  // positions are contiguous
+  __syncthreads();
   const int nf = (np + 15) / 16;
-  v4f acc[2][4];
+  v4f acc[1][2][4];
   for (int f = 0; f < 2; ++f)
-    for (int c = 0; c < 4; ++c) acc[f][c] = (v4f){0.f, 0.f, 0.f, 0.f};
+    for (int c = 0; c < 4; ++c) acc[0][f][c] = (v4f){0.f, 0.f, 0.f, 0.f};
   const int rbase = rt * GT_TM + 32 * wv;
-  for (int sw = 0; sw < nsw; ++sw) {
-    __syncthreads();
-    stage_b16(bt, a.yb, rows_s, I, sw);
-    uint4 A[2][4];
-    for (int f = 0; f < 2; ++f) load_a_bf16<AFMT>(A[f], W, S, rbase + 16 * f + l % 16, I, sw, l);
-    __syncthreads();
-    for (int c = 0; c < 4; ++c) {
-      if (c >= nf) break;
-      uint4 B[4];
-      load_b_ops(B, bt, 16 * c + l % 16, l);
+  const BufRsrc W[1] = {buf_rsrc(Wp, wbytes)};
+  const BufRsrc S[1] = {buf_rsrc(Sp, sbytes)};
+  gemm_k_loop<AFMT, 1>(acc, W, S, buf_rsrc(a.yb, a.yb_bytes), I, rbase, rows_s[tid >> 2], nf, bt);
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        for (int f = 0; f < 2; ++f) acc[f][c] = mfma_bf16(A[f][q], B[q], acc[f][c]);
-    }
-  }
-  for (int c = 0; c < nf; ++c) {
+  for (int c = 0; c < 4; ++c) {
     const int j = 16 * c + l % 16;
-    if (j >= np) continue;
+    if (c >= nf || j >= np) continue;
     const int pos = p0 + j;
     const int t = a.pos_token[pos], k = a.pos_route[pos];
     uint16_t *dst = a.ro + ((size_t)t * (a.K + 1) + k) * H;
+#pragma unroll
     for (int f = 0; f < 2; ++f) {
       const int row = rbase + 16 * f + 4 * (l / 16);
       uint2 o;
-      o.x = (f2u(bf16_round(acc[f][c][0])) >> 16) | (f2u(bf16_round(acc[f][c][1])) & 0xFFFF0000u);
-      o.y = (f2u(bf16_round(acc[f][c][2])) >> 16) | (f2u(bf16_round(acc[f][c][3])) & 0xFFFF0000u);
+      o.x = (f2u(bf16_round(acc[0][f][c][0])) >> 16) |
+            (f2u(bf16_round(acc[0][f][c][1])) & 0xFFFF0000u);
+      o.y = (f2u(bf16_round(acc[0][f][c][2])) >> 16) |
+            (f2u(bf16_round(acc[0][f][c][3])) & 0xFFFF0000u);
       *reinterpret_cast<uint2 *>(dst + row) = o;
     }
   }
 }
 
+template <int AFMT>
 __global__ __launch_bounds__(256) void k_grouped_down(GroupedArgs a) {
-  __shared__ __align__(16) uint8_t bt[GT_TN * GT_BROW2];
+  __shared__ __align__(16) uint8_t bt[2 * GT_BT_BYTES];
   __shared__ int rows_s[GT_TN];
-  const int rt = blockIdx.x % a.row_tiles, tt = blockIdx.x / a.row_tiles;
-  if (tt >= a.tile_off[a.E + 1]) return;
-  const int e = tile_expert(a.tile_off, a.E, tt);
+  int tt, rt;
+  tile_coords(a.row_tiles, tt, rt);
+  if (AFMT == MX_FP8) tt += a.tile_off[a.E];
+  if (tt >= a.tile_off[AFMT == MX_FP8 ? a.E + 1 : a.E]) return;
+  const int e = AFMT == MX_FP8 ? a.E : tile_expert(a.tile_off, a.E, tt);
   const int p0 = a.pos_off[e] + (tt - a.tile_off[e]) * GT_TN;
   const int np = min(GT_TN, a.pos_off[e + 1] - p0);
-  if (e == a.E)
-    down_tile<MX_FP8>(a, e, rt, p0, np, bt, rows_s);
-  else
-    down_tile<MX_FP4>(a, e, rt, p0, np, bt, rows_s);
+  down_tile<AFMT>(a, e, rt, p0, np, bt, rows_s);
 }
 
 // out[t][i] = bf16(((0 + r_0) + ... + r_{K-1}) + shared), routes in
@@ -887,6 +1010,9 @@ int dsv4g_moe_forward_batch(float *out, const float *x, const DSV4GLayer *L,
     return dsv4g_fail(DSV4G_EINVAL, "moe_forward_batch: unsupported shape");
   if (L->tid2eid && !token_ids)
     return dsv4g_fail(DSV4G_EINVAL, "moe_forward_batch: hash layer needs token_ids");
+  // the GEMMs address the activation buffers with 32-bit offsets below 2 GiB
+  if ((size_t)T * (K + 1) * I * 2 >= (1ull << 31) || (size_t)T * H * 2 >= (1ull << 31))
+    return dsv4g_fail(DSV4G_EINVAL, "moe_forward_batch: too many tokens for one call (%d)", T);
   if (workspace_bytes < dsv4g_moe_batch_workspace_bytes(L, T))
     return dsv4g_fail(DSV4G_EINVAL, "moe_forward_batch: workspace too small (%zu < %zu)",
                       workspace_bytes, dsv4g_moe_batch_workspace_bytes(L, T));
@@ -936,6 +1062,8 @@ int dsv4g_moe_forward_batch(float *out, const float *x, const DSV4GLayer *L,
   g.pos_wt = w.pos_wt;
   g.xb = w.xb;
   g.yb = w.yb;
+  g.xb_bytes = (uint32_t)((size_t)T * H * 2);
+  g.yb_bytes = (uint32_t)((size_t)T * (K + 1) * I * 2);
   g.ro = w.ro;
   g.H = H;
   g.I = I;
@@ -943,15 +1071,24 @@ int dsv4g_moe_forward_batch(float *out, const float *x, const DSV4GLayer *L,
   g.K = K;
   g.T = T;
   g.limit = (float)(int)L->swiglu_limit;
-  const long tile_bound = ((long)T * K + GT_TN - 1) / GT_TN + E + (T + GT_TN - 1) / GT_TN;
+  // routed token tiles: at most ceil(T K / 64) + E (one partial tile per
+  // expert); the shared expert's: ceil(T / 64)
+  const long routed_bound = ((long)T * K + GT_TN - 1) / GT_TN + E;
+  const long shared_tiles = (T + GT_TN - 1) / GT_TN;
   g.row_tiles = I / GT_TM;
-  hipLaunchKernelGGL(k_grouped_gateup, dim3((unsigned)(tile_bound * g.row_tiles)), dim3(256), 0,
-                     st, g);
+  hipLaunchKernelGGL(k_grouped_gateup<MX_FP4>, dim3((unsigned)(routed_bound * g.row_tiles)),
+                     dim3(256), 0, st, g);
   DSV4G_TRY(dsv4g_check_launch("grouped_gateup"));
+  hipLaunchKernelGGL(k_grouped_gateup<MX_FP8>, dim3((unsigned)(shared_tiles * g.row_tiles)),
+                     dim3(256), 0, st, g);
+  DSV4G_TRY(dsv4g_check_launch("grouped_gateup_shared"));
   g.row_tiles = H / GT_TM;
-  hipLaunchKernelGGL(k_grouped_down, dim3((unsigned)(tile_bound * g.row_tiles)), dim3(256), 0,
-                     st, g);
+  hipLaunchKernelGGL(k_grouped_down<MX_FP4>, dim3((unsigned)(routed_bound * g.row_tiles)),
+                     dim3(256), 0, st, g);
   DSV4G_TRY(dsv4g_check_launch("grouped_down"));
+  hipLaunchKernelGGL(k_grouped_down<MX_FP8>, dim3((unsigned)(shared_tiles * g.row_tiles)),
+                     dim3(256), 0, st, g);
+  DSV4G_TRY(dsv4g_check_launch("grouped_down_shared"));
   // 6. combine
   const size_t total = (size_t)T * H;
   hipLaunchKernelGGL(k_combine_batch, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st,
