@@ -747,7 +747,7 @@ __device__ __forceinline__ void gemm_k_loop(v4f (&acc)[NM][2][4], const BufRsrc 
 template <int AFMT>
 __device__ __forceinline__ void gateup_tile(const GroupedArgs &a, int e, int rt, int p0, int np,
                                             uint8_t *bt, int *rows_s, float *wt_s,
-                                            float (*amax_s)[GT_TN]) {
+                                            float (*amax_s)[GT_TN], uint64_t *s_tab) {
   const int tid = threadIdx.x, wv = tid / 64, l = tid % 64;
   const int H = a.H, I = a.I;
   const uint8_t *Wg, *Wu, *Sg, *Su;
@@ -775,6 +775,7 @@ __device__ __forceinline__ void gateup_tile(const GroupedArgs &a, int e, int rt,
     rows_s[tid] = tid < np ? a.pos_token[p0 + tid] : -1;
     wt_s[tid] = tid < np ? a.pos_wt[p0 + tid] : 0.0f;
   }
+  libm_stage_table(s_tab);  // SwiGLU's expf table, read from LDS in the epilogue
   __syncthreads();
   const int nf = (np + 15) / 16;  // active token fragments (block-uniform)
   v4f acc[2][2][4];
@@ -799,7 +800,7 @@ __device__ __forceinline__ void gateup_tile(const GroupedArgs &a, int e, int rt,
         float yy = 0.0f;
         if (c < nf) {
           const float g = bf16_round(acc[0][f][c][v]), u = bf16_round(acc[1][f][c][v]);
-          yy = bf16_round(swiglu_t(g, u, a.limit) * wt_s[j]);
+          yy = bf16_round(swiglu_t(g, u, a.limit, s_tab) * wt_s[j]);
         }
         y[f][c][v] = yy;
         m = fmaxf(m, fabsf(yy));
@@ -839,6 +840,7 @@ __global__ __launch_bounds__(256) void k_grouped_gateup(GroupedArgs a) {
   __shared__ int rows_s[GT_TN];
   __shared__ float wt_s[GT_TN];
   __shared__ float amax_s[4][GT_TN];
+  __shared__ uint64_t s_tab[32];
   int tt, rt;
   tile_coords(a.row_tiles, tt, rt);
   if (AFMT == MX_FP8) tt += a.tile_off[a.E];
@@ -846,7 +848,7 @@ __global__ __launch_bounds__(256) void k_grouped_gateup(GroupedArgs a) {
   const int e = AFMT == MX_FP8 ? a.E : tile_expert(a.tile_off, a.E, tt);
   const int p0 = a.pos_off[e] + (tt - a.tile_off[e]) * GT_TN;
   const int np = min(GT_TN, a.pos_off[e + 1] - p0);
-  gateup_tile<AFMT>(a, e, rt, p0, np, bt, rows_s, wt_s, amax_s);
+  gateup_tile<AFMT>(a, e, rt, p0, np, bt, rows_s, wt_s, amax_s, s_tab);
 }
 
 template <int AFMT>
