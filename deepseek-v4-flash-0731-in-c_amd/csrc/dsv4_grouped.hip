@@ -1,6 +1,6 @@
 // dsv4_grouped.hip - the batched MoE layer for gfx950 (speculative verify and
-// prefill): moe_forward_batch (src/dsv4/dsv4_model.c:6812-7117) as a grouped
-// GEMM on the CDNA4 block-scaled MFMA.
+// prefill): moe_forward_batch (src/dsv4/dsv4_model.c:6812-7117) as grouped
+// GEMMs on the CDNA4 BF16 MFMA with exact FP4/FP8 x E8M0 operands.
 //
 // Pipeline (one stream):
 //   1. activations -> FP8 E4M3 codes + per-128 E8M0 scale codes
