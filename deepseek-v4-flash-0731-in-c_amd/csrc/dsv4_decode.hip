@@ -4,10 +4,11 @@
 //
 //   k_dec_router   approximate router logits z and sum|w*x| for every
 //                  (token, expert) and the approximate choice
-//                  sqrt_softplus(z) + bias; the FP8 activation quant of x.
-//                  The last logit workgroup to finish derives each token's
-//                  candidate experts (below).
-//   k_dec_gateup   gate and up GEMVs of every candidate (FP4) and of the
+//                  sqrt_softplus(z) + bias, one workgroup per expert; the
+//                  FP8 activation quant of x.
+//   k_dec_gateup   every workgroup that needs them derives the token's
+//                  candidate experts (below) from the approximate choices
+//                  first; then gate and up GEMVs of every candidate (FP4) and of the
 //                  shared expert (FP8), a workgroup holding the same rows of
 //                  both so that it writes t = silu(bf16 gate) * bf16 up
 //                  (src/dsv4/dsv4_model.c:6264-6268); beside them one
@@ -22,21 +23,25 @@
 //                  rounded to BF16 (src/dsv4/dsv4_model.c:6795-6805).
 //
 // Candidates. A parallel logit differs from the sequential fmaf chain by at
-// most gamma_{H/64+8} + gamma_H times sum|w*x|. Mapped through
-// |d score / dz| <= 1/2 plus slack for the score's own rounding, and doubled
-// for both sides, that gives delta: an expert whose approximate choice is
-// below (k-th best approximate choice) - delta has k experts surely above it
-// and cannot be selected. The others are the candidates, in ascending expert
-// id. Gate/up runs for the first `maxc` of them while the exact chains run
-// beside it, so the chains' latency (a 4096-long dependent fmaf chain, about
-// 15 us) hides under the weight stream. With more candidates than slots
-// (near-ties such as a constant gate) the chains cover every candidate and
-// the down kernel computes t for a selected expert without a slot itself:
-// slow, still exact.
+// most gamma_d + gamma_H times sum|w*x| (d: the parallel sum's rounding
+// depth, dec_par_depth). Mapped through |d score / dz| <= 1/2 plus slack for
+// the score's own rounding, and doubled for both sides, that gives delta: an
+// expert whose approximate choice is below (k-th best approximate choice) -
+// delta has k experts surely above it and cannot be selected. The others are
+// the candidates, in ascending expert id. Gate/up runs for every candidate
+// (persistent workgroups over (candidate, tile) items) while the exact
+// chains run beside it, one chain workgroup per candidate position modulo
+// maxc, so the chains' latency (a 4096-long dependent fmaf chain, about
+// 15 us) hides under the weight stream. Near-ties (a constant gate) only
+// make more items.
 //
-// Cross-workgroup hand-offs (logits -> candidates, chains -> selection) use
-// one device-scope release fence and counter increment per workgroup; the
-// last arrival acquires, does the work and resets its counter. The counters
+// The candidates are derived redundantly by each workgroup of k_dec_gateup
+// that needs them (a few hundred cycles of one wave, beside the workgroup's
+// first loads): a last-arrival hand-off in k_dec_router would cost a
+// device-scope fence and a memory round trip on the critical path. The
+// hand-off from the chains to the selection uses one device-scope release
+// fence and counter increment per workgroup; the last arrival acquires, does
+// the work and resets its counter. The counters
 // sit in the first bytes of the workspace, which must be zero before the
 // first call (dsv4g_moe_workspace_init); every call leaves them zero.
 #include "dsv4_device.h"
@@ -58,7 +63,7 @@ struct DecArgs {
   const uint8_t *experts;
   size_t expert_stride, scale_run;
   const uint8_t *sh[3], *sh_s[3];  // shared gate, up, down
-  unsigned *ctl;                   // [0] logit arrivals, [1 + t] chain arrivals of token t
+  unsigned *ctl;                   // [1 + t] chain arrivals of token t ([0] unused)
   uint8_t *qx8;                    // [n][H] E4M3 codes of the quantised activation
   float *qxs;                      // [n][H/128] its scales
   float *ch, *zabs, *za;           // [n][E]: approximate choice, sum|w*x|, logit
@@ -68,14 +73,15 @@ struct DecArgs {
   int *sel_e;                      // [n][K] routing, ascending id (moe_forward's idx)
   int *sel_pos;                    // [n][K] candidate position of each route
   float *sel_w;                    // [n][K] route weights (moe_forward's wt)
-  float *sv;                       // [n][maxc + 1][I] SwiGLU t; slot maxc = shared expert
-  float *fb;                       // [n][K][I] t of selected experts without a slot
+  float *sv;                       // [n][E + 1][I] SwiGLU t per candidate position; slot E = shared
   float *ro;                       // [n][K + 1][H] per-route outputs (BF16 values)
   int *idx_out;                    // optional copies of the routing
   float *wt_out;
   int n, H, I, E, K, maxc;
   int gu_tiles, dn_tiles;  // paired gate/up tiles (rows I, in H); down tiles (rows H, in I)
+  int gu_nb;               // persistent routed gate/up workgroups per token
   float route_scale, limit;
+  float gamma;  // gamma_{dec_par_depth(H)} + gamma_H, the candidates' bound factor
   int fast;  // routing from the parallel logits when the candidates are exactly top-k
 };
 
@@ -124,14 +130,21 @@ __device__ __forceinline__ bool dec_arrive_last(unsigned *cnt, unsigned total, i
 __device__ __forceinline__ void dec_select_finish(const DecArgs &a, int t, int my_e, float my_sc,
                                                   int my_pos);
 
+// Rounding depth of a parallel logit of dec_logit_block: the product (one
+// rounding), a lane's sequential sum of its 8-column pieces (at most
+// 8 ceil(H / 2048) products), the 6-level wave butterfly, the 3 additions of
+// the four waves' partials, and one more for the rounding of the computed
+// sum|w*x| that the bound is scaled by.
+__device__ __host__ __forceinline__ int dec_par_depth(int H) { return 8 * ((H / 4 + 511) / 512) + 11; }
+
 // Candidates of token t in ascending expert id (whole calling wave) into
-// cand[0 .. count); returns the count. A hash layer's candidates are its
-// tid2eid row. NPER = experts per lane (E <= 64 * NPER).
-// In fast mode, when the candidates are exactly the top-k, the routing is
-// taken here from the approximate choices (selection order) and the parallel
-// logits (scores), with no further memory round trip.
+// cand[0 .. count) (LDS); returns the count. A hash layer's candidates are its
+// tid2eid row. NPER = experts per lane (E <= 64 * NPER). One workgroup per
+// token publishes: it also writes the list to a.cand / a.ncand and, in fast
+// mode when the candidates are exactly the top-k, the routing, taken from
+// the approximate choices (selection order) and the parallel logits (scores).
 template <int NPER>
-__device__ __forceinline__ int dec_candidates_t(const DecArgs &a, int t, int *cand,
+__device__ __forceinline__ int dec_candidates_t(const DecArgs &a, int t, int *cand, bool publish,
                                                 const uint64_t *tab) {
   const int lane = threadIdx.x % 64;
   const size_t row = (size_t)t * a.E;
@@ -182,7 +195,7 @@ __device__ __forceinline__ int dec_candidates_t(const DecArgs &a, int t, int *ca
     kth = wm;
   }
   const float sum_abs = wave_max_dpp(amax);
-  const float bound_z = (gamma_n(a.H / 64 + 8) + gamma_n(a.H)) * sum_abs;
+  const float bound_z = a.gamma * sum_abs;  // gamma_{dec_par_depth(H)} + gamma_H
   const float thr = kth - 2.0f * (0.5f * bound_z + 1e-5f);
   int base = 0;
 #pragma unroll
@@ -191,32 +204,52 @@ __device__ __forceinline__ int dec_candidates_t(const DecArgs &a, int t, int *ca
     const bool p = e < a.E && v[j] >= thr;
     const unsigned long long bal = __ballot(p);
     const int pos = base + __popcll(bal & ((1ull << lane) - 1ull));
-    if (p) cand[pos] = e;
+    if (p) {
+      cand[pos] = e;
+      if (publish) a.cand[row + pos] = e;
+    }
     base += __popcll(bal);
   }
-  if (a.fast && base == a.K) {  // the same test as dec_chain_block's early exit
-    // candidates == top-k: sel_pos is the rank by id (dec_select_finish)
-    dec_select_finish(a, t, my_e, lane < a.K ? sqrt_softplus(my_z, tab) : 0.0f, -1);
+  if (publish) {
+    if (lane == 0) a.ncand[t] = base;
+    if (a.fast && base == a.K) {  // the same test as dec_chain_block's early exit
+      // candidates == top-k: sel_pos is the rank by id (dec_select_finish)
+      dec_select_finish(a, t, my_e, lane < a.K ? sqrt_softplus(my_z, tab) : 0.0f, -1);
+    }
   }
   return base;
 }
 
-__device__ __forceinline__ int dec_candidates(const DecArgs &a, int t, int *cand,
+__device__ __forceinline__ void dec_select(const DecArgs &a, int t, const uint64_t *tab, float *lds);
+
+__device__ __forceinline__ int dec_candidates(const DecArgs &a, int t, int *cand, bool publish,
                                               const uint64_t *tab) {
   if (a.tid2eid) {
     const int64_t *row = a.tid2eid + (size_t)a.token_ids[t] * a.K;
     for (int k = threadIdx.x % 64; k < a.K; k += 64) {
       const int e = (int)row[k];
       cand[k] = e;
-      if (a.fast) a.zx[(size_t)t * a.E + k] = (e >= 0 && e < a.E) ? a.za[(size_t)t * a.E + e] : 0.0f;
+      if (publish) {
+        a.cand[(size_t)t * a.E + k] = e;
+        if (a.fast) a.zx[(size_t)t * a.E + k] = (e >= 0 && e < a.E) ? a.za[(size_t)t * a.E + e] : 0.0f;
+      }
+    }
+    if (publish) {
+      if (threadIdx.x % 64 == 0) a.ncand[t] = a.K;
+      if (a.fast) {
+        // the tid2eid row routes; weights from the parallel logits just
+        // copied to zx by this wave
+        __threadfence_block();
+        dec_select(a, t, tab, nullptr);  // a hash layer never takes the LDS path
+      }
     }
     return a.K;
   }
-  if (a.E <= 64) return dec_candidates_t<1>(a, t, cand, tab);
-  if (a.E <= 128) return dec_candidates_t<2>(a, t, cand, tab);
-  if (a.E <= 256) return dec_candidates_t<4>(a, t, cand, tab);
-  if (a.E <= 512) return dec_candidates_t<8>(a, t, cand, tab);
-  return dec_candidates_t<16>(a, t, cand, tab);
+  if (a.E <= 64) return dec_candidates_t<1>(a, t, cand, publish, tab);
+  if (a.E <= 128) return dec_candidates_t<2>(a, t, cand, publish, tab);
+  if (a.E <= 256) return dec_candidates_t<4>(a, t, cand, publish, tab);
+  if (a.E <= 512) return dec_candidates_t<8>(a, t, cand, publish, tab);
+  return dec_candidates_t<16>(a, t, cand, publish, tab);
 }
 
 
@@ -369,76 +402,61 @@ __device__ __forceinline__ void dec_select(const DecArgs &a, int t, const uint64
 }
 
 // ------------------------------------------------------------ router ----
-// Router logits of experts 4 b .. 4 b + 3 (one wave each, for every token;
-// the gate row stays in registers, x is staged in LDS): approximate choice
-// sqrt_softplus(z) + bias, sum|w*x| and z. The last of these blocks derives
-// the candidates and, in fast mode, the routing of every token whose
-// candidates are exactly its top-k.
-__device__ __forceinline__ void dec_router_block(const DecArgs &a, int b, float *xs, uint64_t *s_tab,
-                                 int *s_flag) {
+// Router logit of expert e for every token, one workgroup: wave wv takes the
+// columns [wv H/4, (wv + 1) H/4), lane l its 8-column pieces l, l + 64, ...
+// (the gate row stays in registers, x is read directly); approximate choice
+// sqrt_softplus(z) + bias, sum|w*x| and z (rounding depth: dec_par_depth).
+__device__ __forceinline__ void dec_logit_block(const DecArgs &a, int e, float *s_part,
+                                                uint64_t *s_tab) {
   const int tid = threadIdx.x, wv = tid / 64, lane = tid % 64;
-  const int H = a.H;
-  const int nlog = (a.E + 3) / 4;
-  const int e = __builtin_amdgcn_readfirstlane(b * 4 + wv);
-  const bool act = e < a.E;
-  // lane holds columns 8 lane + 512 i; an inactive wave reads zeros
-  const BufRsrc rg = buf_rsrc(a.gate + (size_t)(act ? e : 0) * H, act ? 2u * H : 0u);
-  uint4 w[16];
+  const int H = a.H, Q = H / 4;
+  const BufRsrc rg = buf_rsrc(a.gate + (size_t)e * H + (size_t)wv * Q, 2u * (uint32_t)Q);
+  uint4 w[4];  // Q <= 2048: at most 4 pieces per lane; pieces past Q read zeros
 #pragma unroll
-  for (int i = 0; i < 16; ++i) w[i] = buf_load16(rg, 16u * (lane + 64 * i));
+  for (int i = 0; i < 4; ++i) w[i] = buf_load16(rg, 16u * (uint32_t)(lane + 64 * i));
   const uint64_t tabv = libm_table_load();
   for (int t = 0; t < a.n; ++t) {
-    __syncthreads();
-    const BufRsrc rx = buf_rsrc(a.x + (size_t)t * H, 4u * H);
-    uint4 xv4[8];  // H <= 8192
+    const BufRsrc rx = buf_rsrc(a.x + (size_t)t * H + (size_t)wv * Q, 4u * (uint32_t)Q);
+    uint4 xv[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) xv4[j] = buf_load16(rx, 16u * (tid + 256 * j));
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      if (4 * (tid + 256 * j) < H) *reinterpret_cast<uint4 *>(xs + 4 * (tid + 256 * j)) = xv4[j];
-    if (t == 0) libm_table_store(s_tab, tabv);
-    __syncthreads();
+    for (int i = 0; i < 4; ++i) {
+      xv[2 * i] = buf_load16(rx, 32u * (uint32_t)(lane + 64 * i));
+      xv[2 * i + 1] = buf_load16(rx, 32u * (uint32_t)(lane + 64 * i) + 16u);
+    }
     float acc = 0.0f, aabs = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int c = 8 * lane + 512 * i;
-      if (c < H) {
-        const float4 xa = *reinterpret_cast<const float4 *>(xs + c);
-        const float4 xb = *reinterpret_cast<const float4 *>(xs + c + 4);
-        const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
-        const uint32_t wd[4] = {w[i].x, w[i].y, w[i].z, w[i].w};
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t wd[4] = {w[i].x, w[i].y, w[i].z, w[i].w};
+      const uint32_t xd[8] = {xv[2 * i].x,     xv[2 * i].y,     xv[2 * i].z,     xv[2 * i].w,
+                              xv[2 * i + 1].x, xv[2 * i + 1].y, xv[2 * i + 1].z, xv[2 * i + 1].w};
 #pragma unroll
-        for (int d = 0; d < 4; ++d) {
-          const float p0 = u2f(wd[d] << 16) * xv[2 * d];
-          const float p1 = u2f(wd[d] & 0xFFFF0000u) * xv[2 * d + 1];
-          acc += p0;
-          acc += p1;
-          aabs += fabsf(p0);
-          aabs += fabsf(p1);
-        }
+      for (int d = 0; d < 4; ++d) {
+        const float p0 = u2f(wd[d] << 16) * u2f(xd[2 * d]);
+        const float p1 = u2f(wd[d] & 0xFFFF0000u) * u2f(xd[2 * d + 1]);
+        acc += p0;
+        acc += p1;
+        aabs += fabsf(p0);
+        aabs += fabsf(p1);
       }
     }
     acc = wave_sum(acc);
     aabs = wave_sum(aabs);
-    if (act && lane == 0) {
+    if (t == 0) libm_table_store(s_tab, tabv);
+    if (lane == 0) {
+      s_part[2 * wv] = acc;
+      s_part[2 * wv + 1] = aabs;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      const float z = ((s_part[0] + s_part[2]) + s_part[4]) + s_part[6];
+      const float zs = ((s_part[1] + s_part[3]) + s_part[5]) + s_part[7];
       const size_t o = (size_t)t * a.E + e;
-      a.ch[o] = sqrt_softplus(acc, s_tab) + (a.bias ? a.bias[e] : 0.0f);
-      a.zabs[o] = aabs;
-      a.za[o] = acc;
+      a.ch[o] = sqrt_softplus(z, s_tab) + (a.bias ? a.bias[e] : 0.0f);
+      a.zabs[o] = zs;
+      a.za[o] = z;
     }
+    __syncthreads();  // s_part is reused by the next token
   }
-  if (!dec_arrive_last(&a.ctl[0], (unsigned)nlog, s_flag)) return;
-  for (int t = wv; t < a.n; t += 4) {
-    const int nc = dec_candidates(a, t, a.cand + (size_t)t * a.E, s_tab);
-    if (lane == 0) a.ncand[t] = nc;
-    if (a.fast && a.tid2eid) {
-      // hash layer: its tid2eid row routes; weights from the parallel logits
-      // copied to zx by dec_candidates (this wave's writes)
-      __threadfence_block();
-      dec_select(a, t, s_tab, xs);
-    }
-  }
-  if (tid == 0) a.ctl[0] = 0u;
 }
 
 // quant_fp8_act (src/dsv4/dsv4_ops.c:96-121) of one 128-group per wave, for
@@ -496,18 +514,16 @@ __device__ __forceinline__ void dec_shared_gateup(const DecArgs &a, int t, int t
   libm_table_store(s_tab, tabv);
   __syncthreads();
   if (tid < FP8_TR / 2 && r0 + tid < I)
-    a.sv[((size_t)t * (a.maxc + 1) + a.maxc) * I + r0 + tid] =
+    a.sv[((size_t)t * (a.E + 1) + a.E) * I + r0 + tid] =
         swiglu_t(s_y[tid], s_y[tid + FP8_TR / 2], a.limit, s_tab);
 }
 
-// Blocks: [ceil(E/4) router logits][quant of x].
+// Blocks: [E router logits][quant of x].
 __global__ __launch_bounds__(256) void k_dec_router(DecArgs a) {
-  extern __shared__ __align__(16) float lds[];  // H floats
   __shared__ uint64_t s_tab[32];
-  __shared__ int s_flag;
-  const int nlog = (a.E + 3) / 4;
-  if ((int)blockIdx.x < nlog) return dec_router_block(a, blockIdx.x, lds, s_tab, &s_flag);
-  dec_quant_block(a, blockIdx.x - nlog);
+  __shared__ float s_part[8];
+  if ((int)blockIdx.x < a.E) return dec_logit_block(a, blockIdx.x, s_part, s_tab);
+  dec_quant_block(a, blockIdx.x - a.E);
 }
 
 // ------------------------------------------------------------ chains ----
@@ -560,27 +576,35 @@ __device__ __forceinline__ float chain_cols(const float4 *g, const float4 *x, fl
 // block stages x and the candidate's gate row (widened to fp32) into LDS in
 // one shot, then lane 0 of wave 0 runs the reference's fmaf chain in column
 // order (dsv4_gemv_bf16, src/dsv4/dsv4_model.c:298-303) from LDS alone.
-// The last chain workgroup of the token selects the routes.
-__device__ __forceinline__ void dec_chain_block(const DecArgs &a, int t, int c, float *lds, uint64_t *s_tab,
-                                int *s_flag) {
+// The chain workgroup of position 0 publishes the candidates (and, in fast
+// mode, the routing); the last chain workgroup of the token selects the
+// routes.
+__device__ __forceinline__ void dec_chain_block(const DecArgs &a, int t, int c, float *lds,
+                                                uint64_t *s_tab, int *s_cand, int *s_nc,
+                                                int *s_flag) {
   const int tid = threadIdx.x, wv = tid / 64, lane = tid % 64;
   const int H = a.H;
-  const int nc = a.ncand[t];
-  if (a.fast && nc == a.K) return;  // routed by the router kernel already
   float *xs = lds, *gs = lds + H;  // H floats each
   const uint64_t tabv = libm_table_load();
-  if (c < nc) {
-    const BufRsrc rx = buf_rsrc(a.x + (size_t)t * H, 4u * (uint32_t)H);
-    uint4 xv[8];  // H <= 8192: 8 pieces per thread
+  // x is issued before the candidates are known
+  const BufRsrc rx = buf_rsrc(a.x + (size_t)t * H, 4u * (uint32_t)H);
+  uint4 xv[8];  // H <= 8192: 8 pieces per thread
 #pragma unroll
-    for (int j = 0; j < 8; ++j) xv[j] = buf_load16(rx, 16u * (uint32_t)(tid + 256 * j));
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      if (4 * (tid + 256 * j) < H) reinterpret_cast<uint4 *>(xs)[tid + 256 * j] = xv[j];
-  }
+  for (int j = 0; j < 8; ++j) xv[j] = buf_load16(rx, 16u * (uint32_t)(tid + 256 * j));
   libm_table_store(s_tab, tabv);
+  if (wv == 0) {
+    __builtin_amdgcn_wave_barrier();  // the table, for the publishing fast path
+    const int n = dec_candidates(a, t, s_cand, c == 0, s_tab);
+    if (lane == 0) *s_nc = n;
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    if (4 * (tid + 256 * j) < H) reinterpret_cast<uint4 *>(xs)[tid + 256 * j] = xv[j];
+  __syncthreads();
+  const int nc = *s_nc;
+  if (a.fast && nc == a.K) return;  // routed by the publishing workgroup already
   for (int pos = c; pos < nc; pos += a.maxc) {
-    const int e = a.cand[(size_t)t * a.E + pos];
+    const int e = s_cand[pos];
     float acc = 0.0f;
     if (e >= 0 && e < a.E) {
       const BufRsrc rg = buf_rsrc(a.gate + (size_t)e * H, 2u * (uint32_t)H);
@@ -619,49 +643,109 @@ __device__ __forceinline__ void dec_chain_block(const DecArgs &a, int t, int c, 
 }
 
 // --------------------------------------------------------- gate / up ----
-// Blocks: [n*maxc chain workgroups][n*(I/8) shared FP8 gate/up pairs]
-// [maxc*n*gu_tiles routed FP4 pairs, candidate-major]; routed tiles of
-// candidate slots a token does not use exit at once.
+// Routed gate/up item j of token t: candidate position c = j / gu_tiles, rows
+// [r0, r0 + tr / 2) of its gate and up matrices (tile j % gu_tiles). Loads
+// the activation codes and the pair into R; an item past the end (or a
+// malformed tid2eid entry) loads zero-length ranges, which read zeros without
+// touching memory, so every load is issued unconditionally.
+__device__ __forceinline__ void dec_gu_load(const DecArgs &a, Fp4RegsT<DEC_NP> &R, int t, int j,
+                                            int nitems, const int *s_cand, const Fp4Geom &q,
+                                            int &c, int &r0, bool &live) {
+  const int H = a.H, I = a.I;
+  c = j / a.gu_tiles;
+  r0 = (j - c * a.gu_tiles) * (q.tr / 2);
+  const int e = __builtin_amdgcn_readfirstlane(j < nitems ? s_cand[min(c, a.E - 1)] : -1);
+  live = e >= 0 && e < a.E;
+  const uint8_t *W0, *S0, *W1, *S1;
+  expert_mat(a, live ? e : 0, 0, W0, S0);
+  expert_mat(a, live ? e : 0, 1, W1, S1);
+  fp4_tile_x(R, a.qx8 + (size_t)t * H, a.qxs + (size_t)t * (H / 128), q);
+  fp4_pair_load_near(R, W0, S0, W1, S1, H, live ? I : 0, r0, q);  // S1 after S0 in the slot
+}
+
+// The item's group chains, then t = silu(bf16 gate) * bf16 up for its rows
+// (src/dsv4/dsv4_model.c:6264-6268) into the candidate's slot of sv.
+__device__ __forceinline__ void dec_gu_finish(const DecArgs &a, const Fp4RegsT<DEC_NP> &R, int t,
+                                              int c, int r0, const Fp4Geom &q, float *lds,
+                                              float *s_y, const uint64_t *s_tab) {
+  const int tid = threadIdx.x, I = a.I, half = q.tr / 2;
+  fp4_pair_finish(R, s_y, I, r0, q, reinterpret_cast<float2 *>(lds), fp4_scale_lds(lds, q));
+  __syncthreads();
+  if (tid < half && r0 + tid < I)
+    a.sv[((size_t)t * (a.E + 1) + c) * I + r0 + tid] =
+        swiglu_t(s_y[tid], s_y[tid + half], a.limit, s_tab);
+}
+
+// Persistent routed gate/up of token t, workgroup bb of gu_nb: items
+// bb, bb + nb, ... of the token's ncand * gu_tiles, in two register tiles
+// used in turn: the next item's loads are issued before an item is computed,
+// so weights stream while the workgroup computes.
+__device__ __forceinline__ void dec_gu_routed(const DecArgs &a, int t, int bb, float *lds,
+                                              float *s_y, uint64_t *s_tab, int *s_cand,
+                                              int *s_nc) {
+  const int tid = threadIdx.x;
+  const Fp4Geom q = fp4_geom_np(a.H, DEC_NP);
+  const uint64_t tabv = libm_table_load();
+  if (tid < 64) {
+    const int n = dec_candidates(a, t, s_cand, false, s_tab);
+    if (tid == 0) *s_nc = n;
+  }
+  libm_table_store(s_tab, tabv);
+  __syncthreads();
+  const int nitems = __builtin_amdgcn_readfirstlane(*s_nc) * a.gu_tiles;
+  const int nb = a.gu_nb;
+  if (bb >= nitems) return;
+  // two register tiles used in turn, unrolled over the first four items (a
+  // loop would carry loads in flight across its back edge, which the
+  // compiler drains); more items (many candidates) run one at a time
+  Fp4RegsT<DEC_NP> A, B;
+  int cA, rA, cB, rB;
+  bool lA, lB;
+  int j = bb;
+  dec_gu_load(a, A, t, j, nitems, s_cand, q, cA, rA, lA);
+  dec_gu_load(a, B, t, j + nb, nitems, s_cand, q, cB, rB, lB);
+  if (lA) dec_gu_finish(a, A, t, cA, rA, q, lds, s_y, s_tab);
+  j += nb;
+  dec_gu_load(a, A, t, j + nb, nitems, s_cand, q, cA, rA, lA);
+  if (j < nitems && lB) dec_gu_finish(a, B, t, cB, rB, q, lds, s_y, s_tab);
+  j += nb;
+  dec_gu_load(a, B, t, j + nb, nitems, s_cand, q, cB, rB, lB);
+  if (j < nitems && lA) dec_gu_finish(a, A, t, cA, rA, q, lds, s_y, s_tab);
+  j += nb;
+  if (j < nitems && lB) dec_gu_finish(a, B, t, cB, rB, q, lds, s_y, s_tab);
+  for (j += nb; j < nitems; j += nb) {
+    dec_gu_load(a, A, t, j, nitems, s_cand, q, cA, rA, lA);
+    if (lA) dec_gu_finish(a, A, t, cA, rA, q, lds, s_y, s_tab);
+  }
+}
+
+// Blocks: [n*maxc chain workgroups][n*gu_nb persistent routed FP4
+// workgroups][n*(I/8) shared FP8 gate/up pairs]. Workgroups are dispatched in
+// index order, so the small loads that gate the critical path (the
+// candidates' choices, the chains' gate rows) are issued before the shared
+// expert's weight stream.
 __global__ __launch_bounds__(256) void k_dec_gateup(DecArgs a) {
   extern __shared__ __align__(16) float lds[];
   __shared__ uint64_t s_tab[32];
   __shared__ float s_y[256];
-  __shared__ int s_flag;
-  const int tid = threadIdx.x;
-  const int H = a.H, I = a.I;
+  __shared__ int s_cand[ROUTER_MAX_EXPERTS];
+  __shared__ int s_nc, s_flag;
+  const int I = a.I;
   const int nchain = a.n * a.maxc;
   const int t8 = (I + FP8_TR / 2 - 1) / (FP8_TR / 2);
   const int nshared = a.n * t8;
   int b = blockIdx.x;
   if (b < nchain) {
-    dec_chain_block(a, b / a.maxc, b % a.maxc, lds, s_tab, &s_flag);
+    dec_chain_block(a, b / a.maxc, b % a.maxc, lds, s_tab, s_cand, &s_nc, &s_flag);
     return;
   }
   b -= nchain;
-  if (b < nshared) return dec_shared_gateup(a, b / t8, b % t8, lds, s_y, s_tab);
-  b -= nshared;
-  const int tile = b % a.gu_tiles;
-  b /= a.gu_tiles;
-  const int t = b % a.n, c = b / a.n;
-  const int nc = a.ncand[t];
-  if (c >= min(nc, a.maxc)) return;
-  const int e = a.cand[(size_t)t * a.E + c];
-  if (e < 0 || e >= a.E) return;  // malformed tid2eid entry: the route contributes zeros
-  const Fp4Geom q = fp4_geom_np(H, DEC_NP);
-  const int half = q.tr / 2, r0 = tile * half;
-  const uint8_t *W0, *S0, *W1, *S1;
-  expert_mat(a, e, 0, W0, S0);
-  expert_mat(a, e, 1, W1, S1);
-  Fp4RegsT<DEC_NP> R;
-  fp4_tile_x(R, a.qx8 + (size_t)t * H, a.qxs + (size_t)t * (H / 128), q);
-  fp4_pair_load(R, W0, S0, W1, S1, H, I, r0, q);
-  const uint64_t tabv = libm_table_load();
-  fp4_pair_finish(R, s_y, I, r0, q, reinterpret_cast<float2 *>(lds), fp4_scale_lds(lds, q));
-  libm_table_store(s_tab, tabv);
-  __syncthreads();
-  if (tid < half && r0 + tid < I)
-    a.sv[((size_t)t * (a.maxc + 1) + c) * I + r0 + tid] =
-        swiglu_t(s_y[tid], s_y[tid + half], a.limit, s_tab);
+  if (b < a.n * a.gu_nb) {
+    dec_gu_routed(a, b / a.gu_nb, b % a.gu_nb, lds, s_y, s_tab, s_cand, &s_nc);
+    return;
+  }
+  b -= a.n * a.gu_nb;
+  if (b < nshared) dec_shared_gateup(a, b / t8, b % t8, lds, s_y, s_tab);
 }
 
 // -------------------------------------------------------------- down ----
@@ -718,52 +802,11 @@ __device__ void dec_requant(void *qyv, float *qys, const TvRegs &T, const float 
   __syncthreads();
 }
 
-// One FP4 row in the reference's order (per-32 partials, then the group
-// chain; src/dsv4/dsv4_model.c:651-673), by a single lane, BF16-rounded.
-__device__ float dec_row_exact(const uint8_t *W, const uint8_t *S, const uint8_t *qx8,
-                               const float *qxs, int in, int row) {
-  const int G = in / 32;
-  const uint8_t *wr = W + (size_t)row * (in / 2);
-  const uint8_t *sr = S + (size_t)row * G;
-  float acc = 0.0f;
-  for (int g = 0; g < G; ++g) {
-    const uint32_t code = sr[g];
-    if (code == 255u) continue;  // NaN scale: the reference skips the group
-    float xq[32];
-#pragma unroll
-    for (int i = 0; i < 32; ++i) xq[i] = e4m3_decode(qx8[32 * g + i]);
-    const float p = fp4_group_partial(*reinterpret_cast<const uint4 *>(wr + 16 * g), xq);
-    acc = fmaf(p, qxs[g / 4] * e8m0(code), acc);
-  }
-  return bf16_round(acc);
-}
-
-// t of expert e for token t into fb (route slot k), for a selected expert
-// that had no candidate slot: one row per lane, few registers (this path
-// only runs on near-ties). Every workgroup of that route computes the same
-// values and reads back only its own writes (ordered by the barrier).
-__device__ __forceinline__ void dec_fallback_t(const DecArgs &a, int t, int k, int e, uint64_t *tab) {
-  libm_stage_table(tab);
-  __syncthreads();
-  const uint8_t *W0, *S0, *W1, *S1;
-  expert_mat(a, e, 0, W0, S0);
-  expert_mat(a, e, 1, W1, S1);
-  const uint8_t *qx = a.qx8 + (size_t)t * a.H;
-  const float *qxs = a.qxs + (size_t)t * (a.H / 128);
-  float *dst = a.fb + ((size_t)t * a.K + k) * a.I;
-  for (int r = threadIdx.x; r < a.I; r += 256) {
-    const float g = dec_row_exact(W0, S0, qx, qxs, a.H, r);
-    const float u = dec_row_exact(W1, S1, qx, qxs, a.H, r);
-    dst[r] = swiglu_t(g, u, a.limit, tab);
-  }
-  __syncthreads();
-}
-
 // Shared expert down, rows [16 tile, 16 tile + 16): its t (weight 1)
 // requantised into LDS, then the FP8 tile into route slot K of ro.
 __device__ __forceinline__ void dec_shared_down(const DecArgs &a, int t, int tile, float *lds) {
   const int H = a.H, I = a.I, K = a.K;
-  const float *tv = a.sv + ((size_t)t * (a.maxc + 1) + a.maxc) * I;
+  const float *tv = a.sv + ((size_t)t * (a.E + 1) + a.E) * I;
   TvRegs T;
   dec_tv_load(T, tv, I);
   Fp8Regs R;
@@ -797,9 +840,7 @@ __global__ __launch_bounds__(256) void k_dec_down(DecArgs a) {
       for (int r = r0 + tid; r < min(H, r0 + q.tr); r += 256) ro[r] = 0.0f;
       return;
     }
-    if (pos >= a.maxc) dec_fallback_t(a, t, k, e, s_tab);
-    const float *tv = pos < a.maxc ? a.sv + ((size_t)t * (a.maxc + 1) + pos) * I
-                                   : a.fb + ((size_t)t * K + k) * I;
+    const float *tv = a.sv + ((size_t)t * (a.E + 1) + pos) * I;
     const uint8_t *W, *S;
     expert_mat(a, e, 2, W, S);
     TvRegs T;
@@ -849,7 +890,7 @@ namespace {
 struct DecWs {
   unsigned *ctl;
   uint8_t *qx8;
-  float *qxs, *ch, *zabs, *za, *zx, *sel_w, *sv, *fb, *ro;
+  float *qxs, *ch, *zabs, *za, *zx, *sel_w, *sv, *ro;
   int *cand, *ncand, *sel_e, *sel_pos;
   size_t bytes;
 };
@@ -864,7 +905,7 @@ int dec_maxc(const DSV4GLayer *L) {
 // rest, each piece 256-byte aligned.
 DecWs dec_ws_layout(const DSV4GLayer *L, int n_tokens, void *base) {
   const size_t n = (size_t)n_tokens, K = (size_t)L->topk, E = (size_t)L->n_experts;
-  const size_t H = (size_t)L->hidden, I = (size_t)L->inter, C = (size_t)dec_maxc(L);
+  const size_t H = (size_t)L->hidden, I = (size_t)L->inter;
   DecWs w = {};
   uintptr_t p = (uintptr_t)base;
   auto take = [&](size_t bytes) {
@@ -884,14 +925,37 @@ DecWs dec_ws_layout(const DSV4GLayer *L, int n_tokens, void *base) {
   w.sel_e = (int *)take(n * K * 4);
   w.sel_w = (float *)take(n * K * 4);
   w.sel_pos = (int *)take(n * K * 4);
-  w.sv = (float *)take(n * (C + 1) * I * 4);
-  w.fb = (float *)take(n * K * I * 4);
+  w.sv = (float *)take(n * (E + 1) * I * 4);
   w.ro = (float *)take(n * (K + 1) * H * 4);
   w.bytes = (size_t)(p - (uintptr_t)base);
   return w;
 }
 
 size_t max_sz(size_t a, size_t b) { return a > b ? a : b; }
+
+// Workgroups of k_dec_gateup resident at once on the current device (its
+// occupancy times the CU count), cached per device and LDS size.
+int gateup_slots(size_t lds, int *slots) {
+  static int cache_slots[64];
+  static size_t cache_lds[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0)
+    return dsv4g_fail(DSV4G_EHIP, "moe_decode: hipGetDevice failed");
+  if (dev < 64 && cache_slots[dev] > 0 && cache_lds[dev] == lds) {
+    *slots = cache_slots[dev];
+    return DSV4G_OK;
+  }
+  int per_cu = 0, cus = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_dec_gateup, 256, lds) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return dsv4g_fail(DSV4G_EHIP, "moe_decode: occupancy query failed");
+  *slots = max(1, per_cu) * max(1, cus);
+  if (dev < 64) {
+    cache_lds[dev] = lds;
+    cache_slots[dev] = *slots;
+  }
+  return DSV4G_OK;
+}
 
 int dec_launch(int phase, float *out, const float *x, const DSV4GLayer *L, const int *token_ids,
                int n_tokens, void *workspace, size_t workspace_bytes, int *idx_out,
@@ -936,7 +1000,6 @@ int dec_launch(int phase, float *out, const float *x, const DSV4GLayer *L, const
   a.sel_w = w.sel_w;
   a.sel_pos = w.sel_pos;
   a.sv = w.sv;
-  a.fb = w.fb;
   a.ro = w.ro;
   a.idx_out = idx_out;
   a.wt_out = wt_out;
@@ -949,7 +1012,12 @@ int dec_launch(int phase, float *out, const float *x, const DSV4GLayer *L, const
   const Fp4Geom qg = fp4_geom_np(a.H, DEC_NP), qd = fp4_geom_np(a.I, DEC_NP);
   a.gu_tiles = (a.I + qg.tr / 2 - 1) / (qg.tr / 2);
   a.dn_tiles = (a.H + qd.tr - 1) / qd.tr;
+
   a.route_scale = L->route_scale;
+  {
+    const double d = dec_par_depth(a.H) * 0x1p-24, h = a.H * 0x1p-24;
+    a.gamma = (float)(d / (1.0 - d) + h / (1.0 - h));
+  }
   a.limit = (float)(int)L->swiglu_limit;  // the reference passes the limit as int
   a.fast = fast;
   const int n = n_tokens, H = a.H, I = a.I;
@@ -961,16 +1029,21 @@ int dec_launch(int phase, float *out, const float *x, const DSV4GLayer *L, const
   const size_t lds_fp8_dn = (size_t)(I / 128) * 132 * 4 + (size_t)((I / 128 + 3) & ~3) * 4 +
                             (size_t)FP8_TR * pair_stride(I / 128) * 8;
   if (phase == 0) {
-    const int blocks = (a.E + 3) / 4 + (n * (H / 128) + 3) / 4;
-    hipLaunchKernelGGL(k_dec_router, dim3(blocks), dim3(256), (size_t)H * 4, st, a);
+    const int blocks = a.E + (n * (H / 128) + 3) / 4;
+    hipLaunchKernelGGL(k_dec_router, dim3(blocks), dim3(256), 0, st, a);
     return dsv4g_check_launch("dec_router");
   }
   if (phase == 1) {
     // routed pairs: the tile's pairs and scales; chains: x and a gate row
     const size_t lds_fp4 = (size_t)qg.tr * pair_stride(qg.G) * 8 + 4096;
     const size_t lds = max_sz(max_sz(lds_fp4, (size_t)H * 8), lds_fp8_gu);
-    const long blocks = (long)n * a.maxc + (long)n * ((I + FP8_TR / 2 - 1) / (FP8_TR / 2)) +
-                        (long)a.maxc * n * a.gu_tiles;
+    // persistent routed workgroups: the resident slots left beside the chain
+    // and shared workgroups, split over the tokens (at least 128 each)
+    const int fixed = n * (a.maxc + (I + FP8_TR / 2 - 1) / (FP8_TR / 2));
+    int slots = 0;
+    DSV4G_TRY(gateup_slots(lds, &slots));
+    a.gu_nb = max(128, (slots - fixed) / n);
+    const long blocks = (long)fixed + (long)n * a.gu_nb;
     hipLaunchKernelGGL(k_dec_gateup, dim3((unsigned)blocks), dim3(256), lds, st, a);
     return dsv4g_check_launch("dec_gateup");
   }

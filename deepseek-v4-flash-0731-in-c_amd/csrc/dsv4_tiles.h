@@ -314,6 +314,9 @@ __device__ __forceinline__ void fp4_step4(const uint32_t (&wd)[4], float x0, flo
   for (int i = 0; i < 4; ++i) p[i] = fmaf(v[i].x, x0, p[i]);
 #pragma unroll
   for (int i = 0; i < 4; ++i) p[i] = fmaf(v[i].y, x1, p[i]);
+  // two columns at a time: at most 8 converted weights are live (a
+  // pipelined caller holds a second tile in registers meanwhile)
+  __builtin_amdgcn_sched_barrier(0);
 }
 
 // Partials of passes u0 .. u0 + 3: four 32-long fmaf chains, each in the
@@ -348,7 +351,10 @@ __device__ __forceinline__ void fp4_partials4(const Fp4RegsT<NP> &R, int u0, flo
 // is a buffer load over the tile's existing rows of one matrix (at most 64 KB,
 // 32-bit offsets): rows past the matrix, passes past npass and lanes g >= G
 // read zeros without touching memory.
-template <int NP>
+// NEAR (paired only): S1 lies after S0 within 2 GiB, so one range covers
+// both matrices' scale rows and each scale dword is one load (half the
+// registers in flight of the two-range form).
+template <int NP, bool NEAR = false>
 __device__ __forceinline__ void fp4_load_w(Fp4RegsT<NP> &R, const uint8_t *__restrict__ W0,
                                            const uint8_t *__restrict__ S0,
                                            const uint8_t *__restrict__ W1,
@@ -369,6 +375,21 @@ __device__ __forceinline__ void fp4_load_w(Fp4RegsT<NP> &R, const uint8_t *__res
     // Dword loads: the ranges are multiples of 4 bytes, not always of 16.
     const uint32_t o = 16u * (uint32_t)t;
     uint32_t v[4];
+    if (NEAR) {
+      // one range from W0's tile rows to W1's (dist bytes on): a dword of
+      // the first segment reads W0's rows, of the second W1's; padding rows
+      // (nrow < half) and lanes past both segments read zeros
+      const uint32_t seg = (uint32_t)half * G, nb = nrow * G, dist = (uint32_t)(S1 - S0);
+      const BufRsrc rs = buf_rsrc(S0 + (size_t)r0 * G, nb ? dist + nb : 0u);
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const uint32_t od = o + 4u * (uint32_t)d;
+        const uint32_t off = od < seg ? (od < nb ? od : 0xFFFFFFF0u)
+                                      : (od - seg < nb ? dist + (od - seg) : 0xFFFFFFF0u);
+        v[d] = buf_load4(rs, off);
+      }
+      R.sc = make_uint4(v[0], v[1], v[2], v[3]);
+    } else {
 #pragma unroll
     for (int d = 0; d < 4; ++d) v[d] = buf_load4(rs0, o + 4u * d);
     if (pair) {
@@ -377,6 +398,7 @@ __device__ __forceinline__ void fp4_load_w(Fp4RegsT<NP> &R, const uint8_t *__res
       for (int d = 0; d < 4; ++d) v[d] |= buf_load4(rs1, o + 4u * d - seg);  // o < seg wraps
     }
     R.sc = make_uint4(v[0], v[1], v[2], v[3]);
+    }
   }
   const uint32_t gcol = g < q.G ? 16u * (uint32_t)g : 0xFFFFFFF0u;  // g >= G: out of range
 #pragma unroll
@@ -443,6 +465,16 @@ __device__ __forceinline__ void fp4_tile_finish(const Fp4RegsT<NP> &R, float *y,
                                                 const Fp4Geom &q, float2 *ps, uint8_t *cl) {
   const float v = fp4_tile_rows(R, rows, r0, q, ps, cl, false);
   if (threadIdx.x < q.tr && r0 + (int)threadIdx.x < rows) y[r0 + threadIdx.x] = v;
+}
+
+// Paired, with S1 after S0 within 2 GiB (the slots of one expert).
+template <int NP>
+__device__ __forceinline__ void fp4_pair_load_near(Fp4RegsT<NP> &R, const uint8_t *__restrict__ W0,
+                                                   const uint8_t *__restrict__ S0,
+                                                   const uint8_t *__restrict__ W1,
+                                                   const uint8_t *__restrict__ S1, int in,
+                                                   int rows, int r0, const Fp4Geom &q) {
+  fp4_load_w<NP, true>(R, W0, S0, W1, S1, in, rows, r0, q, true);
 }
 
 // Paired: yl[lr] (LDS) for lr < tr.
