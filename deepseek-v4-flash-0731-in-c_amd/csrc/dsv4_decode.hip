@@ -484,6 +484,14 @@ __device__ __forceinline__ void dec_quant_block(const DecArgs &a, int b) {
 __device__ __forceinline__ void dec_shared_gateup(const DecArgs &a, int t, int tile, float *lds,
                                                   float *s_y, uint64_t *s_tab) {
   const int tid = threadIdx.x;
+  {
+    // the shared expert's weight stream starts 2 us into the kernel: at
+    // launch the routed path's critical loads (the candidates' choices, the
+    // chains' staging) are served about twice as fast by an otherwise idle
+    // memory system, and the shared expert is needed only by k_dec_down
+    const long long t0 = wall_clock64();  // 100 MHz
+    while (wall_clock64() - t0 < 200) __builtin_amdgcn_s_sleep(8);
+  }
   const int H = a.H, I = a.I, r0 = tile * (FP8_TR / 2);
   // the activation codes (at most 8192: 8 words per thread) and its
   // per-128 scales ahead of the weights
@@ -767,7 +775,11 @@ __device__ __forceinline__ void dec_tv_load(TvRegs &T, const float *tv, int I) {
     T.v[2 * j] = buf_loadf(r, 4u * (g * 128u + lane));
     T.v[2 * j + 1] = buf_loadf(r, 4u * (g * 128u + 64u + lane));
   }
-  __builtin_amdgcn_sched_barrier(0);  // issued before the weights that follow
+  // t has arrived before this workgroup's weights are requested: issued at
+  // the same time, the few t lines would queue in the memory channels
+  // behind the whole kernel's weight stream (about 5 us)
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
 }
 
 // CODES: qy receives E4M3 codes as bytes (the FP4 down tile), otherwise the
@@ -785,7 +797,7 @@ __device__ void dec_requant(void *qyv, float *qys, const TvRegs &T, const float 
     const float t1 = j < 8 ? T.v[(2 * j + 1) & 15] : tv[i1];
     const float y0 = bf16_round(t0 * w);
     const float y1 = bf16_round(t1 * w);
-    const float amax = wave_max(fmaxf(fabsf(y0), fabsf(y1)));
+    const float amax = wave_max_dpp(fmaxf(fabsf(y0), fabsf(y1)));
     const float scale = act_scale(amax);
     const float inv = 1.0f / scale;
     if (CODES) {
