@@ -69,7 +69,8 @@ struct DecArgs {
   float *ch, *zabs, *za;           // [n][E]: approximate choice, sum|w*x|, logit
   int *cand;                       // [n][E] candidate ids, ascending
   int *ncand;                      // [n]
-  float *zx;                       // [n][E] exact logit per candidate position
+  float *zx, *zc;                  // [n][E] exact score sqrt_softplus(z) and choice score + bias
+                                   // per candidate position
   int *sel_e;                      // [n][K] routing, ascending id (moe_forward's idx)
   int *sel_pos;                    // [n][K] candidate position of each route
   float *sel_w;                    // [n][K] route weights (moe_forward's wt)
@@ -220,27 +221,24 @@ __device__ __forceinline__ int dec_candidates_t(const DecArgs &a, int t, int *ca
   return base;
 }
 
-__device__ __forceinline__ void dec_select(const DecArgs &a, int t, const uint64_t *tab, float *lds);
-
 __device__ __forceinline__ int dec_candidates(const DecArgs &a, int t, int *cand, bool publish,
                                               const uint64_t *tab) {
   if (a.tid2eid) {
+    // the tid2eid row (K <= 32 <= lanes), in row order
+    const int lane = threadIdx.x % 64;
     const int64_t *row = a.tid2eid + (size_t)a.token_ids[t] * a.K;
-    for (int k = threadIdx.x % 64; k < a.K; k += 64) {
-      const int e = (int)row[k];
-      cand[k] = e;
-      if (publish) {
-        a.cand[(size_t)t * a.E + k] = e;
-        if (a.fast) a.zx[(size_t)t * a.E + k] = (e >= 0 && e < a.E) ? a.za[(size_t)t * a.E + e] : 0.0f;
-      }
+    const int e = lane < a.K ? (int)row[lane] : -1;
+    if (lane < a.K) {
+      cand[lane] = e;
+      if (publish) a.cand[(size_t)t * a.E + lane] = e;
     }
     if (publish) {
-      if (threadIdx.x % 64 == 0) a.ncand[t] = a.K;
+      if (lane == 0) a.ncand[t] = a.K;
       if (a.fast) {
-        // the tid2eid row routes; weights from the parallel logits just
-        // copied to zx by this wave
-        __threadfence_block();
-        dec_select(a, t, tab, nullptr);  // a hash layer never takes the LDS path
+        // the row routes; weights from the parallel logits (route k = lane k)
+        const bool ok = e >= 0 && e < a.E;
+        dec_select_finish(a, t, e, ok ? sqrt_softplus(a.za[(size_t)t * a.E + e], tab) : 0.0f,
+                          lane);
       }
     }
     return a.K;
@@ -253,24 +251,23 @@ __device__ __forceinline__ int dec_candidates(const DecArgs &a, int t, int *cand
 }
 
 
-// Exact top-k of token t from the candidates' exact logits (one whole wave):
+// Exact top-k of token t from the candidates' exact scores and choices (one
+// whole wave; the nc candidates ct in ascending id, from the caller's LDS):
 // routes ascending by id with weights and candidate positions, written to
 // sel_* (and idx_out / wt_out) (src/dsv4/dsv4_model.c:6615-6676). Lane k
 // carries route k in selection order.
 template <int NPER>
-__device__ __forceinline__ void dec_select_t(const DecArgs &a, int t, const uint64_t *tab) {
+__device__ __forceinline__ void dec_select_t(const DecArgs &a, int t, int nc, const int *ct) {
   const int lane = threadIdx.x % 64;
   const int K = a.K;
-  const int nc = a.ncand[t];
-  const int *ct = a.cand + (size_t)t * a.E;
-  const float *zt = a.zx + (size_t)t * a.E;
+  const float *zt = a.zx + (size_t)t * a.E, *zc = a.zc + (size_t)t * a.E;
   int my_e = -1, my_pos = -1;
   float my_sc = 0.0f;
   if (a.tid2eid) {
     if (lane < K) {
       my_e = ct[lane];
       my_pos = lane;
-      my_sc = (my_e >= 0 && my_e < a.E) ? sqrt_softplus(zt[lane], tab) : 0.0f;
+      my_sc = (my_e >= 0 && my_e < a.E) ? zt[lane] : 0.0f;
     }
   } else {
     const float ninf = -__builtin_inff();
@@ -284,8 +281,8 @@ __device__ __forceinline__ void dec_select_t(const DecArgs &a, int t, const uint
       ce[j] = -1;
       if (pos < nc) {
         ce[j] = ct[pos];
-        sc[j] = sqrt_softplus(zt[pos], tab);
-        chv[j] = sc[j] + (a.bias ? a.bias[ce[j]] : 0.0f);
+        sc[j] = zt[pos];
+        chv[j] = zc[pos];
       }
     }
     unsigned used = 0u;
@@ -356,16 +353,15 @@ __device__ __forceinline__ void dec_select_finish(const DecArgs &a, int t, int m
 
 // More than 256 candidates (near-ties or large expert counts): scores in
 // LDS (2 * nc floats, nc <= 1024), scanned with plain loops.
-__device__ __forceinline__ void dec_select_big(const DecArgs &a, int t, const uint64_t *tab, float *lds) {
+__device__ __forceinline__ void dec_select_big(const DecArgs &a, int t, int nc, const int *ct,
+                                               float *lds) {
   const int lane = threadIdx.x % 64;
-  const int nc = a.ncand[t];
-  const int *ct = a.cand + (size_t)t * a.E;
-  const float *zt = a.zx + (size_t)t * a.E;
+  const float *zt = a.zx + (size_t)t * a.E, *zc = a.zc + (size_t)t * a.E;
   const float ninf = -__builtin_inff();
   float *sc = lds, *chv = lds + nc;
   for (int pos = lane; pos < nc; pos += 64) {
-    sc[pos] = sqrt_softplus(zt[pos], tab);
-    chv[pos] = sc[pos] + (a.bias ? a.bias[ct[pos]] : 0.0f);
+    sc[pos] = zt[pos];
+    chv[pos] = zc[pos];
   }
   __builtin_amdgcn_wave_barrier();
   int my_e = -1, my_pos = -1;
@@ -393,12 +389,12 @@ __device__ __forceinline__ void dec_select_big(const DecArgs &a, int t, const ui
   dec_select_finish(a, t, my_e, my_sc, my_pos);
 }
 
-__device__ __forceinline__ void dec_select(const DecArgs &a, int t, const uint64_t *tab, float *lds) {
-  const int nc = a.tid2eid ? 0 : a.ncand[t];
-  if (nc <= 64) return dec_select_t<1>(a, t, tab);
-  if (nc <= 128) return dec_select_t<2>(a, t, tab);
-  if (nc <= 256) return dec_select_t<4>(a, t, tab);
-  dec_select_big(a, t, tab, lds);
+__device__ __forceinline__ void dec_select(const DecArgs &a, int t, int nc, const int *ct,
+                                           float *lds) {
+  if (a.tid2eid || nc <= 64) return dec_select_t<1>(a, t, nc, ct);
+  if (nc <= 128) return dec_select_t<2>(a, t, nc, ct);
+  if (nc <= 256) return dec_select_t<4>(a, t, nc, ct);
+  dec_select_big(a, t, nc, ct, lds);
 }
 
 // ------------------------------------------------------------ router ----
@@ -613,8 +609,10 @@ __device__ __forceinline__ void dec_chain_block(const DecArgs &a, int t, int c, 
   if (a.fast && nc == a.K) return;  // routed by the publishing workgroup already
   for (int pos = c; pos < nc; pos += a.maxc) {
     const int e = s_cand[pos];
+    const bool ok = e >= 0 && e < a.E;
+    const float be = ok && a.bias ? a.bias[e] : 0.0f;  // in flight during the chain
     float acc = 0.0f;
-    if (e >= 0 && e < a.E) {
+    if (ok) {
       const BufRsrc rg = buf_rsrc(a.gate + (size_t)e * H, 2u * (uint32_t)H);
       uint4 gv[4];  // H / 8 <= 1024 pieces: 4 per thread
 #pragma unroll
@@ -643,10 +641,18 @@ __device__ __forceinline__ void dec_chain_block(const DecArgs &a, int t, int c, 
       }
       __syncthreads();  // the next candidate restages the gate row
     }
-    if (tid == 0) a.zx[(size_t)t * a.E + pos] = acc;
+    if (tid == 0) {
+      // the reference's score and choice (src/dsv4/dsv4_model.c:5827-5831,
+      // 6627-6634), here so that the selection after the hand-off only reads
+      const float sc = ok ? sqrt_softplus(acc, s_tab) : 0.0f;
+      a.zx[(size_t)t * a.E + pos] = sc;
+      a.zc[(size_t)t * a.E + pos] = sc + be;
+    }
   }
   if (!dec_arrive_last(&a.ctl[1 + t], (unsigned)a.maxc, s_flag)) return;
-  if (wv == 0) dec_select(a, t, s_tab, lds);
+  // the candidates are this workgroup's own (LDS); nc > 256 uses lds
+  // (2 nc floats) for the scores, past the x and gate rows no longer needed
+  if (wv == 0) dec_select(a, t, nc, s_cand, lds);
   if (tid == 0) a.ctl[1 + t] = 0u;
 }
 
@@ -703,6 +709,12 @@ __device__ __forceinline__ void dec_gu_routed(const DecArgs &a, int t, int bb, f
   const int nitems = __builtin_amdgcn_readfirstlane(*s_nc) * a.gu_tiles;
   const int nb = a.gu_nb;
   if (bb >= nitems) return;
+  if (!a.fast) {
+    // exact mode: the chains bound the kernel and this stream has slack; it
+    // starts 1 us later so that the chains' gate rows are staged first
+    const long long t0 = wall_clock64();  // 100 MHz
+    while (wall_clock64() - t0 < 100) __builtin_amdgcn_s_sleep(8);
+  }
   // two register tiles used in turn, unrolled over the first four items (a
   // loop would carry loads in flight across its back edge, which the
   // compiler drains); more items (many candidates) run one at a time
@@ -902,7 +914,7 @@ namespace {
 struct DecWs {
   unsigned *ctl;
   uint8_t *qx8;
-  float *qxs, *ch, *zabs, *za, *zx, *sel_w, *sv, *ro;
+  float *qxs, *ch, *zabs, *za, *zx, *zc, *sel_w, *sv, *ro;
   int *cand, *ncand, *sel_e, *sel_pos;
   size_t bytes;
 };
@@ -934,6 +946,7 @@ DecWs dec_ws_layout(const DSV4GLayer *L, int n_tokens, void *base) {
   w.cand = (int *)take(n * E * 4);
   w.ncand = (int *)take(n * 4);
   w.zx = (float *)take(n * E * 4);
+  w.zc = (float *)take(n * E * 4);
   w.sel_e = (int *)take(n * K * 4);
   w.sel_w = (float *)take(n * K * 4);
   w.sel_pos = (int *)take(n * K * 4);
@@ -1008,6 +1021,7 @@ int dec_launch(int phase, float *out, const float *x, const DSV4GLayer *L, const
   a.cand = w.cand;
   a.ncand = w.ncand;
   a.zx = w.zx;
+  a.zc = w.zc;
   a.sel_e = w.sel_e;
   a.sel_w = w.sel_w;
   a.sel_pos = w.sel_pos;
