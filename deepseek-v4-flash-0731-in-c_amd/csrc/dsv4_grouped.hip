@@ -594,8 +594,10 @@ struct WinRaw {
 };
 
 // W[m], S[m]: buffers of matrix m and its scales; in: K width; rbase: the
-// wave's first row; brow: this thread's activation row (-1: none); bsrc:
-// buffer over the activation matrix (row stride in BF16 elements). The loads
+// wave's first row; brow[k]: the activation row of tile row tid / 16 + 16 k
+// (-1: none), of which this thread stages the 16-byte piece tid % 16 (a
+// wave's load covers 4 whole 256-byte rows: 8 cache lines); bsrc: buffer
+// over the activation matrix (row stride in BF16 elements). The loads
 // of a window come in four parts (matrix 0, matrix 1, two halves of the
 // activation row), issued between MFMA steps so that the vector memory path
 // works while the matrix cores do; every part of a window is issued before
@@ -603,9 +605,9 @@ struct WinRaw {
 template <int AFMT, int NM>
 __device__ __forceinline__ void win_load_part(WinRaw<AFMT, NM> &R, int part,
                                               const BufRsrc (&W)[NM], const BufRsrc (&S)[NM],
-                                              BufRsrc bsrc, int in, int rbase, int brow, int sw,
-                                              int nsw) {
-  const int l = threadIdx.x % 64, g = l / 16, q = threadIdx.x & 3;
+                                              BufRsrc bsrc, int in, int rbase, const int (&brow)[4],
+                                              int sw, int nsw) {
+  const int l = threadIdx.x % 64, g = l / 16;
   const bool ok = sw < nsw;
   if (part < 2) {
     const int m = part;
@@ -627,11 +629,15 @@ __device__ __forceinline__ void win_load_part(WinRaw<AFMT, NM> &R, int part,
       }
     }
   } else {
-    const uint32_t bo =
-        (ok && brow >= 0) ? 2u * ((uint32_t)brow * (uint32_t)in + sw * 128u + q * 32u) : GT_BAD;
-    const int i0 = (part - 2) * 2;
-    R.b[i0] = buf_load16(bsrc, bo + 16u * i0);
-    R.b[i0 + 1] = buf_load16(bsrc, bo + 16u * (i0 + 1));
+    const int k0 = (part - 2) * 2;
+#pragma unroll
+    for (int k = k0; k < k0 + 2; ++k) {
+      const uint32_t bo = (ok && brow[k] >= 0)
+                              ? 2u * ((uint32_t)brow[k] * (uint32_t)in + sw * 128u) +
+                                    16u * (uint32_t)(threadIdx.x % 16)
+                              : GT_BAD;
+      R.b[k] = buf_load16(bsrc, bo);
+    }
   }
   __builtin_amdgcn_sched_barrier(0);  // keep the parts in order
 }
@@ -639,7 +645,7 @@ __device__ __forceinline__ void win_load_part(WinRaw<AFMT, NM> &R, int part,
 template <int AFMT, int NM>
 __device__ __forceinline__ void win_load(WinRaw<AFMT, NM> &R, const BufRsrc (&W)[NM],
                                          const BufRsrc (&S)[NM], BufRsrc bsrc, int in, int rbase,
-                                         int brow, int sw, int nsw) {
+                                         const int (&brow)[4], int sw, int nsw) {
 #pragma unroll
   for (int part = 0; part < 4; ++part)
     win_load_part<AFMT, NM>(R, part, W, S, bsrc, in, rbase, brow, sw, nsw);
@@ -671,14 +677,17 @@ __device__ __forceinline__ uint4 win_op(uint4 r0, uint4 r1, uint32_t code, int q
 }
 
 // The K loop of one tile: acc[m][f][c] += A_m rows (rbase + 16 f ..) x the
-// staged activation rows of fragment c < nf. brow: this thread's activation
-// row; the caller has published rows before (barrier).
+// staged activation rows of fragment c < nf. rows: the tile's activation
+// rows (LDS, -1: none), published by the caller before (barrier).
 template <int AFMT, int NM>
 __device__ __forceinline__ void gemm_k_loop(v4f (&acc)[NM][2][4], const BufRsrc (&W)[NM],
                                             const BufRsrc (&S)[NM], BufRsrc bsrc, int in,
-                                            int rbase, int brow, int nf, uint8_t *bt) {
+                                            int rbase, const int *rows, int nf, uint8_t *bt) {
   const int tid = threadIdx.x, l = tid % 64;
   const int nsw = in / 128;
+  int brow[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) brow[k] = rows[tid / 16 + 16 * k];
   for (int c0 = 0; c0 < nsw; c0 += GT_CHUNK) {
     WinRaw<AFMT, NM> R[GT_DEPTH];
 #pragma unroll
@@ -690,9 +699,10 @@ __device__ __forceinline__ void gemm_k_loop(v4f (&acc)[NM][2][4], const BufRsrc 
       WinRaw<AFMT, NM> &Rc = R[i % GT_DEPTH];
       uint8_t *bb = bt + (sw & 1) * GT_BT_BYTES;
       {
-        uint4 *d = reinterpret_cast<uint4 *>(bb + (tid >> 2) * GT_BROW2 + (tid & 3) * 64);
 #pragma unroll
-        for (int k = 0; k < 4; ++k) d[k] = Rc.b[k];
+        for (int k = 0; k < 4; ++k)
+          *reinterpret_cast<uint4 *>(bb + (tid / 16 + 16 * k) * GT_BROW2 + 16 * (tid % 16)) =
+              Rc.b[k];
       }
       // this window's A bytes, kept while the ring slot is refilled
       uint4 A0[NM][2], A1[NM][2];
@@ -785,7 +795,7 @@ __device__ __forceinline__ void gateup_tile(const GroupedArgs &a, int e, int rt,
   const int rbase = rt * GT_TM + 32 * wv;
   const BufRsrc W[2] = {buf_rsrc(Wg, wbytes), buf_rsrc(Wu, wbytes)};
   const BufRsrc S[2] = {buf_rsrc(Sg, sbytes), buf_rsrc(Su, sbytes)};
-  gemm_k_loop<AFMT, 2>(acc, W, S, buf_rsrc(a.xb, a.xb_bytes), H, rbase, rows_s[tid >> 2], nf, bt);
+  gemm_k_loop<AFMT, 2>(acc, W, S, buf_rsrc(a.xb, a.xb_bytes), H, rbase, rows_s, nf, bt);
   // epilogue: y = bf16((silu(bf16(g)) * bf16(u)) * w), per-128 requant,
   // stored as the exact BF16 of the dequantised FP8 value
   float y[2][4][4];
@@ -879,7 +889,7 @@ __device__ __forceinline__ void down_tile(const GroupedArgs &a, int e, int rt, i
   const int rbase = rt * GT_TM + 32 * wv;
   const BufRsrc W[1] = {buf_rsrc(Wp, wbytes)};
   const BufRsrc S[1] = {buf_rsrc(Sp, sbytes)};
-  gemm_k_loop<AFMT, 1>(acc, W, S, buf_rsrc(a.yb, a.yb_bytes), I, rbase, rows_s[tid >> 2], nf, bt);
+  gemm_k_loop<AFMT, 1>(acc, W, S, buf_rsrc(a.yb, a.yb_bytes), I, rbase, rows_s, nf, bt);
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
     const int j = 16 * c + l % 16;
