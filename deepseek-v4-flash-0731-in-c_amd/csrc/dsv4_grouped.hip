@@ -926,16 +926,31 @@ __global__ __launch_bounds__(256) void k_grouped_down(GroupedArgs a) {
 
 // out[t][i] = bf16(((0 + r_0) + ... + r_{K-1}) + shared), routes in
 // ascending expert id (src/dsv4/dsv4_model.c:7096-7112).
+// out[t][c .. c + 7]: the routes in ascending expert id, then the shared
+// expert (route slot K), each element summed in that order
+// (src/dsv4/dsv4_model.c:6795-6805); 16-byte loads of 8 BF16 columns.
 __global__ void k_combine_batch(float *__restrict__ out, const uint16_t *__restrict__ ro, int T,
                                 int K, int H) {
-  const size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
-  if (i >= (size_t)T * H) return;
-  const size_t t = i / H, c = i % H;
+  const size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;  // 8-column group
+  const size_t g8 = (size_t)H / 8;
+  if (i >= (size_t)T * g8) return;
+  const size_t t = i / g8, c = (i % g8) * 8;
   const uint16_t *r = ro + t * (size_t)(K + 1) * H + c;
-  float acc = 0.0f;
-  for (int k = 0; k < K; ++k) acc += bf16_to_f32(r[(size_t)k * H]);
-  acc += bf16_to_f32(r[(size_t)K * H]);
-  out[i] = bf16_round(acc);
+  float acc[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
+  for (int k = 0; k <= K; ++k) {
+    const uint4 v = *reinterpret_cast<const uint4 *>(r + (size_t)k * H);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      acc[2 * j] += u2f(w[j] << 16);
+      acc[2 * j + 1] += u2f(w[j] & 0xFFFF0000u);
+    }
+  }
+  float4 *o = reinterpret_cast<float4 *>(out + t * (size_t)H + c);
+  o[0] = make_float4(bf16_round(acc[0]), bf16_round(acc[1]), bf16_round(acc[2]), bf16_round(acc[3]));
+  o[1] = make_float4(bf16_round(acc[4]), bf16_round(acc[5]), bf16_round(acc[6]), bf16_round(acc[7]));
 }
 
 }  // namespace dsv4
@@ -1102,7 +1117,7 @@ int dsv4g_moe_forward_batch(float *out, const float *x, const DSV4GLayer *L,
                      dim3(256), 0, st, g);
   DSV4G_TRY(dsv4g_check_launch("grouped_down_shared"));
   // 6. combine
-  const size_t total = (size_t)T * H;
+  const size_t total = (size_t)T * H / 8;  // 8-column groups (H % 128 == 0)
   hipLaunchKernelGGL(k_combine_batch, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st,
                      out, w.ro, T, K, H);
   DSV4G_TRY(dsv4g_check_launch("combine_batch"));
