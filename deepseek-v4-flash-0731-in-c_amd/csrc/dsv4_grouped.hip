@@ -132,51 +132,116 @@ __global__ __launch_bounds__(64) void k_batch_quant(uint16_t *__restrict__ xb,
 
 // ---------------------------------------------------------- router ------
 // Approximate logits and sum|g*x| with BF16 MFMA. Tile: 64 tokens x 64
-// experts; wave w takes experts e0+16w..+15 against all 64 tokens.
-__global__ __launch_bounds__(256) void k_router_logits_mfma(float *__restrict__ z,
-                                                            float *__restrict__ zabs,
-                                                            const float *__restrict__ x,
-                                                            const uint16_t *__restrict__ G,
-                                                            int T, int H, int E) {
-  __shared__ __align__(16) uint16_t xs[64 * 40];  // [token][32 + 8 pad] bf16
-  const int t0 = blockIdx.x * 64, e0 = blockIdx.y * 64;
-  const int tid = threadIdx.x, wv = tid / 64, l = tid % 64;
-  const int erow = e0 + 16 * wv + l % 16;
-  v4f acc[4], aab[4];
-  for (int f = 0; f < 4; ++f) {
-    acc[f] = (v4f){0.f, 0.f, 0.f, 0.f};
-    aab[f] = (v4f){0.f, 0.f, 0.f, 0.f};
+// experts; wave w takes experts e0+16w..+15 against all 64 tokens. K runs in
+// steps of 128: x (truncated to BF16: exact for BF16-valued inputs) is staged
+// into a double-buffered LDS tile, one barrier per step; each thread's x and
+// gate operands are loaded two steps ahead into a register ring of
+// range-checked loads (rows past T or E read zeros).
+struct RlRegs {
+  uint4 x[8];  // 4 columns (fp32) of tokens 16 w + 2 i + l / 32, i = 0..7
+  uint4 g[4];  // this lane's gate operands of the step's 4 MFMA k-steps
+};
+
+__device__ __forceinline__ void rl_load(RlRegs &R, BufRsrc rx, uint32_t xo, uint32_t xstep,
+                                        BufRsrc rg, uint32_t go, int k0) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) R.x[i] = buf_load16(rx, xo + i * xstep + 4u * (uint32_t)k0);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) R.g[j] = buf_load16(rg, go + 2u * (uint32_t)(k0 + 32 * j));
+  __builtin_amdgcn_sched_barrier(0);  // issue here, not next to the first use
+}
+
+__device__ __forceinline__ void rl_store(const RlRegs &R, uint16_t *xs, int wv, int l) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint4 u = R.x[i];
+    *reinterpret_cast<uint2 *>(xs + (16 * wv + 2 * i + l / 32) * 136 + 4 * (l % 32)) =
+        make_uint2((u.x >> 16) | (u.y & 0xFFFF0000u), (u.z >> 16) | (u.w & 0xFFFF0000u));
   }
-  const int st = tid / 4, sq = tid % 4;  // staging: token st, 8 columns sq
-  for (int k0 = 0; k0 < H; k0 += 32) {
-    __syncthreads();
-    {
-      uint32_t p[4] = {0, 0, 0, 0};
-      if (t0 + st < T) {
-        const float4 u = *reinterpret_cast<const float4 *>(x + (size_t)(t0 + st) * H + k0 + 8 * sq);
-        const float4 v = *reinterpret_cast<const float4 *>(x + (size_t)(t0 + st) * H + k0 + 8 * sq + 4);
-        // BF16-valued inputs convert exactly (truncation of zero bits)
-        p[0] = (f2u(u.x) >> 16) | (f2u(u.y) & 0xFFFF0000u);
-        p[1] = (f2u(u.z) >> 16) | (f2u(u.w) & 0xFFFF0000u);
-        p[2] = (f2u(v.x) >> 16) | (f2u(v.y) & 0xFFFF0000u);
-        p[3] = (f2u(v.z) >> 16) | (f2u(v.w) & 0xFFFF0000u);
-      }
-      *reinterpret_cast<uint4 *>(xs + st * 40 + 8 * sq) = make_uint4(p[0], p[1], p[2], p[3]);
-    }
-    __syncthreads();
-    uint4 a = make_uint4(0, 0, 0, 0);
-    if (erow < E) a = *reinterpret_cast<const uint4 *>(G + (size_t)erow * H + k0 + 8 * (l / 16));
+}
+
+__device__ __forceinline__ void rl_mfma(v4f (&acc)[4], v4f (&aab)[4], const RlRegs &R,
+                                        const uint16_t *xs, int l) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint4 a = R.g[j];
     const uint4 aa = make_uint4(a.x & 0x7FFF7FFFu, a.y & 0x7FFF7FFFu, a.z & 0x7FFF7FFFu,
                                 a.w & 0x7FFF7FFFu);
 #pragma unroll
     for (int f = 0; f < 4; ++f) {
-      const uint4 b = *reinterpret_cast<const uint4 *>(xs + (16 * f + l % 16) * 40 + 8 * (l / 16));
+      const uint4 b =
+          *reinterpret_cast<const uint4 *>(xs + (16 * f + l % 16) * 136 + 32 * j + 8 * (l / 16));
       const uint4 bb = make_uint4(b.x & 0x7FFF7FFFu, b.y & 0x7FFF7FFFu, b.z & 0x7FFF7FFFu,
                                   b.w & 0x7FFF7FFFu);
       acc[f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
                                                        __builtin_bit_cast(bf16x8, b), acc[f], 0, 0, 0);
       aab[f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, aa),
                                                        __builtin_bit_cast(bf16x8, bb), aab[f], 0, 0, 0);
+    }
+  }
+}
+
+template <int NS>  // H / 128 when known at compile time (fully unrolled K), else 0
+__global__ __launch_bounds__(256) void k_router_logits_mfma(float *__restrict__ z,
+                                                            float *__restrict__ zabs,
+                                                            const float *__restrict__ x,
+                                                            const uint16_t *__restrict__ G,
+                                                            int T, int H, int E) {
+  __shared__ __align__(16) uint16_t xs[2][64 * 136];  // [buf][token][128 + 8 pad] bf16
+  const int t0 = blockIdx.x * 64, e0 = blockIdx.y * 64;
+  const int tid = threadIdx.x, l = tid % 64;
+  const int wv = __builtin_amdgcn_readfirstlane(tid / 64);
+  v4f acc[4], aab[4];
+  for (int f = 0; f < 4; ++f) {
+    acc[f] = (v4f){0.f, 0.f, 0.f, 0.f};
+    aab[f] = (v4f){0.f, 0.f, 0.f, 0.f};
+  }
+  // staging: wave w brings tokens 16 w .. + 15, two 512-byte rows per load
+  // (rows past T lie beyond the range and read zeros)
+  const BufRsrc rx = buf_rsrc(x + (size_t)t0 * H, 4u * (uint32_t)(min(T - t0, 64) * H));
+  const uint32_t xo = 4u * (uint32_t)((16 * wv + l / 32) * H + 4 * (l % 32)), xstep = 8u * H;
+  // one range per wave (a per-lane range would serialise the loads); expert
+  // rows past E lie beyond it and read zeros
+  const int we = e0 + 16 * wv;
+  const uint32_t grange = __builtin_amdgcn_readfirstlane(2u * (uint32_t)(max(min(E - we, 16), 0) * H));
+  const BufRsrc rg = buf_rsrc(G + (size_t)min(we, E - 1) * H, grange);
+  const uint32_t go = 2u * (uint32_t)((l % 16) * H + 8 * (l / 16));
+  RlRegs R[3];
+  rl_load(R[0], rx, xo, xstep, rg, go, 0);
+  rl_load(R[1], rx, xo, xstep, rg, go, 128);
+  rl_store(R[0], xs[0], wv, l);
+  __syncthreads();
+  // step s computes from xs[s & 1] with the gate operands of ring slot s % 3,
+  // stores step s + 1 into the other buffer and loads step s + 2 (loads past
+  // the row end are never used)
+  if constexpr (NS > 0) {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      if (s + 2 < NS) rl_load(R[(s + 2) % 3], rx, xo, xstep, rg, go, 128 * (s + 2));
+      rl_mfma(acc, aab, R[s % 3], xs[s & 1], l);
+      if (s + 1 < NS) {
+        rl_store(R[(s + 1) % 3], xs[(s + 1) & 1], wv, l);
+        __syncthreads();
+      }
+    }
+  } else {
+    // unrolled by three so that the ring slots are compile-time
+    const int ns = H / 128;  // H % 128 == 0
+    for (int s = 0; s < ns; s += 3) {
+      rl_load(R[2], rx, xo, xstep, rg, go, 128 * (s + 2));
+      rl_mfma(acc, aab, R[0], xs[s & 1], l);
+      if (s + 1 < ns) rl_store(R[1], xs[(s + 1) & 1], wv, l);
+      __syncthreads();
+      if (s + 1 >= ns) break;
+      rl_load(R[0], rx, xo, xstep, rg, go, 128 * (s + 3));
+      rl_mfma(acc, aab, R[1], xs[(s + 1) & 1], l);
+      if (s + 2 < ns) rl_store(R[2], xs[s & 1], wv, l);
+      __syncthreads();
+      if (s + 2 >= ns) break;
+      rl_load(R[1], rx, xo, xstep, rg, go, 128 * (s + 4));
+      rl_mfma(acc, aab, R[2], xs[s & 1], l);
+      if (s + 3 < ns) rl_store(R[0], xs[(s + 1) & 1], wv, l);
+      __syncthreads();
     }
   }
   for (int f = 0; f < 4; ++f) {
@@ -1051,8 +1116,15 @@ int dsv4g_moe_forward_batch(float *out, const float *x, const DSV4GLayer *L,
   hipLaunchKernelGGL(k_batch_quant, dim3(H / 128, T), dim3(64), 0, st, w.xb, w.not_bf16, x, H);
   DSV4G_TRY(dsv4g_check_launch("batch_quant"));
   // 2. router
-  hipLaunchKernelGGL(k_router_logits_mfma, dim3((T + 63) / 64, (E + 63) / 64), dim3(256), 0, st,
-                     w.z, w.zabs, x, L->gate_w, T, H, E);
+  {
+    const dim3 grid((T + 63) / 64, (E + 63) / 64);
+    if (H == 4096)
+      hipLaunchKernelGGL(k_router_logits_mfma<32>, grid, dim3(256), 0, st, w.z, w.zabs, x,
+                         L->gate_w, T, H, E);
+    else
+      hipLaunchKernelGGL(k_router_logits_mfma<0>, grid, dim3(256), 0, st, w.z, w.zabs, x,
+                         L->gate_w, T, H, E);
+  }
   hipLaunchKernelGGL(k_router_cand, dim3((T + 3) / 4), dim3(256), 0, st, w.cand, w.ncand, w.z,
                      w.zabs, w.not_bf16, L->bias, L->tid2eid, token_ids, T, H, E, K);
   hipLaunchKernelGGL(k_scan_counts, dim3(1), dim3(1024), 0, st, w.chain_off, w.ncand, T);
