@@ -654,9 +654,33 @@ __device__ __forceinline__ void load_b_ops(uint4 (&op)[4], const uint8_t *bt, in
 template <int AFMT, int NM>
 struct WinRaw {
   uint4 a0[NM][2], a1[NM][2];  // a1: the second 16 bytes of an FP8 fragment
-  uint32_t code[NM][2];
+  uint32_t code[NM][2];        // FP8 only (FP4 codes are staged in LDS per tile)
   uint4 b[4];
 };
+
+// FP4 tiles: the E8M0 codes of the tile's 128 rows of each matrix (in / 32
+// bytes a row, contiguous in the scale matrix) are copied once per tile into
+// LDS with direct-to-LDS loads (1 KB per wave instruction, whole cache
+// lines), instead of one byte per lane per window: a per-window byte load
+// fetches a whole line for every row and misses the L1 each time. Region m
+// starts at m * codes_stride(in). The copy is the first load of each wave,
+// so the in-order wait on the tile's first window covers it, and the
+// first window's barrier publishes it.
+__host__ __device__ constexpr uint32_t codes_stride(int in) {
+  return ((uint32_t)GT_TM * (uint32_t)(in / 32) + 1023u) & ~1023u;
+}
+
+template <int NM>
+__device__ __forceinline__ void stage_codes(uint8_t *cs, const BufRsrc (&S)[NM], int rt, int in) {
+  const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), l = threadIdx.x % 64;
+  const uint32_t bytes = (uint32_t)GT_TM * (uint32_t)(in / 32), cst = codes_stride(in);
+#pragma unroll
+  for (int m = 0; m < NM; ++m)
+    for (uint32_t o = 1024u * wv; o < cst; o += 4096u)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          S[m], (__attribute__((address_space(3))) void *)(cs + m * cst + o), 16,
+          (uint32_t)rt * bytes + o + 16u * l, 0, 0, 0);
+}
 
 // W[m], S[m]: buffers of matrix m and its scales; in: K width; rbase: the
 // wave's first row; brow[k]: the activation row of tile row tid / 16 + 16 k
@@ -682,8 +706,6 @@ __device__ __forceinline__ void win_load_part(WinRaw<AFMT, NM> &R, int part,
         const uint32_t row = (uint32_t)(rbase + 16 * f + l % 16);
         if (AFMT == MX_FP4) {
           R.a0[m][f] = buf_load16(W[m], ok ? row * (uint32_t)(in / 2) + sw * 64u + g * 16u : GT_BAD);
-          R.code[m][f] = __builtin_amdgcn_raw_buffer_load_b8(
-              S[m], ok ? row * (uint32_t)(in / 32) + sw * 4u + g : GT_BAD, 0, 0);
         } else {
           const uint32_t o = ok ? row * (uint32_t)in + sw * 128u + g * 32u : GT_BAD;
           R.a0[m][f] = buf_load16(W[m], o);
@@ -747,7 +769,8 @@ __device__ __forceinline__ uint4 win_op(uint4 r0, uint4 r1, uint32_t code, int q
 template <int AFMT, int NM>
 __device__ __forceinline__ void gemm_k_loop(v4f (&acc)[NM][2][4], const BufRsrc (&W)[NM],
                                             const BufRsrc (&S)[NM], BufRsrc bsrc, int in,
-                                            int rbase, const int *rows, int nf, uint8_t *bt) {
+                                            int rbase, const int *rows, int nf, uint8_t *bt,
+                                            const uint8_t *cs) {
   const int tid = threadIdx.x, l = tid % 64;
   const int nsw = in / 128;
   int brow[4];
@@ -778,12 +801,21 @@ __device__ __forceinline__ void gemm_k_loop(v4f (&acc)[NM][2][4], const BufRsrc 
         for (int f = 0; f < 2; ++f) {
           A0[m][f] = Rc.a0[m][f];
           A1[m][f] = Rc.a1[m][f];
-          Ac[m][f] = Rc.code[m][f];
+          Ac[m][f] = AFMT == MX_FP4 ? 0u : Rc.code[m][f];
         }
       const bool pre = i + GT_DEPTH < GT_CHUNK;  // refill this ring slot, window sw + DEPTH
       __syncthreads();
       if (sw >= nsw && pre) win_load<AFMT, NM>(Rc, W, S, bsrc, in, rbase, brow, sw + GT_DEPTH, nsw);
       if (sw < nsw) {
+        if (AFMT == MX_FP4) {
+          // this lane's code of window sw: row rbase % 128 + 16 f + l % 16,
+          // byte 4 sw + l / 16
+          const uint8_t *cp = cs + (rbase % GT_TM + l % 16) * (in / 32) + 4 * sw + l / 16;
+#pragma unroll
+          for (int m = 0; m < NM; ++m)
+#pragma unroll
+            for (int f = 0; f < 2; ++f) Ac[m][f] = cp[m * codes_stride(in) + 16 * f * (in / 32)];
+        }
         // every fragment, whatever nf: rows past the tile are staged as
         // zeros, and branches here would serialise the LDS reads. The
         // activation operands of step q + 1 are read during step q's MFMAs.
@@ -822,7 +854,7 @@ __device__ __forceinline__ void gemm_k_loop(v4f (&acc)[NM][2][4], const BufRsrc 
 template <int AFMT>
 __device__ __forceinline__ void gateup_tile(const GroupedArgs &a, int e, int rt, int p0, int np,
                                             uint8_t *bt, int *rows_s, float *wt_s,
-                                            float (*amax_s)[GT_TN], uint64_t *s_tab) {
+                                            float (*amax_s)[GT_TN], uint64_t *s_tab, uint8_t *cs) {
   const int tid = threadIdx.x, wv = tid / 64, l = tid % 64;
   const int H = a.H, I = a.I;
   const uint8_t *Wg, *Wu, *Sg, *Su;
@@ -860,7 +892,8 @@ __device__ __forceinline__ void gateup_tile(const GroupedArgs &a, int e, int rt,
   const int rbase = rt * GT_TM + 32 * wv;
   const BufRsrc W[2] = {buf_rsrc(Wg, wbytes), buf_rsrc(Wu, wbytes)};
   const BufRsrc S[2] = {buf_rsrc(Sg, sbytes), buf_rsrc(Su, sbytes)};
-  gemm_k_loop<AFMT, 2>(acc, W, S, buf_rsrc(a.xb, a.xb_bytes), H, rbase, rows_s, nf, bt);
+  if (AFMT == MX_FP4) stage_codes<2>(cs, S, rt, H);
+  gemm_k_loop<AFMT, 2>(acc, W, S, buf_rsrc(a.xb, a.xb_bytes), H, rbase, rows_s, nf, bt, cs);
   // epilogue: y = bf16((silu(bf16(g)) * bf16(u)) * w), per-128 requant,
   // stored as the exact BF16 of the dequantised FP8 value
   float y[2][4][4];
@@ -916,6 +949,7 @@ __global__ __launch_bounds__(256) void k_grouped_gateup(GroupedArgs a) {
   __shared__ float wt_s[GT_TN];
   __shared__ float amax_s[4][GT_TN];
   __shared__ uint64_t s_tab[32];
+  extern __shared__ __align__(16) uint8_t codes_s[];  // FP4: 2 x codes_stride(H)
   int tt, rt;
   tile_coords(a.row_tiles, tt, rt);
   if (AFMT == MX_FP8) tt += a.tile_off[a.E];
@@ -923,12 +957,12 @@ __global__ __launch_bounds__(256) void k_grouped_gateup(GroupedArgs a) {
   const int e = AFMT == MX_FP8 ? a.E : tile_expert(a.tile_off, a.E, tt);
   const int p0 = a.pos_off[e] + (tt - a.tile_off[e]) * GT_TN;
   const int np = min(GT_TN, a.pos_off[e + 1] - p0);
-  gateup_tile<AFMT>(a, e, rt, p0, np, bt, rows_s, wt_s, amax_s, s_tab);
+  gateup_tile<AFMT>(a, e, rt, p0, np, bt, rows_s, wt_s, amax_s, s_tab, codes_s);
 }
 
 template <int AFMT>
 __device__ __forceinline__ void down_tile(const GroupedArgs &a, int e, int rt, int p0, int np,
-                                          uint8_t *bt, int *rows_s) {
+                                          uint8_t *bt, int *rows_s, uint8_t *cs) {
   const int tid = threadIdx.x, wv = tid / 64, l = tid % 64;
   const int H = a.H, I = a.I;
   const uint8_t *Wp, *Sp;
@@ -954,7 +988,8 @@ __device__ __forceinline__ void down_tile(const GroupedArgs &a, int e, int rt, i
   const int rbase = rt * GT_TM + 32 * wv;
   const BufRsrc W[1] = {buf_rsrc(Wp, wbytes)};
   const BufRsrc S[1] = {buf_rsrc(Sp, sbytes)};
-  gemm_k_loop<AFMT, 1>(acc, W, S, buf_rsrc(a.yb, a.yb_bytes), I, rbase, rows_s, nf, bt);
+  if (AFMT == MX_FP4) stage_codes<1>(cs, S, rt, I);
+  gemm_k_loop<AFMT, 1>(acc, W, S, buf_rsrc(a.yb, a.yb_bytes), I, rbase, rows_s, nf, bt, cs);
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
     const int j = 16 * c + l % 16;
@@ -979,6 +1014,7 @@ template <int AFMT>
 __global__ __launch_bounds__(256) void k_grouped_down(GroupedArgs a) {
   __shared__ __align__(16) uint8_t bt[2 * GT_BT_BYTES];
   __shared__ int rows_s[GT_TN];
+  extern __shared__ __align__(16) uint8_t codes_s[];  // FP4: codes_stride(I)
   int tt, rt;
   tile_coords(a.row_tiles, tt, rt);
   if (AFMT == MX_FP8) tt += a.tile_off[a.E];
@@ -986,7 +1022,7 @@ __global__ __launch_bounds__(256) void k_grouped_down(GroupedArgs a) {
   const int e = AFMT == MX_FP8 ? a.E : tile_expert(a.tile_off, a.E, tt);
   const int p0 = a.pos_off[e] + (tt - a.tile_off[e]) * GT_TN;
   const int np = min(GT_TN, a.pos_off[e + 1] - p0);
-  down_tile<AFMT>(a, e, rt, p0, np, bt, rows_s);
+  down_tile<AFMT>(a, e, rt, p0, np, bt, rows_s, codes_s);
 }
 
 // out[t][i] = bf16(((0 + r_0) + ... + r_{K-1}) + shared), routes in
@@ -1175,15 +1211,26 @@ int dsv4g_moe_forward_batch(float *out, const float *x, const DSV4GLayer *L,
   const long routed_bound = ((long)T * K + GT_TN - 1) / GT_TN + E;
   const long shared_tiles = (T + GT_TN - 1) / GT_TN;
   g.row_tiles = I / GT_TM;
+  const uint32_t gu_codes = 2u * codes_stride(H), dn_codes = codes_stride(I);
+  {
+    static int attr_set = 0;  // the kernels' dynamic LDS limit (H, I <= 8192: <= 64 KiB)
+    if (!attr_set) {
+      DSV4G_HIP(hipFuncSetAttribute((const void *)k_grouped_gateup<MX_FP4>,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, 65536));
+      DSV4G_HIP(hipFuncSetAttribute((const void *)k_grouped_down<MX_FP4>,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, 65536));
+      attr_set = 1;
+    }
+  }
   hipLaunchKernelGGL(k_grouped_gateup<MX_FP4>, dim3((unsigned)(routed_bound * g.row_tiles)),
-                     dim3(256), 0, st, g);
+                     dim3(256), gu_codes, st, g);
   DSV4G_TRY(dsv4g_check_launch("grouped_gateup"));
   hipLaunchKernelGGL(k_grouped_gateup<MX_FP8>, dim3((unsigned)(shared_tiles * g.row_tiles)),
                      dim3(256), 0, st, g);
   DSV4G_TRY(dsv4g_check_launch("grouped_gateup_shared"));
   g.row_tiles = H / GT_TM;
   hipLaunchKernelGGL(k_grouped_down<MX_FP4>, dim3((unsigned)(routed_bound * g.row_tiles)),
-                     dim3(256), 0, st, g);
+                     dim3(256), dn_codes, st, g);
   DSV4G_TRY(dsv4g_check_launch("grouped_down"));
   hipLaunchKernelGGL(k_grouped_down<MX_FP8>, dim3((unsigned)(shared_tiles * g.row_tiles)),
                      dim3(256), 0, st, g);
