@@ -851,7 +851,121 @@ __device__ __forceinline__ void gemm_k_loop(v4f (&acc)[NM][2][4], const BufRsrc 
   }
 }
 
-template <int AFMT>
+// ---- the FP4 K loop. A row's FP4 weights of two consecutive 128-K windows
+// share one 128-byte cache line (64 bytes each); fetched a window apart,
+// the line leaves the L1 in between and is fetched twice. So the weights are
+// loaded a window pair at a time (both halves of every line back to back)
+// into a two-slot pair ring, issued during the first window of the pair
+// before it (distance 2-3 windows); the activation rows keep one window per
+// slot, two slots, distance 2. Codes come from the tile's LDS copy. The
+// windows are fully unrolled for the model's widths (H = 4096 for gate/up,
+// I = 2048 for down): a loop carrying loads across its back edge is drained
+// at the loop head. Other widths take the per-window loop.
+template <int NM>
+struct Fp4Pair {
+  uint4 w[NM][2][2];  // [matrix][fragment][window of the pair]
+};
+
+template <int NM>
+__device__ __forceinline__ void fp4_pair_load(Fp4Pair<NM> &P, int m, const BufRsrc (&W)[NM],
+                                              int in, int rbase, int pw, int nsw) {
+  const int l = threadIdx.x % 64, g = l / 16;
+#pragma unroll
+  for (int f = 0; f < 2; ++f) {
+    const uint32_t row = (uint32_t)(rbase + 16 * f + l % 16);
+    const uint32_t o = row * (uint32_t)(in / 2) + pw * 64u + g * 16u;
+    P.w[m][f][0] = buf_load16(W[m], pw < nsw ? o : GT_BAD);
+    P.w[m][f][1] = buf_load16(W[m], pw + 1 < nsw ? o + 64u : GT_BAD);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// half h of this thread's activation staging loads of window sw (tile rows
+// tid / 16 + 16 k, k = 2 h, 2 h + 1; 16-byte piece tid % 16)
+__device__ __forceinline__ void act_load(uint4 (&b)[4], int h, BufRsrc bsrc, int in,
+                                         const int (&brow)[4], int sw, int nsw) {
+#pragma unroll
+  for (int k = 2 * h; k < 2 * h + 2; ++k) {
+    const uint32_t bo = (sw < nsw && brow[k] >= 0)
+                            ? 2u * ((uint32_t)brow[k] * (uint32_t)in + sw * 128u) +
+                                  16u * (uint32_t)(threadIdx.x % 16)
+                            : GT_BAD;
+    b[k] = buf_load16(bsrc, bo);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+template <int NM, int NSW>  // NSW = in / 128 windows, fully unrolled
+__device__ __forceinline__ void gemm_k_loop_fp4(v4f (&acc)[NM][2][4], const BufRsrc (&W)[NM],
+                                                BufRsrc bsrc, int in, int rbase, const int *rows,
+                                                uint8_t *bt, const uint8_t *cs) {
+  const int tid = threadIdx.x, l = tid % 64;
+  int brow[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) brow[k] = rows[tid / 16 + 16 * k];
+  // this lane's codes: row rbase % 128 + 16 f + l % 16, byte 4 sw + l / 16
+  const uint8_t *cp = cs + (rbase % GT_TM + l % 16) * (in / 32) + l / 16;
+  Fp4Pair<NM> P[2];
+  uint4 B[2][4];
+#pragma unroll
+  for (int m = 0; m < NM; ++m) fp4_pair_load<NM>(P[0], m, W, in, rbase, 0, NSW);
+  act_load(B[0], 0, bsrc, in, brow, 0, NSW);
+  act_load(B[0], 1, bsrc, in, brow, 0, NSW);
+  act_load(B[1], 0, bsrc, in, brow, 1, NSW);
+  act_load(B[1], 1, bsrc, in, brow, 1, NSW);
+#pragma unroll
+  for (int sw = 0; sw < NSW; ++sw) {
+    uint8_t *bb = bt + (sw & 1) * GT_BT_BYTES;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      *reinterpret_cast<uint4 *>(bb + (tid / 16 + 16 * k) * GT_BROW2 + 16 * (tid % 16)) =
+          B[sw & 1][k];
+    __syncthreads();
+    const bool pre = sw + 2 < NSW;
+    uint32_t Ac[NM][2];
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+      for (int f = 0; f < 2; ++f)
+        Ac[m][f] = cp[m * codes_stride(in) + 16 * f * (in / 32) + 4 * sw];
+    const uint8_t *brow_p = bb + (l % 16) * GT_BROW2 + (l / 16) * 64;
+    uint4 Bq[2][4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      Bq[0][c] = *reinterpret_cast<const uint4 *>(brow_p + 16 * c * GT_BROW2);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (pre) {
+        if (sw % 2 == 0 && q < NM)
+          fp4_pair_load<NM>(P[(sw / 2 + 1) & 1], q, W, in, rbase, sw + 2, NSW);
+        if (q >= 2) act_load(B[sw & 1], q - 2, bsrc, in, brow, sw + 2, NSW);
+      }
+      if (q + 1 < 4) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          Bq[(q + 1) & 1][c] =
+              *reinterpret_cast<const uint4 *>(brow_p + 16 * c * GT_BROW2 + 16 * (q + 1));
+      }
+      uint4 A[NM][2];
+#pragma unroll
+      for (int m = 0; m < NM; ++m)
+#pragma unroll
+        for (int f = 0; f < 2; ++f) {
+          const uint4 r = P[(sw / 2) & 1].w[m][f][sw & 1];
+          A[m][f] = win_op<MX_FP4>(r, r, Ac[m][f], q);
+        }
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int m = 0; m < NM; ++m)
+#pragma unroll
+          for (int f = 0; f < 2; ++f)
+            acc[m][f][c] = mfma_bf16(A[m][f], Bq[q & 1][c], acc[m][f][c]);
+    }
+  }
+}
+
+template <int AFMT, int NSW>  // NSW > 0: FP4 with H = 128 NSW, the unrolled loop
 __device__ __forceinline__ void gateup_tile(const GroupedArgs &a, int e, int rt, int p0, int np,
                                             uint8_t *bt, int *rows_s, float *wt_s,
                                             float (*amax_s)[GT_TN], uint64_t *s_tab, uint8_t *cs) {
@@ -893,7 +1007,10 @@ __device__ __forceinline__ void gateup_tile(const GroupedArgs &a, int e, int rt,
   const BufRsrc W[2] = {buf_rsrc(Wg, wbytes), buf_rsrc(Wu, wbytes)};
   const BufRsrc S[2] = {buf_rsrc(Sg, sbytes), buf_rsrc(Su, sbytes)};
   if (AFMT == MX_FP4) stage_codes<2>(cs, S, rt, H);
-  gemm_k_loop<AFMT, 2>(acc, W, S, buf_rsrc(a.xb, a.xb_bytes), H, rbase, rows_s, nf, bt, cs);
+  if constexpr (NSW > 0)
+    gemm_k_loop_fp4<2, NSW>(acc, W, buf_rsrc(a.xb, a.xb_bytes), H, rbase, rows_s, bt, cs);
+  else
+    gemm_k_loop<AFMT, 2>(acc, W, S, buf_rsrc(a.xb, a.xb_bytes), H, rbase, rows_s, nf, bt, cs);
   // epilogue: y = bf16((silu(bf16(g)) * bf16(u)) * w), per-128 requant,
   // stored as the exact BF16 of the dequantised FP8 value
   float y[2][4][4];
@@ -942,7 +1059,7 @@ __device__ __forceinline__ void gateup_tile(const GroupedArgs &a, int e, int rt,
 // each with the registers of its own format. grid.x = token-tile bound x row
 // tiles (I / 128); FP4: tiles [0, tile_off[E]) (beyond the actual count exit
 // at once); FP8: the shared expert's tiles from tile_off[E].
-template <int AFMT>
+template <int AFMT, int NSW>
 __global__ __launch_bounds__(256) void k_grouped_gateup(GroupedArgs a) {
   __shared__ __align__(16) uint8_t bt[2 * GT_BT_BYTES];
   __shared__ int rows_s[GT_TN];
@@ -957,10 +1074,10 @@ __global__ __launch_bounds__(256) void k_grouped_gateup(GroupedArgs a) {
   const int e = AFMT == MX_FP8 ? a.E : tile_expert(a.tile_off, a.E, tt);
   const int p0 = a.pos_off[e] + (tt - a.tile_off[e]) * GT_TN;
   const int np = min(GT_TN, a.pos_off[e + 1] - p0);
-  gateup_tile<AFMT>(a, e, rt, p0, np, bt, rows_s, wt_s, amax_s, s_tab, codes_s);
+  gateup_tile<AFMT, NSW>(a, e, rt, p0, np, bt, rows_s, wt_s, amax_s, s_tab, codes_s);
 }
 
-template <int AFMT>
+template <int AFMT, int NSW>  // NSW > 0: FP4 with I = 128 NSW, the unrolled loop
 __device__ __forceinline__ void down_tile(const GroupedArgs &a, int e, int rt, int p0, int np,
                                           uint8_t *bt, int *rows_s, uint8_t *cs) {
   const int tid = threadIdx.x, wv = tid / 64, l = tid % 64;
@@ -989,7 +1106,10 @@ __device__ __forceinline__ void down_tile(const GroupedArgs &a, int e, int rt, i
   const BufRsrc W[1] = {buf_rsrc(Wp, wbytes)};
   const BufRsrc S[1] = {buf_rsrc(Sp, sbytes)};
   if (AFMT == MX_FP4) stage_codes<1>(cs, S, rt, I);
-  gemm_k_loop<AFMT, 1>(acc, W, S, buf_rsrc(a.yb, a.yb_bytes), I, rbase, rows_s, nf, bt, cs);
+  if constexpr (NSW > 0)
+    gemm_k_loop_fp4<1, NSW>(acc, W, buf_rsrc(a.yb, a.yb_bytes), I, rbase, rows_s, bt, cs);
+  else
+    gemm_k_loop<AFMT, 1>(acc, W, S, buf_rsrc(a.yb, a.yb_bytes), I, rbase, rows_s, nf, bt, cs);
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
     const int j = 16 * c + l % 16;
@@ -1010,7 +1130,7 @@ __device__ __forceinline__ void down_tile(const GroupedArgs &a, int e, int rt, i
   }
 }
 
-template <int AFMT>
+template <int AFMT, int NSW>
 __global__ __launch_bounds__(256) void k_grouped_down(GroupedArgs a) {
   __shared__ __align__(16) uint8_t bt[2 * GT_BT_BYTES];
   __shared__ int rows_s[GT_TN];
@@ -1022,7 +1142,7 @@ __global__ __launch_bounds__(256) void k_grouped_down(GroupedArgs a) {
   const int e = AFMT == MX_FP8 ? a.E : tile_expert(a.tile_off, a.E, tt);
   const int p0 = a.pos_off[e] + (tt - a.tile_off[e]) * GT_TN;
   const int np = min(GT_TN, a.pos_off[e + 1] - p0);
-  down_tile<AFMT>(a, e, rt, p0, np, bt, rows_s, codes_s);
+  down_tile<AFMT, NSW>(a, e, rt, p0, np, bt, rows_s, codes_s);
 }
 
 // out[t][i] = bf16(((0 + r_0) + ... + r_{K-1}) + shared), routes in
@@ -1212,27 +1332,35 @@ int dsv4g_moe_forward_batch(float *out, const float *x, const DSV4GLayer *L,
   const long shared_tiles = (T + GT_TN - 1) / GT_TN;
   g.row_tiles = I / GT_TM;
   const uint32_t gu_codes = 2u * codes_stride(H), dn_codes = codes_stride(I);
+  // FP4 kernels: the unrolled K loop for the model's widths, else the
+  // per-window loop
+  const void *gu4 = H == 4096 ? (const void *)k_grouped_gateup<MX_FP4, 32>
+                              : (const void *)k_grouped_gateup<MX_FP4, 0>;
+  const void *dn4 = I == 2048 ? (const void *)k_grouped_down<MX_FP4, 16>
+                              : (const void *)k_grouped_down<MX_FP4, 0>;
   {
     static int attr_set = 0;  // the kernels' dynamic LDS limit (H, I <= 8192: <= 64 KiB)
     if (!attr_set) {
-      DSV4G_HIP(hipFuncSetAttribute((const void *)k_grouped_gateup<MX_FP4>,
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, 65536));
-      DSV4G_HIP(hipFuncSetAttribute((const void *)k_grouped_down<MX_FP4>,
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, 65536));
+      const void *fs[4] = {(const void *)k_grouped_gateup<MX_FP4, 32>,
+                           (const void *)k_grouped_gateup<MX_FP4, 0>,
+                           (const void *)k_grouped_down<MX_FP4, 16>,
+                           (const void *)k_grouped_down<MX_FP4, 0>};
+      for (int i = 0; i < 4; ++i)
+        DSV4G_HIP(hipFuncSetAttribute(fs[i], hipFuncAttributeMaxDynamicSharedMemorySize, 65536));
       attr_set = 1;
     }
   }
-  hipLaunchKernelGGL(k_grouped_gateup<MX_FP4>, dim3((unsigned)(routed_bound * g.row_tiles)),
+  hipLaunchKernelGGL((void (*)(GroupedArgs))gu4, dim3((unsigned)(routed_bound * g.row_tiles)),
                      dim3(256), gu_codes, st, g);
   DSV4G_TRY(dsv4g_check_launch("grouped_gateup"));
-  hipLaunchKernelGGL(k_grouped_gateup<MX_FP8>, dim3((unsigned)(shared_tiles * g.row_tiles)),
+  hipLaunchKernelGGL((k_grouped_gateup<MX_FP8, 0>), dim3((unsigned)(shared_tiles * g.row_tiles)),
                      dim3(256), 0, st, g);
   DSV4G_TRY(dsv4g_check_launch("grouped_gateup_shared"));
   g.row_tiles = H / GT_TM;
-  hipLaunchKernelGGL(k_grouped_down<MX_FP4>, dim3((unsigned)(routed_bound * g.row_tiles)),
+  hipLaunchKernelGGL((void (*)(GroupedArgs))dn4, dim3((unsigned)(routed_bound * g.row_tiles)),
                      dim3(256), dn_codes, st, g);
   DSV4G_TRY(dsv4g_check_launch("grouped_down"));
-  hipLaunchKernelGGL(k_grouped_down<MX_FP8>, dim3((unsigned)(shared_tiles * g.row_tiles)),
+  hipLaunchKernelGGL((k_grouped_down<MX_FP8, 0>), dim3((unsigned)(shared_tiles * g.row_tiles)),
                      dim3(256), 0, st, g);
   DSV4G_TRY(dsv4g_check_launch("grouped_down_shared"));
   // 6. combine
