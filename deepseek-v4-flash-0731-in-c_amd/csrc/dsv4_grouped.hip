@@ -659,27 +659,37 @@ struct WinRaw {
 };
 
 // FP4 tiles: the E8M0 codes of the tile's 128 rows of each matrix (in / 32
-// bytes a row, contiguous in the scale matrix) are copied once per tile into
-// LDS with direct-to-LDS loads (1 KB per wave instruction, whole cache
-// lines), instead of one byte per lane per window: a per-window byte load
-// fetches a whole line for every row and misses the L1 each time. Region m
-// starts at m * codes_stride(in). The copy is the first load of each wave,
-// so the in-order wait on the tile's first window covers it, and the
-// first window's barrier publishes it.
+// bytes a row in the scale matrix) are copied once per tile into LDS with
+// direct-to-LDS loads, instead of one byte per lane per window: a
+// per-window byte load fetches a whole line for every row and misses the L1
+// each time. LDS layout of matrix m (from m * codes_stride(in)): [window
+// quad j][row][16 bytes: codes of windows 4 j .. 4 j + 3, 4 per window].
+// A window's code reads (16 rows x 4 bytes, the four lanes of a row reading
+// one dword) then fall in 16 distinct banks; row-major rows of 128 bytes
+// put all 16 rows in two banks (8-way conflicts). Each load instruction
+// moves one quad of 64 rows (the source rows are 16-byte pieces, one per
+// lane). The copy is the first load of each wave, so the in-order wait on
+// the tile's first window covers it, and the first window's barrier
+// publishes it.
 __host__ __device__ constexpr uint32_t codes_stride(int in) {
-  return ((uint32_t)GT_TM * (uint32_t)(in / 32) + 1023u) & ~1023u;
+  return (uint32_t)((in / 128 + 3) / 4) * 16u * GT_TM;
+}
+
+__device__ __forceinline__ uint32_t code_offset(int row, int sw, int g) {
+  return (uint32_t)(sw / 4) * 16u * GT_TM + 16u * row + 4u * (sw % 4) + g;
 }
 
 template <int NM>
 __device__ __forceinline__ void stage_codes(uint8_t *cs, const BufRsrc (&S)[NM], int rt, int in) {
   const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), l = threadIdx.x % 64;
-  const uint32_t bytes = (uint32_t)GT_TM * (uint32_t)(in / 32), cst = codes_stride(in);
+  const uint32_t rowb = (uint32_t)(in / 32), cst = codes_stride(in);
+  const uint32_t nu = 2u * ((in / 128 + 3) / 4);  // (quad, half of the rows) pieces
 #pragma unroll
   for (int m = 0; m < NM; ++m)
-    for (uint32_t o = 1024u * wv; o < cst; o += 4096u)
+    for (uint32_t u = wv; u < nu; u += 4u)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          S[m], (__attribute__((address_space(3))) void *)(cs + m * cst + o), 16,
-          (uint32_t)rt * bytes + o + 16u * l, 0, 0, 0);
+          S[m], (__attribute__((address_space(3))) void *)(cs + m * cst + 1024u * u), 16,
+          ((uint32_t)rt * GT_TM + 64u * (u % 2) + l) * rowb + 16u * (u / 2), 0, 0, 0);
 }
 
 // W[m], S[m]: buffers of matrix m and its scales; in: K width; rbase: the
@@ -810,11 +820,12 @@ __device__ __forceinline__ void gemm_k_loop(v4f (&acc)[NM][2][4], const BufRsrc 
         if (AFMT == MX_FP4) {
           // this lane's code of window sw: row rbase % 128 + 16 f + l % 16,
           // byte 4 sw + l / 16
-          const uint8_t *cp = cs + (rbase % GT_TM + l % 16) * (in / 32) + 4 * sw + l / 16;
 #pragma unroll
           for (int m = 0; m < NM; ++m)
 #pragma unroll
-            for (int f = 0; f < 2; ++f) Ac[m][f] = cp[m * codes_stride(in) + 16 * f * (in / 32)];
+            for (int f = 0; f < 2; ++f)
+              Ac[m][f] = cs[m * codes_stride(in) +
+                            code_offset(rbase % GT_TM + 16 * f + l % 16, sw, l / 16)];
         }
         // every fragment, whatever nf: rows past the tile are staged as
         // zeros, and branches here would serialise the LDS reads. The
@@ -903,8 +914,10 @@ __device__ __forceinline__ void gemm_k_loop_fp4(v4f (&acc)[NM][2][4], const BufR
   int brow[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k) brow[k] = rows[tid / 16 + 16 * k];
-  // this lane's codes: row rbase % 128 + 16 f + l % 16, byte 4 sw + l / 16
-  const uint8_t *cp = cs + (rbase % GT_TM + l % 16) * (in / 32) + l / 16;
+  // this lane's codes: row rbase % 128 + 16 f + l % 16, group l / 16
+  auto code = [&](int m, int f, int sw) -> uint32_t {
+    return cs[m * codes_stride(in) + code_offset(rbase % GT_TM + 16 * f + l % 16, sw, l / 16)];
+  };
   Fp4Pair<NM> P[2];
   uint4 B[2][4];
 #pragma unroll
@@ -913,6 +926,19 @@ __device__ __forceinline__ void gemm_k_loop_fp4(v4f (&acc)[NM][2][4], const BufR
   act_load(B[0], 1, bsrc, in, brow, 0, NSW);
   act_load(B[1], 0, bsrc, in, brow, 1, NSW);
   act_load(B[1], 1, bsrc, in, brow, 1, NSW);
+  // A operands are converted one MFMA step ahead (step q + 1, or the next
+  // window's step 0, during step q's MFMAs), so that the conversions can
+  // issue between the MFMAs instead of in front of them
+  uint32_t Ac[NM][2], Acn[NM][2];
+#pragma unroll
+  for (int m = 0; m < NM; ++m)
+#pragma unroll
+    for (int f = 0; f < 2; ++f) Ac[m][f] = code(m, f, 0);
+  uint4 A[NM][2];
+#pragma unroll
+  for (int m = 0; m < NM; ++m)
+#pragma unroll
+    for (int f = 0; f < 2; ++f) A[m][f] = win_op<MX_FP4>(P[0].w[m][f][0], P[0].w[m][f][0], Ac[m][f], 0);
 #pragma unroll
   for (int sw = 0; sw < NSW; ++sw) {
     uint8_t *bb = bt + (sw & 1) * GT_BT_BYTES;
@@ -922,12 +948,6 @@ __device__ __forceinline__ void gemm_k_loop_fp4(v4f (&acc)[NM][2][4], const BufR
           B[sw & 1][k];
     __syncthreads();
     const bool pre = sw + 2 < NSW;
-    uint32_t Ac[NM][2];
-#pragma unroll
-    for (int m = 0; m < NM; ++m)
-#pragma unroll
-      for (int f = 0; f < 2; ++f)
-        Ac[m][f] = cp[m * codes_stride(in) + 16 * f * (in / 32) + 4 * sw];
     const uint8_t *brow_p = bb + (l % 16) * GT_BROW2 + (l / 16) * 64;
     uint4 Bq[2][4];
 #pragma unroll
@@ -946,14 +966,31 @@ __device__ __forceinline__ void gemm_k_loop_fp4(v4f (&acc)[NM][2][4], const BufR
           Bq[(q + 1) & 1][c] =
               *reinterpret_cast<const uint4 *>(brow_p + 16 * c * GT_BROW2 + 16 * (q + 1));
       }
-      uint4 A[NM][2];
+      if (q == 1 && sw + 1 < NSW) {
 #pragma unroll
-      for (int m = 0; m < NM; ++m)
+        for (int m = 0; m < NM; ++m)
 #pragma unroll
-        for (int f = 0; f < 2; ++f) {
-          const uint4 r = P[(sw / 2) & 1].w[m][f][sw & 1];
-          A[m][f] = win_op<MX_FP4>(r, r, Ac[m][f], q);
-        }
+          for (int f = 0; f < 2; ++f)
+            Acn[m][f] = code(m, f, sw + 1);
+      }
+      uint4 An[NM][2];
+      if (q + 1 < 4) {
+#pragma unroll
+        for (int m = 0; m < NM; ++m)
+#pragma unroll
+          for (int f = 0; f < 2; ++f) {
+            const uint4 r = P[(sw / 2) & 1].w[m][f][sw & 1];
+            An[m][f] = win_op<MX_FP4>(r, r, Ac[m][f], q + 1);
+          }
+      } else if (sw + 1 < NSW) {
+#pragma unroll
+        for (int m = 0; m < NM; ++m)
+#pragma unroll
+          for (int f = 0; f < 2; ++f) {
+            const uint4 r = P[((sw + 1) / 2) & 1].w[m][f][(sw + 1) & 1];
+            An[m][f] = win_op<MX_FP4>(r, r, Acn[m][f], 0);
+          }
+      }
 #pragma unroll
       for (int c = 0; c < 4; ++c)
 #pragma unroll
@@ -961,7 +998,23 @@ __device__ __forceinline__ void gemm_k_loop_fp4(v4f (&acc)[NM][2][4], const BufR
 #pragma unroll
           for (int f = 0; f < 2; ++f)
             acc[m][f][c] = mfma_bf16(A[m][f], Bq[q & 1][c], acc[m][f][c]);
+      // one MFMA, then up to two VALU instructions, repeated
+#pragma unroll
+      for (int i = 0; i < 4 * NM * 2; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+      }
+      if (q + 1 < 4 || sw + 1 < NSW) {
+#pragma unroll
+        for (int m = 0; m < NM; ++m)
+#pragma unroll
+          for (int f = 0; f < 2; ++f) A[m][f] = An[m][f];
+      }
     }
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+      for (int f = 0; f < 2; ++f) Ac[m][f] = Acn[m][f];
   }
 }
 
