@@ -906,14 +906,16 @@ __device__ __forceinline__ void act_load(uint4 (&b)[4], int h, BufRsrc bsrc, int
   __builtin_amdgcn_sched_barrier(0);
 }
 
-template <int NM, int NSW>  // NSW = in / 128 windows, fully unrolled
+// NSW = in / 128 windows, fully unrolled; NF: token fragments computed (a
+// tile of at most 16 NF positions skips the MFMAs and staging of the rest)
+template <int NM, int NSW, int NF>
 __device__ __forceinline__ void gemm_k_loop_fp4(v4f (&acc)[NM][2][4], const BufRsrc (&W)[NM],
                                                 BufRsrc bsrc, int in, int rbase, const int *rows,
                                                 uint8_t *bt, const uint8_t *cs) {
   const int tid = threadIdx.x, l = tid % 64;
   int brow[4];
 #pragma unroll
-  for (int k = 0; k < 4; ++k) brow[k] = rows[tid / 16 + 16 * k];
+  for (int k = 0; k < 4; ++k) brow[k] = k < NF ? rows[tid / 16 + 16 * k] : -1;
   // this lane's codes: row rbase % 128 + 16 f + l % 16, group l / 16
   auto code = [&](int m, int f, int sw) -> uint32_t {
     return cs[m * codes_stride(in) + code_offset(rbase % GT_TM + 16 * f + l % 16, sw, l / 16)];
@@ -943,7 +945,7 @@ __device__ __forceinline__ void gemm_k_loop_fp4(v4f (&acc)[NM][2][4], const BufR
   for (int sw = 0; sw < NSW; ++sw) {
     uint8_t *bb = bt + (sw & 1) * GT_BT_BYTES;
 #pragma unroll
-    for (int k = 0; k < 4; ++k)
+    for (int k = 0; k < NF; ++k)
       *reinterpret_cast<uint4 *>(bb + (tid / 16 + 16 * k) * GT_BROW2 + 16 * (tid % 16)) =
           B[sw & 1][k];
     __syncthreads();
@@ -951,7 +953,7 @@ __device__ __forceinline__ void gemm_k_loop_fp4(v4f (&acc)[NM][2][4], const BufR
     const uint8_t *brow_p = bb + (l % 16) * GT_BROW2 + (l / 16) * 64;
     uint4 Bq[2][4];
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
+    for (int c = 0; c < NF; ++c)
       Bq[0][c] = *reinterpret_cast<const uint4 *>(brow_p + 16 * c * GT_BROW2);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -962,7 +964,7 @@ __device__ __forceinline__ void gemm_k_loop_fp4(v4f (&acc)[NM][2][4], const BufR
       }
       if (q + 1 < 4) {
 #pragma unroll
-        for (int c = 0; c < 4; ++c)
+        for (int c = 0; c < NF; ++c)
           Bq[(q + 1) & 1][c] =
               *reinterpret_cast<const uint4 *>(brow_p + 16 * c * GT_BROW2 + 16 * (q + 1));
       }
@@ -992,7 +994,7 @@ __device__ __forceinline__ void gemm_k_loop_fp4(v4f (&acc)[NM][2][4], const BufR
           }
       }
 #pragma unroll
-      for (int c = 0; c < 4; ++c)
+      for (int c = 0; c < NF; ++c)
 #pragma unroll
         for (int m = 0; m < NM; ++m)
 #pragma unroll
@@ -1000,7 +1002,7 @@ __device__ __forceinline__ void gemm_k_loop_fp4(v4f (&acc)[NM][2][4], const BufR
             acc[m][f][c] = mfma_bf16(A[m][f], Bq[q & 1][c], acc[m][f][c]);
       // one MFMA, then up to two VALU instructions, repeated
 #pragma unroll
-      for (int i = 0; i < 4 * NM * 2; ++i) {
+      for (int i = 0; i < NF * NM * 2; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
       }
@@ -1060,9 +1062,12 @@ __device__ __forceinline__ void gateup_tile(const GroupedArgs &a, int e, int rt,
   const BufRsrc W[2] = {buf_rsrc(Wg, wbytes), buf_rsrc(Wu, wbytes)};
   const BufRsrc S[2] = {buf_rsrc(Sg, sbytes), buf_rsrc(Su, sbytes)};
   if (AFMT == MX_FP4) stage_codes<2>(cs, S, rt, H);
-  if constexpr (NSW > 0)
-    gemm_k_loop_fp4<2, NSW>(acc, W, buf_rsrc(a.xb, a.xb_bytes), H, rbase, rows_s, bt, cs);
-  else
+  if constexpr (NSW > 0) {
+    if (nf <= 2)
+      gemm_k_loop_fp4<2, NSW, 2>(acc, W, buf_rsrc(a.xb, a.xb_bytes), H, rbase, rows_s, bt, cs);
+    else
+      gemm_k_loop_fp4<2, NSW, 4>(acc, W, buf_rsrc(a.xb, a.xb_bytes), H, rbase, rows_s, bt, cs);
+  } else
     gemm_k_loop<AFMT, 2>(acc, W, S, buf_rsrc(a.xb, a.xb_bytes), H, rbase, rows_s, nf, bt, cs);
   // epilogue: y = bf16((silu(bf16(g)) * bf16(u)) * w), per-128 requant,
   // stored as the exact BF16 of the dequantised FP8 value
@@ -1159,9 +1164,12 @@ __device__ __forceinline__ void down_tile(const GroupedArgs &a, int e, int rt, i
   const BufRsrc W[1] = {buf_rsrc(Wp, wbytes)};
   const BufRsrc S[1] = {buf_rsrc(Sp, sbytes)};
   if (AFMT == MX_FP4) stage_codes<1>(cs, S, rt, I);
-  if constexpr (NSW > 0)
-    gemm_k_loop_fp4<1, NSW>(acc, W, buf_rsrc(a.yb, a.yb_bytes), I, rbase, rows_s, bt, cs);
-  else
+  if constexpr (NSW > 0) {
+    if (nf <= 2)
+      gemm_k_loop_fp4<1, NSW, 2>(acc, W, buf_rsrc(a.yb, a.yb_bytes), I, rbase, rows_s, bt, cs);
+    else
+      gemm_k_loop_fp4<1, NSW, 4>(acc, W, buf_rsrc(a.yb, a.yb_bytes), I, rbase, rows_s, bt, cs);
+  } else
     gemm_k_loop<AFMT, 1>(acc, W, S, buf_rsrc(a.yb, a.yb_bytes), I, rbase, rows_s, nf, bt, cs);
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
