@@ -906,41 +906,91 @@ __device__ __forceinline__ void act_load(uint4 (&b)[4], int h, BufRsrc bsrc, int
   __builtin_amdgcn_sched_barrier(0);
 }
 
+// FP8 weights: a window of a row is one whole 128-byte line (32 bytes a
+// lane). Two window slots; window sw + 2 is loaded into the slot of window
+// sw during its last MFMA step (the slot's last conversion is done by then),
+// with the block's E8M0 code (one per 128 rows x 128 K: one byte a wave).
+template <int NM>
+struct Fp8Win {
+  uint4 a0[NM][2], a1[NM][2];
+  uint32_t code[NM];
+};
+
+template <int NM>
+__device__ __forceinline__ void fp8_win_load(Fp8Win<NM> &R, const BufRsrc (&W)[NM],
+                                             const BufRsrc (&S)[NM], int in, int rbase, int sw,
+                                             int nsw) {
+  const int l = threadIdx.x % 64, g = l / 16;
+#pragma unroll
+  for (int m = 0; m < NM; ++m) {
+#pragma unroll
+    for (int f = 0; f < 2; ++f) {
+      const uint32_t row = (uint32_t)(rbase + 16 * f + l % 16);
+      const uint32_t o = sw < nsw ? row * (uint32_t)in + sw * 128u + g * 32u : GT_BAD;
+      R.a0[m][f] = buf_load16(W[m], o);
+      R.a1[m][f] = buf_load16(W[m], o + 16u);
+    }
+    R.code[m] = __builtin_amdgcn_raw_buffer_load_b8(
+        S[m], sw < nsw ? (uint32_t)(rbase / 128) * (uint32_t)(in / 128) + sw : GT_BAD, 0, 0);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+}
+
 // NSW = in / 128 windows, fully unrolled; NF: token fragments computed (a
-// tile of at most 16 NF positions skips the MFMAs and staging of the rest)
-template <int NM, int NSW, int NF>
-__device__ __forceinline__ void gemm_k_loop_fp4(v4f (&acc)[NM][2][4], const BufRsrc (&W)[NM],
-                                                BufRsrc bsrc, int in, int rbase, const int *rows,
-                                                uint8_t *bt, const uint8_t *cs) {
+// tile of at most 16 NF positions skips the MFMAs and staging of the rest).
+// FP4 weights come in window pairs, FP8 weights in window slots (above).
+template <int AFMT, int NM, int NSW, int NF>
+__device__ __forceinline__ void gemm_k_loop_fast(v4f (&acc)[NM][2][4], const BufRsrc (&W)[NM],
+                                                 const BufRsrc (&S)[NM], BufRsrc bsrc, int in,
+                                                 int rbase, const int *rows, uint8_t *bt,
+                                                 const uint8_t *cs) {
+  constexpr bool FP4 = AFMT == MX_FP4;
   const int tid = threadIdx.x, l = tid % 64;
   int brow[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k) brow[k] = k < NF ? rows[tid / 16 + 16 * k] : -1;
-  // this lane's codes: row rbase % 128 + 16 f + l % 16, group l / 16
+  // FP4: this lane's codes: row rbase % 128 + 16 f + l % 16, group l / 16
   auto code = [&](int m, int f, int sw) -> uint32_t {
     return cs[m * codes_stride(in) + code_offset(rbase % GT_TM + 16 * f + l % 16, sw, l / 16)];
   };
   Fp4Pair<NM> P[2];
+  Fp8Win<NM> R8[2];
   uint4 B[2][4];
+  if constexpr (FP4) {
 #pragma unroll
-  for (int m = 0; m < NM; ++m) fp4_pair_load<NM>(P[0], m, W, in, rbase, 0, NSW);
+    for (int m = 0; m < NM; ++m) fp4_pair_load<NM>(P[0], m, W, in, rbase, 0, NSW);
+  } else {
+    fp8_win_load<NM>(R8[0], W, S, in, rbase, 0, NSW);
+    fp8_win_load<NM>(R8[1], W, S, in, rbase, 1, NSW);
+  }
   act_load(B[0], 0, bsrc, in, brow, 0, NSW);
   act_load(B[0], 1, bsrc, in, brow, 0, NSW);
   act_load(B[1], 0, bsrc, in, brow, 1, NSW);
   act_load(B[1], 1, bsrc, in, brow, 1, NSW);
+  // the A operand of (window w, step q): BF16 weights x block scale
+  auto a_op = [&](int w, int m, int f, int q, uint32_t c) -> uint4 {
+    if constexpr (FP4) {
+      const uint4 r = P[(w / 2) & 1].w[m][f][w & 1];
+      return win_op<MX_FP4>(r, r, c, q);
+    } else {
+      return win_op<MX_FP8>(R8[w & 1].a0[m][f], R8[w & 1].a1[m][f], R8[w & 1].code[m], q);
+    }
+  };
   // A operands are converted one MFMA step ahead (step q + 1, or the next
   // window's step 0, during step q's MFMAs), so that the conversions can
   // issue between the MFMAs instead of in front of them
-  uint32_t Ac[NM][2], Acn[NM][2];
+  uint32_t Ac[NM][2] = {}, Acn[NM][2] = {};
+  if constexpr (FP4) {
 #pragma unroll
-  for (int m = 0; m < NM; ++m)
+    for (int m = 0; m < NM; ++m)
 #pragma unroll
-    for (int f = 0; f < 2; ++f) Ac[m][f] = code(m, f, 0);
+      for (int f = 0; f < 2; ++f) Ac[m][f] = code(m, f, 0);
+  }
   uint4 A[NM][2];
 #pragma unroll
   for (int m = 0; m < NM; ++m)
 #pragma unroll
-    for (int f = 0; f < 2; ++f) A[m][f] = win_op<MX_FP4>(P[0].w[m][f][0], P[0].w[m][f][0], Ac[m][f], 0);
+    for (int f = 0; f < 2; ++f) A[m][f] = a_op(0, m, f, 0, Ac[m][f]);
 #pragma unroll
   for (int sw = 0; sw < NSW; ++sw) {
     uint8_t *bb = bt + (sw & 1) * GT_BT_BYTES;
@@ -958,8 +1008,12 @@ __device__ __forceinline__ void gemm_k_loop_fp4(v4f (&acc)[NM][2][4], const BufR
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       if (pre) {
-        if (sw % 2 == 0 && q < NM)
-          fp4_pair_load<NM>(P[(sw / 2 + 1) & 1], q, W, in, rbase, sw + 2, NSW);
+        if constexpr (FP4) {
+          if (sw % 2 == 0 && q < NM)
+            fp4_pair_load<NM>(P[(sw / 2 + 1) & 1], q, W, in, rbase, sw + 2, NSW);
+        } else {
+          if (q == 3) fp8_win_load<NM>(R8[sw & 1], W, S, in, rbase, sw + 2, NSW);
+        }
         if (q >= 2) act_load(B[sw & 1], q - 2, bsrc, in, brow, sw + 2, NSW);
       }
       if (q + 1 < 4) {
@@ -968,30 +1022,23 @@ __device__ __forceinline__ void gemm_k_loop_fp4(v4f (&acc)[NM][2][4], const BufR
           Bq[(q + 1) & 1][c] =
               *reinterpret_cast<const uint4 *>(brow_p + 16 * c * GT_BROW2 + 16 * (q + 1));
       }
-      if (q == 1 && sw + 1 < NSW) {
+      if (FP4 && q == 1 && sw + 1 < NSW) {
 #pragma unroll
         for (int m = 0; m < NM; ++m)
 #pragma unroll
-          for (int f = 0; f < 2; ++f)
-            Acn[m][f] = code(m, f, sw + 1);
+          for (int f = 0; f < 2; ++f) Acn[m][f] = code(m, f, sw + 1);
       }
       uint4 An[NM][2];
       if (q + 1 < 4) {
 #pragma unroll
         for (int m = 0; m < NM; ++m)
 #pragma unroll
-          for (int f = 0; f < 2; ++f) {
-            const uint4 r = P[(sw / 2) & 1].w[m][f][sw & 1];
-            An[m][f] = win_op<MX_FP4>(r, r, Ac[m][f], q + 1);
-          }
+          for (int f = 0; f < 2; ++f) An[m][f] = a_op(sw, m, f, q + 1, Ac[m][f]);
       } else if (sw + 1 < NSW) {
 #pragma unroll
         for (int m = 0; m < NM; ++m)
 #pragma unroll
-          for (int f = 0; f < 2; ++f) {
-            const uint4 r = P[((sw + 1) / 2) & 1].w[m][f][(sw + 1) & 1];
-            An[m][f] = win_op<MX_FP4>(r, r, Acn[m][f], 0);
-          }
+          for (int f = 0; f < 2; ++f) An[m][f] = a_op(sw + 1, m, f, 0, Acn[m][f]);
       }
 #pragma unroll
       for (int c = 0; c < NF; ++c)
@@ -1020,7 +1067,7 @@ __device__ __forceinline__ void gemm_k_loop_fp4(v4f (&acc)[NM][2][4], const BufR
   }
 }
 
-template <int AFMT, int NSW>  // NSW > 0: FP4 with H = 128 NSW, the unrolled loop
+template <int AFMT, int NSW>  // NSW > 0: H = 128 NSW, the unrolled loop
 __device__ __forceinline__ void gateup_tile(const GroupedArgs &a, int e, int rt, int p0, int np,
                                             uint8_t *bt, int *rows_s, float *wt_s,
                                             float (*amax_s)[GT_TN], uint64_t *s_tab, uint8_t *cs) {
@@ -1063,10 +1110,11 @@ __device__ __forceinline__ void gateup_tile(const GroupedArgs &a, int e, int rt,
   const BufRsrc S[2] = {buf_rsrc(Sg, sbytes), buf_rsrc(Su, sbytes)};
   if (AFMT == MX_FP4) stage_codes<2>(cs, S, rt, H);
   if constexpr (NSW > 0) {
-    if (nf <= 2)
-      gemm_k_loop_fp4<2, NSW, 2>(acc, W, buf_rsrc(a.xb, a.xb_bytes), H, rbase, rows_s, bt, cs);
+    const BufRsrc xr = buf_rsrc(a.xb, a.xb_bytes);
+    if (AFMT == MX_FP4 && nf <= 2)
+      gemm_k_loop_fast<AFMT, 2, NSW, 2>(acc, W, S, xr, H, rbase, rows_s, bt, cs);
     else
-      gemm_k_loop_fp4<2, NSW, 4>(acc, W, buf_rsrc(a.xb, a.xb_bytes), H, rbase, rows_s, bt, cs);
+      gemm_k_loop_fast<AFMT, 2, NSW, 4>(acc, W, S, xr, H, rbase, rows_s, bt, cs);
   } else
     gemm_k_loop<AFMT, 2>(acc, W, S, buf_rsrc(a.xb, a.xb_bytes), H, rbase, rows_s, nf, bt, cs);
   // epilogue: y = bf16((silu(bf16(g)) * bf16(u)) * w), per-128 requant,
@@ -1135,7 +1183,7 @@ __global__ __launch_bounds__(256) void k_grouped_gateup(GroupedArgs a) {
   gateup_tile<AFMT, NSW>(a, e, rt, p0, np, bt, rows_s, wt_s, amax_s, s_tab, codes_s);
 }
 
-template <int AFMT, int NSW>  // NSW > 0: FP4 with I = 128 NSW, the unrolled loop
+template <int AFMT, int NSW>  // NSW > 0: I = 128 NSW, the unrolled loop
 __device__ __forceinline__ void down_tile(const GroupedArgs &a, int e, int rt, int p0, int np,
                                           uint8_t *bt, int *rows_s, uint8_t *cs) {
   const int tid = threadIdx.x, wv = tid / 64, l = tid % 64;
@@ -1165,10 +1213,11 @@ __device__ __forceinline__ void down_tile(const GroupedArgs &a, int e, int rt, i
   const BufRsrc S[1] = {buf_rsrc(Sp, sbytes)};
   if (AFMT == MX_FP4) stage_codes<1>(cs, S, rt, I);
   if constexpr (NSW > 0) {
-    if (nf <= 2)
-      gemm_k_loop_fp4<1, NSW, 2>(acc, W, buf_rsrc(a.yb, a.yb_bytes), I, rbase, rows_s, bt, cs);
+    const BufRsrc yr = buf_rsrc(a.yb, a.yb_bytes);
+    if (AFMT == MX_FP4 && nf <= 2)
+      gemm_k_loop_fast<AFMT, 1, NSW, 2>(acc, W, S, yr, I, rbase, rows_s, bt, cs);
     else
-      gemm_k_loop_fp4<1, NSW, 4>(acc, W, buf_rsrc(a.yb, a.yb_bytes), I, rbase, rows_s, bt, cs);
+      gemm_k_loop_fast<AFMT, 1, NSW, 4>(acc, W, S, yr, I, rbase, rows_s, bt, cs);
   } else
     gemm_k_loop<AFMT, 1>(acc, W, S, buf_rsrc(a.yb, a.yb_bytes), I, rbase, rows_s, nf, bt, cs);
 #pragma unroll
@@ -1393,12 +1442,16 @@ int dsv4g_moe_forward_batch(float *out, const float *x, const DSV4GLayer *L,
   const long shared_tiles = (T + GT_TN - 1) / GT_TN;
   g.row_tiles = I / GT_TM;
   const uint32_t gu_codes = 2u * codes_stride(H), dn_codes = codes_stride(I);
-  // FP4 kernels: the unrolled K loop for the model's widths, else the
+  // the unrolled K loops for the model's widths, else the
   // per-window loop
   const void *gu4 = H == 4096 ? (const void *)k_grouped_gateup<MX_FP4, 32>
                               : (const void *)k_grouped_gateup<MX_FP4, 0>;
   const void *dn4 = I == 2048 ? (const void *)k_grouped_down<MX_FP4, 16>
                               : (const void *)k_grouped_down<MX_FP4, 0>;
+  const void *gu8 = H == 4096 ? (const void *)k_grouped_gateup<MX_FP8, 32>
+                              : (const void *)k_grouped_gateup<MX_FP8, 0>;
+  const void *dn8 = I == 2048 ? (const void *)k_grouped_down<MX_FP8, 16>
+                              : (const void *)k_grouped_down<MX_FP8, 0>;
   {
     static int attr_set = 0;  // the kernels' dynamic LDS limit (H, I <= 8192: <= 64 KiB)
     if (!attr_set) {
@@ -1414,14 +1467,14 @@ int dsv4g_moe_forward_batch(float *out, const float *x, const DSV4GLayer *L,
   hipLaunchKernelGGL((void (*)(GroupedArgs))gu4, dim3((unsigned)(routed_bound * g.row_tiles)),
                      dim3(256), gu_codes, st, g);
   DSV4G_TRY(dsv4g_check_launch("grouped_gateup"));
-  hipLaunchKernelGGL((k_grouped_gateup<MX_FP8, 0>), dim3((unsigned)(shared_tiles * g.row_tiles)),
+  hipLaunchKernelGGL((void (*)(GroupedArgs))gu8, dim3((unsigned)(shared_tiles * g.row_tiles)),
                      dim3(256), 0, st, g);
   DSV4G_TRY(dsv4g_check_launch("grouped_gateup_shared"));
   g.row_tiles = H / GT_TM;
   hipLaunchKernelGGL((void (*)(GroupedArgs))dn4, dim3((unsigned)(routed_bound * g.row_tiles)),
                      dim3(256), dn_codes, st, g);
   DSV4G_TRY(dsv4g_check_launch("grouped_down"));
-  hipLaunchKernelGGL((k_grouped_down<MX_FP8, 0>), dim3((unsigned)(shared_tiles * g.row_tiles)),
+  hipLaunchKernelGGL((void (*)(GroupedArgs))dn8, dim3((unsigned)(shared_tiles * g.row_tiles)),
                      dim3(256), 0, st, g);
   DSV4G_TRY(dsv4g_check_launch("grouped_down_shared"));
   // 6. combine
