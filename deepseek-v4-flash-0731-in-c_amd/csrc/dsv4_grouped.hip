@@ -382,8 +382,16 @@ __global__ __launch_bounds__(1024) void k_scan_counts(int *__restrict__ off,
 }
 
 // Exact logits of every candidate: the reference's column-order fmaf chain
-// (src/dsv4/dsv4_model.c:298-303), one lane per (token, candidate), packed
-// across tokens; grid-stride over all chains.
+// (src/dsv4/dsv4_model.c:298-303), one lane per (token, candidate). A wave
+// takes 64 consecutive chains (the candidates of a few consecutive tokens).
+// Per 64-column step the wave's 64 gate pieces (128 bytes each) are loaded
+// as whole lines, 8 lanes a row, and staged in the wave's own LDS rows, from
+// which each lane reads its row; x is loaded directly (the lanes of one
+// token share its lines). Both are loaded a step ahead into registers. A
+// lane per chain reading its own row straight from memory touches 64 lines
+// per load instruction, and the L1 cannot hold the rows between uses.
+#define RC_ROW 144          // LDS bytes per staged gate piece (128 + 16: conflict-free row reads)
+#define RC_BAD 0x80000000u  // an offset past the gate matrix (reads zeros)
 __global__ __launch_bounds__(256) void k_router_chains(float *__restrict__ cscore,
                                                        float *__restrict__ cchoice,
                                                        const int *__restrict__ cand,
@@ -392,27 +400,64 @@ __global__ __launch_bounds__(256) void k_router_chains(float *__restrict__ cscor
                                                        const uint16_t *__restrict__ G,
                                                        const float *__restrict__ bias, int T,
                                                        int H, int E) {
+  __shared__ __align__(16) uint8_t gs[4][64 * RC_ROW];
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), l = threadIdx.x % 64;
   const int total = chain_off[T];
-  for (int g = blockIdx.x * blockDim.x + threadIdx.x; g < total; g += gridDim.x * blockDim.x) {
-    int lo = 0, hi = T;  // chain_off[lo] <= g < chain_off[lo+1]
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) / 2;
-      if (chain_off[mid] <= g) lo = mid;
-      else hi = mid;
+  const BufRsrc rg = buf_rsrc(G, 2u * (uint32_t)E * (uint32_t)H);
+  uint8_t *buf = gs[wv];
+  const int nst = H / 64;  // H % 128 == 0
+  for (int g0 = (blockIdx.x * 4 + wv) * 64; g0 < total; g0 += gridDim.x * 256) {
+    const int g = g0 + l;
+    int t = 0, c = 0, e = -1;
+    if (g < total) {
+      int lo = 0, hi = T;  // chain_off[lo] <= g < chain_off[lo+1]
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) / 2;
+        if (chain_off[mid] <= g) lo = mid;
+        else hi = mid;
+      }
+      t = lo;
+      c = g - chain_off[t];
+      e = cand[(size_t)t * E + c];
+      if (e < 0 || e >= E) e = -1;
     }
-    const int t = lo, c = g - chain_off[t];
-    const int e = cand[(size_t)t * E + c];
-    float sc = 0.0f, ch = -__builtin_inff();
-    if (e >= 0 && e < E) {
-      const uint16_t *gr = G + (size_t)e * H;
-      const float *xr = x + (size_t)t * H;
-      float acc = 0.0f;
-      uint4 w0 = *reinterpret_cast<const uint4 *>(gr);
-      for (int c0 = 0; c0 < H; c0 += 8) {
-        const uint4 w = w0;
-        if (c0 + 8 < H) w0 = *reinterpret_cast<const uint4 *>(gr + c0 + 8);
-        const float4 xa = *reinterpret_cast<const float4 *>(xr + c0);
-        const float4 xb = *reinterpret_cast<const float4 *>(xr + c0 + 4);
+    // staging: load k brings piece l % 8 of chain 8 k + l / 8's row
+    uint32_t srow[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int ek = __shfl(e, 8 * k + l / 8, 64);
+      srow[k] = ek >= 0 ? 2u * (uint32_t)ek * (uint32_t)H + 16u * (l % 8) : RC_BAD;
+    }
+    auto goff = [&](int k, int st) { return srow[k] == RC_BAD ? RC_BAD : srow[k] + 128u * st; };
+    const float *xr = x + (size_t)t * H;
+    uint4 gv[8];
+    float4 xv[16];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) gv[k] = buf_load16(rg, goff(k, 0));
+#pragma unroll
+    for (int i = 0; i < 16; ++i) xv[i] = *reinterpret_cast<const float4 *>(xr + 4 * i);
+    float acc = 0.0f;
+    for (int st = 0; st < nst; ++st) {
+      // the wave's LDS operations run in order: these writes follow the
+      // previous step's reads and precede this step's
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        *reinterpret_cast<uint4 *>(buf + (8 * k + l / 8) * RC_ROW + 16 * (l % 8)) = gv[k];
+      float4 xc[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) xc[i] = xv[i];
+      if (st + 1 < nst) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) gv[k] = buf_load16(rg, goff(k, st + 1));
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          xv[i] = *reinterpret_cast<const float4 *>(xr + 64 * (st + 1) + 4 * i);
+      }
+      const uint8_t *mine = buf + l * RC_ROW;
+#pragma unroll
+      for (int cc = 0; cc < 8; ++cc) {
+        const uint4 w = *reinterpret_cast<const uint4 *>(mine + 16 * cc);
+        const float4 xa = xc[2 * cc], xb = xc[2 * cc + 1];
         acc = fmaf(u2f(w.x << 16), xa.x, acc);
         acc = fmaf(u2f(w.x & 0xFFFF0000u), xa.y, acc);
         acc = fmaf(u2f(w.y << 16), xa.z, acc);
@@ -422,13 +467,19 @@ __global__ __launch_bounds__(256) void k_router_chains(float *__restrict__ cscor
         acc = fmaf(u2f(w.w << 16), xb.z, acc);
         acc = fmaf(u2f(w.w & 0xFFFF0000u), xb.w, acc);
       }
-      sc = sqrt_softplus(acc);
-      ch = sc + (bias ? bias[e] : 0.0f);
     }
-    cscore[(size_t)t * E + c] = sc;
-    cchoice[(size_t)t * E + c] = ch;
+    if (g < total) {
+      float sc = 0.0f, ch = -__builtin_inff();
+      if (e >= 0) {
+        sc = sqrt_softplus(acc);
+        ch = sc + (bias ? bias[e] : 0.0f);
+      }
+      cscore[(size_t)t * E + c] = sc;
+      cchoice[(size_t)t * E + c] = ch;
+    }
   }
 }
+
 
 // Per token: the reference selection over the candidates (ascending id,
 // strict '>'), weights from the unbiased scores, exchange sort by id
