@@ -110,23 +110,36 @@ __global__ void k_probe_bf16(float *D, const uint16_t *A, const uint16_t *B) {
 }
 
 // ------------------------------------------------------- batch quant ----
-// Per (token, 128-group) wave: the reference activation quant, stored as the
+// The reference activation quant per (token, 128-group), stored as the
 // exact BF16 value of each quantised element (E4M3 grid value x scale); flags
 // tokens whose x is not BF16-valued (the router bound then widens for them).
-__global__ __launch_bounds__(64) void k_batch_quant(uint16_t *__restrict__ xb,
-                                                    int *__restrict__ not_bf16,
-                                                    const float *__restrict__ x, int H) {
-  const int g = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
-  const float *xr = x + (size_t)t * H + g * 128;
-  const float a = xr[lane], b = xr[lane + 64];
-  const float amax = wave_max(fmaxf(fabsf(a), fabsf(b)));
-  const float scale = act_scale(amax);
+// 16-byte loads: a half wave per group.
+__global__ __launch_bounds__(256) void k_batch_quant(uint16_t *__restrict__ xb,
+                                                     int *__restrict__ not_bf16,
+                                                     const float *__restrict__ x, int T, int H) {
+  // a wave: 256 columns of one token (two groups, 32 lanes x 4 columns each)
+  const size_t w = (blockIdx.x * (size_t)blockDim.x + threadIdx.x) / 64;
+  const int lane = threadIdx.x % 64;
+  const size_t per = (size_t)H / 256;  // H % 128 == 0; an odd half group is handled below
+  const size_t t = w / (per + (H % 256 ? 1 : 0)), c0 = (w % (per + (H % 256 ? 1 : 0))) * 256;
+  if (t >= (size_t)T) return;
+  const int c = (int)c0 + 4 * lane;
+  const bool live = c < H;  // false only for the upper half of a trailing 128-group
+  float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (live) v = *reinterpret_cast<const float4 *>(x + t * H + c);
+  float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));  // within 32 lanes
+  const float scale = act_scale(m);
   const float inv = 1.0f / scale;
-  uint16_t *q = xb + (size_t)t * H + g * 128;
   // dequantised grid value qx * scale: <= 4 significant bits, exact in BF16
-  q[lane] = (uint16_t)(f2u(quant_e4m3(a, inv) * scale) >> 16);
-  q[lane + 64] = (uint16_t)(f2u(quant_e4m3(b, inv) * scale) >> 16);
-  const bool exact = bf16_round(a) == a && bf16_round(b) == b;
+  const uint32_t h0 = f2u(quant_e4m3(v.x, inv) * scale) >> 16;
+  const uint32_t h1 = f2u(quant_e4m3(v.y, inv) * scale) >> 16;
+  const uint32_t h2 = f2u(quant_e4m3(v.z, inv) * scale) >> 16;
+  const uint32_t h3 = f2u(quant_e4m3(v.w, inv) * scale) >> 16;
+  if (live) *reinterpret_cast<uint2 *>(xb + t * H + c) = make_uint2(h0 | (h1 << 16), h2 | (h3 << 16));
+  const bool exact = bf16_round(v.x) == v.x && bf16_round(v.y) == v.y &&
+                     bf16_round(v.z) == v.z && bf16_round(v.w) == v.w;
   if (__any(!exact) && lane == 0) not_bf16[t] = 1;
 }
 
@@ -539,87 +552,109 @@ __global__ void k_router_finalize(int *__restrict__ idx, float *__restrict__ wt,
 }
 
 // -------------------------------------------------------- dispatch -------
-// counts[e] = routes to expert e (block e < E); counts[E] = T (shared).
-__global__ __launch_bounds__(256) void k_dispatch_count(int *__restrict__ counts,
-                                                        const int *__restrict__ idx, int T,
-                                                        int K, int E) {
-  __shared__ int red[4];
-  const int e = blockIdx.x;
-  if (e == E) {
-    if (threadIdx.x == 0) counts[E] = T;
-    return;
-  }
-  int c = 0;
-  for (int i = threadIdx.x; i < T * K; i += 256) c += idx[i] == e;
-  for (int o = 32; o > 0; o >>= 1) c += __shfl_xor(c, o, 64);
-  if (threadIdx.x % 64 == 0) red[threadIdx.x / 64] = c;
+// Dispatch in three passes over the T K routes, in blocks of 256 routes:
+// per-block expert histograms (LDS atomics: counts do not depend on order),
+// prefixes (each block's base within each expert, then expert and tile
+// offsets), and the placement: block b writes its routes of expert e
+// from its base, in route order (a route's rank among the block's earlier
+// routes of the same expert). Positions of an expert are thus in ascending
+// (token, route) order, as one sequential pass would give them.
+#define DP_ROUTES 256
+__global__ __launch_bounds__(256) void k_dispatch_hist(int *__restrict__ bh,
+                                                       const int *__restrict__ idx, int TK,
+                                                       int E) {
+  __shared__ int hist[1024];  // E <= 1024
+  const int b = blockIdx.x, nb = gridDim.x;
+  for (int e = threadIdx.x; e < E; e += 256) hist[e] = 0;
   __syncthreads();
-  if (threadIdx.x == 0) counts[e] = red[0] + red[1] + red[2] + red[3];
+  const int i = b * DP_ROUTES + threadIdx.x;
+  const int e = i < TK ? idx[i] : -1;
+  if (e >= 0 && e < E) atomicAdd(&hist[e], 1);
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += 256) bh[(size_t)e * nb + b] = hist[e];
 }
 
-// Block e: its position and tile offsets (prefix over lower experts) and its
-// position list in ascending (token, route) order.
+// block e: bh[e][b] -> exclusive prefix over the route blocks b; the total
+// into cnt[e]
+__global__ __launch_bounds__(256) void k_dispatch_scan_blocks(int *__restrict__ bh,
+                                                              int *__restrict__ cnt, int nb) {
+  __shared__ int part[256];
+  int *row = bh + (size_t)blockIdx.x * nb;
+  int carry = 0;
+  for (int b0 = 0; b0 < nb; b0 += 256) {
+    const int b = b0 + threadIdx.x;
+    const int v = b < nb ? row[b] : 0;
+    part[threadIdx.x] = v;
+    __syncthreads();
+    for (int o = 1; o < 256; o <<= 1) {
+      const int a = threadIdx.x >= (unsigned)o ? part[threadIdx.x - o] : 0;
+      __syncthreads();
+      part[threadIdx.x] += a;
+      __syncthreads();
+    }
+    if (b < nb) row[b] = carry + part[threadIdx.x] - v;
+    carry += part[255];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) cnt[blockIdx.x] = carry;
+}
+
+// one block of 1024 threads: position and tile offsets over experts (the
+// shared expert is group E)
+__global__ __launch_bounds__(1024) void k_dispatch_scan(const int *__restrict__ cnt,
+                                                        int *__restrict__ pos_off,
+                                                        int *__restrict__ tile_off, int T, int E) {
+  __shared__ int sp[1024], st[1024];
+  const int e = threadIdx.x;
+  const int tot = e < E ? cnt[e] : 0;
+  sp[e] = tot;
+  st[e] = (tot + GT_TN - 1) / GT_TN;
+  __syncthreads();
+  for (int o = 1; o < 1024; o <<= 1) {  // inclusive scans
+    const int a = e >= o ? sp[e - o] : 0, c = e >= o ? st[e - o] : 0;
+    __syncthreads();
+    sp[e] += a;
+    st[e] += c;
+    __syncthreads();
+  }
+  if (e < E) {
+    pos_off[e] = sp[e] - tot;
+    tile_off[e] = st[e] - (tot + GT_TN - 1) / GT_TN;
+  }
+  if (e == 0) {
+    const int P = sp[E - 1], TT = st[E - 1];
+    pos_off[E] = P;
+    tile_off[E] = TT;
+    pos_off[E + 1] = P + T;
+    tile_off[E + 1] = TT + (T + GT_TN - 1) / GT_TN;
+  }
+}
+
 __global__ __launch_bounds__(256) void k_dispatch_fill(
-    int *__restrict__ pos_off, int *__restrict__ tile_off, int *__restrict__ pos_token,
-    int *__restrict__ pos_route, float *__restrict__ pos_wt, const int *__restrict__ counts,
-    const int *__restrict__ idx, const float *__restrict__ wt, int T, int K, int E) {
-  __shared__ int red[8];
-  __shared__ int run;
-  const int e = blockIdx.x, tid = threadIdx.x;
-  int po = 0, to = 0;
-  for (int i = tid; i < e; i += 256) {
-    po += counts[i];
-    to += (counts[i] + GT_TN - 1) / GT_TN;
-  }
-  for (int o = 32; o > 0; o >>= 1) {
-    po += __shfl_xor(po, o, 64);
-    to += __shfl_xor(to, o, 64);
-  }
-  if (tid % 64 == 0) {
-    red[tid / 64] = po;
-    red[4 + tid / 64] = to;
-  }
+    int *__restrict__ pos_token, int *__restrict__ pos_route, float *__restrict__ pos_wt,
+    const int *__restrict__ bh, const int *__restrict__ pos_off, const int *__restrict__ idx,
+    const float *__restrict__ wt, int T, int K, int E) {
+  __shared__ int es[DP_ROUTES];
+  const int b = blockIdx.x, nb = gridDim.x, TK = T * K;
+  const int i = b * DP_ROUTES + threadIdx.x;
+  int e = i < TK ? idx[i] : -1;
+  if (e >= E) e = -1;
+  es[threadIdx.x] = e;
   __syncthreads();
-  po = red[0] + red[1] + red[2] + red[3];
-  to = red[4] + red[5] + red[6] + red[7];
-  if (tid == 0) {
-    pos_off[e] = po;
-    tile_off[e] = to;
-    if (e == E) {
-      pos_off[E + 1] = po + T;
-      tile_off[E + 1] = to + (T + GT_TN - 1) / GT_TN;
-    }
-    run = 0;
+  if (e >= 0) {
+    int rank = 0;
+    for (int k = 0; k < (int)threadIdx.x; ++k) rank += es[k] == e;
+    const int p = pos_off[e] + bh[(size_t)e * nb + b] + rank;
+    pos_token[p] = i / K;
+    pos_route[p] = i % K;
+    pos_wt[p] = wt[i];
   }
-  __syncthreads();
-  if (e == E) {
-    for (int t = tid; t < T; t += 256) {
-      pos_token[po + t] = t;
-      pos_route[po + t] = K;
-      pos_wt[po + t] = 1.0f;
-    }
-    return;
-  }
-  __shared__ int wtot[4];
-  const int wv = tid / 64, l = tid % 64;
-  for (int b = 0; b < T * K; b += 256) {
-    const int i = b + tid;
-    const bool hit = i < T * K && idx[i] == e;
-    const unsigned long long m = __ballot(hit);
-    const int before = __popcll(m & ((1ull << l) - 1ull));
-    if (l == 0) wtot[wv] = __popcll(m);
-    __syncthreads();
-    int woff = 0;
-    for (int q = 0; q < wv; ++q) woff += wtot[q];
-    if (hit) {
-      const int p = po + run + woff + before;
-      pos_token[p] = i / K;
-      pos_route[p] = i % K;
-      pos_wt[p] = wt[i];
-    }
-    __syncthreads();
-    if (tid == 0) run += wtot[0] + wtot[1] + wtot[2] + wtot[3];
-    __syncthreads();
+  // the shared expert's positions: every token, route slot K, weight 1
+  const int p0 = pos_off[E];
+  for (int t = b * DP_ROUTES + threadIdx.x; t < T; t += nb * DP_ROUTES) {
+    pos_token[p0 + t] = t;
+    pos_route[p0 + t] = K;
+    pos_wt[p0 + t] = 1.0f;
   }
 }
 
@@ -1344,7 +1379,7 @@ namespace {
 struct BatchWs {
   uint16_t *xb, *yb;
   float *z, *zabs, *cscore, *cchoice, *wt, *pos_wt;
-  int *not_bf16, *cand, *ncand, *chain_off, *idx, *counts, *pos_off, *tile_off, *pos_token,
+  int *not_bf16, *cand, *ncand, *chain_off, *idx, *counts, *bh, *pos_off, *tile_off, *pos_token,
       *pos_route;
   uint16_t *ro;
   size_t bytes;
@@ -1374,7 +1409,8 @@ BatchWs batch_ws_layout(const DSV4GLayer *L, int T, void *base) {
   w.cchoice = (float *)take(t * E * 4);
   w.idx = (int *)take(t * K * 4);
   w.wt = (float *)take(t * K * 4);
-  w.counts = (int *)take((E + 1) * 4);
+  w.counts = (int *)take(E * 4);
+  w.bh = (int *)take(((t * K + DP_ROUTES - 1) / DP_ROUTES) * E * 4);
   w.pos_off = (int *)take((E + 2) * 4);
   w.tile_off = (int *)take((E + 2) * 4);
   w.pos_token = (int *)take(P * 4);
@@ -1430,7 +1466,11 @@ int dsv4g_moe_forward_batch(float *out, const float *x, const DSV4GLayer *L,
 
   // 1. activation quant (+ BF16-valued check for the router bound)
   hipLaunchKernelGGL(k_fill_zero_i32, dim3((T + 255) / 256), dim3(256), 0, st, w.not_bf16, T);
-  hipLaunchKernelGGL(k_batch_quant, dim3(H / 128, T), dim3(64), 0, st, w.xb, w.not_bf16, x, H);
+  {
+    const size_t waves = (size_t)T * ((H + 255) / 256);
+    hipLaunchKernelGGL(k_batch_quant, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st, w.xb,
+                       w.not_bf16, x, T, H);
+  }
   DSV4G_TRY(dsv4g_check_launch("batch_quant"));
   // 2. router
   {
@@ -1456,9 +1496,15 @@ int dsv4g_moe_forward_batch(float *out, const float *x, const DSV4GLayer *L,
                      L->route_scale);
   DSV4G_TRY(dsv4g_check_launch("router"));
   // 3. dispatch
-  hipLaunchKernelGGL(k_dispatch_count, dim3(E + 1), dim3(256), 0, st, w.counts, w.idx, T, K, E);
-  hipLaunchKernelGGL(k_dispatch_fill, dim3(E + 1), dim3(256), 0, st, w.pos_off, w.tile_off,
-                     w.pos_token, w.pos_route, w.pos_wt, w.counts, w.idx, w.wt, T, K, E);
+  {
+    const int nb = (T * K + DP_ROUTES - 1) / DP_ROUTES;
+    hipLaunchKernelGGL(k_dispatch_hist, dim3(nb), dim3(256), 0, st, w.bh, w.idx, T * K, E);
+    hipLaunchKernelGGL(k_dispatch_scan_blocks, dim3(E), dim3(256), 0, st, w.bh, w.counts, nb);
+    hipLaunchKernelGGL(k_dispatch_scan, dim3(1), dim3(1024), 0, st, w.counts, w.pos_off,
+                       w.tile_off, T, E);
+    hipLaunchKernelGGL(k_dispatch_fill, dim3(nb), dim3(256), 0, st, w.pos_token, w.pos_route,
+                       w.pos_wt, w.bh, w.pos_off, w.idx, w.wt, T, K, E);
+  }
   DSV4G_TRY(dsv4g_check_launch("dispatch"));
   // 4-5. grouped GEMMs
   GroupedArgs g = {};
