@@ -96,23 +96,25 @@ __global__ __launch_bounds__(256) void k_gemv_fp8(GemvArgs a) {
 }
 
 // ======================================================== BF16 GEMV =====
-// y[r] = sum_c bf16(W[r][c]) * x[c], fp32. One wave per row; each lane takes
-// 8-column chunks, fmaf chain in-lane, then a wave tree sum. Not the
-// reference's single column-order chain: results agree to fp32 rounding.
-__global__ __launch_bounds__(256) void k_gemv_bf16(float *__restrict__ y,
-                                                   const float *__restrict__ x,
-                                                   const uint16_t *__restrict__ W, int in,
-                                                   int out, int round_out, size_t y_stride,
-                                                   size_t x_stride) {
-  const int lane = threadIdx.x % 64;
-  const int row = blockIdx.x * 4 + threadIdx.x / 64;
+// y[r] = the reference's column-order chain acc = fmaf(bf16(W[r][c]), x[c],
+// acc) (src/dsv4/dsv4_model.c:298-303; its 8-row AVX2 path runs the same
+// chain per row): one lane per (row, token), the row read 16 bytes at a
+// time, x shared by the wave (one line per load). Bit-exact; the cost is
+// one dependent fmaf per column.
+__global__ __launch_bounds__(64) void k_gemv_bf16(float *__restrict__ y,
+                                                  const float *__restrict__ x,
+                                                  const uint16_t *__restrict__ W, int in,
+                                                  int out, int round_out, size_t y_stride,
+                                                  size_t x_stride) {
+  const int row = blockIdx.x * 64 + threadIdx.x;
   const int b = blockIdx.y;
   if (row >= out) return;
   const float *xb = x + (size_t)b * x_stride;
   const uint16_t *wr = W + (size_t)row * in;
   float acc = 0.0f;
+  int c = 0;
   if ((in & 7) == 0) {
-    for (int c = 8 * lane; c < in; c += 512) {
+    for (; c < in; c += 8) {
       const uint4 w = *reinterpret_cast<const uint4 *>(wr + c);
       const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
@@ -121,60 +123,56 @@ __global__ __launch_bounds__(256) void k_gemv_bf16(float *__restrict__ y,
         acc = fmaf(u2f(wd[d] & 0xFFFF0000u), xb[c + 2 * d + 1], acc);
       }
     }
-  } else {
-    for (int c = lane; c < in; c += 64) acc = fmaf(bf16_to_f32(wr[c]), xb[c], acc);
   }
-  acc = wave_sum(acc);
-  if (lane == 0) y[(size_t)b * y_stride + row] = round_out ? bf16_round(acc) : acc;
+  for (; c < in; ++c) acc = fmaf(bf16_to_f32(wr[c]), xb[c], acc);
+  y[(size_t)b * y_stride + row] = round_out ? bf16_round(acc) : acc;
 }
 
 // ============================================= public float-scale GEMVs ===
 // dsv4_gemv_fp8 / dsv4_gemv_fp8_tbl (src/dsv4/dsv4_ops.c:176-239) and
-// dsv4_gemv_fp4 (src/dsv4/dsv4_ops.c:249-284): one sequential unfused chain
-// per row in the reference; here one wave per row with a tree sum, so results
-// agree to fp32 rounding (max relative error ~1e-6).
-// mode 0: w*(x*s); mode 1: (w*x)*s.
-__global__ __launch_bounds__(256) void k_gemv_fp8_float(float *__restrict__ y,
-                                                        const float *__restrict__ x,
-                                                        const uint8_t *__restrict__ W,
-                                                        const float *__restrict__ wscale,
-                                                        int in, int rows, int block, int mode) {
-  const int lane = threadIdx.x % 64;
-  const int row = blockIdx.x * 4 + threadIdx.x / 64;
+// dsv4_gemv_fp4 (src/dsv4/dsv4_ops.c:249-284): one sequential chain per row,
+// unfused (the reference builds with -ffp-contract=off), here one lane per
+// row with the same expression and column order. Bit-exact.
+// mode 0 (dsv4_gemv_fp8): acc += w * (x * s); mode 1 (_tbl): acc += (w * x) * s.
+__global__ __launch_bounds__(64) void k_gemv_fp8_float(float *__restrict__ y,
+                                                       const float *__restrict__ x,
+                                                       const uint8_t *__restrict__ W,
+                                                       const float *__restrict__ wscale, int in,
+                                                       int rows, int block, int mode) {
+  const int row = blockIdx.x * 64 + threadIdx.x;
   if (row >= rows) return;
   const int cblocks = (in + block - 1) / block;
   const float *srow = wscale + (size_t)(row / block) * cblocks;
   const uint8_t *wr = W + (size_t)row * in;
   float acc = 0.0f;
-  for (int c = lane; c < in; c += 64) {
+  for (int c = 0; c < in; ++c) {
     const float w = e4m3_decode(wr[c]);
     const float s = srow[c / block];
     acc += mode == 0 ? w * (x[c] * s) : (w * x[c]) * s;
   }
-  acc = wave_sum(acc);
-  if (lane == 0) y[row] = acc;
+  y[row] = acc;
 }
 
-__global__ __launch_bounds__(256) void k_gemv_fp4_float(float *__restrict__ y,
-                                                        const float *__restrict__ qx,
-                                                        const float *__restrict__ qscale,
-                                                        const uint8_t *__restrict__ W,
-                                                        const float *__restrict__ wscale,
-                                                        int in, int rows, int group) {
-  const int lane = threadIdx.x % 64;
-  const int row = blockIdx.x * 4 + threadIdx.x / 64;
+// acc += (w * (qx * qs)) * ws, columns in order
+__global__ __launch_bounds__(64) void k_gemv_fp4_float(float *__restrict__ y,
+                                                       const float *__restrict__ qx,
+                                                       const float *__restrict__ qscale,
+                                                       const uint8_t *__restrict__ W,
+                                                       const float *__restrict__ wscale, int in,
+                                                       int rows, int group) {
+  const int row = blockIdx.x * 64 + threadIdx.x;
   if (row >= rows) return;
   const size_t pcols = (size_t)(in + 1) / 2, gcols = (size_t)(in + group - 1) / group;
   const uint8_t *wr = W + (size_t)row * pcols;
+  const float *ws = wscale + (size_t)row * gcols;
   float acc = 0.0f;
-  for (int c = lane; c < in; c += 64) {
+  for (int c = 0; c < in; ++c) {
     const uint32_t b = wr[c >> 1];
     const float w = e2m1_decode((c & 1) ? (b >> 4) : (b & 15u));
     const float xd = qx[c] * qscale[c / 128];
-    acc += (w * xd) * wscale[(size_t)row * gcols + c / group];
+    acc += (w * xd) * ws[c / group];
   }
-  acc = wave_sum(acc);
-  if (lane == 0) y[row] = acc;
+  y[row] = acc;
 }
 
 // ================================================ synthetic quantisers ===
@@ -452,8 +450,8 @@ int dsv4g_gemv_fp8_batch_q(float *y, const float *qx, const float *qscale, int b
 int dsv4g_gemv_bf16(float *y, const float *x, const uint16_t *W, int in, int out,
                     int round_out, int batch, void *stream) {
   if (in <= 0 || out <= 0 || batch <= 0) return dsv4g_fail(DSV4G_EINVAL, "gemv_bf16: bad size");
-  dim3 grid((out + 3) / 4, batch);
-  hipLaunchKernelGGL(k_gemv_bf16, grid, dim3(256), 0, (hipStream_t)stream, y, x, W, in, out,
+  dim3 grid((out + 63) / 64, batch);
+  hipLaunchKernelGGL(k_gemv_bf16, grid, dim3(64), 0, (hipStream_t)stream, y, x, W, in, out,
                      round_out, (size_t)out, (size_t)in);
   return dsv4g_check_launch("gemv_bf16");
 }
@@ -462,7 +460,7 @@ int dsv4g_gemv_fp8_float(float *y, const float *x, const uint8_t *W, const float
                          int in, int rows, int block, int mode, void *stream) {
   if (in <= 0 || rows <= 0 || block <= 0)
     return dsv4g_fail(DSV4G_EINVAL, "gemv_fp8_float: bad size");
-  hipLaunchKernelGGL(k_gemv_fp8_float, dim3((rows + 3) / 4), dim3(256), 0,
+  hipLaunchKernelGGL(k_gemv_fp8_float, dim3((rows + 63) / 64), dim3(64), 0,
                      (hipStream_t)stream, y, x, W, wscale, in, rows, block, mode);
   return dsv4g_check_launch("gemv_fp8_float");
 }
@@ -471,7 +469,7 @@ int dsv4g_gemv_fp4_float(float *y, const float *qx, const float *qscale, const u
                          const float *wscale, int in, int rows, int group, void *stream) {
   if (in <= 0 || rows <= 0 || group <= 0)
     return dsv4g_fail(DSV4G_EINVAL, "gemv_fp4_float: bad size");
-  hipLaunchKernelGGL(k_gemv_fp4_float, dim3((rows + 3) / 4), dim3(256), 0,
+  hipLaunchKernelGGL(k_gemv_fp4_float, dim3((rows + 63) / 64), dim3(64), 0,
                      (hipStream_t)stream, y, qx, qscale, W, wscale, in, rows, group);
   return dsv4g_check_launch("gemv_fp4_float");
 }

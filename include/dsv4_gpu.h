@@ -20,11 +20,11 @@
  *    replace the static moe_forward / moe_forward_batch of
  *    src/dsv4/dsv4_model.c:6599, 6812, which have no exported symbol).
  *
- * Numerics: the decode-path GEMVs, activation quantisation, SwiGLU requant,
- * router (indices and weights) and combine are bit-identical to the
- * reference's scalar loop order. The public float-scale GEMVs, the BF16 GEMV
- * and the grouped-GEMM batch path agree to fp32 rounding (documented
- * tolerance), not bit for bit.
+ * Numerics: the decode-path GEMVs, the public float-scale and BF16 GEMVs,
+ * activation quantisation, SwiGLU requant, router (indices and weights) and
+ * combine are bit-identical to the reference's scalar loop order. The
+ * grouped-GEMM batch path has bit-identical routing and agrees to fp32
+ * rounding otherwise (documented tolerance), not bit for bit.
  */
 #ifndef DSV4_GPU_H
 #define DSV4_GPU_H

@@ -106,16 +106,18 @@ def test_gemvs_golden(env):
     bqx, bqs = T(env, g["g_bqx"]), T(env, g["g_bqs"])
     assert same_bits(H(lib.gemv_fp4_batch_q(bqx, bqs, W4, S4, IN, R)), g["g_fp4_batch"])
     assert same_bits(H(lib.gemv_fp8_batch_q(bqx, bqs, W8, S8, IN, R, 1)), g["g_fp8_batch"])
+    # the standalone BF16 and float-scale GEMVs run the reference's sequential
+    # column-order chain per row: bit-exact
     y = H(lib.gemv_bf16(T(env, g["g_bf16_x"]), T(env, g["g_bf16_W"]), IN, R, 0))[0]
-    assert max_rel_err(y, g["g_bf16"]) < 1e-5
+    assert same_bits(y, g["g_bf16"])
     y = H(lib.gemv_fp8_float(T(env, g["g_bf16_x"]), T(env, g["g_f8_codes"]),
                              T(env, g["g_f8_scales"]), IN, R, 128, 0))
-    assert max_rel_err(y, g["g_fp8_legacy"]) < 1e-5
+    assert same_bits(y, g["g_fp8_legacy"])
     y = H(lib.gemv_fp8_float(T(env, g["g_bf16_x"]), T(env, g["g_f8_codes"]),
                              T(env, g["g_f8_scales"]), IN, R, 128, 1))
-    assert max_rel_err(y, g["g_fp8_tbl"]) < 1e-5
+    assert same_bits(y, g["g_fp8_tbl"])
     y = H(lib.gemv_fp4_float(qx, qs, W4, T(env, g["g_fp4_wscale"]), IN, R, 32))
-    assert max_rel_err(y, g["g_fp4_legacy"]) < 1e-5
+    assert same_bits(y, g["g_fp4_legacy"])
 
 
 @pytest.mark.parametrize("rows,in_", [(2048, 4096), (4096, 2048), (16, 128), (200, 1024)])
@@ -149,6 +151,35 @@ def test_fp8_gemv_full_size_bit_exact(env, rows, in_):
                          orc.gemv_fp8_q(qx[0], qs[0], W, S, in_, rows, ro))
     assert same_bits(H(lib.gemv_fp8_batch_q(gq, gs, gW, gS, in_, rows, 1)),
                      orc.gemv_fp8_batch_q(qx, qs, W, S, in_, rows, 1))
+
+
+@pytest.mark.parametrize("rows,in_", [(256, 4096), (2048, 4096), (37, 200)])
+def test_bf16_and_float_gemvs_full_size_bit_exact(env, rows, in_):
+    """The standalone BF16 GEMV (batch of 3, with and without BF16 output
+    rounding) and the float-scale FP8 / FP4 GEMVs against the oracle's
+    sequential chains at the router's and an expert's full shapes."""
+    orc, lib = env["orc"], env["lib"]
+    rng = np.random.default_rng(rows * 7 + in_)
+    Gb = bf16_bits(rng.standard_normal((rows, in_), dtype=np.float32) * 0.02)
+    x = bf16_input(rng, (3, in_))
+    for ro in (0, 1):
+        y = H(lib.gemv_bf16(T(env, x), T(env, Gb), in_, rows, ro))
+        for t in range(3):
+            assert same_bits(y[t], orc.gemv_bf16(x[t], Gb, in_, rows, ro)), (t, ro)
+    codes = rng.integers(0, 256, (rows, in_), dtype=np.uint8)
+    codes[(codes & 0x7F) == 0x7F] = 0x33
+    fsc = (rng.random(((rows + 127) // 128, (in_ + 127) // 128)) * 0.01 + 1e-4).astype(np.float32)
+    gx, gc, gs = T(env, x[0]), T(env, codes), T(env, fsc)
+    assert same_bits(H(lib.gemv_fp8_float(gx, gc, gs, in_, rows, 128, 0)),
+                     orc.gemv_fp8_legacy(x[0], codes, fsc, in_, rows, 128))
+    assert same_bits(H(lib.gemv_fp8_float(gx, gc, gs, in_, rows, 128, 1)),
+                     orc.gemv_fp8_tbl(x[0], codes, fsc, in_, rows, 128))
+    W4 = rng.integers(0, 256, (rows, (in_ + 1) // 2), dtype=np.uint8)
+    w4s = (rng.random((rows, (in_ + 31) // 32)) * 0.05 + 1e-3).astype(np.float32)
+    qx, qs = orc.quant_fp8_act(x)
+    assert same_bits(H(lib.gemv_fp4_float(T(env, qx[0]), T(env, qs[0]), T(env, W4),
+                                          T(env, w4s), in_, rows, 32)),
+                     orc.gemv_fp4_legacy(qx[0], qs[0], W4, w4s, in_, rows, 32))
 
 
 def test_reference_bench_checksums_on_gpu(env):
