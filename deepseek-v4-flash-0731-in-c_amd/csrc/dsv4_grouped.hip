@@ -31,6 +31,8 @@
 #include "dsv4_device.h"
 #include "dsv4_gpu_internal.h"
 
+#include <mutex>
+
 using namespace dsv4;
 
 typedef int v8i __attribute__((ext_vector_type(8)));
@@ -678,6 +680,7 @@ struct GroupedArgs {
   uint32_t xb_bytes, yb_bytes;
   int H, I, E, K, T, row_tiles;
   float limit;
+  int sh_base;  // the shared expert's positions: sh_base + token (yb rows)
 };
 
 // (token tile, row tile) of this workgroup. Workgroups go to the 8 XCDs
@@ -1181,8 +1184,13 @@ __device__ __forceinline__ void gateup_tile(const GroupedArgs &a, int e, int rt,
     sbytes = (uint32_t)((I + 127) / 128) * (uint32_t)(H / 128);
   }
   if (tid < GT_TN) {
-    rows_s[tid] = tid < np ? a.pos_token[p0 + tid] : -1;
-    wt_s[tid] = tid < np ? a.pos_wt[p0 + tid] : 0.0f;
+    if (AFMT == MX_FP8) {  // shared expert: position sh_base + t, weight 1
+      rows_s[tid] = tid < np ? p0 - a.sh_base + tid : -1;
+      wt_s[tid] = tid < np ? 1.0f : 0.0f;
+    } else {
+      rows_s[tid] = tid < np ? a.pos_token[p0 + tid] : -1;
+      wt_s[tid] = tid < np ? a.pos_wt[p0 + tid] : 0.0f;
+    }
   }
   libm_stage_table(s_tab);  // SwiGLU's expf table, read from LDS in the epilogue
   __syncthreads();
@@ -1259,13 +1267,19 @@ __global__ __launch_bounds__(256) void k_grouped_gateup(GroupedArgs a) {
   __shared__ float amax_s[4][GT_TN];
   __shared__ uint64_t s_tab[32];
   extern __shared__ __align__(16) uint8_t codes_s[];  // FP4: 2 x codes_stride(H)
-  int tt, rt;
+  int tt, rt, e, p0, np;
   tile_coords(a.row_tiles, tt, rt);
-  if (AFMT == MX_FP8) tt += a.tile_off[a.E];
-  if (tt >= a.tile_off[AFMT == MX_FP8 ? a.E + 1 : a.E]) return;
-  const int e = AFMT == MX_FP8 ? a.E : tile_expert(a.tile_off, a.E, tt);
-  const int p0 = a.pos_off[e] + (tt - a.tile_off[e]) * GT_TN;
-  const int np = min(GT_TN, a.pos_off[e + 1] - p0);
+  if (AFMT == MX_FP8) {  // the shared expert: every token, no routing needed
+    if (tt * GT_TN >= a.T) return;
+    e = a.E;
+    p0 = a.sh_base + tt * GT_TN;
+    np = min(GT_TN, a.T - tt * GT_TN);
+  } else {
+    if (tt >= a.tile_off[a.E]) return;
+    e = tile_expert(a.tile_off, a.E, tt);
+    p0 = a.pos_off[e] + (tt - a.tile_off[e]) * GT_TN;
+    np = min(GT_TN, a.pos_off[e + 1] - p0);
+  }
   gateup_tile<AFMT, NSW>(a, e, rt, p0, np, bt, rows_s, wt_s, amax_s, s_tab, codes_s);
 }
 
@@ -1311,7 +1325,8 @@ __device__ __forceinline__ void down_tile(const GroupedArgs &a, int e, int rt, i
     const int j = 16 * c + l % 16;
     if (c >= nf || j >= np) continue;
     const int pos = p0 + j;
-    const int t = a.pos_token[pos], k = a.pos_route[pos];
+    const int t = AFMT == MX_FP8 ? pos - a.sh_base : a.pos_token[pos];
+    const int k = AFMT == MX_FP8 ? a.K : a.pos_route[pos];
     uint16_t *dst = a.ro + ((size_t)t * (a.K + 1) + k) * H;
 #pragma unroll
     for (int f = 0; f < 2; ++f) {
@@ -1331,13 +1346,19 @@ __global__ __launch_bounds__(256) void k_grouped_down(GroupedArgs a) {
   __shared__ __align__(16) uint8_t bt[2 * GT_BT_BYTES];
   __shared__ int rows_s[GT_TN];
   extern __shared__ __align__(16) uint8_t codes_s[];  // FP4: codes_stride(I)
-  int tt, rt;
+  int tt, rt, e, p0, np;
   tile_coords(a.row_tiles, tt, rt);
-  if (AFMT == MX_FP8) tt += a.tile_off[a.E];
-  if (tt >= a.tile_off[AFMT == MX_FP8 ? a.E + 1 : a.E]) return;
-  const int e = AFMT == MX_FP8 ? a.E : tile_expert(a.tile_off, a.E, tt);
-  const int p0 = a.pos_off[e] + (tt - a.tile_off[e]) * GT_TN;
-  const int np = min(GT_TN, a.pos_off[e + 1] - p0);
+  if (AFMT == MX_FP8) {  // the shared expert: every token, no routing needed
+    if (tt * GT_TN >= a.T) return;
+    e = a.E;
+    p0 = a.sh_base + tt * GT_TN;
+    np = min(GT_TN, a.T - tt * GT_TN);
+  } else {
+    if (tt >= a.tile_off[a.E]) return;
+    e = tile_expert(a.tile_off, a.E, tt);
+    p0 = a.pos_off[e] + (tt - a.tile_off[e]) * GT_TN;
+    np = min(GT_TN, a.pos_off[e + 1] - p0);
+  }
   down_tile<AFMT, NSW>(a, e, rt, p0, np, bt, rows_s, codes_s);
 }
 
@@ -1384,6 +1405,38 @@ struct BatchWs {
   uint16_t *ro;
   size_t bytes;
 };
+
+// The shared expert's stream of each device, created on the first call that
+// is not being captured into a graph (creating a stream there is not
+// allowed; such a call runs the shared expert on the caller's stream).
+// Default priority, non-blocking.
+struct SideStream {
+  hipStream_t s;
+  hipEvent_t fork, join;
+};
+std::mutex g_side_mu;
+SideStream g_side[64];
+bool g_side_made[64];
+
+int side_stream(hipStream_t st, SideStream **out) {
+  *out = nullptr;
+  int dev = 0;
+  DSV4G_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= 64) return 0;
+  if (!g_side_made[dev]) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    DSV4G_HIP(hipStreamIsCapturing(st, &cs));
+    if (cs != hipStreamCaptureStatusNone) return 0;
+    SideStream n;
+    DSV4G_HIP(hipStreamCreateWithFlags(&n.s, hipStreamNonBlocking));
+    DSV4G_HIP(hipEventCreateWithFlags(&n.fork, hipEventDisableTiming));
+    DSV4G_HIP(hipEventCreateWithFlags(&n.join, hipEventDisableTiming));
+    g_side[dev] = n;
+    g_side_made[dev] = true;
+  }
+  *out = &g_side[dev];
+  return 0;
+}
 
 BatchWs batch_ws_layout(const DSV4GLayer *L, int T, void *base) {
   const size_t t = (size_t)T, K = (size_t)L->topk, E = (size_t)L->n_experts;
@@ -1472,6 +1525,81 @@ int dsv4g_moe_forward_batch(float *out, const float *x, const DSV4GLayer *L,
                        w.not_bf16, x, T, H);
   }
   DSV4G_TRY(dsv4g_check_launch("batch_quant"));
+  GroupedArgs g = {};
+  g.experts = L->experts;
+  g.expert_stride = L->expert_stride;
+  g.scale_run = L->scale_run;
+  g.shw[0] = L->sh1;
+  g.shw[1] = L->sh3;
+  g.shw[2] = L->sh2;
+  g.shs[0] = L->sh1_s;
+  g.shs[1] = L->sh3_s;
+  g.shs[2] = L->sh2_s;
+  g.tile_off = w.tile_off;
+  g.pos_off = w.pos_off;
+  g.pos_token = w.pos_token;
+  g.pos_route = w.pos_route;
+  g.pos_wt = w.pos_wt;
+  g.xb = w.xb;
+  g.yb = w.yb;
+  g.xb_bytes = (uint32_t)((size_t)T * H * 2);
+  g.yb_bytes = (uint32_t)((size_t)T * (K + 1) * I * 2);
+  g.ro = w.ro;
+  g.H = H;
+  g.I = I;
+  g.E = E;
+  g.K = K;
+  g.T = T;
+  g.limit = (float)(int)L->swiglu_limit;
+  g.sh_base = T * K;  // past every routed position (at most T K)
+  // routed token tiles: at most ceil(T K / 64) + E (one partial tile per
+  // expert); the shared expert's: ceil(T / 64)
+  const long routed_bound = ((long)T * K + GT_TN - 1) / GT_TN + E;
+  const long shared_tiles = (T + GT_TN - 1) / GT_TN;
+  const uint32_t gu_codes = 2u * codes_stride(H), dn_codes = codes_stride(I);
+  // the unrolled K loops for the model's widths, else the
+  // per-window loop
+  const void *gu4 = H == 4096 ? (const void *)k_grouped_gateup<MX_FP4, 32>
+                              : (const void *)k_grouped_gateup<MX_FP4, 0>;
+  const void *dn4 = I == 2048 ? (const void *)k_grouped_down<MX_FP4, 16>
+                              : (const void *)k_grouped_down<MX_FP4, 0>;
+  const void *gu8 = H == 4096 ? (const void *)k_grouped_gateup<MX_FP8, 32>
+                              : (const void *)k_grouped_gateup<MX_FP8, 0>;
+  const void *dn8 = I == 2048 ? (const void *)k_grouped_down<MX_FP8, 16>
+                              : (const void *)k_grouped_down<MX_FP8, 0>;
+  {
+    static int attr_set = 0;  // the kernels' dynamic LDS limit (H, I <= 8192: <= 64 KiB)
+    if (!attr_set) {
+      const void *fs[4] = {(const void *)k_grouped_gateup<MX_FP4, 32>,
+                           (const void *)k_grouped_gateup<MX_FP4, 0>,
+                           (const void *)k_grouped_down<MX_FP4, 16>,
+                           (const void *)k_grouped_down<MX_FP4, 0>};
+      for (int i = 0; i < 4; ++i)
+        DSV4G_HIP(hipFuncSetAttribute(fs[i], hipFuncAttributeMaxDynamicSharedMemorySize, 65536));
+      attr_set = 1;
+    }
+  }
+  // the shared expert needs only the quantised activations: its gate/up and
+  // down run on a second stream beside the router, dispatch and routed
+  // GEMMs (joined before the combine). Calls hold a lock while they enqueue,
+  // so the fork and join events of two calls cannot interleave.
+  std::lock_guard<std::mutex> lock(g_side_mu);
+  SideStream *side = nullptr;
+  DSV4G_TRY(side_stream(st, &side));
+  hipStream_t sst = side ? side->s : st;
+  if (side) {
+    DSV4G_HIP(hipEventRecord(side->fork, st));
+    DSV4G_HIP(hipStreamWaitEvent(sst, side->fork, 0));
+  }
+  g.row_tiles = I / GT_TM;
+  hipLaunchKernelGGL((void (*)(GroupedArgs))gu8, dim3((unsigned)(shared_tiles * g.row_tiles)),
+                     dim3(256), 0, sst, g);
+  DSV4G_TRY(dsv4g_check_launch("grouped_gateup_shared"));
+  g.row_tiles = H / GT_TM;
+  hipLaunchKernelGGL((void (*)(GroupedArgs))dn8, dim3((unsigned)(shared_tiles * g.row_tiles)),
+                     dim3(256), 0, sst, g);
+  DSV4G_TRY(dsv4g_check_launch("grouped_down_shared"));
+  if (side) DSV4G_HIP(hipEventRecord(side->join, sst));
   // 2. router
   {
     const dim3 grid((T + 63) / 64, (E + 63) / 64);
@@ -1506,75 +1634,17 @@ int dsv4g_moe_forward_batch(float *out, const float *x, const DSV4GLayer *L,
                        w.pos_wt, w.bh, w.pos_off, w.idx, w.wt, T, K, E);
   }
   DSV4G_TRY(dsv4g_check_launch("dispatch"));
-  // 4-5. grouped GEMMs
-  GroupedArgs g = {};
-  g.experts = L->experts;
-  g.expert_stride = L->expert_stride;
-  g.scale_run = L->scale_run;
-  g.shw[0] = L->sh1;
-  g.shw[1] = L->sh3;
-  g.shw[2] = L->sh2;
-  g.shs[0] = L->sh1_s;
-  g.shs[1] = L->sh3_s;
-  g.shs[2] = L->sh2_s;
-  g.tile_off = w.tile_off;
-  g.pos_off = w.pos_off;
-  g.pos_token = w.pos_token;
-  g.pos_route = w.pos_route;
-  g.pos_wt = w.pos_wt;
-  g.xb = w.xb;
-  g.yb = w.yb;
-  g.xb_bytes = (uint32_t)((size_t)T * H * 2);
-  g.yb_bytes = (uint32_t)((size_t)T * (K + 1) * I * 2);
-  g.ro = w.ro;
-  g.H = H;
-  g.I = I;
-  g.E = E;
-  g.K = K;
-  g.T = T;
-  g.limit = (float)(int)L->swiglu_limit;
-  // routed token tiles: at most ceil(T K / 64) + E (one partial tile per
-  // expert); the shared expert's: ceil(T / 64)
-  const long routed_bound = ((long)T * K + GT_TN - 1) / GT_TN + E;
-  const long shared_tiles = (T + GT_TN - 1) / GT_TN;
+  // 4-5. routed grouped GEMMs
   g.row_tiles = I / GT_TM;
-  const uint32_t gu_codes = 2u * codes_stride(H), dn_codes = codes_stride(I);
-  // the unrolled K loops for the model's widths, else the
-  // per-window loop
-  const void *gu4 = H == 4096 ? (const void *)k_grouped_gateup<MX_FP4, 32>
-                              : (const void *)k_grouped_gateup<MX_FP4, 0>;
-  const void *dn4 = I == 2048 ? (const void *)k_grouped_down<MX_FP4, 16>
-                              : (const void *)k_grouped_down<MX_FP4, 0>;
-  const void *gu8 = H == 4096 ? (const void *)k_grouped_gateup<MX_FP8, 32>
-                              : (const void *)k_grouped_gateup<MX_FP8, 0>;
-  const void *dn8 = I == 2048 ? (const void *)k_grouped_down<MX_FP8, 16>
-                              : (const void *)k_grouped_down<MX_FP8, 0>;
-  {
-    static int attr_set = 0;  // the kernels' dynamic LDS limit (H, I <= 8192: <= 64 KiB)
-    if (!attr_set) {
-      const void *fs[4] = {(const void *)k_grouped_gateup<MX_FP4, 32>,
-                           (const void *)k_grouped_gateup<MX_FP4, 0>,
-                           (const void *)k_grouped_down<MX_FP4, 16>,
-                           (const void *)k_grouped_down<MX_FP4, 0>};
-      for (int i = 0; i < 4; ++i)
-        DSV4G_HIP(hipFuncSetAttribute(fs[i], hipFuncAttributeMaxDynamicSharedMemorySize, 65536));
-      attr_set = 1;
-    }
-  }
   hipLaunchKernelGGL((void (*)(GroupedArgs))gu4, dim3((unsigned)(routed_bound * g.row_tiles)),
                      dim3(256), gu_codes, st, g);
   DSV4G_TRY(dsv4g_check_launch("grouped_gateup"));
-  hipLaunchKernelGGL((void (*)(GroupedArgs))gu8, dim3((unsigned)(shared_tiles * g.row_tiles)),
-                     dim3(256), 0, st, g);
-  DSV4G_TRY(dsv4g_check_launch("grouped_gateup_shared"));
   g.row_tiles = H / GT_TM;
   hipLaunchKernelGGL((void (*)(GroupedArgs))dn4, dim3((unsigned)(routed_bound * g.row_tiles)),
                      dim3(256), dn_codes, st, g);
   DSV4G_TRY(dsv4g_check_launch("grouped_down"));
-  hipLaunchKernelGGL((void (*)(GroupedArgs))dn8, dim3((unsigned)(shared_tiles * g.row_tiles)),
-                     dim3(256), 0, st, g);
-  DSV4G_TRY(dsv4g_check_launch("grouped_down_shared"));
-  // 6. combine
+  // 6. combine, after the shared expert's stream
+  if (side) DSV4G_HIP(hipStreamWaitEvent(st, side->join, 0));
   const size_t total = (size_t)T * H / 8;  // 8-column groups (H % 128 == 0)
   hipLaunchKernelGGL(k_combine_batch, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st,
                      out, w.ro, T, K, H);

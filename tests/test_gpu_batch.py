@@ -153,3 +153,37 @@ def test_prefill_4096_tokens(env):
     print("\n  tokens per expert: max", counts.max(), "median", int(np.median(counts)))
     check_batch(env, L, X, np.zeros(4096, np.int32), out, idx, wt,
                 list(rng.choice(4096, 24, replace=False)))
+
+
+def test_batch_graph_replay_matches_eager(env):
+    """The batched entry captured into a HIP graph (the shared expert's fork
+    onto the library's second stream and the join become graph edges),
+    replayed three times with eager calls between the replays: every replay
+    gives the eager result bit for bit."""
+    import torch
+    orc, lib, dg = env["orc"], env["lib"], env["dg"]
+    L = make_layer(orc, 4096, 512, 16, 4, seed=12, bias=True)
+    DL = dg.DeviceLayer.from_host(L, env["dev"])
+    X = T(env, bf16_input(np.random.default_rng(5), (40, 4096)))
+    ref, ri, rw = lib.moe_forward_batch(DL, X)  # eager: also creates the second stream
+    ref, ri, rw = ref.cpu().numpy(), ri.cpu().numpy(), rw.cpu().numpy()
+    ws = torch.empty(lib.moe_batch_workspace_bytes(DL, 40), dtype=torch.uint8, device=X.device)
+    out = torch.empty_like(X)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        lib.moe_forward_batch(DL, X, workspace=ws, out=out)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        _, gi, gw = lib.moe_forward_batch(DL, X, workspace=ws, out=out)
+    for r in range(3):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert same_bits(out.cpu().numpy(), ref), r
+        assert np.array_equal(gi.cpu().numpy(), ri) and same_bits(gw.cpu().numpy(), rw), r
+        e, _, _ = lib.moe_forward_batch(DL, X)  # eager work between the replays
+        torch.cuda.synchronize()
+        assert same_bits(e.cpu().numpy(), ref), r
