@@ -196,12 +196,16 @@ __device__ __forceinline__ void rl_mfma(v4f (&acc)[4], v4f (&aab)[4], const RlRe
   }
 }
 
-template <int NS>  // H / 128 when known at compile time (fully unrolled K), else 0
+// Split K (few tokens, too few tiles to fill the GPU): block z takes columns
+// [z ncols, (z + 1) ncols) and writes its partial sums at z T E; a second
+// kernel adds the partials in split order. Any summation order of the H
+// products stays within the candidates' any-order bound.
+template <int NS>  // ncols / 128 when known at compile time (fully unrolled K), else 0
 __global__ __launch_bounds__(256) void k_router_logits_mfma(float *__restrict__ z,
                                                             float *__restrict__ zabs,
                                                             const float *__restrict__ x,
                                                             const uint16_t *__restrict__ G,
-                                                            int T, int H, int E) {
+                                                            int T, int H, int E, int ncols) {
   __shared__ __align__(16) uint16_t xs[2][64 * 136];  // [buf][token][128 + 8 pad] bf16
   const int t0 = blockIdx.x * 64, e0 = blockIdx.y * 64;
   const int tid = threadIdx.x, l = tid % 64;
@@ -214,13 +218,16 @@ __global__ __launch_bounds__(256) void k_router_logits_mfma(float *__restrict__ 
   // staging: wave w brings tokens 16 w .. + 15, two 512-byte rows per load
   // (rows past T lie beyond the range and read zeros)
   const BufRsrc rx = buf_rsrc(x + (size_t)t0 * H, 4u * (uint32_t)(min(T - t0, 64) * H));
-  const uint32_t xo = 4u * (uint32_t)((16 * wv + l / 32) * H + 4 * (l % 32)), xstep = 8u * H;
+  const int kb = blockIdx.z * ncols;
+  z += (size_t)blockIdx.z * T * E;
+  zabs += (size_t)blockIdx.z * T * E;
+  const uint32_t xo = 4u * (uint32_t)((16 * wv + l / 32) * H + 4 * (l % 32) + kb), xstep = 8u * H;
   // one range per wave (a per-lane range would serialise the loads); expert
   // rows past E lie beyond it and read zeros
   const int we = e0 + 16 * wv;
   const uint32_t grange = __builtin_amdgcn_readfirstlane(2u * (uint32_t)(max(min(E - we, 16), 0) * H));
   const BufRsrc rg = buf_rsrc(G + (size_t)min(we, E - 1) * H, grange);
-  const uint32_t go = 2u * (uint32_t)((l % 16) * H + 8 * (l / 16));
+  const uint32_t go = 2u * (uint32_t)((l % 16) * H + 8 * (l / 16) + kb);
   RlRegs R[3];
   rl_load(R[0], rx, xo, xstep, rg, go, 0);
   rl_load(R[1], rx, xo, xstep, rg, go, 128);
@@ -241,7 +248,7 @@ __global__ __launch_bounds__(256) void k_router_logits_mfma(float *__restrict__ 
     }
   } else {
     // unrolled by three so that the ring slots are compile-time
-    const int ns = H / 128;  // H % 128 == 0
+    const int ns = ncols / 128;  // ncols % 128 == 0
     for (int s = 0; s < ns; s += 3) {
       rl_load(R[2], rx, xo, xstep, rg, go, 128 * (s + 2));
       rl_mfma(acc, aab, R[0], xs[s & 1], l);
@@ -270,6 +277,20 @@ __global__ __launch_bounds__(256) void k_router_logits_mfma(float *__restrict__ 
       }
     }
   }
+}
+
+__global__ void k_router_logits_sum(float *__restrict__ z, float *__restrict__ zabs,
+                                    const float *__restrict__ zp, const float *__restrict__ ap,
+                                    int S, size_t n) {
+  const size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float a = zp[i], b = ap[i];
+  for (int k = 1; k < S; ++k) {
+    a += zp[k * n + i];
+    b += ap[k * n + i];
+  }
+  z[i] = a;
+  zabs[i] = b;
 }
 
 // Wave argmax with the reference's tie rule (largest value, lowest index).
@@ -1399,7 +1420,7 @@ using namespace dsv4;
 namespace {
 struct BatchWs {
   uint16_t *xb, *yb;
-  float *z, *zabs, *cscore, *cchoice, *wt, *pos_wt;
+  float *z, *zabs, *zpart, *cscore, *cchoice, *wt, *pos_wt;
   int *not_bf16, *cand, *ncand, *chain_off, *idx, *counts, *bh, *pos_off, *tile_off, *pos_token,
       *pos_route;
   uint16_t *ro;
@@ -1438,6 +1459,11 @@ int side_stream(hipStream_t st, SideStream **out) {
   return 0;
 }
 
+// Router logit K splits: 8 (512 columns each) when the token tiles alone
+// give fewer than 4 x 64 tile blocks' worth of work per 64 experts (T <= 256)
+// and H splits evenly, else 1.
+int rl_splits(int T, int H) { return (T <= 256 && H % 1024 == 0) ? 8 : 1; }
+
 BatchWs batch_ws_layout(const DSV4GLayer *L, int T, void *base) {
   const size_t t = (size_t)T, K = (size_t)L->topk, E = (size_t)L->n_experts;
   const size_t H = (size_t)L->hidden, I = (size_t)L->inter, P = t * K + t;
@@ -1455,6 +1481,7 @@ BatchWs batch_ws_layout(const DSV4GLayer *L, int T, void *base) {
   w.not_bf16 = (int *)take(t * 4);
   w.z = (float *)take(t * E * 4);
   w.zabs = (float *)take(t * E * 4);
+  w.zpart = (float *)take(rl_splits(T, (int)H) > 1 ? 2 * (size_t)rl_splits(T, (int)H) * t * E * 4 : 0);
   w.cand = (int *)take(t * E * 4);
   w.ncand = (int *)take(t * 4);
   w.chain_off = (int *)take((t + 1) * 4);
@@ -1602,13 +1629,23 @@ int dsv4g_moe_forward_batch(float *out, const float *x, const DSV4GLayer *L,
   if (side) DSV4G_HIP(hipEventRecord(side->join, sst));
   // 2. router
   {
-    const dim3 grid((T + 63) / 64, (E + 63) / 64);
-    if (H == 4096)
-      hipLaunchKernelGGL(k_router_logits_mfma<32>, grid, dim3(256), 0, st, w.z, w.zabs, x,
-                         L->gate_w, T, H, E);
+    const int S = rl_splits(T, H);
+    const dim3 grid((T + 63) / 64, (E + 63) / 64, S);
+    float *zo = S > 1 ? w.zpart : w.z, *ao = S > 1 ? w.zpart + (size_t)S * T * E : w.zabs;
+    if (H == 4096 && S == 1)
+      hipLaunchKernelGGL(k_router_logits_mfma<32>, grid, dim3(256), 0, st, zo, ao, x, L->gate_w,
+                         T, H, E, H);
+    else if (H == 4096 && S == 8)
+      hipLaunchKernelGGL(k_router_logits_mfma<4>, grid, dim3(256), 0, st, zo, ao, x, L->gate_w,
+                         T, H, E, H / 8);
     else
-      hipLaunchKernelGGL(k_router_logits_mfma<0>, grid, dim3(256), 0, st, w.z, w.zabs, x,
-                         L->gate_w, T, H, E);
+      hipLaunchKernelGGL(k_router_logits_mfma<0>, grid, dim3(256), 0, st, zo, ao, x, L->gate_w,
+                         T, H, E, H / S);
+    if (S > 1) {
+      const size_t n = (size_t)T * E;
+      hipLaunchKernelGGL(k_router_logits_sum, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                         w.z, w.zabs, zo, ao, S, n);
+    }
   }
   hipLaunchKernelGGL(k_router_cand, dim3((T + 3) / 4), dim3(256), 0, st, w.cand, w.ncand, w.z,
                      w.zabs, w.not_bf16, L->bias, L->tid2eid, token_ids, T, H, E, K);
