@@ -248,4 +248,50 @@ __device__ __forceinline__ float gamma_n(int n) {
   return (float)(nu / (1.0 - nu));
 }
 
+// ---------------------------------------------------- exact chains ----
+// One 8-column batch of the exact chain acc = fmaf(g[c], x[c], acc), in
+// column order.
+__device__ __forceinline__ float chain8(const float4 &ga, const float4 &gb, const float4 &xa,
+                                        const float4 &xb, float acc) {
+  acc = fmaf(ga.x, xa.x, acc);
+  acc = fmaf(ga.y, xa.y, acc);
+  acc = fmaf(ga.z, xa.z, acc);
+  acc = fmaf(ga.w, xa.w, acc);
+  acc = fmaf(gb.x, xb.x, acc);
+  acc = fmaf(gb.y, xb.y, acc);
+  acc = fmaf(gb.z, xb.z, acc);
+  acc = fmaf(gb.w, xb.w, acc);
+  return acc;
+}
+
+// Chain 8 * NB columns from LDS: g, x at the first column (fp32). The reads
+// of the batch two ahead are in flight while a batch is chained; nothing is
+// carried across calls (a loop-carried prefetch costs a full LDS drain per
+// iteration), so the chain runs at the fma dependency latency.
+template <int NB>
+__device__ __forceinline__ float chain_cols(const float4 *g, const float4 *x, float acc) {
+  float4 g0[4], g1[4], x0[4], x1[4];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    g0[j] = g[2 * j];
+    g1[j] = g[2 * j + 1];
+    x0[j] = x[2 * j];
+    x1[j] = x[2 * j + 1];
+  }
+#pragma unroll
+  for (int j = 0; j < NB; ++j) {
+    if (j + 2 < NB) {
+      g0[(j + 2) % 4] = g[2 * (j + 2)];
+      g1[(j + 2) % 4] = g[2 * (j + 2) + 1];
+      x0[(j + 2) % 4] = x[2 * (j + 2)];
+      x1[(j + 2) % 4] = x[2 * (j + 2) + 1];
+    }
+    acc = chain8(g0[j % 4], g1[j % 4], x0[j % 4], x1[j % 4], acc);
+    // pins the batch in place: its fmas before this point, the next reads
+    // after it (otherwise every read is hoisted to the top and the fmas sink)
+    asm volatile("" : "+v"(acc)::"memory");
+  }
+  return acc;
+}
+
 }  // namespace dsv4

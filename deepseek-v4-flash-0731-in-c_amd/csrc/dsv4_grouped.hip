@@ -517,6 +517,78 @@ __global__ __launch_bounds__(256) void k_router_chains(float *__restrict__ cscor
 }
 
 
+// Few tokens (a few hundred chains: a handful of waves of the kernel above,
+// each latency-bound on its x loads): one 64-thread workgroup per chain
+// instead. It stages the token's x and the expert's gate row (widened to
+// fp32) in LDS in one shot, then lane 0 runs the same column-order fmaf
+// chain from LDS at the fma latency (chain_cols). Grid-stride over chains.
+__global__ __launch_bounds__(64) void k_router_chains_small(float *__restrict__ cscore,
+                                                            float *__restrict__ cchoice,
+                                                            const int *__restrict__ cand,
+                                                            const int *__restrict__ chain_off,
+                                                            const float *__restrict__ x,
+                                                            const uint16_t *__restrict__ G,
+                                                            const float *__restrict__ bias,
+                                                            int T, int H, int E) {
+  extern __shared__ __align__(16) float rcs[];  // x, then the gate row: H floats each
+  const int l = threadIdx.x;
+  const int total = chain_off[T];
+  for (int g = blockIdx.x; g < total; g += gridDim.x) {
+    int lo = 0, hi = T;  // chain_off[lo] <= g < chain_off[lo+1]
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) / 2;
+      if (chain_off[mid] <= g) lo = mid;
+      else hi = mid;
+    }
+    const int t = lo, c = g - chain_off[t];
+    int e = cand[(size_t)t * E + c];
+    const bool ok = e >= 0 && e < E;
+    if (!ok) e = 0;
+    const BufRsrc rx = buf_rsrc(x + (size_t)t * H, 4u * (uint32_t)H);
+    const BufRsrc rg = buf_rsrc(G + (size_t)e * H, ok ? 2u * (uint32_t)H : 0u);
+    __syncthreads();  // the previous chain's reads of LDS are done
+    for (int i0 = 0; i0 < H / 4; i0 += 64 * 8) {  // x: 8 pieces of 4 per lane per round
+      uint4 v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = buf_load16(rx, 16u * (uint32_t)(i0 + l + 64 * j));
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (i0 + l + 64 * j < H / 4) reinterpret_cast<uint4 *>(rcs)[i0 + l + 64 * j] = v[j];
+    }
+    float *gs = rcs + H;
+    for (int i0 = 0; i0 < H / 8; i0 += 64 * 8) {  // gate: 8 pieces of 8 per lane per round
+      uint4 v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = buf_load16(rg, 16u * (uint32_t)(i0 + l + 64 * j));
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int i = i0 + l + 64 * j;
+        if (i < H / 8) {
+          float4 *gp = reinterpret_cast<float4 *>(gs) + 2 * i;
+          gp[0] = make_float4(u2f(v[j].x << 16), u2f(v[j].x & 0xFFFF0000u), u2f(v[j].y << 16),
+                              u2f(v[j].y & 0xFFFF0000u));
+          gp[1] = make_float4(u2f(v[j].z << 16), u2f(v[j].z & 0xFFFF0000u), u2f(v[j].w << 16),
+                              u2f(v[j].w & 0xFFFF0000u));
+        }
+      }
+    }
+    const float be = ok && bias ? bias[e] : 0.0f;
+    __syncthreads();
+    if (l == 0) {
+      float acc = 0.0f;
+      const float4 *gp = reinterpret_cast<const float4 *>(gs);
+      const float4 *xp = reinterpret_cast<const float4 *>(rcs);
+      if (H % 256 == 0)
+        for (int cc = 0; cc < H / 4; cc += 64) acc = chain_cols<32>(gp + cc, xp + cc, acc);
+      else
+        for (int cc = 0; cc < H / 4; cc += 32) acc = chain_cols<16>(gp + cc, xp + cc, acc);
+      const float sc = ok ? sqrt_softplus(acc) : 0.0f;
+      cscore[(size_t)t * E + c] = sc;
+      cchoice[(size_t)t * E + c] = ok ? sc + be : -__builtin_inff();
+    }
+  }
+}
+
 // Per token: the reference selection over the candidates (ascending id,
 // strict '>'), weights from the unbiased scores, exchange sort by id
 // (src/dsv4/dsv4_model.c:6866-6906).
@@ -1650,7 +1722,12 @@ int dsv4g_moe_forward_batch(float *out, const float *x, const DSV4GLayer *L,
   hipLaunchKernelGGL(k_router_cand, dim3((T + 3) / 4), dim3(256), 0, st, w.cand, w.ncand, w.z,
                      w.zabs, w.not_bf16, L->bias, L->tid2eid, token_ids, T, H, E, K);
   hipLaunchKernelGGL(k_scan_counts, dim3(1), dim3(1024), 0, st, w.chain_off, w.ncand, T);
-  {
+  if (T <= 256) {
+    // about T (K + 2) chains: one workgroup each
+    hipLaunchKernelGGL(k_router_chains_small, dim3((unsigned)(T * (K + 4))), dim3(64),
+                       (size_t)H * 8, st, w.cscore, w.cchoice, w.cand, w.chain_off, x,
+                       L->gate_w, L->bias, T, H, E);
+  } else {
     const long bound = (long)T * (K + 4);
     const int blocks = (int)((bound + 255) / 256 < 4096 ? (bound + 255) / 256 : 4096);
     hipLaunchKernelGGL(k_router_chains, dim3(blocks), dim3(256), 0, st, w.cscore, w.cchoice,
