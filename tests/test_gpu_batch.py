@@ -187,3 +187,21 @@ def test_batch_graph_replay_matches_eager(env):
         e, _, _ = lib.moe_forward_batch(DL, X)  # eager work between the replays
         torch.cuda.synchronize()
         assert same_bits(e.cpu().numpy(), ref), r
+
+
+@pytest.mark.parametrize("hidden,inter,experts,n", [(1280, 384, 40, 100), (512, 256, 24, 300),
+                                                    (2048, 640, 16, 257)])
+def test_batch_generic_widths(env, hidden, inter, experts, n):
+    """Widths off the model's (the per-window GEMM loops, the unsplit or
+    generic router logits), token counts on both sides of the few-token
+    router kernels (256) and not a multiple of the 64-token tile: routing
+    bit-exact, outputs within the tolerance, every token checked."""
+    orc, lib, dg = env["orc"], env["lib"], env["dg"]
+    L = make_layer(orc, hidden, inter, experts, 4, seed=hidden + n, bias=True)
+    L["bias"] = zipf_bias(experts, 3)
+    DL = dg.DeviceLayer.from_host(L, env["dev"])
+    X = bf16_input(np.random.default_rng(n), (n, hidden))
+    out, idx, wt = lib.moe_forward_batch(DL, T(env, X))
+    out, idx, wt = out.cpu().numpy(), idx.cpu().numpy(), wt.cpu().numpy()
+    assert np.all(np.isfinite(out))
+    check_batch(env, L, X, np.zeros(n, np.int32), out, idx, wt, range(n))
