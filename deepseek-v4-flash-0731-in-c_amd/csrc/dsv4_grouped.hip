@@ -313,6 +313,7 @@ __device__ __forceinline__ float gamma_n2(int n) {
 
 // One wave per token: approximate choices, the k-th best, and every expert
 // within the rigorous error margin of it -> candidate list (ascending id).
+template <int PER>  // experts per lane: E <= 64 PER
 __global__ __launch_bounds__(256) void k_router_cand(int *__restrict__ cand,
                                                      int *__restrict__ ncand,
                                                      const float *__restrict__ z,
@@ -331,7 +332,6 @@ __global__ __launch_bounds__(256) void k_router_cand(int *__restrict__ cand,
     return;
   }
   const float *zt = z + (size_t)t * E, *at = zabs + (size_t)t * E;
-  constexpr int PER = 16;  // E <= 1024
   float ch[PER];
   float amax = 0.0f;
   for (int j = 0; j < PER; ++j) {
@@ -592,57 +592,70 @@ __global__ __launch_bounds__(64) void k_router_chains_small(float *__restrict__ 
 // Per token: the reference selection over the candidates (ascending id,
 // strict '>'), weights from the unbiased scores, exchange sort by id
 // (src/dsv4/dsv4_model.c:6866-6906).
-__global__ void k_router_finalize(int *__restrict__ idx, float *__restrict__ wt,
-                                  const int *__restrict__ cand, const int *__restrict__ ncand,
-                                  const float *__restrict__ cscore,
-                                  const float *__restrict__ cchoice, int hash, int T, int E,
-                                  int K, float route_scale) {
-  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+__global__ __launch_bounds__(256) void k_router_finalize(
+    int *__restrict__ idx, float *__restrict__ wt, const int *__restrict__ cand,
+    const int *__restrict__ ncand, const float *__restrict__ cscore,
+    const float *__restrict__ cchoice, int hash, int T, int E, int K, float route_scale) {
+  // one wave per token; lane k carries route k in selection order
+  const int t = blockIdx.x * 4 + threadIdx.x / 64, l = threadIdx.x % 64;
   if (t >= T) return;
   const int nc = ncand[t];
   const int *ct = cand + (size_t)t * E;
   const float *cs = cscore + (size_t)t * E, *cc = cchoice + (size_t)t * E;
-  int order[32];
-  float sel[32], w[32];
-  uint32_t used[32] = {0};
-  for (int k = 0; k < K; ++k) {
-    if (hash) {
-      order[k] = ct[k];
-      sel[k] = cs[k];
-      continue;
+  int my_e = -1;
+  float my_sc = 0.0f;
+  if (hash) {
+    if (l < K) {
+      my_e = ct[l];
+      my_sc = cs[l];
     }
-    int bi = -1;
-    float bv = -__builtin_inff();
-    for (int i = 0; i < nc; ++i)
-      if (!((used[i >> 5] >> (i & 31)) & 1u) && cc[i] > bv) {
-        bv = cc[i];
-        bi = i;
-      }
-    if (bi >= 0) used[bi >> 5] |= 1u << (bi & 31);
-    order[k] = bi >= 0 ? ct[bi] : -1;
-    sel[k] = bi >= 0 ? cs[bi] : 0.0f;
-  }
-  float sum = 0.0f;
-  for (int k = 0; k < K; ++k) sum += sel[k];
-  if (sum > 0.0f) {
-    const float rs = route_scale / sum;
-    for (int k = 0; k < K; ++k) w[k] = sel[k] * rs;
   } else {
-    for (int k = 0; k < K; ++k) w[k] = 0.0f;
-  }
-  for (int i = 0; i < K; ++i)
-    for (int j = i + 1; j < K; ++j)
-      if (order[j] < order[i]) {
-        const int ti = order[i];
-        order[i] = order[j];
-        order[j] = ti;
-        const float tw = w[i];
-        w[i] = w[j];
-        w[j] = tw;
+    constexpr int PER = 16;  // nc <= E <= 1024
+    float v[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int i = l + 64 * j;
+      const float c = i < nc ? cc[i] : -__builtin_inff();
+      v[j] = c == c ? c : -__builtin_inff();  // NaN is never selected
+    }
+    for (int k = 0; k < K; ++k) {
+      // strict '>' in ascending position: the lowest position (id) wins a tie
+      float bv = -__builtin_inff();
+      int bi = -1;
+#pragma unroll
+      for (int j = 0; j < PER; ++j)
+        if (v[j] > bv) {
+          bv = v[j];
+          bi = l + 64 * j;
+        }
+      wave_argmax(bv, bi);
+      if (bi < 0 || !(bv > -__builtin_inff())) continue;  // nothing left: route k empty
+      if (bi % 64 == l) {
+#pragma unroll
+        for (int j = 0; j < PER; ++j)
+          if (j == bi / 64) v[j] = -__builtin_inff();  // taken
       }
+      if (l == k) {
+        my_e = ct[bi];
+        my_sc = cs[bi];
+      }
+    }
+  }
+  // weights: the unbiased scores summed in selection order, then the routes
+  // sorted by id (equal ids carry equal weights)
+  float sum = 0.0f;
+  for (int k = 0; k < K; ++k)
+    sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_sc), k));
+  const float rs = sum > 0.0f ? route_scale / sum : 0.0f;
+  const float my_w = sum > 0.0f ? my_sc * rs : 0.0f;
+  int rank = 0;
   for (int k = 0; k < K; ++k) {
-    idx[(size_t)t * K + k] = order[k];
-    wt[(size_t)t * K + k] = w[k];
+    const int ek = __builtin_amdgcn_readlane(my_e, k);
+    rank += (ek < my_e || (ek == my_e && k < l)) ? 1 : 0;
+  }
+  if (l < K) {
+    idx[(size_t)t * K + rank] = my_e;
+    wt[(size_t)t * K + rank] = my_w;
   }
 }
 
@@ -1719,8 +1732,12 @@ int dsv4g_moe_forward_batch(float *out, const float *x, const DSV4GLayer *L,
                          w.z, w.zabs, zo, ao, S, n);
     }
   }
-  hipLaunchKernelGGL(k_router_cand, dim3((T + 3) / 4), dim3(256), 0, st, w.cand, w.ncand, w.z,
-                     w.zabs, w.not_bf16, L->bias, L->tid2eid, token_ids, T, H, E, K);
+  {
+    auto cand = E <= 64 ? k_router_cand<1> : E <= 128 ? k_router_cand<2> : E <= 256 ? k_router_cand<4>
+              : E <= 512 ? k_router_cand<8> : k_router_cand<16>;
+    hipLaunchKernelGGL(cand, dim3((T + 3) / 4), dim3(256), 0, st, w.cand, w.ncand, w.z, w.zabs,
+                       w.not_bf16, L->bias, L->tid2eid, token_ids, T, H, E, K);
+  }
   hipLaunchKernelGGL(k_scan_counts, dim3(1), dim3(1024), 0, st, w.chain_off, w.ncand, T);
   if (T <= 256) {
     // about T (K + 2) chains: one workgroup each
@@ -1733,7 +1750,7 @@ int dsv4g_moe_forward_batch(float *out, const float *x, const DSV4GLayer *L,
     hipLaunchKernelGGL(k_router_chains, dim3(blocks), dim3(256), 0, st, w.cscore, w.cchoice,
                        w.cand, w.chain_off, x, L->gate_w, L->bias, T, H, E);
   }
-  hipLaunchKernelGGL(k_router_finalize, dim3((T + 255) / 256), dim3(256), 0, st, w.idx, w.wt,
+  hipLaunchKernelGGL(k_router_finalize, dim3((T + 3) / 4), dim3(256), 0, st, w.idx, w.wt,
                      w.cand, w.ncand, w.cscore, w.cchoice, L->tid2eid ? 1 : 0, T, E, K,
                      L->route_scale);
   DSV4G_TRY(dsv4g_check_launch("router"));
