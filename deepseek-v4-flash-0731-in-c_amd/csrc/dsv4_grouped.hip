@@ -1680,15 +1680,19 @@ int dsv4g_moe_forward_batch(float *out, const float *x, const DSV4GLayer *L,
   const void *dn8 = I == 2048 ? (const void *)k_grouped_down<MX_FP8, 16>
                               : (const void *)k_grouped_down<MX_FP8, 0>;
   {
-    static int attr_set = 0;  // the kernels' dynamic LDS limit (H, I <= 8192: <= 64 KiB)
-    if (!attr_set) {
+    // the kernels' dynamic LDS limit (H, I <= 8192: <= 64 KiB), once per
+    // device (under the enqueue lock)
+    static bool attr_set[64];
+    int dev = 0;
+    DSV4G_HIP(hipGetDevice(&dev));
+    if (dev >= 0 && dev < 64 && !attr_set[dev]) {
       const void *fs[4] = {(const void *)k_grouped_gateup<MX_FP4, 32>,
                            (const void *)k_grouped_gateup<MX_FP4, 0>,
                            (const void *)k_grouped_down<MX_FP4, 16>,
                            (const void *)k_grouped_down<MX_FP4, 0>};
       for (int i = 0; i < 4; ++i)
         DSV4G_HIP(hipFuncSetAttribute(fs[i], hipFuncAttributeMaxDynamicSharedMemorySize, 65536));
-      attr_set = 1;
+      attr_set[dev] = true;
     }
   }
   // the shared expert needs only the quantised activations: its gate/up and
