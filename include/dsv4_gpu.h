@@ -156,8 +156,8 @@ int dsv4g_moe_workspace_init(void *workspace, size_t workspace_bytes, void *stre
 int dsv4g_moe_forward(float *out, const float *x, const DSV4GLayer *L, const int *token_ids,
                       int n_tokens, void *workspace, size_t workspace_bytes, int *idx_out,
                       float *wt_out, void *stream);
-/* The same layer with the tolerance of the north-star contract instead of
- * bit-exactness: top-k indices identical to the reference's always; when a
+/* The same layer with a tolerance (expert outputs within 1e-3 relative) instead
+ * of bit-exactness: top-k indices identical to the reference's always; when a
  * token's candidate experts are exactly its top-k (the rigorous bound of the
  * parallel router logits separates the k-th from the (k+1)-th), the route
  * weights come from the parallel logits (within a few fp32 ulps of the
