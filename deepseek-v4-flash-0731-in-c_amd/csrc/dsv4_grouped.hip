@@ -1311,8 +1311,12 @@ __device__ __forceinline__ void gateup_tile(const GroupedArgs &a, int e, int rt,
   if (AFMT == MX_FP4) stage_codes<2>(cs, S, rt, H);
   if constexpr (NSW > 0) {
     const BufRsrc xr = buf_rsrc(a.xb, a.xb_bytes);
-    if (AFMT == MX_FP4 && nf <= 2)
+    if (AFMT == MX_FP4 && nf <= 1)
+      gemm_k_loop_fast<AFMT, 2, NSW, 1>(acc, W, S, xr, H, rbase, rows_s, bt, cs);
+    else if (AFMT == MX_FP4 && nf <= 2)
       gemm_k_loop_fast<AFMT, 2, NSW, 2>(acc, W, S, xr, H, rbase, rows_s, bt, cs);
+    else if (AFMT == MX_FP4 && nf <= 3)
+      gemm_k_loop_fast<AFMT, 2, NSW, 3>(acc, W, S, xr, H, rbase, rows_s, bt, cs);
     else
       gemm_k_loop_fast<AFMT, 2, NSW, 4>(acc, W, S, xr, H, rbase, rows_s, bt, cs);
   } else
@@ -1420,8 +1424,12 @@ __device__ __forceinline__ void down_tile(const GroupedArgs &a, int e, int rt, i
   if (AFMT == MX_FP4) stage_codes<1>(cs, S, rt, I);
   if constexpr (NSW > 0) {
     const BufRsrc yr = buf_rsrc(a.yb, a.yb_bytes);
-    if (AFMT == MX_FP4 && nf <= 2)
+    if (AFMT == MX_FP4 && nf <= 1)
+      gemm_k_loop_fast<AFMT, 1, NSW, 1>(acc, W, S, yr, I, rbase, rows_s, bt, cs);
+    else if (AFMT == MX_FP4 && nf <= 2)
       gemm_k_loop_fast<AFMT, 1, NSW, 2>(acc, W, S, yr, I, rbase, rows_s, bt, cs);
+    else if (AFMT == MX_FP4 && nf <= 3)
+      gemm_k_loop_fast<AFMT, 1, NSW, 3>(acc, W, S, yr, I, rbase, rows_s, bt, cs);
     else
       gemm_k_loop_fast<AFMT, 1, NSW, 4>(acc, W, S, yr, I, rbase, rows_s, bt, cs);
   } else
