@@ -366,6 +366,8 @@ __global__ __launch_bounds__(256) void k_router_cand(int *__restrict__ cand,
     kth = bv;
   }
   const float thr = kth - delta;
+  // compaction in ascending id: pass j holds ids 64j .. 64j + 63 in lane
+  // order, and each pass appends after the previous one
   int base = 0;
   for (int j = 0; j < PER; ++j) {
     const int e = l + 64 * j;
@@ -375,20 +377,7 @@ __global__ __launch_bounds__(256) void k_router_cand(int *__restrict__ cand,
     if (take) ct[base + before] = e;
     base += __popcll(m);
   }
-  // candidates were written in order e = l + 64j, i.e. j-major: re-sort
-  // ascending (small lists; one lane)
-  if (l == 0) {
-    for (int i = 1; i < base; ++i) {
-      const int v = ct[i];
-      int j = i - 1;
-      while (j >= 0 && ct[j] > v) {
-        ct[j + 1] = ct[j];
-        --j;
-      }
-      ct[j + 1] = v;
-    }
-    ncand[t] = base;
-  }
+  if (l == 0) ncand[t] = base;
 }
 
 // Exclusive prefix sum of n[0..T) into off[0..T], one workgroup.
@@ -1370,7 +1359,7 @@ __device__ __forceinline__ void gateup_tile(const GroupedArgs &a, int e, int rt,
 // tiles (I / 128); FP4: tiles [0, tile_off[E]) (beyond the actual count exit
 // at once); FP8: the shared expert's tiles from tile_off[E].
 template <int AFMT, int NSW>
-__global__ __launch_bounds__(256) void k_grouped_gateup(GroupedArgs a) {
+__device__ __forceinline__ void grouped_gateup(const GroupedArgs &a) {
   __shared__ __align__(16) uint8_t bt[2 * GT_BT_BYTES];
   __shared__ int rows_s[GT_TN];
   __shared__ float wt_s[GT_TN];
@@ -1391,6 +1380,19 @@ __global__ __launch_bounds__(256) void k_grouped_gateup(GroupedArgs a) {
     np = min(GT_TN, a.pos_off[e + 1] - p0);
   }
   gateup_tile<AFMT, NSW>(a, e, rt, p0, np, bt, rows_s, wt_s, amax_s, s_tab, codes_s);
+}
+
+template <int AFMT, int NSW>
+__global__ __launch_bounds__(256) void k_grouped_gateup(GroupedArgs a) {
+  grouped_gateup<AFMT, NSW>(a);
+}
+
+// The shared expert's FP8 gate/up at hidden 4096, held to 256 registers (two
+// waves per SIMD instead of one): it runs beside the router kernels, whose
+// workgroups otherwise wait for the CU slots it holds.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void
+k_grouped_gateup_fp8_h4096(GroupedArgs a) {
+  grouped_gateup<MX_FP8, 32>(a);
 }
 
 template <int AFMT, int NSW>  // NSW > 0: I = 128 NSW, the unrolled loop
@@ -1683,7 +1685,7 @@ int dsv4g_moe_forward_batch(float *out, const float *x, const DSV4GLayer *L,
                               : (const void *)k_grouped_gateup<MX_FP4, 0>;
   const void *dn4 = I == 2048 ? (const void *)k_grouped_down<MX_FP4, 16>
                               : (const void *)k_grouped_down<MX_FP4, 0>;
-  const void *gu8 = H == 4096 ? (const void *)k_grouped_gateup<MX_FP8, 32>
+  const void *gu8 = H == 4096 ? (const void *)k_grouped_gateup_fp8_h4096
                               : (const void *)k_grouped_gateup<MX_FP8, 0>;
   const void *dn8 = I == 2048 ? (const void *)k_grouped_down<MX_FP8, 16>
                               : (const void *)k_grouped_down<MX_FP8, 0>;
