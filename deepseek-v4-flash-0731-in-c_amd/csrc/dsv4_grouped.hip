@@ -1689,6 +1689,9 @@ int dsv4g_moe_forward_batch(float *out, const float *x, const DSV4GLayer *L,
                               : (const void *)k_grouped_gateup<MX_FP8, 0>;
   const void *dn8 = I == 2048 ? (const void *)k_grouped_down<MX_FP8, 16>
                               : (const void *)k_grouped_down<MX_FP8, 0>;
+  // calls hold this lock while they set up and enqueue: the attribute
+  // flags below, and the fork and join events of two calls, cannot interleave
+  std::lock_guard<std::mutex> lock(g_side_mu);
   {
     // the kernels' dynamic LDS limit (H, I <= 8192: <= 64 KiB), once per
     // device (under the enqueue lock)
@@ -1709,7 +1712,6 @@ int dsv4g_moe_forward_batch(float *out, const float *x, const DSV4GLayer *L,
   // down run on a second stream beside the router, dispatch and routed
   // GEMMs (joined before the combine). Calls hold a lock while they enqueue,
   // so the fork and join events of two calls cannot interleave.
-  std::lock_guard<std::mutex> lock(g_side_mu);
   SideStream *side = nullptr;
   DSV4G_TRY(side_stream(st, &side));
   hipStream_t sst = side ? side->s : st;
