@@ -116,11 +116,33 @@ def bench_batch(lib, layer, n_tokens, iters):
     }
 
 
-def cpu_baseline(layer_dev, xs, seconds):
-    """Reference moe_forward (compiled from the reference sources) on the host,
-    one warm-up token, then tokens until `seconds` have elapsed."""
-    threads = min(16, os.cpu_count() or 1)
-    os.environ["OMP_NUM_THREADS"] = str(threads)
+def host_cores():
+    """Threads for the CPU legs: the box's CPU share (OMP_NUM_THREADS where set,
+    else the CPUs this process may run on), with what the host reports."""
+    avail = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    env = os.environ.get("OMP_NUM_THREADS")
+    threads = int(env) if env and env.isdigit() else (avail or 1)
+    return threads, {"nproc": os.cpu_count(), "affinity_cpus": avail,
+                     "omp_num_threads_env": env}
+
+
+def set_omp_threads(n):
+    """OpenMP team size for the reference's parallel regions started from this
+    thread (libgomp read OMP_NUM_THREADS when torch loaded it already)."""
+    import ctypes
+    try:
+        ctypes.CDLL("libgomp.so.1").omp_set_num_threads(int(n))
+    except OSError:
+        pass
+
+
+def cpu_baseline(layer_dev, tokens, gpu_out, seconds):
+    """Reference moe_forward (compiled from the reference sources) on the host
+    on the tokens the GPU decoded through the same layer: each GPU output is
+    compared bit for bit with the reference's, then tokens are repeated until
+    `seconds` have elapsed (one warm-up token first)."""
+    threads, hw = host_cores()
+    set_omp_threads(threads)
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     sys.path.insert(0, os.path.join(ROOT, "deepseek-v4-flash-0731-in-c_amd", "python"))
     import numpy as np
@@ -130,22 +152,31 @@ def cpu_baseline(layer_dev, xs, seconds):
         return None
     ref = pyoracle.RefLib()
     L = synth.host_copy(layer_dev)
-    x = xs.cpu().numpy()
-    ref.moe_forward(L, x[0])
+    x = tokens.cpu().numpy()
+    go = gpu_out.cpu().numpy()
+    o, _, _ = ref.moe_forward(L, x[0])
+    same = int(np.array_equal(o.view(np.uint32), go[0].view(np.uint32)))
+    checked = 1
     n, t0 = 0, time.perf_counter()
     while True:
-        ref.moe_forward(L, x[(n + 1) % x.shape[0]])
+        i = (n + 1) % x.shape[0]
+        o, _, _ = ref.moe_forward(L, x[i])
+        if n + 1 < x.shape[0]:
+            same += int(np.array_equal(o.view(np.uint32), go[i].view(np.uint32)))
+            checked += 1
         n += 1
         el = time.perf_counter() - t0
-        if el >= seconds or n >= 2000:
+        if (el >= seconds and n + 1 >= x.shape[0]) or n >= 2000:
             break
     sec = el / n
     return {"value": round(DECODE_BYTES / sec / 1e9, 3), "unit": "GB/s", "cores": threads,
-            "kind": "reference", "ms_per_step": round(sec * 1e3, 3),
+            "kind": "reference", "ms_per_step": round(sec * 1e3, 3), "host": hw,
+            "gpu_outputs_bit_exact_vs_reference": f"{same}/{checked}",
             "sample": f"{n} decode tokens through the reference moe_forward (oracle/_ref, built "
                       f"from src/dsv4/*.c with -O3 -mavx2 -mfma -fopenmp) on one full "
                       f"synthetic layer (256 FP4 experts + FP8 shared), OMP_NUM_THREADS="
-                      f"{threads}, after one warm-up token"}
+                      f"{threads}, after one warm-up token; the tokens are those the GPU "
+                      f"decoded through this layer, whose outputs are compared bit for bit"}
 
 
 def ref_kernel_bench():
@@ -154,7 +185,7 @@ def ref_kernel_bench():
     if not os.path.exists(exe):
         return None
     import subprocess
-    env = dict(os.environ, OMP_NUM_THREADS=str(min(16, os.cpu_count() or 1)))
+    env = dict(os.environ, OMP_NUM_THREADS=str(host_cores()[0]))
     out = subprocess.run([exe], capture_output=True, text=True, env=env, timeout=300).stdout
     res, name = {}, None
     for ln in out.splitlines():
@@ -272,7 +303,7 @@ def bench_decode(args, lib, layers):
     torch.cuda.synchronize()
     ms_gateup = ev0.elapsed_time(ev1) / (args.replays * nsteps)
     del graph, g2
-    return ms_step, ms_gateup, ms_fast, eager_ok and replay_ok, X
+    return ms_step, ms_gateup, ms_fast, eager_ok and replay_ok, X, OUT
 
 
 def main():
@@ -323,7 +354,7 @@ def main():
         print(json.dumps(result))
         return
 
-    ms_step, ms_gateup, ms_fast, graph_ok, X = bench_decode(args, lib, layers)
+    ms_step, ms_gateup, ms_fast, graph_ok, X, OUT = bench_decode(args, lib, layers)
     if args.copy_calibration:
         src = torch.ones(1 << 30, dtype=torch.uint8, device=dev)
         dst = torch.empty_like(src)
@@ -381,7 +412,8 @@ def main():
         },
     }
     if not args.no_cpu:
-        cb = cpu_baseline(layers[0], X[:64], args.cpu_seconds)
+        # the steps the GPU ran through layer 0 (step i uses layer i % nl)
+        cb = cpu_baseline(layers[0], X[:args.steps:nl], OUT[:args.steps:nl], args.cpu_seconds)
         if cb:
             result["cpu_baseline"] = cb
             result["config"]["speedup_vs_cpu"] = round(value / cb["value"], 1)

@@ -772,6 +772,7 @@ struct GroupedArgs {
   const uint16_t *xb;  // [T][H] BF16 activations (dequantised FP8)
   uint16_t *yb;        // [P][I] BF16 intermediate (dequantised FP8)
   uint16_t *ro;        // [T][K+1][H] BF16 bits
+  float *ro32;         // optional [T][K+1][H]: the same outputs before BF16 rounding
   uint32_t xb_bytes, yb_bytes;
   int H, I, E, K, T, row_tiles;
   float limit;
@@ -1453,6 +1454,9 @@ __device__ __forceinline__ void down_tile(const GroupedArgs &a, int e, int rt, i
       o.y = (f2u(bf16_round(acc[0][f][c][2])) >> 16) |
             (f2u(bf16_round(acc[0][f][c][3])) & 0xFFFF0000u);
       *reinterpret_cast<uint2 *>(dst + row) = o;
+      if (a.ro32)  // validation output: the fp32 accumulators themselves
+        *reinterpret_cast<float4 *>(a.ro32 + ((size_t)t * (a.K + 1) + k) * H + row) =
+            make_float4(acc[0][f][c][0], acc[0][f][c][1], acc[0][f][c][2], acc[0][f][c][3]);
     }
   }
 }
@@ -1483,8 +1487,11 @@ __global__ __launch_bounds__(256) void k_grouped_down(GroupedArgs a) {
 // out[t][c .. c + 7]: the routes in ascending expert id, then the shared
 // expert (route slot K), each element summed in that order
 // (src/dsv4/dsv4_model.c:6795-6805); 16-byte loads of 8 BF16 columns.
-__global__ void k_combine_batch(float *__restrict__ out, const uint16_t *__restrict__ ro, int T,
-                                int K, int H) {
+// A route without an expert (idx outside [0, E): no selectable choice was
+// left, or a tid2eid entry out of range) was never dispatched, so its slot
+// holds no output of this call: it adds nothing.
+__global__ void k_combine_batch(float *__restrict__ out, const uint16_t *__restrict__ ro,
+                                const int *__restrict__ idx, int T, int K, int H, int E) {
   const size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;  // 8-column group
   const size_t g8 = (size_t)H / 8;
   if (i >= (size_t)T * g8) return;
@@ -1494,6 +1501,7 @@ __global__ void k_combine_batch(float *__restrict__ out, const uint16_t *__restr
 #pragma unroll
   for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
   for (int k = 0; k <= K; ++k) {
+    if (k < K && (unsigned)idx[t * K + k] >= (unsigned)E) continue;
     const uint4 v = *reinterpret_cast<const uint4 *>(r + (size_t)k * H);
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
@@ -1622,6 +1630,14 @@ int dsv4g_moe_forward_batch(float *out, const float *x, const DSV4GLayer *L,
                             const int *token_ids, int n_tokens, void *workspace,
                             size_t workspace_bytes, int *idx_out, float *wt_out,
                             void *stream) {
+  return dsv4g_moe_forward_batch_routes(out, x, L, token_ids, n_tokens, workspace,
+                                        workspace_bytes, idx_out, wt_out, nullptr, stream);
+}
+
+int dsv4g_moe_forward_batch_routes(float *out, const float *x, const DSV4GLayer *L,
+                                   const int *token_ids, int n_tokens, void *workspace,
+                                   size_t workspace_bytes, int *idx_out, float *wt_out,
+                                   float *route_out, void *stream) {
   if (!L || !L->gate_w || !L->experts || !L->sh1 || !L->sh2 || !L->sh3)
     return dsv4g_fail(DSV4G_EINVAL, "moe_forward_batch: layer descriptor incomplete");
   const int T = n_tokens, K = L->topk, E = L->n_experts, H = L->hidden, I = L->inter;
@@ -1667,6 +1683,7 @@ int dsv4g_moe_forward_batch(float *out, const float *x, const DSV4GLayer *L,
   g.xb_bytes = (uint32_t)((size_t)T * H * 2);
   g.yb_bytes = (uint32_t)((size_t)T * (K + 1) * I * 2);
   g.ro = w.ro;
+  g.ro32 = route_out;
   g.H = H;
   g.I = I;
   g.E = E;
@@ -1714,6 +1731,18 @@ int dsv4g_moe_forward_batch(float *out, const float *x, const DSV4GLayer *L,
   // so the fork and join events of two calls cannot interleave.
   SideStream *side = nullptr;
   DSV4G_TRY(side_stream(st, &side));
+  if (side) {
+    // a capture forked into the side stream stays open there until its
+    // caller ends it: a call that is not part of that same capture runs the
+    // shared expert on its own stream instead of joining a foreign graph
+    hipStreamCaptureStatus cs_side = hipStreamCaptureStatusNone, cs = hipStreamCaptureStatusNone;
+    unsigned long long id_side = 0, id = 0;
+    DSV4G_HIP(hipStreamGetCaptureInfo(side->s, &cs_side, &id_side));
+    if (cs_side != hipStreamCaptureStatusNone) {
+      DSV4G_HIP(hipStreamGetCaptureInfo(st, &cs, &id));
+      if (cs != hipStreamCaptureStatusActive || id != id_side) side = nullptr;
+    }
+  }
   hipStream_t sst = side ? side->s : st;
   if (side) {
     DSV4G_HIP(hipEventRecord(side->fork, st));
@@ -1794,7 +1823,7 @@ int dsv4g_moe_forward_batch(float *out, const float *x, const DSV4GLayer *L,
   if (side) DSV4G_HIP(hipStreamWaitEvent(st, side->join, 0));
   const size_t total = (size_t)T * H / 8;  // 8-column groups (H % 128 == 0)
   hipLaunchKernelGGL(k_combine_batch, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st,
-                     out, w.ro, T, K, H);
+                     out, w.ro, w.idx, T, K, H, E);
   DSV4G_TRY(dsv4g_check_launch("combine_batch"));
   if (idx_out)
     DSV4G_HIP(hipMemcpyAsync(idx_out, w.idx, (size_t)T * K * sizeof(int),

@@ -9,7 +9,8 @@
  *  - batched calls accept at most 33 token vectors (DSV4_MAX_TOPK + 1);
  *  - calls may come from several threads (src/dsv4/dsv4_model.c:6703-6726):
  *    one process-wide mutex serialises GPU use.
- * Weights (host pointers) are uploaded to HBM on first use and stay resident;
+ * Weights (host pointers) stay resident in HBM when their range is
+ * registered and are uploaded per call otherwise (the weight cache below);
  * activations and outputs are copied per call on the default stream.
  */
 #include <math.h>
@@ -42,6 +43,14 @@ static void check(int rc, const char *what)
 }
 
 /* ------------------------------------------------------ weight cache ---- */
+/* Weights stay resident in HBM only for host ranges the caller registered
+ * (dsv4_gpu_register_weights): registration is the caller's promise that the
+ * range's contents stay as they are until it forgets or re-registers the
+ * range. Registering a range again uploads its current contents afresh, so a
+ * caller that refills a buffer with other weights (the reference's expert
+ * cache refills its slot buffers on a miss, src/dsv4/dsv4_model.c:3430-3458)
+ * re-registers it, or forgets it. Weights passed from an unregistered range
+ * are uploaded for that call only, so they can never be stale. */
 typedef struct WeightEntry {
     const unsigned char *host;
     size_t bytes;
@@ -60,8 +69,53 @@ static void *weights_find(const void *host, size_t bytes)
     return NULL;
 }
 
-static void *weights_upload(const void *host, size_t bytes)
+/* caller holds g_lock: drop every entry that overlaps [host, host + bytes)
+ * (bytes = 0: every entry containing host) */
+static void weights_drop(const void *host, size_t bytes)
 {
+    const unsigned char *lo = (const unsigned char *)host;
+    const unsigned char *hi = lo + (bytes ? bytes : 1);
+    WeightEntry **pp = &g_weights;
+    while (*pp) {
+        WeightEntry *w = *pp;
+        if (w->host < hi && lo < w->host + w->bytes) {
+            *pp = w->next;
+            dsv4g_free(w->dev);
+            free(w);
+        } else {
+            pp = &w->next;
+        }
+    }
+}
+
+/* Per-call staging of unregistered weights: one grow-only device buffer per
+ * weight operand of a call (a call passes at most four). */
+#define DSV4_HOST_WSLOTS 4
+static void *g_wstage[DSV4_HOST_WSLOTS];
+static size_t g_wstage_bytes[DSV4_HOST_WSLOTS];
+
+/* caller holds g_lock; slot: the operand's index within the call */
+static void *weights_get(const void *host, size_t bytes, int slot)
+{
+    if (!host) return NULL;
+    void *d = weights_find(host, bytes);
+    if (d) return d;
+    if (bytes > g_wstage_bytes[slot]) {
+        if (g_wstage[slot]) dsv4g_free(g_wstage[slot]);
+        g_wstage[slot] = NULL;
+        g_wstage_bytes[slot] = 0;
+        check(dsv4g_malloc(&g_wstage[slot], bytes), "weight staging");
+        g_wstage_bytes[slot] = bytes;
+    }
+    check(dsv4g_memcpy_h2d(g_wstage[slot], host, bytes, NULL), "weight staging");
+    return g_wstage[slot];
+}
+
+int dsv4_gpu_register_weights(const void *host, size_t bytes)
+{
+    if (!host || !bytes) return -1;
+    pthread_mutex_lock(&g_lock);
+    weights_drop(host, bytes);
     WeightEntry *w = (WeightEntry *)calloc(1, sizeof(*w));
     if (!w) fatal("out of memory in the weight cache");
     check(dsv4g_malloc(&w->dev, bytes), "weight upload");
@@ -71,39 +125,21 @@ static void *weights_upload(const void *host, size_t bytes)
     w->bytes = bytes;
     w->next = g_weights;
     g_weights = w;
-    return w->dev;
-}
-
-/* caller holds g_lock */
-static void *weights_get(const void *host, size_t bytes)
-{
-    if (!host) return NULL;
-    void *d = weights_find(host, bytes);
-    return d ? d : weights_upload(host, bytes);
-}
-
-int dsv4_gpu_register_weights(const void *host, size_t bytes)
-{
-    pthread_mutex_lock(&g_lock);
-    void *d = weights_get(host, bytes);
     pthread_mutex_unlock(&g_lock);
-    return d ? 0 : -1;
+    return 0;
 }
 
 void dsv4_gpu_forget_weights(const void *host)
 {
     pthread_mutex_lock(&g_lock);
-    WeightEntry **pp = &g_weights;
-    while (*pp) {
-        if ((*pp)->host == (const unsigned char *)host) {
-            WeightEntry *w = *pp;
-            *pp = w->next;
-            dsv4g_free(w->dev);
-            free(w);
-        } else {
-            pp = &(*pp)->next;
-        }
-    }
+    weights_drop(host, 0);
+    pthread_mutex_unlock(&g_lock);
+}
+
+void dsv4_gpu_forget_weights_range(const void *host, size_t bytes)
+{
+    pthread_mutex_lock(&g_lock);
+    weights_drop(host, bytes);
     pthread_mutex_unlock(&g_lock);
 }
 
@@ -276,8 +312,8 @@ void dsv4_gemv_fp4_batch_q(float *const *y, const float *const *qx,
     batch_guard(batch, "FP4");
     pthread_mutex_lock(&g_lock);
     const size_t qn = (size_t)(in + 127) / 128;
-    const uint8_t *dW = weights_get(W, fp4_w_bytes(in, rows));
-    const uint8_t *dS = weights_get(wscale_code, fp4_s_bytes(in, rows));
+    const uint8_t *dW = weights_get(W, fp4_w_bytes(in, rows), 0);
+    const uint8_t *dS = weights_get(wscale_code, fp4_s_bytes(in, rows), 1);
     Carver c = {arena((size_t)batch * (in + qn + rows) * 4 + 3 * 256), 0};
     float *dq = carve(&c, (size_t)batch * in * 4), *ds = carve(&c, (size_t)batch * qn * 4);
     float *dy = carve(&c, (size_t)batch * rows * 4);
@@ -301,10 +337,10 @@ void dsv4_gemv_fp4_pair_q(float *y0, float *y1, const float *qx, const float *qs
     if (rows <= 0) return;
     pthread_mutex_lock(&g_lock);
     const size_t qn = (size_t)(in + 127) / 128;
-    const uint8_t *dW0 = weights_get(W0, fp4_w_bytes(in, rows));
-    const uint8_t *dS0 = weights_get(S0, fp4_s_bytes(in, rows));
-    const uint8_t *dW1 = weights_get(W1, fp4_w_bytes(in, rows));
-    const uint8_t *dS1 = weights_get(S1, fp4_s_bytes(in, rows));
+    const uint8_t *dW0 = weights_get(W0, fp4_w_bytes(in, rows), 0);
+    const uint8_t *dS0 = weights_get(S0, fp4_s_bytes(in, rows), 1);
+    const uint8_t *dW1 = weights_get(W1, fp4_w_bytes(in, rows), 2);
+    const uint8_t *dS1 = weights_get(S1, fp4_s_bytes(in, rows), 3);
     Carver c = {arena(((size_t)in + qn + 2 * (size_t)rows) * 4 + 4 * 256), 0};
     float *dq = carve(&c, (size_t)in * 4), *ds = carve(&c, qn * 4);
     float *d0 = carve(&c, (size_t)rows * 4), *d1 = carve(&c, (size_t)rows * 4);
@@ -325,8 +361,8 @@ void dsv4_gemv_fp8_batch_q(float *const *y, const float *const *qx,
     batch_guard(batch, "FP8");
     pthread_mutex_lock(&g_lock);
     const size_t qn = (size_t)(in + 127) / 128;
-    const uint8_t *dW = weights_get(W, fp8_w_bytes(in, out));
-    const uint8_t *dS = weights_get(wscale_code, fp8_s_bytes(in, out));
+    const uint8_t *dW = weights_get(W, fp8_w_bytes(in, out), 0);
+    const uint8_t *dS = weights_get(wscale_code, fp8_s_bytes(in, out), 1);
     Carver c = {arena((size_t)batch * (in + qn + out) * 4 + 3 * 256), 0};
     float *dq = carve(&c, (size_t)batch * in * 4), *ds = carve(&c, (size_t)batch * qn * 4);
     float *dy = carve(&c, (size_t)batch * out * 4);
@@ -351,10 +387,10 @@ void dsv4_gemv_fp8_pair_q(float *y0, float *y1, const float *qx, const float *qs
     if (out <= 0) return;
     pthread_mutex_lock(&g_lock);
     const size_t qn = (size_t)(in + 127) / 128;
-    const uint8_t *dW0 = weights_get(W0, fp8_w_bytes(in, out));
-    const uint8_t *dS0 = weights_get(S0, fp8_s_bytes(in, out));
-    const uint8_t *dW1 = weights_get(W1, fp8_w_bytes(in, out));
-    const uint8_t *dS1 = weights_get(S1, fp8_s_bytes(in, out));
+    const uint8_t *dW0 = weights_get(W0, fp8_w_bytes(in, out), 0);
+    const uint8_t *dS0 = weights_get(S0, fp8_s_bytes(in, out), 1);
+    const uint8_t *dW1 = weights_get(W1, fp8_w_bytes(in, out), 2);
+    const uint8_t *dS1 = weights_get(S1, fp8_s_bytes(in, out), 3);
     Carver c = {arena(((size_t)in + qn + 2 * (size_t)out) * 4 + 4 * 256), 0};
     float *dq = carve(&c, (size_t)in * 4), *ds = carve(&c, qn * 4);
     float *d0 = carve(&c, (size_t)out * 4), *d1 = carve(&c, (size_t)out * 4);
@@ -373,7 +409,7 @@ void dsv4_gemv_bf16_batch(float *const *y, const float *const *x, int batch,
     if (batch <= 0 || out <= 0) return;
     batch_guard(batch, "BF16");
     pthread_mutex_lock(&g_lock);
-    const uint16_t *dW = weights_get(W, (size_t)in * out * 2);
+    const uint16_t *dW = weights_get(W, (size_t)in * out * 2, 0);
     Carver c = {arena((size_t)batch * (in + out) * 4 + 2 * 256), 0};
     float *dx = carve(&c, (size_t)batch * in * 4), *dy = carve(&c, (size_t)batch * out * 4);
     up_rows(dx, x, batch, (size_t)in);
@@ -394,8 +430,8 @@ static void gemv_fp8_float(float *y, const float *x, const uint8_t *W, const flo
     if (rows <= 0) return;
     pthread_mutex_lock(&g_lock);
     const size_t nsc = (size_t)((rows + block - 1) / block) * ((in + block - 1) / block);
-    const uint8_t *dW = weights_get(W, (size_t)rows * in);
-    const float *dS = weights_get(wscale, nsc * 4);
+    const uint8_t *dW = weights_get(W, (size_t)rows * in, 0);
+    const float *dS = weights_get(wscale, nsc * 4, 1);
     Carver c = {arena(((size_t)in + rows) * 4 + 512), 0};
     float *dx = carve(&c, (size_t)in * 4), *dy = carve(&c, (size_t)rows * 4);
     up(dx, x, (size_t)in * 4);
@@ -423,8 +459,8 @@ void dsv4_gemv_fp4(float *y, const float *qx, const float *qscale, const uint8_t
     pthread_mutex_lock(&g_lock);
     const size_t qn = (size_t)(in + 127) / 128;
     const size_t gcols = (size_t)(in + group - 1) / group;
-    const uint8_t *dW = weights_get(W, fp4_w_bytes(in, rows));
-    const float *dS = weights_get(wscale, (size_t)rows * gcols * 4);
+    const uint8_t *dW = weights_get(W, fp4_w_bytes(in, rows), 0);
+    const float *dS = weights_get(wscale, (size_t)rows * gcols * 4, 1);
     Carver c = {arena(((size_t)in + qn + rows) * 4 + 768), 0};
     float *dq = carve(&c, (size_t)in * 4), *ds = carve(&c, qn * 4);
     float *dy = carve(&c, (size_t)rows * 4);
@@ -444,8 +480,8 @@ void dsv4_router(int *idx, float *wt, const float *x, const float *gate, const f
     if (topk <= 0) return;
     pthread_mutex_lock(&g_lock);
     /* gate is a BF16 matrix passed as const float * (src/dsv4/dsv4_ops.c:494) */
-    const uint16_t *dG = weights_get(gate, (size_t)n_experts * hidden * 2);
-    const float *dB = bias ? weights_get(bias, (size_t)n_experts * 4) : NULL;
+    const uint16_t *dG = weights_get(gate, (size_t)n_experts * hidden * 2, 0);
+    const float *dB = bias ? weights_get(bias, (size_t)n_experts * 4, 1) : NULL;
     const int64_t *dT = NULL; /* hash layers: the token's tid2eid row only */
     Carver c = {arena(((size_t)hidden + 2 * (size_t)n_experts + 2 * (size_t)topk) * 4 +
                       (size_t)topk * 8 + 8 * 256), 0};

@@ -58,6 +58,8 @@ _SIGS = {
     "dsv4g_moe_workspace_init": [_vp, _Z, _vp],
     "dsv4g_moe_forward_batch": [_vp, _vp, C.POINTER(DSV4GLayer), _vp, _I, _vp, _Z, _vp, _vp,
                                 _vp],
+    "dsv4g_moe_forward_batch_routes": [_vp, _vp, C.POINTER(DSV4GLayer), _vp, _I, _vp, _Z, _vp,
+                                       _vp, _vp, _vp],
     "dsv4g_probe_mfma": [_I, _vp, _vp, _vp, _vp, _vp, _vp],
     "dsv4g_quant_fp4_rows": [_vp, _vp, _vp, _I, _I, _vp],
     "dsv4g_quant_fp8_blocks": [_vp, _vp, _vp, _I, _I, _I, _vp],
@@ -268,7 +270,11 @@ class GpuLib:
     def moe_batch_workspace_bytes(self, layer, n_tokens):
         return int(self.lib.dsv4g_moe_batch_workspace_bytes(C.byref(layer.struct), n_tokens))
 
-    def moe_forward_batch(self, layer, x, token_ids=None, workspace=None, out=None):
+    def moe_forward_batch(self, layer, x, token_ids=None, workspace=None, out=None,
+                          route_out=None):
+        """dsv4g_moe_forward_batch; with route_out ([n][topk+1][hidden] fp32)
+        dsv4g_moe_forward_batch_routes, which also writes the per-route
+        outputs before their BF16 rounding."""
         import torch
         n = x.shape[0]
         L = layer.struct
@@ -278,8 +284,14 @@ class GpuLib:
         out = torch.empty_like(x) if out is None else out
         idx = torch.empty(n, L.topk, dtype=torch.int32, device=x.device)
         wt = torch.empty(n, L.topk, dtype=torch.float32, device=x.device)
-        self._call("dsv4g_moe_forward_batch", _ptr(out), _ptr(x), C.byref(L), _ptr(token_ids), n,
-                   _ptr(workspace), workspace.numel(), _ptr(idx), _ptr(wt), self._stream())
+        if route_out is None:
+            self._call("dsv4g_moe_forward_batch", _ptr(out), _ptr(x), C.byref(L),
+                       _ptr(token_ids), n, _ptr(workspace), workspace.numel(), _ptr(idx),
+                       _ptr(wt), self._stream())
+        else:
+            self._call("dsv4g_moe_forward_batch_routes", _ptr(out), _ptr(x), C.byref(L),
+                       _ptr(token_ids), n, _ptr(workspace), workspace.numel(), _ptr(idx),
+                       _ptr(wt), _ptr(route_out), self._stream())
         return out, idx, wt
 
     def probe_mfma(self, kind, A, B, sa=None, sb=None):

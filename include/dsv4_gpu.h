@@ -8,10 +8,11 @@
  *    libdsv4_gpu.so next to layer 2 and replace:
  *      include/dsv4/dsv4.h:185-211, 251-254  (public kernels, router)
  *      src/dsv4/dsv4_internal.h:256-286, 326-331 (internal GEMVs, quant)
- *    Weights passed by host pointer are uploaded to HBM on first use and kept
- *    resident, keyed by host address and size (weights are const in the
- *    reference); dsv4_gpu_register_weights()/dsv4_gpu_forget_weights() manage
- *    that cache explicitly. Activations are copied per call.
+ *    Weights stay resident in HBM for host ranges registered with
+ *    dsv4_gpu_register_weights() (re-registering a range uploads its current
+ *    contents; dsv4_gpu_forget_weights*() drop it); weights from an
+ *    unregistered range are uploaded for that call only, so a refilled host
+ *    buffer can never be served stale. Activations are copied per call.
  *
  * 2. Device-pointer API (dsv4g_*): every pointer is device memory, every call
  *    is asynchronous on the given HIP stream (NULL = default stream) and
@@ -183,16 +184,29 @@ int dsv4g_moe_decode_routing(int *idx_out, float *wt_out, const DSV4GLayer *L, i
                              void *workspace, void *stream);
 
 /* Batched MoE layer: moe_forward_batch (src/dsv4/dsv4_model.c:6812-7117) for
- * n_tokens rows of x (speculative verify, prefill) as a grouped GEMM on the
- * block-scaled MFMA. Routing (idx, wt) is bit-exact; expert outputs agree to
- * fp32 rounding of the MFMA accumulation. x must hold BF16 values for the
+ * n_tokens rows of x (speculative verify, prefill) as grouped GEMMs on the
+ * BF16 MFMA (v_mfma_f32_16x16x32_bf16) with exactly scaled operands: FP4/FP8
+ * weights times their E8M0 scale and the E4M3-quantised activations are
+ * exact in BF16, so every product is exact and only the fp32 summation order
+ * differs from the reference. Routing (idx, wt) is bit-exact; expert outputs
+ * agree to fp32 rounding of the accumulation. x must hold BF16 values for the
  * tightest router bound (other inputs are handled with a wider margin).
+ * A route without a selectable expert adds nothing to its token's output.
  * workspace: at least dsv4g_moe_batch_workspace_bytes(L, n_tokens). */
 size_t dsv4g_moe_batch_workspace_bytes(const DSV4GLayer *L, int n_tokens);
 int dsv4g_moe_forward_batch(float *out, const float *x, const DSV4GLayer *L,
                             const int *token_ids, int n_tokens, void *workspace,
                             size_t workspace_bytes, int *idx_out, float *wt_out,
                             void *stream);
+/* The same, also writing each route's expert output before its BF16 rounding
+ * to route_out [n_tokens][topk + 1][hidden] (fp32; routes in ascending expert
+ * id, slot topk the shared expert; slots of routes without an expert are not
+ * written). No counterpart in the reference, which rounds each expert output
+ * to BF16 (src/dsv4/dsv4_model.c:1073): for validating the accumulation. */
+int dsv4g_moe_forward_batch_routes(float *out, const float *x, const DSV4GLayer *L,
+                                   const int *token_ids, int n_tokens, void *workspace,
+                                   size_t workspace_bytes, int *idx_out, float *wt_out,
+                                   float *route_out, void *stream);
 /* One 16x16 tile of the MFMA forms the batch path uses, from row-major
  * operands (kind 0: FP4 x FP8 block-scaled, 1: FP8 x FP8 block-scaled,
  * 2: BF16), for validating operand layouts. D: 16x16 fp32 row-major. */
@@ -245,9 +259,17 @@ void dsv4_router(int *idx, float *wt, const float *x, const float *gate, const f
                  const int64_t *tid2eid, int token_id, int hidden, int n_experts,
                  int topk, int hash_layer, float route_scale, float rms_eps); /* dsv4.h:251 */
 
-/* Weight residency for the drop-in entry points. */
+/* Weight residency for the drop-in entry points (no counterpart in the
+ * reference, whose weights are host memory). register: keep [host, host +
+ * bytes) resident, uploading its current contents (again, if it overlaps a
+ * registered range: that range is dropped first); the caller keeps the
+ * contents unchanged until it forgets or re-registers the range. forget:
+ * drop every registered range containing host; forget_range: every range
+ * overlapping [host, host + bytes). Unregistered weights are uploaded per
+ * call. */
 int dsv4_gpu_register_weights(const void *host, size_t bytes);
 void dsv4_gpu_forget_weights(const void *host);
+void dsv4_gpu_forget_weights_range(const void *host, size_t bytes);
 void dsv4_gpu_forget_all_weights(void);
 
 #ifdef __cplusplus

@@ -622,6 +622,83 @@ void orc_moe_forward(const OrcLayer *L, const float *x, int token_id,
     free(routed);
 }
 
+/* The router of moe_forward / moe_forward_batch for n tokens at once
+ * (src/dsv4/dsv4_model.c:6615-6676, 6865-6906): per token the BF16 gate GEMV
+ * and orc_route, tokens spread over OpenMP threads. idx, wt: [n][topk]. */
+void orc_route_tokens(const OrcLayer *L, const float *x, const int *token_ids,
+                      int n_tokens, int *idx, float *wt)
+{
+    const int H = L->hidden, E = L->n_experts, K = L->topk;
+    #pragma omp parallel
+    {
+        float *z = (float *)orc_alloc((size_t)E * sizeof(float));
+        #pragma omp for schedule(dynamic, 4)
+        for (int t = 0; t < n_tokens; t++) {
+            const float *xt = x + (size_t)t * H;
+            for (int e = 0; e < E; e++)
+                z[e] = orc_bf16_row(L->gate_w + (size_t)e * H, xt, H);
+            orc_route(idx + (size_t)t * K, wt + (size_t)t * K, z, L->bias,
+                      L->is_hash ? L->tid2eid + (size_t)token_ids[t] * K : NULL,
+                      E, K, L->route_scale);
+        }
+        free(z);
+    }
+}
+
+/* The per-route expert outputs of moe_forward before their BF16 rounding:
+ * routes[k] = the down GEMV accumulators of route k (ascending expert id, as
+ * moe_forward visits them), routes[K] those of the shared expert. The
+ * reference rounds each to BF16 (dsv4_gemv_fp4_q, src/dsv4/dsv4_model.c:1073;
+ * dsv4_gemv_fp8_q with round_out = 1, :6433), and bf16(routes) are the
+ * outputs orc_moe_forward sums. idx, wt: the routing (optional). */
+void orc_moe_route_outputs(const OrcLayer *L, const float *x, int token_id,
+                           float *routes, int *idx_out, float *wt_out)
+{
+    const int H = L->hidden, I = L->inter, K = L->topk;
+    const int limit = (int)L->swiglu_limit;
+    const int qn = (H + 127) / 128;
+    float *z = (float *)orc_alloc((size_t)L->n_experts * sizeof(float));
+    float *qx = (float *)orc_alloc((size_t)H * sizeof(float));
+    float *qsc = (float *)orc_alloc((size_t)qn * sizeof(float));
+    float *work = (float *)orc_alloc((size_t)(4 * I + (I + 127) / 128) * sizeof(float));
+    float *gate = work, *up = work + I, *y = work + 2 * I, *qy = work + 3 * I;
+    float *qys = work + 4 * I;
+    int idx[64];
+    float wt[64];
+    orc_gemv_bf16(z, x, L->gate_w, H, L->n_experts, 0);
+    orc_route(idx, wt, z, L->bias,
+              L->is_hash ? L->tid2eid + (size_t)token_id * K : NULL,
+              L->n_experts, K, L->route_scale);
+    orc_quant_fp8_act(qx, qsc, x, H);
+    const size_t w1 = (size_t)I * ((H + 1) / 2), w2 = (size_t)H * ((I + 1) / 2);
+    const size_t s1 = (size_t)I * ((H + ORC_FP4_GROUP - 1) / ORC_FP4_GROUP);
+    const size_t s2 = (size_t)H * ((I + ORC_FP4_GROUP - 1) / ORC_FP4_GROUP);
+    const size_t dpc = (size_t)(I + 1) / 2, dgc = (size_t)(I + ORC_FP4_GROUP - 1) / ORC_FP4_GROUP;
+    for (int k = 0; k < K; k++) {
+        float *r = routes + (size_t)k * H;
+        if (idx[k] < 0 || idx[k] >= L->n_experts) {
+            for (int i = 0; i < H; i++) r[i] = 0.0f;
+            continue;
+        }
+        const uint8_t *s, *w;
+        orc_layer_expert(L, idx[k], &s, &w);
+        orc_gemv_fp4_pair_q(gate, up, qx, qsc, w, s, w + w1 + w2, s + s1 + s2, H, I);
+        orc_swiglu_quant(y, qy, qys, gate, up, I, limit, wt[k]);
+        #pragma omp parallel for schedule(static)
+        for (int row = 0; row < H; row++)
+            r[row] = orc_fp4_row(w + w1 + row * dpc, s + s1 + row * dgc, qy, qys, I);
+    }
+    orc_gemv_fp8_pair_q(gate, up, qx, qsc, L->sh1, L->sh1_s, L->sh3, L->sh3_s, H, I);
+    orc_swiglu_quant(y, qy, qys, gate, up, I, limit, 1.0f);
+    orc_gemv_fp8_q(routes + (size_t)K * H, qy, qys, L->sh2, L->sh2_s, I, H, 0);
+    if (idx_out) memcpy(idx_out, idx, (size_t)K * sizeof(int));
+    if (wt_out) memcpy(wt_out, wt, (size_t)K * sizeof(float));
+    free(z);
+    free(qx);
+    free(qsc);
+    free(work);
+}
+
 /* moe_forward_batch (src/dsv4/dsv4_model.c:6812-7117): route every token,
  * visit the distinct experts in ascending id, run each on its tokens in
  * chunks of topk+1 (expert_forward_batch_routes, :6486-6524) and add every

@@ -109,6 +109,10 @@ typedef struct {
 
 void orc_moe_forward(const OrcLayer *L, const float *x, int token_id,
                      float *out, int *idx_out, float *wt_out);
+void orc_route_tokens(const OrcLayer *L, const float *x, const int *token_ids,
+                      int n_tokens, int *idx, float *wt);
+void orc_moe_route_outputs(const OrcLayer *L, const float *x, int token_id,
+                           float *routes, int *idx_out, float *wt_out);
 void orc_moe_forward_batch(const OrcLayer *L, const float *x,
                            const int *token_ids, int n_tokens, float *out,
                            int *idx_out, float *wt_out);

@@ -133,6 +133,31 @@ class Oracle(_Base):
     def fp4_table(self):
         return np.array([self.lib.orc_fp4_e2m1(i) for i in range(16)], np.float32)
 
+    def route_tokens(self, layer, x, token_ids=None):
+        """Router of moe_forward for every row of x: idx, wt [n][topk]."""
+        x = f32(x)
+        n = x.shape[0]
+        tok = np.ascontiguousarray(np.zeros(n) if token_ids is None else token_ids, np.int32)
+        L = make_layer_struct(layer)
+        idx = np.empty((n, layer["topk"]), np.int32)
+        wt = np.empty((n, layer["topk"]), np.float32)
+        self.lib.orc_route_tokens(C.byref(L), _p(x, _f32p), _p(tok, _i32p), n, _p(idx, _i32p),
+                                  _p(wt, _f32p))
+        return idx, wt
+
+    def moe_route_outputs(self, layer, x, token_id=0):
+        """Per-route expert outputs of moe_forward before BF16 rounding:
+        [topk + 1][hidden] (routes in ascending id, then the shared expert),
+        with the routing."""
+        L = make_layer_struct(layer)
+        K, H = layer["topk"], layer["hidden"]
+        routes = np.empty((K + 1, H), np.float32)
+        idx = np.empty(K, np.int32)
+        wt = np.empty(K, np.float32)
+        self.lib.orc_moe_route_outputs(C.byref(L), _p(f32(x), _f32p), int(token_id),
+                                       _p(routes, _f32p), _p(idx, _i32p), _p(wt, _f32p))
+        return routes, idx, wt
+
     # ---- GEMVs ----
     def gemv_bf16(self, x, W, in_, out, round_out=0):
         x = f32(x)

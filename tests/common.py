@@ -111,3 +111,20 @@ def same_bits(a, b):
     a = np.ascontiguousarray(a, np.float32).view(np.uint32)
     b = np.ascontiguousarray(b, np.float32).view(np.uint32)
     return a.shape == b.shape and bool(np.array_equal(a, b))
+
+
+def zipf_bias(n_experts, seed=8, s=1.2, strength=0.15):
+    """Router bias giving Zipf(s)-skewed expert popularity over a seeded
+    permutation of the experts: strength * (log p_rank - mean), p ~ rank^-s
+    (the bias bench.py times the batched path with)."""
+    rng = np.random.default_rng(seed)
+    p = np.arange(1, n_experts + 1, dtype=np.float64) ** -s
+    b = np.empty(n_experts)
+    b[rng.permutation(n_experts)] = np.log(p / p.sum())
+    return (strength * (b - b.mean())).astype(np.float32)
+
+
+def bf16_ulp(v):
+    """Spacing of BF16 values at |v| (normal range)."""
+    e = np.floor(np.log2(np.maximum(np.abs(v), 2.0 ** -126)))
+    return np.ldexp(1.0, (e - 7).astype(int))

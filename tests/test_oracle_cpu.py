@@ -7,6 +7,7 @@ import json
 import os
 import re
 import subprocess
+import sys
 
 import numpy as np
 import pytest
@@ -109,6 +110,33 @@ def test_golden_moe(orc, gold, tag):
     s, w = expert_slot(L, 3)
     assert same_bits(orc.expert_forward(qx, qs, s, w, 256, 128, 10, 0.41), gold[f"{tag}_exp3"])
     assert same_bits(orc.shared_expert_forward(qx, qs, L, 256, 128, 10), gold[f"{tag}_shared"])
+
+
+@pytest.mark.parametrize("tag", ["moe", "moeh"])
+def test_route_tokens_and_route_outputs_pinned(orc, gold, tag):
+    """The many-token router and the pre-BF16 per-route outputs (the checks
+    the full-size GPU tests use) against the golden moe_forward: same
+    routing; each route rounded to BF16 equals the reference's expert output
+    (expert_forward / shared_expert_forward) and their ordered sum is the
+    golden layer output."""
+    L = layer_from_golden(gold, tag)
+    X, tok = gold[f"{tag}_x"], gold[f"{tag}_tok"]
+    idx, wt = orc.route_tokens(L, X, tok)
+    assert np.array_equal(idx, gold[f"{tag}_idx"]) and same_bits(wt, gold[f"{tag}_wt"])
+    H, I = L["hidden"], L["inter"]
+    for t in range(X.shape[0]):
+        routes, i, w = orc.moe_route_outputs(L, X[t], int(tok[t]))
+        assert np.array_equal(i, gold[f"{tag}_idx"][t]) and same_bits(w, gold[f"{tag}_wt"][t])
+        qx, qs = orc.quant_fp8_act(X[t])
+        for k in range(L["topk"]):
+            s, wb = expert_slot(L, i[k])
+            assert same_bits(bf16_values(routes[k]),
+                             orc.expert_forward(qx, qs, s, wb, H, I, 10, w[k])), (t, k)
+        assert same_bits(bf16_values(routes[-1]), orc.shared_expert_forward(qx, qs, L, H, I, 10))
+        acc = np.zeros(H, np.float32)
+        for k in range(L["topk"] + 1):
+            acc = (acc + bf16_values(routes[k])).astype(np.float32)
+        assert same_bits(bf16_values(acc), gold[f"{tag}_out"][t])
 
 
 # ------------------------------------------------ reference unit-test KATs
@@ -398,3 +426,22 @@ def test_library_scalar_entry_points(orc):
     assert same_bits(got, orc.round_e4m3(v))
     got = np.array([lib.dsv4_f32_to_bf16(float(a)) for a in v], np.uint16)
     assert np.array_equal(got, orc.f32_to_bf16(v))
+
+
+@pytest.mark.skipif(not os.path.exists(LIB), reason="library not built")
+@pytest.mark.parametrize("fn,kind", [("dsv4_gemv_fp4_batch_q", "FP4"),
+                                     ("dsv4_gemv_fp8_batch_q", "FP8"),
+                                     ("dsv4_gemv_bf16_batch", "BF16")])
+def test_dropin_batch_limit_exits_like_the_reference(fn, kind):
+    """The batched drop-ins exit(1) with a message above 33 token vectors, as
+    the reference does (src/dsv4/dsv4_model.c:689-693, 1094-1098); the check
+    comes before any GPU work, so it runs here in a child process."""
+    args = {"dsv4_gemv_fp4_batch_q": "None, None, None, 34, None, None, 4096, 2048",
+            "dsv4_gemv_fp8_batch_q": "None, None, None, 34, None, None, 4096, 2048, 1",
+            "dsv4_gemv_bf16_batch": "None, None, 34, None, 4096, 256, 0"}[fn]
+    code = f"import ctypes as C; C.CDLL({LIB!r}).{fn}({args}); print('returned')"
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 1, (r.returncode, r.stdout, r.stderr)
+    assert f"dsv4: {kind} batch 34 exceeds 33" in r.stderr
+    assert "returned" not in r.stdout
