@@ -1165,17 +1165,13 @@ __device__ __forceinline__ void gemm_k_loop_fast(v4f (&acc)[NM][2][4], const Buf
   // window's step 0, during step q's MFMAs), so that the conversions can
   // issue between the MFMAs instead of in front of them
   uint32_t Ac[NM][2] = {}, Acn[NM][2] = {};
-  if constexpr (FP4) {
+  uint4 A[NM][2];
+  if constexpr (!FP4) {
 #pragma unroll
     for (int m = 0; m < NM; ++m)
 #pragma unroll
-      for (int f = 0; f < 2; ++f) Ac[m][f] = code(m, f, 0);
+      for (int f = 0; f < 2; ++f) A[m][f] = a_op(0, m, f, 0, 0u);
   }
-  uint4 A[NM][2];
-#pragma unroll
-  for (int m = 0; m < NM; ++m)
-#pragma unroll
-    for (int f = 0; f < 2; ++f) A[m][f] = a_op(0, m, f, 0, Ac[m][f]);
 #pragma unroll
   for (int sw = 0; sw < NSW; ++sw) {
     uint8_t *bb = bt + (sw & 1) * GT_BT_BYTES;
@@ -1184,6 +1180,21 @@ __device__ __forceinline__ void gemm_k_loop_fast(v4f (&acc)[NM][2][4], const Buf
       *reinterpret_cast<uint4 *>(bb + (tid / 16 + 16 * k) * GT_BROW2 + 16 * (tid % 16)) =
           B[sw & 1][k];
     __syncthreads();
+    if (FP4 && sw == 0) {
+      // the tile's codes were staged into LDS by every wave's direct-to-LDS
+      // loads (stage_codes), and a wave reads rows another wave staged: only
+      // after this barrier, which every wave reaches with its own staging
+      // complete (the staging loads precede the activation loads whose
+      // values it just stored, and loads complete in order), are they all in
+      // place
+#pragma unroll
+      for (int m = 0; m < NM; ++m)
+#pragma unroll
+        for (int f = 0; f < 2; ++f) {
+          Ac[m][f] = code(m, f, 0);
+          A[m][f] = a_op(0, m, f, 0, Ac[m][f]);
+        }
+    }
     const bool pre = sw + 2 < NSW;
     const uint8_t *brow_p = bb + (l % 16) * GT_BROW2 + (l / 16) * 64;
     uint4 Bq[2][4];

@@ -82,10 +82,12 @@ def check_route_outputs(orc, L, X, ro32, idx, sample):
     for t in sample:
         ref, i, _ = orc.moe_route_outputs(L, X[t])
         assert np.array_equal(i, idx[t]), t
-        for k in range(ref.shape[0]):
-            e = max_rel_err(ro32[t, k], ref[k])
-            assert e <= 1e-3, (t, k, e)
-            worst = max(worst, e)
+        errs = [max_rel_err(ro32[t, k], ref[k]) for k in range(ref.shape[0])]
+        if max(errs) > 1e-5:
+            print(f"\n  sample {t}: per-route max|d|/max|ref| " +
+                  " ".join(f"{e:.1e}" for e in errs))
+        assert max(errs) <= 1e-3, (t, errs)
+        worst = max(worst, max(errs))
     return worst
 
 
@@ -166,9 +168,9 @@ def test_prefill_4096_full_size(env, full_layer):
     print(f"\n  prefill 4096: experts hit {(counts > 0).sum()}, max {counts.max()}, "
           f"median {np.median(counts)}")
     sample = list(np.random.default_rng(3).choice(4096, 16, replace=False))
+    ro = H(ro32[torch.tensor(sample, device=env["dev"])])
+    wr = check_route_outputs(orc, L, Xh[sample], ro, idx[sample], range(len(sample)))
     worst, exact = check_tolerance(orc, L, Xh, out, sample)
-    ro = H(ro32[torch.tensor(sample[:6], device=env["dev"])])
-    wr = check_route_outputs(orc, L, Xh[sample[:6]], ro, idx[sample[:6]], range(6))
     print(f"  sample outputs: bit-exact {exact}/16, max norm-relative {worst:.2e}; "
           f"per-route fp32 max|d|/max|ref| {wr:.2e}")
 
@@ -194,3 +196,25 @@ def test_512_experts_decode_and_batch(env):
         ri, rw = orc.route_tokens(L, Xh[:n])
         assert np.array_equal(idx, ri) and same_bits(wt, rw), n
         check_tolerance(orc, L, Xh, out, range(0, n, 3))
+
+
+@pytest.mark.parametrize("n", [64, 4096])
+def test_batch_result_independent_of_workspace_contents(env, full_layer, n):
+    """The batched layer reads nothing of its workspace that it has not
+    written in the same call: a workspace full of 0xFF bytes (NaN patterns)
+    and one full of zeros give the same bits."""
+    torch, lib, synth = env["torch"], env["lib"], env["synth"]
+    DL, L = with_zipf(env, *full_layer, 256)
+    X = synth.bf16_tokens(n, 4096, seed=11 + n, device=env["dev"])
+    need = lib.moe_batch_workspace_bytes(DL, n)
+    res = []
+    for fill in (0x00, 0xFF, 0x00):
+        ws = torch.full((need,), fill, dtype=torch.uint8, device=env["dev"])
+        out, idx, wt = lib.moe_forward_batch(DL, X, workspace=ws)
+        torch.cuda.synchronize()
+        res.append((H(out), H(idx), H(wt)))
+        del ws
+    for r in res[1:]:
+        assert np.array_equal(r[1], res[0][1]) and same_bits(r[2], res[0][2])
+        diff = np.nonzero(~np.all(r[0].view(np.uint32) == res[0][0].view(np.uint32), axis=1))[0]
+        assert diff.size == 0, (diff.size, diff[:10])
