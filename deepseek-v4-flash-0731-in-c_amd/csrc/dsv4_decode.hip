@@ -44,6 +44,8 @@
 // the work and resets its counter. The counters
 // sit in the first bytes of the workspace, which must be zero before the
 // first call (dsv4g_moe_workspace_init); every call leaves them zero.
+#include <mutex>
+
 #include "dsv4_device.h"
 #include "dsv4_gpu_internal.h"
 #include "dsv4_tiles.h"
@@ -1042,6 +1044,44 @@ int dec_launch(int phase, float *out, const float *x, const DSV4GLayer *L, const
   return dsv4g_fail(DSV4G_EINVAL, "moe_decode: bad phase %d", phase);
 }
 
+// The no-allocation entry's workspace: one array per device, held until the
+// process ends. In host code `scratch` names a host-side stand-in, not device
+// memory: kernels and fills take the device address that hipGetSymbolAddress
+// returns for the current device, kept in g_scratch_ptr.
+#define DEC_SCRATCH_BYTES ((size_t)16 << 20)
+static __device__ __align__(256) uint8_t scratch[DEC_SCRATCH_BYTES];
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[64];
+
+// The current device's scratch address, resolved once per device. Device
+// globals start zeroed when the code object loads; a first call that is not
+// being captured also clears the control words with the fill kernel (no
+// memset: the call may be captured into a graph).
+int scratch_ptr(hipStream_t st, void **out) {
+  int dev = 0;
+  DSV4G_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= 64) return dsv4g_fail(DSV4G_EINVAL, "moe_noalloc: device %d", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return dsv4g_fail(DSV4G_EHIP, "moe_noalloc: hipGetSymbolAddress(scratch) failed: %s",
+                        hipGetErrorString(e));
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    DSV4G_HIP(hipStreamIsCapturing(st, &cs));
+    if (cs == hipStreamCaptureStatusNone) {
+      const size_t words = DEC_CTL_BYTES / 4;
+      hipLaunchKernelGGL(k_fill_zero_u32, dim3((unsigned)((words + 255) / 256)), dim3(256), 0,
+                         st, (unsigned *)p, words);
+      DSV4G_TRY(dsv4g_check_launch("moe_noalloc_init"));
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1099,3 +1139,19 @@ int dsv4g_moe_forward_fast(float *out, const float *x, const DSV4GLayer *L,
 }
 
 }  // extern "C"
+
+extern "C" int dsv4g_moe_forward_noalloc(float *out, const float *x, const DSV4GLayer *L,
+                                         const int *token_ids, int n_tokens, int *idx_out,
+                                         float *wt_out, void *stream) {
+  DSV4G_TRY(dsv4g_layer_ok(L, "moe_noalloc"));
+  if (n_tokens <= 0) return dsv4g_fail(DSV4G_EINVAL, "moe_noalloc: n_tokens must be > 0");
+  const size_t need = dsv4g_moe_workspace_bytes(L, n_tokens);
+  if (need > DEC_SCRATCH_BYTES)
+    return dsv4g_fail(DSV4G_EINVAL,
+                      "moe_noalloc: %d tokens of this layer need %zu bytes of workspace, more "
+                      "than the %zu bytes of the library's scratch; pass fewer tokens per call",
+                      n_tokens, need, DEC_SCRATCH_BYTES);
+  void *ws = nullptr;
+  DSV4G_TRY(scratch_ptr((hipStream_t)stream, &ws));
+  return dsv4g_moe_forward(out, x, L, token_ids, n_tokens, ws, need, idx_out, wt_out, stream);
+}

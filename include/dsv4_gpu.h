@@ -169,6 +169,17 @@ int dsv4g_moe_forward(float *out, const float *x, const DSV4GLayer *L, const int
 int dsv4g_moe_forward_fast(float *out, const float *x, const DSV4GLayer *L,
                            const int *token_ids, int n_tokens, void *workspace,
                            size_t workspace_bytes, int *idx_out, float *wt_out, void *stream);
+/* dsv4g_moe_forward with no workspace argument and no allocation of any kind:
+ * the workspace is the library's own 16 MiB device array (one per GPU, held
+ * until the process ends), so the call fits code under HIP graph capture and
+ * loops that may not allocate. No counterpart in the reference: for callers
+ * that cannot allocate. Same results as dsv4g_moe_forward; EINVAL when
+ * dsv4g_moe_workspace_bytes(L, n_tokens) exceeds 16 MiB (about 2.1 MiB per
+ * token at the model's shape: up to 7 tokens per call). Every call on one GPU shares that GPU's array: calls that
+ * overlap on one GPU (two streams, two threads) race and must not be issued. */
+int dsv4g_moe_forward_noalloc(float *out, const float *x, const DSV4GLayer *L,
+                              const int *token_ids, int n_tokens, int *idx_out, float *wt_out,
+                              void *stream);
 /* The same layer as four ordered phases, for callers that interleave or
  * time them: 0 router logits, candidate experts and activation quant; 1
  * gate/up GEMVs of the candidates and the shared expert, with the exact
