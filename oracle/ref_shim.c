@@ -13,7 +13,10 @@
  * The MoE entries run on a hand-built DSV4Model whose expert cache holds every
  * expert of layer 0, so every expert lookup is a hit and no I/O path runs
  * (expert_get_many, src/dsv4/dsv4_model.c:3642-3663).
- * Output goes to oracle/_ref/ only; nothing here is shipped.
+ * Output goes to oracle/_ref/ only: git-ignored, so it never enters the
+ * repository's history, but it travels with the working tree to the GPU
+ * host as a built file, where the benchmark's CPU-baseline leg times it.
+ * It is the checker and the CPU baseline, never part of the product.
  */
 #include "dsv4_model.c"
 
