@@ -1,26 +1,34 @@
 // dsv4_decode.hip - the decode MoE layer on gfx950: moe_forward
-// (src/dsv4/dsv4_model.c:6599-6807) for a few tokens, bit for bit, as four
+// (src/dsv4/dsv4_model.c:6599-6807) for a few tokens, bit for bit, as two
 // kernels per layer.
 //
-//   k_dec_router   approximate router logits z and sum|w*x| for every
-//                  (token, expert) and the approximate choice
-//                  sqrt_softplus(z) + bias, one workgroup per expert; the
-//                  FP8 activation quant of x.
-//   k_dec_gateup   every workgroup that needs them derives the token's
-//                  candidate experts (below) from the approximate choices
-//                  first; then gate and up GEMVs of every candidate (FP4) and of the
-//                  shared expert (FP8), a workgroup holding the same rows of
-//                  both so that it writes t = silu(bf16 gate) * bf16 up
-//                  (src/dsv4/dsv4_model.c:6264-6268); beside them one
-//                  workgroup per candidate slot runs the reference's exact
-//                  sequential logit chain (dsv4_gemv_bf16,
-//                  src/dsv4/dsv4_model.c:298-303), and the last of those
-//                  takes the exact top-k and route weights
-//                  (src/dsv4/dsv4_model.c:6615-6676).
-//   k_dec_down     per (token, route): y = bf16(t * w), per-128 FP8 requant
-//                  into LDS (src/dsv4/dsv4_model.c:6239-6287), the down GEMV.
-//   k_dec_combine  the routes in ascending expert id, then the shared expert,
-//                  rounded to BF16 (src/dsv4/dsv4_model.c:6795-6805).
+//   k_dec_front  one launch with two kinds of workgroups, in this index
+//                order (workgroups are dispatched in index order; a wait
+//                only ever holds a workgroup whose producers were
+//                dispatched before it and never wait on it):
+//                * streaming (the first E of them first route expert j:
+//                  approximate router logits z and sum|w*x| for every token
+//                  and the approximate choice sqrt_softplus(z) + bias,
+//                  published as self-marked 64-bit records): each derives
+//                  every token's candidate experts (below) from the records
+//                  itself, then streams, one register tile at a time, its
+//                  tiles of the shared FP8 expert's gate/up, its FP4 gate/up
+//                  items of the candidates, t = silu(bf16 gate) * bf16 up
+//                  into the candidate's slot (src/dsv4/dsv4_model.c:
+//                  6264-6268), and its tiles of the shared expert's down rows;
+//                * chain, a few per token (between the first E streaming
+//                  workgroups and the rest): for the candidate positions c,
+//                  c + maxc, ... the reference's exact sequential logit chain
+//                  (dsv4_gemv_bf16, src/dsv4/dsv4_model.c:298-303); the last
+//                  of them waits for the others and takes the exact top-k and
+//                  route weights (src/dsv4/dsv4_model.c:6615-6676).
+//   k_dec_back   one workgroup per route: the route weight scales t, the
+//                per-128 FP8 requant (src/dsv4/dsv4_model.c:6239-6287),
+//                published as codes; then one workgroup per 8 output rows:
+//                the FP4 down rows of every route (weights loaded while the
+//                requant runs), then the routes in ascending expert id and the
+//                shared expert, rounded to BF16
+//                (src/dsv4/dsv4_model.c:6795-6805).
 //
 // Candidates. A parallel logit differs from the sequential fmaf chain by at
 // most gamma_d + gamma_H times sum|w*x| (d: the parallel sum's rounding
@@ -28,22 +36,26 @@
 // the score's own rounding, and doubled for both sides, that gives delta: an
 // expert whose approximate choice is below (k-th best approximate choice) -
 // delta has k experts surely above it and cannot be selected. The others are
-// the candidates, in ascending expert id. Gate/up runs for every candidate
-// (persistent workgroups over (candidate, tile) items) while the exact
-// chains run beside it, one chain workgroup per candidate position modulo
-// maxc, so the chains' latency (a 4096-long dependent fmaf chain, about
-// 15 us) hides under the weight stream. Near-ties (a constant gate) only
-// make more items.
+// the candidates, in ascending expert id; gate/up runs for every candidate
+// while their exact chains run. Near-ties (a constant gate) only make more
+// candidates: more chains in parallel and more gate/up items.
 //
-// The candidates are derived redundantly by each workgroup of k_dec_gateup
-// that needs them (a few hundred cycles of one wave, beside the workgroup's
-// first loads): a last-arrival hand-off in k_dec_router would cost a
-// device-scope fence and a memory round trip on the critical path. The
-// hand-off from the chains to the selection uses one device-scope release
-// fence and counter increment per workgroup; the last arrival acquires, does
-// the work and resets its counter. The counters
-// sit in the first bytes of the workspace, which must be zero before the
-// first call (dsv4g_moe_workspace_init); every call leaves them zero.
+// Hand-offs inside a launch. On this part every XCD has its own L2, and a
+// device-scope release fence writes back a whole L2; atomics on one address
+// from many workgroups are serialised at about 170 ns each, and under full
+// memory traffic every dependent round trip costs microseconds. So data that
+// crosses workgroups inside a launch is stored and loaded with agent-scope
+// relaxed atomics (write-through stores, loads of the coherent copy: ld_dev /
+// st_dev) and is either self-marked (the router records: one 64-bit store
+// carries the value and its mark, polled directly) or followed by a flag,
+// one word per producer on a line of its own: a producer waits for its own
+// stores (vmcnt), then sets its flag; the waiter polls all the flags with
+// one wave. Every wait is bounded: one that runs out sets a sticky error
+// word (dsv4g_moe_decode_status) and the workgroup leaves, so a broken
+// hand-off ends as an error, never as a hang. Records and flags live in the
+// workspace, zero before the first call (dsv4g_moe_workspace_init); every
+// call leaves them zero. Data that crosses the launch boundary uses plain
+// loads and stores.
 #include <mutex>
 
 #include "dsv4_device.h"
@@ -52,8 +64,20 @@
 
 namespace dsv4 {
 
-#define DEC_CTL_BYTES 4096  // control words: [0] + one per token, so n <= 1023
-#define DEC_NP 8            // passes per FP4 tile (gate/up pairs and down)
+#define DEC_CTL_BYTES 4096  // control words
+#define DEC_NP 8            // passes per FP4 gate/up tile
+// control word indices
+#define DEC_ERR 0   // sticky error bits (DEC_ERR_*)
+#define DEC_FS 16   // words between two producer flags (one 64-byte line each)
+#define DEC_MAX_TOKENS 1020
+#define DEC_ERR_TIMEOUT 1u
+// polls of a wait before it gives up (each at least one memory round trip,
+// about a microsecond: on the order of a second)
+#define DEC_SPIN_LIMIT (1u << 20)
+#define DB_RC 6  // routes per chunk of k_dec_back
+// set in the high word of a router record once it is written (the low 31
+// bits hold sum|w*x|, whose sign bit is always clear)
+#define DEC_REC_SET 0x80000000u
 
 struct DecArgs {
   const float *x;
@@ -65,31 +89,105 @@ struct DecArgs {
   const uint8_t *experts;
   size_t expert_stride, scale_run;
   const uint8_t *sh[3], *sh_s[3];  // shared gate, up, down
-  unsigned *ctl;                   // [1 + t] chain arrivals of token t ([0] unused)
-  uint8_t *qx8;                    // [n][H] E4M3 codes of the quantised activation
-  float *qxs;                      // [n][H/128] its scales
-  float *ch, *zabs, *za;           // [n][E]: approximate choice, sum|w*x|, logit
-  int *cand;                       // [n][E] candidate ids, ascending
-  int *ncand;                      // [n]
-  float *zx, *zc;                  // [n][E] exact score sqrt_softplus(z) and choice score + bias
-                                   // per candidate position
-  int *sel_e;                      // [n][K] routing, ascending id (moe_forward's idx)
-  int *sel_pos;                    // [n][K] candidate position of each route
-  float *sel_w;                    // [n][K] route weights (moe_forward's wt)
-  float *sv;                       // [n][E + 1][I] SwiGLU t per candidate position; slot E = shared
-  float *ro;                       // [n][K + 1][H] per-route outputs (BF16 values)
+  unsigned *ctl;  // control words (DEC_*)
+  // per-token pieces of the workspace: token t's piece is tb bytes past
+  // token 0's (dec_tok)
+  uint64_t *rec;   // [E] router record: choice | (sum|w*x| + DEC_REC_SET) << 32
+  uint64_t *zrec;  // [E] router logit z | DEC_REC_SET << 32
+  unsigned *sf;    // [I/8] shared gate/up tile flags (DEC_FS words apart)
+  unsigned *cf;    // [E] exact chain done flags per candidate position
+  unsigned *qf;    // [K] route requant done flags (DEC_FS apart)
+  uint32_t *qc;    // [K][I/4] E4M3 codes of the requantised routes
+  float *qcs;      // [K][I/128] their scales
+  float *zx, *zc;  // [E] exact score sqrt_softplus(z) and choice score + bias per
+                   // candidate position
+  int *sel_e;      // [K] routing, ascending id (moe_forward's idx)
+  int *sel_pos;    // [K] candidate position of each route
+  float *sel_w;    // [K] route weights (moe_forward's wt)
+  float *sv;       // [E + 1][I] SwiGLU t per candidate position; slot E = shared
+  float *ro;       // [H] the shared expert's down output (fp32)
+  size_t tb;       // bytes between two tokens' pieces
+  float *route_out;                // optional [n][K + 1][H]: route outputs before BF16
   int *idx_out;                    // optional copies of the routing
   float *wt_out;
-  int n, H, I, E, K, maxc;
-  int gu_tiles, dn_tiles;  // paired gate/up tiles (rows I, in H); down tiles (rows H, in I)
-  int gu_nb;               // persistent routed gate/up workgroups per token
+  int n, H, I, E, K;
+  int gu_tiles;    // paired gate/up tiles (rows I, in H)
+  int maxc;        // chain workgroups per token
+  int n_stream;    // streaming workgroups
   float route_scale, limit;
   float gamma;  // gamma_{dec_par_depth(H)} + gamma_H, the candidates' bound factor
-  int fast;  // routing from the parallel logits when the candidates are exactly top-k
+  int fast;     // routing from the parallel logits when the candidates are exactly top-k
 };
 
+// Token t's piece of a per-token workspace array.
+template <typename T>
+__device__ __forceinline__ T *dec_tok(T *p, const DecArgs &a, int t) {
+  return reinterpret_cast<T *>(reinterpret_cast<uintptr_t>(p) + (size_t)t * a.tb);
+}
+
+// ------------------------------------------------- agent-scope hand-off ----
+template <typename T>
+__device__ __forceinline__ T ld_dev(const T *p) {
+  return __hip_atomic_load(const_cast<T *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename T>
+__device__ __forceinline__ void st_dev(T *p, T v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Sets the calling workgroup's flag once every thread's agent-scope stores
+// are complete.
+__device__ __forceinline__ void dec_signal(unsigned *flag) {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0) st_dev(flag, 1u);
+}
+
+// Raises the sticky error bit (the calling wave's lane 0).
+__device__ __forceinline__ void dec_fail(unsigned *ctl) {
+  if (threadIdx.x % 64 == 0)
+    __hip_atomic_fetch_or(ctl + DEC_ERR, DEC_ERR_TIMEOUT, __ATOMIC_RELAXED,
+                          __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Ends one poll of a bounded wait: false once the wait has run out or another
+// workgroup has reported an error (the error word is then set), else a short
+// sleep before the next poll (the calling wave).
+__device__ __forceinline__ bool dec_spin(unsigned it, unsigned *ctl) {
+  if (it >= DEC_SPIN_LIMIT || ((it & 63u) == 63u && ld_dev(ctl + DEC_ERR) != 0u)) {
+    dec_fail(ctl);
+    return false;
+  }
+  __builtin_amdgcn_s_sleep(2);
+  return true;
+}
+
+// Waits (wave 0 polls, the others at the barrier) until flag f[i * stride] is
+// set for every i < count with use(i) (use: nullptr = all); false if the wait
+// ran out or another workgroup reported an error.
+__device__ __forceinline__ bool dec_wait_flags(const unsigned *f, int count, int stride,
+                                               const int *use, unsigned *ctl, int *s_i) {
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    int ok = 1;
+    for (unsigned it = 0;; ++it) {
+      int mine = 1;
+      for (int i = lane; i < count; i += 64)
+        if (!use || use[i]) mine &= ld_dev(f + (size_t)i * stride) != 0u;
+      if (__all(mine)) break;
+      if (!dec_spin(it, ctl)) {
+        ok = 0;
+        break;
+      }
+    }
+    if (lane == 0) *s_i = ok;
+  }
+  __syncthreads();
+  return *s_i != 0;
+}
+
 // Expert e's matrix m (0 gate w1, 1 up w3, 2 down w2) in the reference slot
-// layout [s1 | s2 | s3 | w1 | w2 | w3] (src/dsv4/dsv4_model.c:1584-1640).
+// layout [s1 | s2 | s3 | w1 | w2 | w3] (src/dsv4/dsv4_model.c:6298-6305).
 __device__ __forceinline__ void expert_mat(const DecArgs &a, int e, int m, const uint8_t *&W,
                                            const uint8_t *&S) {
   const uint8_t *sc = a.experts + (size_t)e * a.expert_stride;
@@ -108,77 +206,142 @@ __device__ __forceinline__ void expert_mat(const DecArgs &a, int e, int m, const
   }
 }
 
-// The 4096 bytes of FP4 tile scales follow the tile's pairs in dynamic LDS.
-__device__ __forceinline__ uint8_t *fp4_scale_lds(float *lds, const Fp4Geom &q) {
-  return reinterpret_cast<uint8_t *>(lds) + (size_t)q.tr * pair_stride(q.G) * 8;
-}
-
-// One arrival on *cnt by the calling workgroup, after its global writes;
-// true (workgroup-uniform) for the arrival that completes `total`, which then
-// sees every other arrival's writes.
-__device__ __forceinline__ bool dec_arrive_last(unsigned *cnt, unsigned total, int *s_flag) {
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    __threadfence();
-    const unsigned old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED,
-                                                __HIP_MEMORY_SCOPE_AGENT);
-    const bool last = old == total - 1u;
-    if (last) __threadfence();
-    *s_flag = last;
-  }
-  __syncthreads();
-  return *s_flag != 0;
-}
-
-__device__ __forceinline__ void dec_select_finish(const DecArgs &a, int t, int my_e, float my_sc,
-                                                  int my_pos);
-
-// Rounding depth of a parallel logit of dec_logit_block: the product (one
+// Rounding depth of a parallel logit of dec_router_block: the product (one
 // rounding), a lane's sequential sum of its 8-column pieces (at most
 // 8 ceil(H / 2048) products), the 6-level wave butterfly, the 3 additions of
 // the four waves' partials, and one more for the rounding of the computed
 // sum|w*x| that the bound is scaled by.
 __device__ __host__ __forceinline__ int dec_par_depth(int H) { return 8 * ((H / 4 + 511) / 512) + 11; }
 
-// Candidates of token t in ascending expert id (whole calling wave) into
-// cand[0 .. count) (LDS); returns the count. A hash layer's candidates are its
-// tid2eid row. NPER = experts per lane (E <= 64 * NPER). One workgroup per
-// token publishes: it also writes the list to a.cand / a.ncand and, in fast
-// mode when the candidates are exactly the top-k, the routing, taken from
-// the approximate choices (selection order) and the parallel logits (scores).
-template <int NPER>
-__device__ __forceinline__ int dec_candidates_t(const DecArgs &a, int t, int *cand, bool publish,
-                                                const uint64_t *tab) {
-  const int lane = threadIdx.x % 64;
-  const size_t row = (size_t)t * a.E;
-  const float ninf = -__builtin_inff();
-  float v[NPER], z[NPER];
-  float amax = 0.0f;
+// ------------------------------------------------------- activation ----
+// quant_fp8_act (src/dsv4/dsv4_ops.c:96-121) of token row xt into LDS: E4M3
+// codes into q8 (H bytes) and/or grid values into xf (padded to 132 floats
+// per 128-group), per-128 scales into qs. Thread i takes 16 consecutive
+// values; a group's 8 threads are neighbouring lanes of one wave.
+__device__ __forceinline__ void dec_quant_x(const float *xt, int H, uint8_t *q8, float *xf,
+                                            float *qs) {
+  const int tid = threadIdx.x;
+  const BufRsrc rx = buf_rsrc(xt, 4u * (uint32_t)H);
+  const int span = (H + 4095) / 4096 * 4096;  // wave-uniform trip count
+  for (int base = 16 * tid; base < span; base += 4096) {
+    float v[16];
 #pragma unroll
-  for (int j = 0; j < NPER; ++j) {
-    const int e = lane + 64 * j;
-    v[j] = ninf;
-    z[j] = 0.0f;
-    if (e < a.E) {
-      const float c = a.ch[row + e];
-      v[j] = c == c ? c : ninf;  // a NaN choice never wins a strict '>'
-      amax = fmaxf(amax, a.zabs[row + e]);
-      if (a.fast) z[j] = a.za[row + e];
+    for (int i = 0; i < 4; ++i) {
+      const uint4 u = buf_load16(rx, 4u * (uint32_t)(base + 4 * i));  // past H: zeros
+      v[4 * i] = u2f(u.x);
+      v[4 * i + 1] = u2f(u.y);
+      v[4 * i + 2] = u2f(u.z);
+      v[4 * i + 3] = u2f(u.w);
+    }
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) m = fmaxf(m, fabsf(v[i]));
+    m = fmaxf(m, __shfl_xor(m, 1, 64));
+    m = fmaxf(m, __shfl_xor(m, 2, 64));
+    m = fmaxf(m, __shfl_xor(m, 4, 64));
+    if (base < H) {
+      const float scale = act_scale(m);
+      const float inv = 1.0f / scale;
+      float g[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) g[i] = quant_e4m3(v[i], inv);
+      if (q8) {
+        uint32_t c[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          c[i] = e4m3_code(g[4 * i]) | (e4m3_code(g[4 * i + 1]) << 8) |
+                 (e4m3_code(g[4 * i + 2]) << 16) | (e4m3_code(g[4 * i + 3]) << 24);
+        *reinterpret_cast<uint4 *>(q8 + base) = make_uint4(c[0], c[1], c[2], c[3]);
+      }
+      if (xf) {
+        float *d = xf + (base / 128) * 132 + base % 128;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          *reinterpret_cast<float4 *>(d + 4 * i) =
+              make_float4(g[4 * i], g[4 * i + 1], g[4 * i + 2], g[4 * i + 3]);
+      }
+      if ((tid & 7) == 0) qs[base / 128] = scale;
     }
   }
+}
+
+// ------------------------------------------------------------ routing ----
+// Route weights from the unbiased scores, summed in selection order, then the
+// routes sorted by id (src/dsv4/dsv4_model.c:6650-6674; equal ids carry
+// equal weights, so any order among them matches the exchange sort). Lane k
+// holds route k in selection order (whole wave).
+__device__ __forceinline__ void dec_select_finish(const DecArgs &a, int t, int my_e, float my_sc,
+                                                  int my_pos) {
+  const int lane = threadIdx.x % 64;
+  const int K = a.K;
+  float sum = 0.0f;
+  for (int k = 0; k < K; ++k) {
+    const int ek = __builtin_amdgcn_readlane(my_e, k);
+    const float sk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_sc), k));
+    sum += ek >= 0 ? sk : 0.0f;
+  }
+  const float rs = sum > 0.0f ? a.route_scale / sum : 0.0f;
+  const float my_w = (sum > 0.0f && my_e >= 0) ? my_sc * rs : 0.0f;
+  int rank = 0;
+  for (int k = 0; k < K; ++k) {
+    const int ek = __builtin_amdgcn_readlane(my_e, k);
+    rank += (ek < my_e || (ek == my_e && k < lane)) ? 1 : 0;
+  }
+  if (lane < K) {
+    dec_tok(a.sel_e, a, t)[rank] = my_e;
+    dec_tok(a.sel_w, a, t)[rank] = my_w;
+    dec_tok(a.sel_pos, a, t)[rank] = my_pos >= 0 ? my_pos : rank;  // candidates == routes
+    const size_t o = (size_t)t * K + rank;
+    if (a.idx_out) a.idx_out[o] = my_e;
+    if (a.wt_out) a.wt_out[o] = my_w;
+  }
+}
+
+// Candidates of token t (one whole wave), from the router records: ct[0, nc)
+// the candidate ids in ascending order, sel[0, K) the K best approximate
+// choices in selection order (-1 past the selectable experts), both in LDS.
+// Returns nc, or -1 if the wait for the records ran out. Every workgroup that
+// calls it for a token derives the same candidates from the same records.
+// NPER = experts per lane (E <= 64 * NPER).
+template <int NPER>
+__device__ __forceinline__ int dec_candidates_t(const DecArgs &a, int t, int *ct, int *sel) {
+  const int lane = threadIdx.x % 64;
+  const float ninf = -__builtin_inff();
+  const uint64_t *rec = dec_tok(a.rec, a, t);
+  float v[NPER];
+  float amax;
+  for (unsigned it = 0;; ++it) {  // until every record carries its mark
+    uint64_t r[NPER];
+    int ready = 1;
+#pragma unroll
+    for (int j = 0; j < NPER; ++j) {
+      const int e = lane + 64 * j;
+      r[j] = e < a.E ? ld_dev(rec + e) : ((uint64_t)DEC_REC_SET << 32);
+    }
+    amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NPER; ++j) {
+      const float c = __uint_as_float((uint32_t)r[j]);
+      const bool in = lane + 64 * j < a.E;
+      ready &= (int)(r[j] >> 63);
+      v[j] = (in && c == c) ? c : ninf;  // a NaN choice never wins a strict '>'
+      if (in) amax = fmaxf(amax, __uint_as_float((uint32_t)(r[j] >> 32) & ~DEC_REC_SET));
+    }
+    if (__all(ready)) break;
+    if (!dec_spin(it, a.ctl)) return -1;
+  }
   // k-th best approximate choice: k times remove one instance of the
-  // maximum; lane k keeps the expert and logit of the k-th removal
-  float kth = ninf, my_z = 0.0f;
-  int my_e = -1;
+  // maximum
+  if (lane < a.K) sel[lane] = -1;
+  float kth = ninf;
   unsigned used = 0u;
   for (int k = 0; k < a.K; ++k) {
-    float m = ninf, mz = 0.0f;
+    float m = ninf;
     int mj = -1;
 #pragma unroll
     for (int j = 0; j < NPER; ++j)
       if (!((used >> j) & 1u) && v[j] > m) {
         m = v[j];
-        mz = z[j];
         mj = j;
       }
     const float wm = wave_max_dpp(m);
@@ -188,17 +351,14 @@ __device__ __forceinline__ int dec_candidates_t(const DecArgs &a, int t, int *ca
       break;
     }
     const int wl = __builtin_ctzll(bal);
-    if (lane == wl) used |= 1u << mj;
-    const int we = wl + 64 * __builtin_amdgcn_readlane(mj, wl);
-    const float wz = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mz), wl));
-    if (lane == k) {
-      my_e = we;
-      my_z = wz;
+    if (lane == wl) {
+      used |= 1u << mj;
+      sel[k] = wl + 64 * mj;
     }
     kth = wm;
   }
   const float sum_abs = wave_max_dpp(amax);
-  const float bound_z = a.gamma * sum_abs;  // gamma_{dec_par_depth(H)} + gamma_H
+  const float bound_z = a.gamma * sum_abs;
   const float thr = kth - 2.0f * (0.5f * bound_z + 1e-5f);
   int base = 0;
 #pragma unroll
@@ -206,70 +366,157 @@ __device__ __forceinline__ int dec_candidates_t(const DecArgs &a, int t, int *ca
     const int e = lane + 64 * j;
     const bool p = e < a.E && v[j] >= thr;
     const unsigned long long bal = __ballot(p);
-    const int pos = base + __popcll(bal & ((1ull << lane) - 1ull));
-    if (p) {
-      cand[pos] = e;
-      if (publish) a.cand[row + pos] = e;
-    }
+    if (p) ct[base + __popcll(bal & ((1ull << lane) - 1ull))] = e;
     base += __popcll(bal);
-  }
-  if (publish) {
-    if (lane == 0) a.ncand[t] = base;
-    if (a.fast && base == a.K) {  // the same test as dec_chain_block's early exit
-      // candidates == top-k: sel_pos is the rank by id (dec_select_finish)
-      dec_select_finish(a, t, my_e, lane < a.K ? sqrt_softplus(my_z, tab) : 0.0f, -1);
-    }
   }
   return base;
 }
 
-__device__ __forceinline__ int dec_candidates(const DecArgs &a, int t, int *cand, bool publish,
-                                              const uint64_t *tab) {
-  if (a.tid2eid) {
-    // the tid2eid row (K <= 32 <= lanes), in row order
-    const int lane = threadIdx.x % 64;
-    const int64_t *row = a.tid2eid + (size_t)a.token_ids[t] * a.K;
-    const int e = lane < a.K ? (int)row[lane] : -1;
-    if (lane < a.K) {
-      cand[lane] = e;
-      if (publish) a.cand[(size_t)t * a.E + lane] = e;
+// The same for more than 256 experts, with the choices in LDS (v: E floats)
+// and plain loops over a lane's experts e = lane + 64 j in ascending j, so
+// that every step takes the same expert as dec_candidates_t; a taken expert
+// is marked -inf in v (no strict '>' takes it again) and set back to the
+// k-th best choice afterwards (it is a candidate either way).
+__device__ __forceinline__ int dec_candidates_lds(const DecArgs &a, int t, int *ct, int *sel,
+                                               float *v) {
+  const int lane = threadIdx.x % 64;
+  const float ninf = -__builtin_inff();
+  const uint64_t *rec = dec_tok(a.rec, a, t);
+  float amax;
+  for (unsigned it = 0;; ++it) {  // until every record carries its mark
+    int ready = 1;
+    amax = 0.0f;
+    for (int e = lane; e < a.E; e += 64) {
+      const uint64_t r = ld_dev(rec + e);
+      const float c = __uint_as_float((uint32_t)r);
+      ready &= (int)(r >> 63);
+      v[e] = c == c ? c : ninf;
+      amax = fmaxf(amax, __uint_as_float((uint32_t)(r >> 32) & ~DEC_REC_SET));
     }
-    if (publish) {
-      if (lane == 0) a.ncand[t] = a.K;
-      if (a.fast) {
-        // the row routes; weights from the parallel logits (route k = lane k)
-        const bool ok = e >= 0 && e < a.E;
-        dec_select_finish(a, t, e, ok ? sqrt_softplus(a.za[(size_t)t * a.E + e], tab) : 0.0f,
-                          lane);
-      }
-    }
-    return a.K;
+    if (__all(ready)) break;
+    if (!dec_spin(it, a.ctl)) return -1;
   }
-  if (a.E <= 64) return dec_candidates_t<1>(a, t, cand, publish, tab);
-  if (a.E <= 128) return dec_candidates_t<2>(a, t, cand, publish, tab);
-  if (a.E <= 256) return dec_candidates_t<4>(a, t, cand, publish, tab);
-  if (a.E <= 512) return dec_candidates_t<8>(a, t, cand, publish, tab);
-  return dec_candidates_t<16>(a, t, cand, publish, tab);
+  __builtin_amdgcn_wave_barrier();
+  if (lane < a.K) sel[lane] = -1;
+  float kth = ninf;
+  for (int k = 0; k < a.K; ++k) {
+    float m = ninf;
+    int me = -1;
+    for (int e = lane; e < a.E; e += 64)
+      if (v[e] > m) {
+        m = v[e];
+        me = e;
+      }
+    const float wm = wave_max_dpp(m);
+    const unsigned long long bal = __ballot(me >= 0 && m == wm);
+    if (bal == 0ull) {
+      kth = ninf;
+      break;
+    }
+    const int wl = __builtin_ctzll(bal);
+    __builtin_amdgcn_wave_barrier();
+    if (lane == wl) {
+      v[me] = ninf;
+      sel[k] = me;
+    }
+    __builtin_amdgcn_wave_barrier();
+    kth = wm;
+  }
+  if (lane < a.K && sel[lane] >= 0) v[sel[lane]] = kth;
+  __builtin_amdgcn_wave_barrier();
+  const float sum_abs = wave_max_dpp(amax);
+  const float thr = kth - 2.0f * (0.5f * (a.gamma * sum_abs) + 1e-5f);
+  int base = 0;
+  for (int e0 = 0; e0 < a.E; e0 += 64) {
+    const int e = e0 + lane;
+    const bool p = e < a.E && v[e] >= thr;
+    const unsigned long long bal = __ballot(p);
+    if (p) ct[base + __popcll(bal & ((1ull << lane) - 1ull))] = e;
+    base += __popcll(bal);
+  }
+  return base;
 }
 
+// The candidates of token t into LDS (ct, nc, and sel: the selection order of
+// the approximate top-k; a hash layer: the tid2eid row, K positions), wave 0
+// deriving them while the others wait (s_v: E floats of LDS for more than 256
+// experts). Returns nc (all threads), -1 if the wait for the router records
+// ran out.
+__device__ __forceinline__ int dec_candidates(const DecArgs &a, int t, int *ct, int *sel,
+                                              float *s_v, int *s_i) {
+  __syncthreads();  // ct, sel and s_i of the previous token have been read
+  if (threadIdx.x < 64) {
+    int nc;
+    if (a.tid2eid) {
+      const int lane = threadIdx.x;
+      const int64_t *row = a.tid2eid + (size_t)a.token_ids[t] * a.K;
+      if (lane < a.K) ct[lane] = sel[lane] = (int)row[lane];
+      nc = a.K;
+    } else if (a.E <= 64) {
+      nc = dec_candidates_t<1>(a, t, ct, sel);
+    } else if (a.E <= 128) {
+      nc = dec_candidates_t<2>(a, t, ct, sel);
+    } else if (a.E <= 256) {
+      nc = dec_candidates_t<4>(a, t, ct, sel);
+    } else {
+      nc = dec_candidates_lds(a, t, ct, sel, s_v);
+    }
+    if (threadIdx.x == 0) *s_i = nc;
+  }
+  __syncthreads();
+  return *s_i;
+}
+
+// Whether the exact chains route token t: not in fast mode when the
+// candidates are exactly the top-k, nor for a hash row in fast mode or
+// without a valid entry (all threads; ct from dec_candidates).
+__device__ __forceinline__ bool dec_need_chain(const DecArgs &a, int nc, const int *ct) {
+  if (!a.tid2eid) return !(a.fast && nc == a.K);
+  if (a.fast) return false;
+  for (int p = 0; p < a.K; ++p)
+    if (ct[p] >= 0 && ct[p] < a.E) return true;
+  return false;
+}
+
+// Routing of a token that needs no chain (wave 0): fast mode: the approximate
+// top-k in selection order, weighted from the parallel logits; a hash row:
+// the tid2eid row, weighted from the parallel logits in fast mode, else
+// (no valid entry) with weights 0. False if the wait for the logits ran out.
+__device__ __forceinline__ bool dec_route_direct(const DecArgs &a, int t, const int *sel,
+                                                 const uint64_t *tab) {
+  const int lane = threadIdx.x % 64;
+  const int e = lane < a.K ? sel[lane] : -1;
+  const bool ok = e >= 0 && e < a.E;
+  const bool use = a.fast && ok;
+  const uint64_t *zr = dec_tok(a.zrec, a, t) + (use ? e : 0);
+  uint64_t r = (uint64_t)DEC_REC_SET << 32;
+  for (unsigned it = 0;; ++it) {
+    if (use) r = ld_dev(zr);
+    if (__all((int)(r >> 63))) break;
+    if (!dec_spin(it, a.ctl)) return false;
+  }
+  const float sc = use ? sqrt_softplus(__uint_as_float((uint32_t)r), tab) : 0.0f;
+  dec_select_finish(a, t, e, sc, a.tid2eid ? lane : -1);
+  return true;
+}
 
 // Exact top-k of token t from the candidates' exact scores and choices (one
 // whole wave; the nc candidates ct in ascending id, from the caller's LDS):
-// routes ascending by id with weights and candidate positions, written to
-// sel_* (and idx_out / wt_out) (src/dsv4/dsv4_model.c:6615-6676). Lane k
-// carries route k in selection order.
+// routes ascending by id with weights and candidate positions
+// (src/dsv4/dsv4_model.c:6615-6676). Lane k carries route k in selection
+// order.
 template <int NPER>
 __device__ __forceinline__ void dec_select_t(const DecArgs &a, int t, int nc, const int *ct) {
   const int lane = threadIdx.x % 64;
   const int K = a.K;
-  const float *zt = a.zx + (size_t)t * a.E, *zc = a.zc + (size_t)t * a.E;
+  const float *zt = dec_tok(a.zx, a, t), *zc = dec_tok(a.zc, a, t);
   int my_e = -1, my_pos = -1;
   float my_sc = 0.0f;
   if (a.tid2eid) {
     if (lane < K) {
       my_e = ct[lane];
       my_pos = lane;
-      my_sc = (my_e >= 0 && my_e < a.E) ? zt[lane] : 0.0f;
+      my_sc = (my_e >= 0 && my_e < a.E) ? ld_dev(zt + lane) : 0.0f;
     }
   } else {
     const float ninf = -__builtin_inff();
@@ -283,8 +530,8 @@ __device__ __forceinline__ void dec_select_t(const DecArgs &a, int t, int nc, co
       ce[j] = -1;
       if (pos < nc) {
         ce[j] = ct[pos];
-        sc[j] = zt[pos];
-        chv[j] = zc[pos];
+        sc[j] = ld_dev(zt + pos);
+        chv[j] = ld_dev(zc + pos);
       }
     }
     unsigned used = 0u;
@@ -323,47 +570,17 @@ __device__ __forceinline__ void dec_select_t(const DecArgs &a, int t, int nc, co
   dec_select_finish(a, t, my_e, my_sc, my_pos);
 }
 
-// Route weights from the unbiased scores, summed in selection order, then the
-// routes sorted by id (src/dsv4/dsv4_model.c:6650-6674; equal ids carry
-// equal weights, so any order among them matches the exchange sort). Lane k
-// holds route k in selection order.
-__device__ __forceinline__ void dec_select_finish(const DecArgs &a, int t, int my_e, float my_sc, int my_pos) {
-  const int lane = threadIdx.x % 64;
-  const int K = a.K;
-  float sum = 0.0f;
-  for (int k = 0; k < K; ++k) {
-    const int ek = __builtin_amdgcn_readlane(my_e, k);
-    const float sk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_sc), k));
-    sum += ek >= 0 ? sk : 0.0f;
-  }
-  const float rs = sum > 0.0f ? a.route_scale / sum : 0.0f;
-  const float my_w = (sum > 0.0f && my_e >= 0) ? my_sc * rs : 0.0f;
-  int rank = 0;
-  for (int k = 0; k < K; ++k) {
-    const int ek = __builtin_amdgcn_readlane(my_e, k);
-    rank += (ek < my_e || (ek == my_e && k < lane)) ? 1 : 0;
-  }
-  if (lane < K) {
-    const size_t o = (size_t)t * K + rank;
-    a.sel_e[o] = my_e;
-    a.sel_w[o] = my_w;
-    a.sel_pos[o] = my_pos >= 0 ? my_pos : rank;  // fast path: candidates == routes
-    if (a.idx_out) a.idx_out[o] = my_e;
-    if (a.wt_out) a.wt_out[o] = my_w;
-  }
-}
-
 // More than 256 candidates (near-ties or large expert counts): scores in
 // LDS (2 * nc floats, nc <= 1024), scanned with plain loops.
 __device__ __forceinline__ void dec_select_big(const DecArgs &a, int t, int nc, const int *ct,
                                                float *lds) {
   const int lane = threadIdx.x % 64;
-  const float *zt = a.zx + (size_t)t * a.E, *zc = a.zc + (size_t)t * a.E;
+  const float *zt = dec_tok(a.zx, a, t), *zc = dec_tok(a.zc, a, t);
   const float ninf = -__builtin_inff();
   float *sc = lds, *chv = lds + nc;
   for (int pos = lane; pos < nc; pos += 64) {
-    sc[pos] = zt[pos];
-    chv[pos] = zc[pos];
+    sc[pos] = ld_dev(zt + pos);
+    chv[pos] = ld_dev(zc + pos);
   }
   __builtin_amdgcn_wave_barrier();
   int my_e = -1, my_pos = -1;
@@ -400,19 +617,25 @@ __device__ __forceinline__ void dec_select(const DecArgs &a, int t, int nc, cons
 }
 
 // ------------------------------------------------------------ router ----
-// Router logit of expert e for every token, one workgroup: wave wv takes the
-// columns [wv H/4, (wv + 1) H/4), lane l its 8-column pieces l, l + 64, ...
-// (the gate row stays in registers, x is read directly); approximate choice
-// sqrt_softplus(z) + bias, sum|w*x| and z (rounding depth: dec_par_depth).
-__device__ __forceinline__ void dec_logit_block(const DecArgs &a, int e, float *s_part,
-                                                uint64_t *s_tab) {
+// Router workgroup of expert e: wave wv takes the columns [wv H/4,
+// (wv + 1) H/4), lane l its 8-column pieces l, l + 64, ... (gate row and x
+// read directly); for every token the approximate choice sqrt_softplus(z) +
+// bias with sum|w*x| (rounding depth: dec_par_depth) and z, each published as
+// one 64-bit record that carries its own DEC_REC_SET mark. Workgroup 0 also
+// clears the previous call's requant flags.
+__device__ __forceinline__ void dec_router_block(const DecArgs &a, int e, uint64_t *s_tab,
+                                                 float *s_part) {
   const int tid = threadIdx.x, wv = tid / 64, lane = tid % 64;
   const int H = a.H, Q = H / 4;
+  if (e == 0)
+    for (int i = tid; i < a.n * a.K; i += 256)
+      st_dev(dec_tok(a.qf, a, i / a.K) + (size_t)(i % a.K) * DEC_FS, 0u);
   const BufRsrc rg = buf_rsrc(a.gate + (size_t)e * H + (size_t)wv * Q, 2u * (uint32_t)Q);
   uint4 w[4];  // Q <= 2048: at most 4 pieces per lane; pieces past Q read zeros
 #pragma unroll
   for (int i = 0; i < 4; ++i) w[i] = buf_load16(rg, 16u * (uint32_t)(lane + 64 * i));
   const uint64_t tabv = libm_table_load();
+  const float be = a.bias ? a.bias[e] : 0.0f;
   for (int t = 0; t < a.n; ++t) {
     const BufRsrc rx = buf_rsrc(a.x + (size_t)t * H + (size_t)wv * Q, 4u * (uint32_t)Q);
     uint4 xv[8];
@@ -448,411 +671,542 @@ __device__ __forceinline__ void dec_logit_block(const DecArgs &a, int e, float *
     if (tid == 0) {
       const float z = ((s_part[0] + s_part[2]) + s_part[4]) + s_part[6];
       const float zs = ((s_part[1] + s_part[3]) + s_part[5]) + s_part[7];
-      const size_t o = (size_t)t * a.E + e;
-      a.ch[o] = sqrt_softplus(z, s_tab) + (a.bias ? a.bias[e] : 0.0f);
-      a.zabs[o] = zs;
-      a.za[o] = z;
+      const float c = sqrt_softplus(z, s_tab) + be;
+      st_dev(dec_tok(a.zrec, a, t) + e, (uint64_t)__float_as_uint(z) | ((uint64_t)DEC_REC_SET << 32));
+      st_dev(dec_tok(a.rec, a, t) + e,
+             (uint64_t)__float_as_uint(c) | ((uint64_t)(__float_as_uint(zs) | DEC_REC_SET) << 32));
     }
     __syncthreads();  // s_part is reused by the next token
   }
 }
 
-// quant_fp8_act (src/dsv4/dsv4_ops.c:96-121) of one 128-group per wave, for
-// the routed experts' gate/up tiles.
-__device__ __forceinline__ void dec_quant_block(const DecArgs &a, int b) {
-  const int wv = threadIdx.x / 64, lane = threadIdx.x % 64;
-  const int H = a.H, gpt = H / 128, gi = b * 4 + wv;
-  if (gi >= a.n * gpt) return;
-  const int t = gi / gpt, g = gi % gpt;
-  const float *xr = a.x + (size_t)t * H + g * 128;
-  const float v0 = xr[lane], v1 = xr[lane + 64];
-  const float amax = wave_max(fmaxf(fabsf(v0), fabsf(v1)));
-  const float scale = act_scale(amax);
-  const float inv = 1.0f / scale;
-  uint8_t *q = a.qx8 + (size_t)t * H + g * 128;
-  q[lane] = (uint8_t)e4m3_code(quant_e4m3(v0, inv));
-  q[lane + 64] = (uint8_t)e4m3_code(quant_e4m3(v1, inv));
-  if (lane == 0) a.qxs[(size_t)t * gpt + g] = scale;
-}
-
-// Shared expert gate/up, rows [r0, r0 + 8) of both, from the quantised x
-// (E4M3 codes and per-128 scales, loaded ahead of the weights, decoded into
-// LDS padded to 132 per group): t = silu(bf16 gate) * bf16 up for the 8 rows
-// (src/dsv4/dsv4_model.c:6264-6268) into the shared slot of sv.
-__device__ __forceinline__ void dec_shared_gateup(const DecArgs &a, int t, int tile, float *lds,
-                                                  float *s_y, uint64_t *s_tab) {
-  const int tid = threadIdx.x;
-  {
-    // the shared expert's weight stream starts 2 us into the kernel: at
-    // launch the routed path's critical loads (the candidates' choices, the
-    // chains' staging) are served about twice as fast by an otherwise idle
-    // memory system, and the shared expert is needed only by k_dec_down
-    const long long t0 = wall_clock64();  // 100 MHz
-    while (wall_clock64() - t0 < 200) __builtin_amdgcn_s_sleep(8);
-  }
-  const int H = a.H, I = a.I, r0 = tile * (FP8_TR / 2);
-  // the activation codes (at most 8192: 8 words per thread) and its
-  // per-128 scales ahead of the weights
-  const BufRsrc rq = buf_rsrc(a.qx8 + (size_t)t * H, (uint32_t)H);
-  const BufRsrc rqs = buf_rsrc(a.qxs + (size_t)t * (H / 128), (uint32_t)(H / 128) * 4u);
-  uint32_t xr[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) xr[j] = buf_load4(rq, 4u * (tid + 256 * j));
-  const float qsv = buf_loadf(rqs, 4u * tid);
-  __builtin_amdgcn_sched_barrier(0);  // issued before the weights
-  Fp8Regs R;
-  fp8_pair_load(R, a.sh[0], a.sh_s[0], a.sh[1], a.sh_s[1], H, I, r0);
-  const uint64_t tabv = libm_table_load();
-  float *xs = lds, *qs = lds + (H / 128) * 132;
-  float2 *ps = reinterpret_cast<float2 *>(qs + ((H / 128 + 3) & ~3));
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int i = 4 * (tid + 256 * j);
-    if (i < H) {
-      const float2 lo = fp8x2<false>(xr[j]), hi = fp8x2<true>(xr[j]);
-      *reinterpret_cast<float4 *>(xs + (i / 128) * 132 + (i % 128)) =
-          make_float4(lo.x, lo.y, hi.x, hi.y);
-    }
-  }
-  if (tid < H / 128) qs[tid] = qsv;
-  __syncthreads();
-  fp8_pair_finish(R, s_y, xs, qs, a.sh[0], a.sh_s[0], a.sh[1], a.sh_s[1], H, I, r0, ps);
-  libm_table_store(s_tab, tabv);
-  __syncthreads();
-  if (tid < FP8_TR / 2 && r0 + tid < I)
-    a.sv[((size_t)t * (a.E + 1) + a.E) * I + r0 + tid] =
-        swiglu_t(s_y[tid], s_y[tid + FP8_TR / 2], a.limit, s_tab);
-}
-
-// Blocks: [E router logits][quant of x].
-__global__ __launch_bounds__(256) void k_dec_router(DecArgs a) {
-  __shared__ uint64_t s_tab[32];
-  __shared__ float s_part[8];
-  if ((int)blockIdx.x < a.E) return dec_logit_block(a, blockIdx.x, s_part, s_tab);
-  dec_quant_block(a, blockIdx.x - a.E);
-}
-
 // ------------------------------------------------------------ chains ----
-// Exact logits of candidate positions c, c + maxc, ... of token t: the whole
-// block stages x and the candidate's gate row (widened to fp32) into LDS in
-// one shot, then lane 0 of wave 0 runs the reference's fmaf chain in column
-// order (dsv4_gemv_bf16, src/dsv4/dsv4_model.c:298-303) from LDS alone.
-// The chain workgroup of position 0 publishes the candidates (and, in fast
-// mode, the routing); the last chain workgroup of the token selects the
-// routes.
+// Exact logits of candidate positions c, c + maxc, ... of token t: x and the
+// candidate's gate row widened to fp32 in LDS, then lane 0 of wave 0 runs
+// the reference's fmaf chain in column order (dsv4_gemv_bf16,
+// src/dsv4/dsv4_model.c:298-303); the score and choice go to the position,
+// then its flag. The token's last chain workgroup (dispatched after the
+// others, so its wait cannot hold a slot they need) then waits for every
+// chain of the token, clears the flags and selects the routes; for a token
+// that needs no chain it routes directly (dec_route_direct).
 __device__ __forceinline__ void dec_chain_block(const DecArgs &a, int t, int c, float *lds,
-                                                uint64_t *s_tab, int *s_cand, int *s_nc,
-                                                int *s_flag) {
+                                                uint64_t *s_tab, int *s_cand, int *s_sel,
+                                                int *s_i) {
   const int tid = threadIdx.x, wv = tid / 64, lane = tid % 64;
   const int H = a.H;
-  float *xs = lds, *gs = lds + H;  // H floats each
+  float *s_v = lds + 2 * H;  // more than 256 experts: the candidates' choices
+  float *xs = lds, *gs = lds + H;
   const uint64_t tabv = libm_table_load();
-  // x is issued before the candidates are known
+  // x is staged before the candidates are known
   const BufRsrc rx = buf_rsrc(a.x + (size_t)t * H, 4u * (uint32_t)H);
-  uint4 xv[8];  // H <= 8192: 8 pieces per thread
 #pragma unroll
-  for (int j = 0; j < 8; ++j) xv[j] = buf_load16(rx, 16u * (uint32_t)(tid + 256 * j));
-  libm_table_store(s_tab, tabv);
-  if (wv == 0) {
-    __builtin_amdgcn_wave_barrier();  // the table, for the publishing fast path
-    const int n = dec_candidates(a, t, s_cand, c == 0, s_tab);
-    if (lane == 0) *s_nc = n;
+  for (int j = 0; j < 8; ++j) {  // H <= 8192: 8 pieces per thread
+    const uint32_t i4 = (uint32_t)(tid + 256 * j);
+    if (4u * i4 < (uint32_t)H) reinterpret_cast<uint4 *>(xs)[i4] = buf_load16(rx, 16u * i4);
   }
-#pragma unroll
-  for (int j = 0; j < 8; ++j)
-    if (4 * (tid + 256 * j) < H) reinterpret_cast<uint4 *>(xs)[tid + 256 * j] = xv[j];
-  __syncthreads();
-  const int nc = *s_nc;
-  if (a.fast && nc == a.K) return;  // routed by the publishing workgroup already
+  libm_table_store(s_tab, tabv);
+  const int nc = dec_candidates(a, t, s_cand, s_sel, s_v, s_i);
+  if (nc < 0) return;
+  if (!dec_need_chain(a, nc, s_cand)) {
+    if (c == a.maxc - 1 && wv == 0) dec_route_direct(a, t, s_sel, s_tab);
+    return;
+  }
   for (int pos = c; pos < nc; pos += a.maxc) {
     const int e = s_cand[pos];
-    const bool ok = e >= 0 && e < a.E;
-    const float be = ok && a.bias ? a.bias[e] : 0.0f;  // in flight during the chain
-    float acc = 0.0f;
-    if (ok) {
-      const BufRsrc rg = buf_rsrc(a.gate + (size_t)e * H, 2u * (uint32_t)H);
-      uint4 gv[4];  // H / 8 <= 1024 pieces: 4 per thread
+    if (e < 0 || e >= a.E) continue;  // a malformed tid2eid entry has no chain
+    const float be = a.bias ? a.bias[e] : 0.0f;
+    const BufRsrc rg = buf_rsrc(a.gate + (size_t)e * H, 2u * (uint32_t)H);
+    uint4 gv[4];  // H / 8 <= 1024 pieces: 4 per thread
 #pragma unroll
-      for (int j = 0; j < 4; ++j) gv[j] = buf_load16(rg, 16u * (uint32_t)(tid + 256 * j));
+    for (int j = 0; j < 4; ++j) gv[j] = buf_load16(rg, 16u * (uint32_t)(tid + 256 * j));
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int i = tid + 256 * j;
-        if (8 * i < H) {
-          float4 *gp = reinterpret_cast<float4 *>(gs) + 2 * i;
-          gp[0] = make_float4(u2f(gv[j].x << 16), u2f(gv[j].x & 0xFFFF0000u),
-                              u2f(gv[j].y << 16), u2f(gv[j].y & 0xFFFF0000u));
-          gp[1] = make_float4(u2f(gv[j].z << 16), u2f(gv[j].z & 0xFFFF0000u),
-                              u2f(gv[j].w << 16), u2f(gv[j].w & 0xFFFF0000u));
-        }
+    for (int j = 0; j < 4; ++j) {
+      const int i = tid + 256 * j;
+      if (8 * i < H) {
+        float4 *gp = reinterpret_cast<float4 *>(gs) + 2 * i;
+        gp[0] = make_float4(u2f(gv[j].x << 16), u2f(gv[j].x & 0xFFFF0000u),
+                            u2f(gv[j].y << 16), u2f(gv[j].y & 0xFFFF0000u));
+        gp[1] = make_float4(u2f(gv[j].z << 16), u2f(gv[j].z & 0xFFFF0000u),
+                            u2f(gv[j].w << 16), u2f(gv[j].w & 0xFFFF0000u));
       }
-      __syncthreads();
-      if (wv == 0 && lane == 0) {
-        __builtin_amdgcn_s_setprio(3);
-        const float4 *g = reinterpret_cast<const float4 *>(gs);
-        const float4 *x = reinterpret_cast<const float4 *>(xs);
-        if (H % 256 == 0)
-          for (int cc = 0; cc < H / 4; cc += 64) acc = chain_cols<32>(g + cc, x + cc, acc);
-        else
-          for (int cc = 0; cc < H / 4; cc += 32) acc = chain_cols<16>(g + cc, x + cc, acc);
-        __builtin_amdgcn_s_setprio(0);
-      }
-      __syncthreads();  // the next candidate restages the gate row
     }
-    if (tid == 0) {
+    __syncthreads();
+    if (wv == 0 && lane == 0) {
+      __builtin_amdgcn_s_setprio(3);
+      float acc = 0.0f;
+      const float4 *g = reinterpret_cast<const float4 *>(gs);
+      const float4 *x = reinterpret_cast<const float4 *>(xs);
+      if (H % 256 == 0)
+        for (int cc = 0; cc < H / 4; cc += 64) acc = chain_cols<32>(g + cc, x + cc, acc);
+      else
+        for (int cc = 0; cc < H / 4; cc += 32) acc = chain_cols<16>(g + cc, x + cc, acc);
+      __builtin_amdgcn_s_setprio(0);
       // the reference's score and choice (src/dsv4/dsv4_model.c:5827-5831,
-      // 6627-6634), here so that the selection after the hand-off only reads
-      const float sc = ok ? sqrt_softplus(acc, s_tab) : 0.0f;
-      a.zx[(size_t)t * a.E + pos] = sc;
-      a.zc[(size_t)t * a.E + pos] = sc + be;
+      // 6627-6634)
+      const float sc = sqrt_softplus(acc, s_tab);
+      st_dev(dec_tok(a.zx, a, t) + pos, sc);
+      st_dev(dec_tok(a.zc, a, t) + pos, sc + be);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the scores before the flag
+      st_dev(dec_tok(a.cf, a, t) + pos, 1u);
     }
+    __syncthreads();  // the next candidate restages the gate row
   }
-  if (!dec_arrive_last(&a.ctl[1 + t], (unsigned)a.maxc, s_flag)) return;
-  // the candidates are this workgroup's own (LDS); nc > 256 uses lds
-  // (2 nc floats) for the scores, past the x and gate rows no longer needed
-  if (wv == 0) dec_select(a, t, nc, s_cand, lds);
-  if (tid == 0) a.ctl[1 + t] = 0u;
+  if (c != a.maxc - 1) return;
+  // the selector: every position with an expert in range has a chain
+  int *use = reinterpret_cast<int *>(lds + 2 * H);  // nc ints
+  for (int p = tid; p < nc; p += 256) use[p] = s_cand[p] >= 0 && s_cand[p] < a.E;
+  __syncthreads();
+  unsigned *cf = dec_tok(a.cf, a, t);
+  if (!dec_wait_flags(cf, nc, 1, use, a.ctl, s_i)) return;
+  for (int p = tid; p < nc; p += 256) st_dev(cf + p, 0u);
+  // more than 256 candidates select from 2 nc floats of LDS past x and the
+  // gate row
+  if (wv == 0) dec_select(a, t, nc, s_cand, lds + 2 * H);
 }
 
-// --------------------------------------------------------- gate / up ----
-// Routed gate/up item j of token t: candidate position c = j / gu_tiles, rows
-// [r0, r0 + tr / 2) of its gate and up matrices (tile j % gu_tiles). Loads
-// the activation codes and the pair into R; an item past the end (or a
-// malformed tid2eid entry) loads zero-length ranges, which read zeros without
-// touching memory, so every load is issued unconditionally.
-__device__ __forceinline__ void dec_gu_load(const DecArgs &a, Fp4RegsT<DEC_NP> &R, int t, int j,
-                                            int nitems, const int *s_cand, const Fp4Geom &q,
-                                            int &c, int &r0, bool &live) {
-  const int H = a.H, I = a.I;
-  c = j / a.gu_tiles;
-  r0 = (j - c * a.gu_tiles) * (q.tr / 2);
-  const int e = __builtin_amdgcn_readfirstlane(j < nitems ? s_cand[min(c, a.E - 1)] : -1);
-  live = e >= 0 && e < a.E;
-  const uint8_t *W0, *S0, *W1, *S1;
-  expert_mat(a, live ? e : 0, 0, W0, S0);
-  expert_mat(a, live ? e : 0, 1, W1, S1);
-  fp4_tile_x(R, a.qx8 + (size_t)t * H, a.qxs + (size_t)t * (H / 128), q);
-  fp4_pair_load_near(R, W0, S0, W1, S1, H, live ? I : 0, r0, q);  // S1 after S0 in the slot
-}
-
-// The item's group chains, then t = silu(bf16 gate) * bf16 up for its rows
-// (src/dsv4/dsv4_model.c:6264-6268) into the candidate's slot of sv.
-__device__ __forceinline__ void dec_gu_finish(const DecArgs &a, const Fp4RegsT<DEC_NP> &R, int t,
-                                              int c, int r0, const Fp4Geom &q, float *lds,
+// ---------------------------------------------------- shared expert ----
+// Shared expert gate/up, rows [r0, r0 + 8) of both, from the quantised x
+// (grid values in LDS, padded to 132 per group): t for the 8 rows into the
+// shared slot of sv, then the tile's flag.
+__device__ __forceinline__ void dec_shared_gu(const DecArgs &a, int t, int tile, float *lds,
                                               float *s_y, const uint64_t *s_tab) {
-  const int tid = threadIdx.x, I = a.I, half = q.tr / 2;
-  fp4_pair_finish(R, s_y, I, r0, q, reinterpret_cast<float2 *>(lds), fp4_scale_lds(lds, q));
-  __syncthreads();
-  if (tid < half && r0 + tid < I)
-    a.sv[((size_t)t * (a.E + 1) + c) * I + r0 + tid] =
-        swiglu_t(s_y[tid], s_y[tid + half], a.limit, s_tab);
-}
-
-// Persistent routed gate/up of token t, workgroup bb of gu_nb: items
-// bb, bb + nb, ... of the token's ncand * gu_tiles, in two register tiles
-// used in turn: the next item's loads are issued before an item is computed,
-// so weights stream while the workgroup computes.
-__device__ __forceinline__ void dec_gu_routed(const DecArgs &a, int t, int bb, float *lds,
-                                              float *s_y, uint64_t *s_tab, int *s_cand,
-                                              int *s_nc) {
   const int tid = threadIdx.x;
-  const Fp4Geom q = fp4_geom_np(a.H, DEC_NP);
-  const uint64_t tabv = libm_table_load();
-  if (tid < 64) {
-    const int n = dec_candidates(a, t, s_cand, false, s_tab);
-    if (tid == 0) *s_nc = n;
-  }
-  libm_table_store(s_tab, tabv);
+  const int H = a.H, I = a.I, r0 = tile * (FP8_TR / 2);
+  Fp8Regs R;
+  fp8_pair_load(R, a.sh[0], a.sh_s[0], a.sh[1], a.sh_s[1], H, I, r0);
+  float *xs = lds, *qs = lds + (H / 128) * 132;
+  float2 *ps = reinterpret_cast<float2 *>(qs + ((H / 128 + 3) & ~3));
+  dec_quant_x(a.x + (size_t)t * H, H, nullptr, xs, qs);
   __syncthreads();
-  const int nitems = __builtin_amdgcn_readfirstlane(*s_nc) * a.gu_tiles;
-  const int nb = a.gu_nb;
-  if (bb >= nitems) return;
-  if (!a.fast) {
-    // exact mode: the chains bound the kernel and this stream has slack; it
-    // starts 1 us later so that the chains' gate rows are staged first
-    const long long t0 = wall_clock64();  // 100 MHz
-    while (wall_clock64() - t0 < 100) __builtin_amdgcn_s_sleep(8);
-  }
-  // two register tiles used in turn, unrolled over the first four items (a
-  // loop would carry loads in flight across its back edge, which the
-  // compiler drains); more items (many candidates) run one at a time
-  Fp4RegsT<DEC_NP> A, B;
-  int cA, rA, cB, rB;
-  bool lA, lB;
-  int j = bb;
-  dec_gu_load(a, A, t, j, nitems, s_cand, q, cA, rA, lA);
-  dec_gu_load(a, B, t, j + nb, nitems, s_cand, q, cB, rB, lB);
-  if (lA) dec_gu_finish(a, A, t, cA, rA, q, lds, s_y, s_tab);
-  j += nb;
-  dec_gu_load(a, A, t, j + nb, nitems, s_cand, q, cA, rA, lA);
-  if (j < nitems && lB) dec_gu_finish(a, B, t, cB, rB, q, lds, s_y, s_tab);
-  j += nb;
-  dec_gu_load(a, B, t, j + nb, nitems, s_cand, q, cB, rB, lB);
-  if (j < nitems && lA) dec_gu_finish(a, A, t, cA, rA, q, lds, s_y, s_tab);
-  j += nb;
-  if (j < nitems && lB) dec_gu_finish(a, B, t, cB, rB, q, lds, s_y, s_tab);
-  for (j += nb; j < nitems; j += nb) {
-    dec_gu_load(a, A, t, j, nitems, s_cand, q, cA, rA, lA);
-    if (lA) dec_gu_finish(a, A, t, cA, rA, q, lds, s_y, s_tab);
-  }
+  fp8_pair_finish(R, s_y, xs, qs, a.sh[0], a.sh_s[0], a.sh[1], a.sh_s[1], H, I, r0, ps);
+  __syncthreads();
+  if (tid < FP8_TR / 2 && r0 + tid < I)
+    st_dev(dec_tok(a.sv, a, t) + (size_t)a.E * I + r0 + tid,
+           swiglu_t(s_y[tid], s_y[tid + FP8_TR / 2], a.limit, s_tab));
+  dec_signal(dec_tok(a.sf, a, t) + (size_t)tile * DEC_FS);
 }
 
-// Blocks: [n*maxc chain workgroups][n*gu_nb persistent routed FP4
-// workgroups][n*(I/8) shared FP8 gate/up pairs]. Workgroups are dispatched in
-// index order, so the small loads that gate the critical path (the
-// candidates' choices, the chains' gate rows) are issued before the shared
-// expert's weight stream.
-__global__ __launch_bounds__(256) void k_dec_gateup(DecArgs a) {
-  extern __shared__ __align__(16) float lds[];
-  __shared__ uint64_t s_tab[32];
-  __shared__ float s_y[256];
-  __shared__ int s_cand[ROUTER_MAX_EXPERTS];
-  __shared__ int s_nc, s_flag;
-  const int I = a.I;
-  const int nchain = a.n * a.maxc;
-  const int t8 = (I + FP8_TR / 2 - 1) / (FP8_TR / 2);
-  const int nshared = a.n * t8;
-  int b = blockIdx.x;
-  if (b < nchain) {
-    dec_chain_block(a, b / a.maxc, b % a.maxc, lds, s_tab, s_cand, &s_nc, &s_flag);
-    return;
-  }
-  b -= nchain;
-  if (b < a.n * a.gu_nb) {
-    dec_gu_routed(a, b / a.gu_nb, b % a.gu_nb, lds, s_y, s_tab, s_cand, &s_nc);
-    return;
-  }
-  b -= a.n * a.gu_nb;
-  if (b < nshared) dec_shared_gateup(a, b / t8, b % t8, lds, s_y, s_tab);
-}
-
-// -------------------------------------------------------------- down ----
 // y = bf16(t * w), then per-128 E4M3 requant into LDS (all threads):
 // qy[i + pad * (i / 128)], qys[i / 128] (src/dsv4/dsv4_model.c:6268-6287).
-// Wave wv takes groups wv, wv + 4, ...; the t values of its first eight
-// groups (all of them for inter <= 4096) are loaded ahead of the weights by
-// dec_tv_load.
+// Wave wv takes groups wv, wv + 4, ...; t comes through agent-scope loads
+// (written by other workgroups of the launch), those of the first eight
+// groups (all of them for inter <= 4096) loaded together ahead.
 struct TvRegs {
   float v[16];
 };
 
-__device__ __forceinline__ void dec_tv_load(TvRegs &T, const float *tv, int I) {
-  const uint32_t wv = threadIdx.x / 64, lane = threadIdx.x % 64;
-  const BufRsrc r = buf_rsrc(tv, 4u * (uint32_t)I);  // groups past I / 128 read zeros
+__device__ __forceinline__ void dec_tv_load_dev(TvRegs &T, const float *tv, int I) {
+  const int wv = threadIdx.x / 64, lane = threadIdx.x % 64;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    const uint32_t g = wv + 4u * j;
-    T.v[2 * j] = buf_loadf(r, 4u * (g * 128u + lane));
-    T.v[2 * j + 1] = buf_loadf(r, 4u * (g * 128u + 64u + lane));
+    const int g = wv + 4 * j;
+    T.v[2 * j] = g * 128 < I ? ld_dev(tv + g * 128 + lane) : 0.0f;
+    T.v[2 * j + 1] = g * 128 < I ? ld_dev(tv + g * 128 + 64 + lane) : 0.0f;
   }
-  // t has arrived before this workgroup's weights are requested: issued at
-  // the same time, the few t lines would queue in the memory channels
-  // behind the whole kernel's weight stream (about 5 us)
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __builtin_amdgcn_sched_barrier(0);
 }
 
-// CODES: qy receives E4M3 codes as bytes (the FP4 down tile), otherwise the
-// grid values as floats, padded by 4 per 128 (the FP8 tile).
-template <bool CODES>
-__device__ void dec_requant(void *qyv, float *qys, const TvRegs &T, const float *tv, float w,
-                            int I) {
+__device__ void dec_requant_f(float *qy, float *qys, const TvRegs &T, const float *tv, float w,
+                              int I) {
   const int wv = threadIdx.x / 64, lane = threadIdx.x % 64;
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
     const int g = wv + 4 * j;
     if (g >= I / 128) break;
     const int i0 = g * 128 + lane, i1 = i0 + 64;
-    const float t0 = j < 8 ? T.v[(2 * j) & 15] : tv[i0];
-    const float t1 = j < 8 ? T.v[(2 * j + 1) & 15] : tv[i1];
+    const float t0 = j < 8 ? T.v[(2 * j) & 15] : ld_dev(tv + i0);
+    const float t1 = j < 8 ? T.v[(2 * j + 1) & 15] : ld_dev(tv + i1);
     const float y0 = bf16_round(t0 * w);
     const float y1 = bf16_round(t1 * w);
     const float amax = wave_max_dpp(fmaxf(fabsf(y0), fabsf(y1)));
     const float scale = act_scale(amax);
     const float inv = 1.0f / scale;
-    if (CODES) {
-      uint8_t *q = reinterpret_cast<uint8_t *>(qyv) + g * 128;
-      q[lane] = (uint8_t)e4m3_code(quant_e4m3(y0, inv));
-      q[lane + 64] = (uint8_t)e4m3_code(quant_e4m3(y1, inv));
-    } else {
-      float *q = reinterpret_cast<float *>(qyv) + g * 132;
-      q[lane] = quant_e4m3(y0, inv);
-      q[lane + 64] = quant_e4m3(y1, inv);
-    }
+    float *q = qy + g * 132;
+    q[lane] = quant_e4m3(y0, inv);
+    q[lane + 64] = quant_e4m3(y1, inv);
     if (lane == 0) qys[g] = scale;
   }
   __syncthreads();
 }
 
-// Shared expert down, rows [16 tile, 16 tile + 16): its t (weight 1)
-// requantised into LDS, then the FP8 tile into route slot K of ro.
-__device__ __forceinline__ void dec_shared_down(const DecArgs &a, int t, int tile, float *lds) {
-  const int H = a.H, I = a.I, K = a.K;
-  const float *tv = a.sv + ((size_t)t * (a.E + 1) + a.E) * I;
-  TvRegs T;
-  dec_tv_load(T, tv, I);
+// Shared expert down, rows [16 tile, 16 tile + 16): the weights are issued
+// first, then (unless the caller has seen them) the wait for the token's
+// shared gate/up tiles, then t (weight 1) requantised into LDS and the FP8
+// tile into ro (fp32; k_dec_back rounds it). False if the wait ran out.
+__device__ __forceinline__ bool dec_shared_dn(const DecArgs &a, int t, int tile, bool wait,
+                                              float *lds, int *s_i) {
+  const int H = a.H, I = a.I;
   Fp8Regs R;
   fp8_tile_load(R, a.sh[2], a.sh_s[2], I, H, tile * FP8_TR);
+  if (wait && !dec_wait_flags(dec_tok(a.sf, a, t), (I + FP8_TR / 2 - 1) / (FP8_TR / 2), DEC_FS,
+                              nullptr, a.ctl, s_i))
+    return false;
+  const float *tv = dec_tok(a.sv, a, t) + (size_t)a.E * I;
+  TvRegs T;
+  dec_tv_load_dev(T, tv, I);
   float *xs = lds, *qys = lds + (I / 128) * 132;
   float2 *ps = reinterpret_cast<float2 *>(qys + ((I / 128 + 3) & ~3));
-  dec_requant<false>(xs, qys, T, tv, 1.0f, I);
-  fp8_tile_finish(R, a.ro + ((size_t)t * (K + 1) + K) * H, xs, qys, a.sh[2], a.sh_s[2], I, H,
-                  tile * FP8_TR, 1, ps);
+  dec_requant_f(xs, qys, T, tv, 1.0f, I);
+  fp8_tile_finish(R, dec_tok(a.ro, a, t), xs, qys, a.sh[2], a.sh_s[2], I, H, tile * FP8_TR, 0,
+                  ps);
+  return true;
 }
 
-// Blocks: [n*K*dn_tiles routed FP4 down tiles][n*(H/16) shared FP8 down].
-__global__ __launch_bounds__(256) void k_dec_down(DecArgs a) {
-  extern __shared__ __align__(16) float lds[];
-  const int tid = threadIdx.x;
-  const int H = a.H, I = a.I, K = a.K;
-  const int nrouted = a.n * K * a.dn_tiles;
-  int b = blockIdx.x;
-  if (b < nrouted) {
-    const int tile = b % a.dn_tiles;
-    b /= a.dn_tiles;
-    const int k = b % K, t = b / K;
-    const size_t o = (size_t)t * K + k;
-    const int e = a.sel_e[o], pos = a.sel_pos[o];
-    const float w = a.sel_w[o];
-    const Fp4Geom q = fp4_geom_np(I, DEC_NP);
-    const int r0 = tile * q.tr;
-    float *ro = a.ro + ((size_t)t * (K + 1) + k) * H;
-    if (e < 0 || e >= a.E) {  // no expert: the route adds zeros
-      for (int r = r0 + tid; r < min(H, r0 + q.tr); r += 256) ro[r] = 0.0f;
-      return;
-    }
-    const float *tv = a.sv + ((size_t)t * (a.E + 1) + pos) * I;
-    const uint8_t *W, *S;
-    expert_mat(a, e, 2, W, S);
-    TvRegs T;
-    dec_tv_load(T, tv, I);
-    Fp4RegsT<DEC_NP> R;
-    fp4_tile_load(R, W, S, I, H, r0, q);
-    // E4M3 codes and scales of y, read into registers before the pairs
-    // overwrite them
-    uint8_t *qy8 = reinterpret_cast<uint8_t *>(lds);  // I + I/32 bytes: within the pairs
-    float *qys = lds + I / 4;
-    dec_requant<true>(qy8, qys, T, tv, w, I);
-    fp4_tile_x_lds(R, qy8, qys, q);
-    fp4_tile_finish(R, ro, H, r0, q, reinterpret_cast<float2 *>(lds), fp4_scale_lds(lds, q));
-    return;
+// --------------------------------------------------- routed gate/up ----
+// Routed gate/up item l of token t: candidate position c = l / gu_tiles, rows
+// [r0, r0 + tr / 2) of its gate and up matrices (tile l % gu_tiles). An item
+// past the end (or a malformed tid2eid entry) loads zero-length ranges,
+// which read zeros without touching memory, so every load is issued
+// unconditionally. The activation codes in R stay as set.
+__device__ __forceinline__ void dec_gu_load(const DecArgs &a, Fp4RegsT<DEC_NP> &R, int l,
+                                            int nitems, const int *s_cand, const Fp4Geom &q,
+                                            int &c, int &r0, bool &live) {
+  const int H = a.H, I = a.I;
+  c = l / a.gu_tiles;
+  r0 = (l - c * a.gu_tiles) * (q.tr / 2);
+  const int e = __builtin_amdgcn_readfirstlane(l < nitems ? s_cand[min(c, a.E - 1)] : -1);
+  live = e >= 0 && e < a.E;
+  const uint8_t *W0, *S0, *W1, *S1;
+  expert_mat(a, live ? e : 0, 0, W0, S0);
+  expert_mat(a, live ? e : 0, 1, W1, S1);
+  fp4_pair_load_near(R, W0, S0, W1, S1, H, live ? I : 0, r0, q);  // S1 after S0 in the slot
+}
+
+// Dynamic LDS of a streaming workgroup for the FP4 items: the pairs of a
+// tile (tr rows, pair_stride(G) apart) and 4096 bytes of its scales, the
+// token's activation codes (H bytes) and per-128 scales, then E floats for
+// the candidates (dec_candidates).
+struct DecLds {
+  float2 *ps;
+  uint8_t *cl;
+  uint8_t *xq8;
+  float *xqs;
+  float *aux;
+};
+
+__device__ __host__ __forceinline__ size_t dec_lds_pairs(const Fp4Geom &q) {
+  return (size_t)q.tr * pair_stride(q.G) * 8;
+}
+__device__ __host__ __forceinline__ size_t dec_lds_x(int H) {
+  return ((size_t)H + (size_t)H / 32 + 15) & ~(size_t)15;
+}
+__device__ __host__ __forceinline__ size_t dec_lds_fp4(const Fp4Geom &q, int H, int E) {
+  return dec_lds_pairs(q) + 4096 + dec_lds_x(H) + 4 * (size_t)E;
+}
+
+__device__ __forceinline__ DecLds dec_lds(float *lds, const Fp4Geom &q, int H) {
+  uint8_t *b = reinterpret_cast<uint8_t *>(lds);
+  const size_t P = dec_lds_pairs(q);
+  DecLds L;
+  L.ps = reinterpret_cast<float2 *>(b);
+  L.cl = b + P;
+  L.xq8 = b + P + 4096;
+  L.xqs = reinterpret_cast<float *>(L.xq8 + H);
+  L.aux = reinterpret_cast<float *>(L.xq8 + dec_lds_x(H));
+  return L;
+}
+
+// The item's group chains over its partials (one lane per tile row,
+// pair_chain, src/dsv4/dsv4_model.c:1049-1074), then t = silu(bf16 gate) *
+// bf16 up for its rows (src/dsv4/dsv4_model.c:6264-6268) into candidate
+// slot c of sv.
+__device__ __forceinline__ void dec_gu_chain(const DecArgs &a, int t, int c, int r0,
+                                             const Fp4Geom &q, const DecLds &L, float *s_y,
+                                             const uint64_t *s_tab) {
+  const int tid = threadIdx.x, I = a.I, half = q.tr / 2;
+  const float v = fp4_tile_chain(q, L.ps);
+  if (tid < q.tr) s_y[tid] = v;
+  __syncthreads();
+  if (tid < half && r0 + tid < I)
+    dec_tok(a.sv, a, t)[(size_t)c * I + r0 + tid] =
+        swiglu_t(s_y[tid], s_y[tid + half], a.limit, s_tab);
+}
+
+// Routed gate/up items l0, l0 + S, ... (below le) of token t (of nc *
+// gu_tiles; nc candidates s_cand in LDS), from the token's quantised
+// activation (in LDS already if have_x, else quantised here), one register
+// tile at a time: a workgroup holding one tile leaves registers for more
+// workgroups per CU, whose loads overlap each other's compute (measured:
+// more bandwidth than two tiles in turn in fewer workgroups).
+__device__ __forceinline__ void dec_routed_items(const DecArgs &a, int t, int l0, int le, int nc,
+                                                 bool have_x, const DecLds &L, float *s_y,
+                                                 const uint64_t *s_tab, const int *s_cand) {
+  const int H = a.H, S = a.n_stream;
+  const Fp4Geom q = fp4_geom_np(H, DEC_NP);
+  const int nitems = nc * a.gu_tiles;
+  if (l0 >= le) return;
+  if (!have_x) {
+    dec_quant_x(a.x + (size_t)t * H, H, L.xq8, nullptr, L.xqs);
+    __syncthreads();
   }
-  b -= nrouted;
-  const int t16 = (H + FP8_TR - 1) / FP8_TR;
-  dec_shared_down(a, b / t16, b % t16, lds);
+  Fp4RegsT<DEC_NP> A;
+  fp4_tile_x_lds(A, L.xq8, L.xqs, q);  // the lane's activation group: the same for every item
+  for (int l = l0; l < le; l += S) {
+    int c, r0;
+    bool live;
+    dec_gu_load(a, A, l, nitems, s_cand, q, c, r0, live);
+    if (!live) continue;
+    fp4_tile_partials(A, a.I, r0, q, L.ps, L.cl, true);
+    dec_gu_chain(a, t, c, r0, q, L, s_y, s_tab);
+  }
+  __syncthreads();  // LDS (candidates, activation) is rewritten by the next token
 }
 
-// out[t][i] = bf16(((0 + ro[t][0][i]) + ... + ro[t][K-1][i]) + ro[t][K][i]):
-// routes in ascending expert id, then the shared expert
-// (src/dsv4/dsv4_model.c:6795-6805).
-__global__ __launch_bounds__(256) void k_dec_combine(DecArgs a) {
-  const int i = blockIdx.x * 256 + threadIdx.x;
-  if (i >= a.n * a.H) return;
-  const int t = i / a.H, c = i % a.H;
-  const float *r = a.ro + (size_t)t * (a.K + 1) * a.H + c;
-  float acc = 0.0f;
-  for (int k = 0; k < a.K; ++k) acc += r[(size_t)k * a.H];
-  acc += r[(size_t)a.K * a.H];
-  a.out[i] = bf16_round(acc);
+// Streaming workgroup j of n_stream: token 0's quantised activation into LDS
+// while the router runs, the candidates of token 0 (dec_candidates), its
+// tiles of the shared gate/up (j, j + S, ...), then per token its routed
+// gate/up items from l0 = j rotated past the workgroups with shared tiles
+// (l0, l0 + S, ...), then its tiles of the shared down rows (rotated
+// likewise). Each workgroup holds one item at a time: per unit of work the
+// latency of a load under full memory traffic, so every workgroup gets about
+// the same number of units (a shared tile counts as two).
+__device__ __forceinline__ void dec_stream_block(const DecArgs &a, int j, float *lds, float *s_y,
+                                                 uint64_t *s_tab, int *s_cand, int *s_sel,
+                                                 int *s_i) {
+  const int S = a.n_stream;
+  const uint64_t tabv = libm_table_load();
+  const int t8 = (a.I + FP8_TR / 2 - 1) / (FP8_TR / 2), nsh = a.n * t8;
+  const int rot = (j + S - nsh % S) % S;
+  const bool sh = j < nsh;
+  const DecLds L = dec_lds(lds, fp4_geom_np(a.H, DEC_NP), a.H);
+  float *s_v = L.aux;  // more than 256 experts: the candidates' choices
+  if (!sh) dec_quant_x(a.x, a.H, L.xq8, nullptr, L.xqs);
+  libm_table_store(s_tab, tabv);
+  int nc = dec_candidates(a, 0, s_cand, s_sel, s_v, s_i);
+  if (nc < 0) return;
+  for (int i = j; i < nsh; i += S) {
+    __syncthreads();  // LDS of the previous tile
+    dec_shared_gu(a, i / t8, i % t8, lds, s_y, s_tab);
+  }
+  for (int t = 0; t < a.n; ++t) {
+    if (t > 0 && (nc = dec_candidates(a, t, s_cand, s_sel, s_v, s_i)) < 0) return;
+    const int nitems = nc * a.gu_tiles;
+    if (rot < nitems) {
+      dec_routed_items(a, t, rot, nitems, nc, t == 0 && !sh, L, s_y, s_tab, s_cand);
+    }
+  }
+  const int t16 = (a.H + FP8_TR - 1) / FP8_TR;
+  int seen = -1;  // the token whose shared gate/up tiles are known written
+  for (int i = rot; i < a.n * t16; i += S) {
+    __syncthreads();
+    const int t = i / t16;
+    if (!dec_shared_dn(a, t, i % t16, t != seen, lds, s_i)) return;
+    seen = t;
+  }
+}
+
+// Blocks: [E streaming that first route expert j][n maxc chain][n_stream - E
+// streaming]: every streaming workgroup is resident from the start where the
+// device holds them all, so each learns the candidates before the weight
+// streams load the memory system.
+__global__ __launch_bounds__(256) void k_dec_front(DecArgs a) {
+  extern __shared__ __align__(16) float lds[];
+  __shared__ uint64_t s_tab[32];
+  __shared__ float s_y[256];
+  __shared__ float s_part[8];
+  __shared__ int s_cand[ROUTER_MAX_EXPERTS];
+  __shared__ int s_sel[32];
+  __shared__ int s_i;
+  int b = blockIdx.x;
+  if (b < a.E) {
+    dec_router_block(a, b, s_tab, s_part);
+    return dec_stream_block(a, b, lds, s_y, s_tab, s_cand, s_sel, &s_i);
+  }
+  b -= a.E;
+  if (b < a.n * a.maxc)
+    return dec_chain_block(a, b / a.maxc, b % a.maxc, lds, s_tab, s_cand, s_sel, &s_i);
+  b -= a.n * a.maxc;
+  if (a.E + b < a.n_stream)
+    dec_stream_block(a, a.E + b, lds, s_y, s_tab, s_cand, s_sel, &s_i);
+}
+
+// ------------------------------------------------------- down + combine ----
+// Requant workgroup of route (t, k): y = bf16(t * w) and the per-128 E4M3
+// requant (src/dsv4/dsv4_model.c:6261-6287), published as codes and scales,
+// then its flag. Thread i takes 8 consecutive values; a 128-group is 16
+// neighbouring lanes. t comes from the front launch (plain loads); a route
+// without an expert, or with a position outside the candidate slots (the
+// routing of a front launch whose waits ran out), reads zeros.
+__device__ __forceinline__ void dec_route_requant(const DecArgs &a, int t, int k) {
+  const int tid = threadIdx.x;
+  const int I = a.I, E = a.E;
+  const int e = dec_tok(a.sel_e, a, t)[k], pos = dec_tok(a.sel_pos, a, t)[k];
+  const float w = dec_tok(a.sel_w, a, t)[k];
+  const bool ok = e >= 0 && e < E && pos >= 0 && pos < E;
+  const BufRsrc rt = buf_rsrc(dec_tok(a.sv, a, t) + (size_t)(ok ? pos : 0) * I,
+                              ok ? 4u * (uint32_t)I : 0u);
+  uint32_t *qc = dec_tok(a.qc, a, t) + (size_t)k * (I / 4);
+  float *qcs = dec_tok(a.qcs, a, t) + (size_t)k * (I / 128);
+  const int span = (I + 2047) / 2048 * 2048;  // wave-uniform trip count
+  for (int base = 8 * tid; base < span; base += 2048) {
+    const uint4 u0 = buf_load16(rt, 4u * (uint32_t)base);  // past I: zeros
+    const uint4 u1 = buf_load16(rt, 4u * (uint32_t)base + 16u);
+    const float v[8] = {u2f(u0.x), u2f(u0.y), u2f(u0.z), u2f(u0.w),
+                        u2f(u1.x), u2f(u1.y), u2f(u1.z), u2f(u1.w)};
+    float y[8], m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      y[i] = bf16_round(v[i] * w);
+      m = fmaxf(m, fabsf(y[i]));
+    }
+    m = fmaxf(m, __shfl_xor(m, 1, 64));
+    m = fmaxf(m, __shfl_xor(m, 2, 64));
+    m = fmaxf(m, __shfl_xor(m, 4, 64));
+    m = fmaxf(m, __shfl_xor(m, 8, 64));
+    if (base < I) {
+      const float scale = act_scale(m);
+      const float inv = 1.0f / scale;
+      uint32_t c[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        c[h] = e4m3_code(quant_e4m3(y[4 * h], inv)) |
+               (e4m3_code(quant_e4m3(y[4 * h + 1], inv)) << 8) |
+               (e4m3_code(quant_e4m3(y[4 * h + 2], inv)) << 16) |
+               (e4m3_code(quant_e4m3(y[4 * h + 3], inv)) << 24);
+      st_dev(qc + base / 4, c[0]);
+      st_dev(qc + base / 4 + 1, c[1]);
+      if ((tid & 15) == 0) st_dev(qcs + base / 128, scale);
+    }
+  }
+  dec_signal(dec_tok(a.qf, a, t) + (size_t)k * DEC_FS);
+}
+
+// Down workgroup (token t, rows [r0, r0 + 8)): the FP4 down rows of every
+// route (routes in chunks of DB_RC; weights issued before the wait for the
+// routes' codes), lane: group g of 32 columns of tile row h rpp + lane / GP,
+// a sequential fmaf partial per group, then one lane per (route, row) chains
+// the groups in order (src/dsv4/dsv4_model.c:1049-1074), y_route =
+// bf16(acc); then out = bf16(((0 + y_0) + ... + y_{K-1}) + shared) in
+// ascending expert id (src/dsv4/dsv4_model.c:6795-6805). NPR: passes per
+// route (inter <= 1024 NPR).
+template <int NPR>
+__device__ __forceinline__ void dec_route_down(const DecArgs &a, int t, int r0, float *lds,
+                                               int *s_e, float *s_r, int *s_i) {
+  const int tid = threadIdx.x;
+  const int H = a.H, I = a.I, K = a.K, E = a.E;
+  const int G = I / 32;
+  int GP = 1;
+  while (GP < G) GP <<= 1;
+  const int rpp = 256 / GP, g = tid % GP, rsub = tid / GP;
+  if (tid < K) s_e[tid] = dec_tok(a.sel_e, a, t)[tid];
+  const float ysh = tid < 8 ? dec_tok(a.ro, a, t)[r0 + tid] : 0.0f;
+  __syncthreads();
+  uint32_t *qy = reinterpret_cast<uint32_t *>(lds);      // [DB_RC][I / 4] codes
+  float *qys = reinterpret_cast<float *>(qy + DB_RC * (I / 4));  // [DB_RC][32]
+  float2 *ps = reinterpret_cast<float2 *>(qys + DB_RC * 32);       // [DB_RC * 8][stride]
+  const int stride = pair_stride(G);
+  for (int k0 = 0; k0 < K; k0 += DB_RC) {
+    const int nk = min(DB_RC, K - k0);
+    uint4 w[DB_RC][NPR];
+    uint32_t code[DB_RC][NPR];
+    bool ok[DB_RC];
+#pragma unroll
+    for (int kk = 0; kk < DB_RC; ++kk) {
+      const int e = kk < nk ? s_e[k0 + kk] : -1;
+      ok[kk] = e >= 0 && e < E;
+      const uint8_t *W, *S;
+      expert_mat(a, ok[kk] ? e : 0, 2, W, S);
+      const BufRsrc rw = buf_rsrc(W + (size_t)r0 * (I / 2), ok[kk] ? 8u * (uint32_t)(I / 2) : 0u);
+      const BufRsrc rs = buf_rsrc(S + (size_t)r0 * G, ok[kk] ? 8u * (uint32_t)G : 0u);
+#pragma unroll
+      for (int h = 0; h < NPR; ++h) {
+        const int lr = h * rpp + rsub;
+        const bool in = lr < 8 && g < G;
+        w[kk][h] = buf_load16(rw, in ? (uint32_t)lr * (uint32_t)(I / 2) + 16u * g : 0xFFFFFFF0u);
+        code[kk][h] = __builtin_amdgcn_raw_buffer_load_b8(
+            rs, in ? (uint32_t)(lr * G + g) : 0xFFFFFFF0u, 0, 0);
+      }
+    }
+    // the chunk's routes requantised: codes and scales into LDS
+    if (!dec_wait_flags(dec_tok(a.qf, a, t) + (size_t)k0 * DEC_FS, nk, DEC_FS, nullptr, a.ctl,
+                        s_i))
+      return;
+    {
+      const uint32_t *src = dec_tok(a.qc, a, t) + (size_t)k0 * (I / 4);
+      for (int i = tid; i < nk * (I / 4); i += 256) qy[i] = ld_dev(src + i);
+      const float *ss = dec_tok(a.qcs, a, t) + (size_t)k0 * (I / 128);
+      for (int i = tid; i < nk * (I / 128); i += 256)
+        qys[(i / (I / 128)) * 32 + i % (I / 128)] = ld_dev(ss + i);
+    }
+    __syncthreads();
+    // partials: a route's passes share the lane's activation group
+#pragma unroll
+    for (int kk = 0; kk < DB_RC; ++kk) {
+      if (kk >= nk) break;
+      const int gc = min(g, G - 1);
+      const uint4 c0 = *reinterpret_cast<const uint4 *>(qy + kk * (I / 4) + 8 * gc);
+      const uint4 c1 = *reinterpret_cast<const uint4 *>(qy + kk * (I / 4) + 8 * gc + 4);
+      const uint32_t cw[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+      float xq[32];
+#pragma unroll
+      for (int d = 0; d < 8; ++d) {
+        const float2 lo = fp8x2<false>(cw[d]), hi = fp8x2<true>(cw[d]);
+        xq[4 * d] = lo.x;
+        xq[4 * d + 1] = lo.y;
+        xq[4 * d + 2] = hi.x;
+        xq[4 * d + 3] = hi.y;
+      }
+      const float as = qys[kk * 32 + gc / 4];
+#pragma unroll
+      for (int h = 0; h < NPR; ++h) {
+        const int lr = h * rpp + rsub;
+        if (lr < 8 && g < G) {
+          float part = fp4_group_partial(w[kk][h], xq);
+          float s = as * e8m0(code[kk][h]);
+          if (code[kk][h] == 255u) {  // NaN scale: the reference skips the group
+            part = 0.0f;
+            s = 0.0f;
+          }
+          ps[(kk * 8 + lr) * stride + g] = make_float2(part, s);
+        }
+      }
+    }
+    __syncthreads();
+    if (tid < DB_RC * 8) {
+      const int kk = tid / 8, lr = tid % 8, k = k0 + kk;
+      if (kk < nk) {
+        const float acc = ok[kk] ? pair_chain(ps + tid * stride, G) : 0.0f;
+        s_r[k * 8 + lr] = bf16_round(acc);  // no expert: the route adds zeros
+        if (a.route_out) a.route_out[((size_t)t * (K + 1) + k) * H + r0 + lr] = acc;
+      }
+    }
+    __syncthreads();  // qy, qys and ps are rewritten by the next chunk
+  }
+  if (tid < 8) {
+    float acc = 0.0f;
+    for (int k = 0; k < K; ++k) acc += s_r[k * 8 + tid];
+    acc += bf16_round(ysh);
+    a.out[(size_t)t * H + r0 + tid] = bf16_round(acc);
+    if (a.route_out) a.route_out[((size_t)t * (K + 1) + K) * H + r0 + tid] = ysh;
+  }
+}
+
+// Blocks: [n K route requants][n (H / 8) down row tiles]. The requant
+// workgroups come first in dispatch order: the down workgroups wait for
+// them. Workgroup 0 also clears the front launch's records and flags (that
+// launch has ended).
+template <int NPR>
+__global__ __launch_bounds__(256) void k_dec_back(DecArgs a) {
+  extern __shared__ __align__(16) float lds[];
+  __shared__ int s_e[32];
+  __shared__ float s_r[32 * 8];
+  __shared__ int s_i;
+  const int nq = a.n * a.K;
+  int b = blockIdx.x;
+  if (b < nq) {
+    if (b == 0) {
+      const int t8 = (a.I + FP8_TR / 2 - 1) / (FP8_TR / 2);
+      for (int i = threadIdx.x; i < a.n * a.E; i += 256) {
+        dec_tok(a.rec, a, i / a.E)[i % a.E] = 0ull;
+        dec_tok(a.zrec, a, i / a.E)[i % a.E] = 0ull;
+      }
+      for (int i = threadIdx.x; i < a.n * t8; i += 256)
+        dec_tok(a.sf, a, i / t8)[(size_t)(i % t8) * DEC_FS] = 0u;
+    }
+    return dec_route_requant(a, b / a.K, b % a.K);
+  }
+  b -= nq;
+  const int nt = a.H / 8;
+  dec_route_down<NPR>(a, b / nt, (b % nt) * 8, lds, s_e, s_r, &s_i);
 }
 
 __global__ void k_fill_zero_u32(unsigned *p, size_t n) {
@@ -868,24 +1222,23 @@ using namespace dsv4;
 namespace {
 
 struct DecWs {
-  unsigned *ctl;
-  uint8_t *qx8;
-  float *qxs, *ch, *zabs, *za, *zx, *zc, *sel_w, *sv, *ro;
-  int *cand, *ncand, *sel_e, *sel_pos;
+  unsigned *ctl, *sf, *cf, *qf;
+  uint64_t *rec, *zrec;
+  uint32_t *qc;
+  float *qcs, *zx, *zc, *sel_w, *sv, *ro;
+  int *sel_e, *sel_pos;
+  size_t tb;  // bytes of one token's piece
   size_t bytes;
 };
 
-int dec_maxc(const DSV4GLayer *L) {
-  int m = L->topk + 10;
-  if (m < 16) m = 16;
-  return m < L->n_experts ? m : L->n_experts;
-}
-
-// The control words come first (offset 0 for every layer shape), then the
-// rest, each piece 256-byte aligned.
+// The control words first, then one piece per token, each holding every
+// per-token array (256-byte aligned): a token's arrays sit at the same
+// offsets whatever the token count of the call, so a workspace serves calls
+// with any token count up to its size without stale words in its flags.
 DecWs dec_ws_layout(const DSV4GLayer *L, int n_tokens, void *base) {
-  const size_t n = (size_t)n_tokens, K = (size_t)L->topk, E = (size_t)L->n_experts;
+  const size_t K = (size_t)L->topk, E = (size_t)L->n_experts;
   const size_t H = (size_t)L->hidden, I = (size_t)L->inter;
+  const size_t t8 = (I + FP8_TR / 2 - 1) / (FP8_TR / 2);
   DecWs w = {};
   uintptr_t p = (uintptr_t)base;
   auto take = [&](size_t bytes) {
@@ -894,40 +1247,44 @@ DecWs dec_ws_layout(const DSV4GLayer *L, int n_tokens, void *base) {
     return r;
   };
   w.ctl = (unsigned *)take(DEC_CTL_BYTES);
-  w.qx8 = (uint8_t *)take(n * H);
-  w.qxs = (float *)take(n * (H / 128) * 4);
-  w.ch = (float *)take(n * E * 4);
-  w.zabs = (float *)take(n * E * 4);
-  w.za = (float *)take(n * E * 4);
-  w.cand = (int *)take(n * E * 4);
-  w.ncand = (int *)take(n * 4);
-  w.zx = (float *)take(n * E * 4);
-  w.zc = (float *)take(n * E * 4);
-  w.sel_e = (int *)take(n * K * 4);
-  w.sel_w = (float *)take(n * K * 4);
-  w.sel_pos = (int *)take(n * K * 4);
-  w.sv = (float *)take(n * (E + 1) * I * 4);
-  w.ro = (float *)take(n * (K + 1) * H * 4);
-  w.bytes = (size_t)(p - (uintptr_t)base);
+  const uintptr_t t0 = p;
+  w.rec = (uint64_t *)take(E * 8);
+  w.zrec = (uint64_t *)take(E * 8);
+  w.sf = (unsigned *)take(t8 * DEC_FS * 4);
+  w.cf = (unsigned *)take(E * 4);
+  w.qf = (unsigned *)take(K * DEC_FS * 4);
+  w.zx = (float *)take(E * 4);
+  w.zc = (float *)take(E * 4);
+  w.sel_e = (int *)take(K * 4);
+  w.sel_w = (float *)take(K * 4);
+  w.sel_pos = (int *)take(K * 4);
+  w.sv = (float *)take((E + 1) * I * 4);
+  w.ro = (float *)take(H * 4);
+  w.qc = (uint32_t *)take(K * I);
+  w.qcs = (float *)take(K * (I / 128) * 4);
+  w.tb = (size_t)(p - t0);
+  w.bytes = DEC_CTL_BYTES + (size_t)n_tokens * w.tb;
   return w;
 }
 
 size_t max_sz(size_t a, size_t b) { return a > b ? a : b; }
 
-// Workgroups of k_dec_gateup resident at once on the current device (its
+// Workgroups of k_dec_front resident at once on the current device (its
 // occupancy times the CU count), cached per device and LDS size.
-int gateup_slots(size_t lds, int *slots) {
+int front_slots(size_t lds, int *slots) {
+  static std::mutex mu;
   static int cache_slots[64];
   static size_t cache_lds[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0)
     return dsv4g_fail(DSV4G_EHIP, "moe_decode: hipGetDevice failed");
+  std::lock_guard<std::mutex> lock(mu);
   if (dev < 64 && cache_slots[dev] > 0 && cache_lds[dev] == lds) {
     *slots = cache_slots[dev];
     return DSV4G_OK;
   }
   int per_cu = 0, cus = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_dec_gateup, 256, lds) != hipSuccess ||
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_dec_front, 256, lds) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
     return dsv4g_fail(DSV4G_EHIP, "moe_decode: occupancy query failed");
   *slots = max(1, per_cu) * max(1, cus);
@@ -940,9 +1297,13 @@ int gateup_slots(size_t lds, int *slots) {
 
 int dec_launch(int phase, float *out, const float *x, const DSV4GLayer *L, const int *token_ids,
                int n_tokens, void *workspace, size_t workspace_bytes, int *idx_out,
-               float *wt_out, hipStream_t st, int fast) {
+               float *wt_out, float *route_out, hipStream_t st, int fast) {
   DSV4G_TRY(dsv4g_layer_ok(L, "moe_decode"));
   if (n_tokens <= 0) return dsv4g_fail(DSV4G_EINVAL, "moe_decode: n_tokens must be > 0");
+  if (n_tokens > DEC_MAX_TOKENS)
+    return dsv4g_fail(DSV4G_EINVAL, "moe_decode: at most %d tokens per call", DEC_MAX_TOKENS);
+  if (L->inter > 4096)
+    return dsv4g_fail(DSV4G_EINVAL, "moe_decode: inter %d above 4096", L->inter);
   if (L->tid2eid && !token_ids)
     return dsv4g_fail(DSV4G_EINVAL, "moe_decode: hash layer needs token_ids");
   if (((uintptr_t)workspace & 255) || ((uintptr_t)x & 15) || ((uintptr_t)out & 15))
@@ -969,13 +1330,14 @@ int dec_launch(int phase, float *out, const float *x, const DSV4GLayer *L, const
   a.sh_s[1] = L->sh3_s;
   a.sh_s[2] = L->sh2_s;
   a.ctl = w.ctl;
-  a.qx8 = w.qx8;
-  a.qxs = w.qxs;
-  a.ch = w.ch;
-  a.zabs = w.zabs;
-  a.za = w.za;
-  a.cand = w.cand;
-  a.ncand = w.ncand;
+  a.rec = w.rec;
+  a.zrec = w.zrec;
+  a.sf = w.sf;
+  a.cf = w.cf;
+  a.qf = w.qf;
+  a.qc = w.qc;
+  a.qcs = w.qcs;
+  a.tb = w.tb;
   a.zx = w.zx;
   a.zc = w.zc;
   a.sel_e = w.sel_e;
@@ -983,6 +1345,7 @@ int dec_launch(int phase, float *out, const float *x, const DSV4GLayer *L, const
   a.sel_pos = w.sel_pos;
   a.sv = w.sv;
   a.ro = w.ro;
+  a.route_out = route_out;
   a.idx_out = idx_out;
   a.wt_out = wt_out;
   a.n = n_tokens;
@@ -990,11 +1353,8 @@ int dec_launch(int phase, float *out, const float *x, const DSV4GLayer *L, const
   a.I = L->inter;
   a.E = L->n_experts;
   a.K = L->topk;
-  a.maxc = dec_maxc(L);
-  const Fp4Geom qg = fp4_geom_np(a.H, DEC_NP), qd = fp4_geom_np(a.I, DEC_NP);
+  const Fp4Geom qg = fp4_geom_np(a.H, DEC_NP);
   a.gu_tiles = (a.I + qg.tr / 2 - 1) / (qg.tr / 2);
-  a.dn_tiles = (a.H + qd.tr - 1) / qd.tr;
-
   a.route_scale = L->route_scale;
   {
     const double d = dec_par_depth(a.H) * 0x1p-24, h = a.H * 0x1p-24;
@@ -1003,43 +1363,44 @@ int dec_launch(int phase, float *out, const float *x, const DSV4GLayer *L, const
   a.limit = (float)(int)L->swiglu_limit;  // the reference passes the limit as int
   a.fast = fast;
   const int n = n_tokens, H = a.H, I = a.I;
-  if (n > DEC_CTL_BYTES / 4 - 1)
-    return dsv4g_fail(DSV4G_EINVAL, "moe_decode: at most %d tokens per call",
-                      DEC_CTL_BYTES / 4 - 1);
-  const size_t lds_fp8_gu = (size_t)(H / 128) * 132 * 4 + (size_t)((H / 128 + 3) & ~3) * 4 +
-                            (size_t)FP8_TR * pair_stride(H / 128) * 8;
-  const size_t lds_fp8_dn = (size_t)(I / 128) * 132 * 4 + (size_t)((I / 128 + 3) & ~3) * 4 +
-                            (size_t)FP8_TR * pair_stride(I / 128) * 8;
   if (phase == 0) {
-    const int blocks = a.E + (n * (H / 128) + 3) / 4;
-    hipLaunchKernelGGL(k_dec_router, dim3(blocks), dim3(256), 0, st, a);
-    return dsv4g_check_launch("dec_router");
+    // streaming: routed pairs and their scales, the activation codes and
+    // scales; the shared FP8 tiles; chains: x and the gate row in fp32, then
+    // nc ints or 2 nc floats
+    const size_t lds_fp4 = dec_lds_fp4(qg, H, a.E);
+    const size_t lds_fp8_gu = (size_t)(H / 128) * 132 * 4 + (size_t)((H / 128 + 3) & ~3) * 4 +
+                              (size_t)FP8_TR * pair_stride(H / 128) * 8;
+    const size_t lds_fp8_dn = (size_t)(I / 128) * 132 * 4 + (size_t)((I / 128 + 3) & ~3) * 4 +
+                              (size_t)FP8_TR * pair_stride(I / 128) * 8;
+    const size_t lds = max_sz(max_sz(lds_fp4, (size_t)8 * H + (size_t)8 * a.E),
+                              max_sz(lds_fp8_gu, lds_fp8_dn));
+    int slots = 0;
+    DSV4G_TRY(front_slots(lds, &slots));
+    // the routing workgroups wait for each other's records: all must be
+    // resident
+    if (a.E > slots)
+      return dsv4g_fail(DSV4G_EINVAL, "moe_decode: %d experts exceed this device's resident "
+                        "workgroups (%d)", a.E, slots);
+    a.maxc = min(max(a.K + 10, 16), a.E);
+    // streaming workgroups: the resident slots beside the chains, at least
+    // one per expert (the first E of them route first)
+    a.n_stream = max(a.E, slots - n * a.maxc);
+    const long blocks = (long)n * a.maxc + a.n_stream;
+    hipLaunchKernelGGL(k_dec_front, dim3((unsigned)blocks), dim3(256), lds, st, a);
+    return dsv4g_check_launch("dec_front");
   }
   if (phase == 1) {
-    // routed pairs: the tile's pairs and scales; chains: x and a gate row
-    const size_t lds_fp4 = (size_t)qg.tr * pair_stride(qg.G) * 8 + 4096;
-    const size_t lds = max_sz(max_sz(lds_fp4, (size_t)H * 8), lds_fp8_gu);
-    // persistent routed workgroups: the resident slots left beside the chain
-    // and shared workgroups, split over the tokens (at least 128 each)
-    const int fixed = n * (a.maxc + (I + FP8_TR / 2 - 1) / (FP8_TR / 2));
-    int slots = 0;
-    DSV4G_TRY(gateup_slots(lds, &slots));
-    a.gu_nb = max(128, (slots - fixed) / n);
-    const long blocks = (long)fixed + (long)n * a.gu_nb;
-    hipLaunchKernelGGL(k_dec_gateup, dim3((unsigned)blocks), dim3(256), lds, st, a);
-    return dsv4g_check_launch("dec_gateup");
-  }
-  if (phase == 2) {
-    const size_t lds = max_sz(max_sz((size_t)qd.tr * pair_stride(qd.G) * 8 + 4096,
-                                     (size_t)I + (size_t)I / 32 + 64),
-                              lds_fp8_dn);
-    const long blocks = (long)n * a.K * a.dn_tiles + (long)n * ((H + FP8_TR - 1) / FP8_TR);
-    hipLaunchKernelGGL(k_dec_down, dim3((unsigned)blocks), dim3(256), lds, st, a);
-    return dsv4g_check_launch("dec_down");
-  }
-  if (phase == 3) {
-    hipLaunchKernelGGL(k_dec_combine, dim3((unsigned)((n * H + 255) / 256)), dim3(256), 0, st, a);
-    return dsv4g_check_launch("dec_combine");
+    const int G = I / 32;
+    const size_t lds =
+        (size_t)DB_RC * I + DB_RC * 32 * 4 + (size_t)DB_RC * 8 * pair_stride(G) * 8;
+    const dim3 grid((unsigned)((long)n * a.K + (long)n * (H / 8)));
+    if (I <= 1024)
+      hipLaunchKernelGGL(k_dec_back<1>, grid, dim3(256), lds, st, a);
+    else if (I <= 2048)
+      hipLaunchKernelGGL(k_dec_back<2>, grid, dim3(256), lds, st, a);
+    else
+      hipLaunchKernelGGL(k_dec_back<4>, grid, dim3(256), lds, st, a);
+    return dsv4g_check_launch("dec_back");
   }
   return dsv4g_fail(DSV4G_EINVAL, "moe_decode: bad phase %d", phase);
 }
@@ -1052,12 +1413,11 @@ int dec_launch(int phase, float *out, const float *x, const DSV4GLayer *L, const
 static __device__ __align__(256) uint8_t scratch[DEC_SCRATCH_BYTES];
 std::mutex g_scratch_mu;
 void *g_scratch_ptr[64];
+uint64_t g_scratch_shape[64];  // the layer shape of the last call per device
 
-// The current device's scratch address, resolved once per device. Device
-// globals start zeroed when the code object loads; a first call that is not
-// being captured also clears the control words with the fill kernel (no
-// memset: the call may be captured into a graph).
-int scratch_ptr(hipStream_t st, void **out) {
+// The current device's scratch address, resolved once per device (device
+// globals start zeroed when the code object loads).
+int scratch_ptr(const DSV4GLayer *L, hipStream_t st, void **out) {
   int dev = 0;
   DSV4G_HIP(hipGetDevice(&dev));
   if (dev < 0 || dev >= 64) return dsv4g_fail(DSV4G_EINVAL, "moe_noalloc: device %d", dev);
@@ -1068,16 +1428,20 @@ int scratch_ptr(hipStream_t st, void **out) {
     if (e != hipSuccess || !p)
       return dsv4g_fail(DSV4G_EHIP, "moe_noalloc: hipGetSymbolAddress(scratch) failed: %s",
                         hipGetErrorString(e));
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    DSV4G_HIP(hipStreamIsCapturing(st, &cs));
-    if (cs == hipStreamCaptureStatusNone) {
-      const size_t words = DEC_CTL_BYTES / 4;
-      hipLaunchKernelGGL(k_fill_zero_u32, dim3((unsigned)((words + 255) / 256)), dim3(256), 0,
-                         st, (unsigned *)p, words);
-      DSV4G_TRY(dsv4g_check_launch("moe_noalloc_init"));
-    }
     g_scratch_ptr[dev] = p;
   }
+  // the records and flags sit at offsets of the layer's shape: another
+  // shape than the last call's finds stale words there, so the array is
+  // cleared first (a fill kernel, which graph capture records as well)
+  const uint64_t shape = (uint64_t)L->hidden ^ ((uint64_t)L->inter << 16) ^
+                         ((uint64_t)L->n_experts << 32) ^ ((uint64_t)L->topk << 48);
+  if (g_scratch_shape[dev] != 0 && g_scratch_shape[dev] != shape) {
+    const size_t words = DEC_SCRATCH_BYTES / 4;
+    hipLaunchKernelGGL(k_fill_zero_u32, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, st,
+                       (unsigned *)g_scratch_ptr[dev], words);
+    DSV4G_TRY(dsv4g_check_launch("moe_noalloc_clear"));
+  }
+  g_scratch_shape[dev] = shape;
   *out = g_scratch_ptr[dev];
   return 0;
 }
@@ -1099,50 +1463,74 @@ int dsv4g_moe_workspace_init(void *workspace, size_t workspace_bytes, void *stre
   return dsv4g_check_launch("moe_workspace_init");
 }
 
+int dsv4g_moe_decode_status(unsigned *status, void *workspace, void *stream) {
+  if (!status || !workspace || ((uintptr_t)workspace & 255))
+    return dsv4g_fail(DSV4G_EINVAL, "moe_decode_status: bad arguments");
+  hipStream_t st = (hipStream_t)stream;
+  DSV4G_HIP(hipMemcpyAsync(status, (const unsigned *)workspace + DEC_ERR, sizeof(unsigned),
+                           hipMemcpyDeviceToHost, st));
+  DSV4G_HIP(hipStreamSynchronize(st));
+  if (*status) {
+    hipLaunchKernelGGL(k_fill_zero_u32, dim3(1), dim3(64), 0, st,
+                       (unsigned *)workspace + DEC_ERR, (size_t)1);
+    DSV4G_TRY(dsv4g_check_launch("moe_decode_status"));
+  }
+  return 0;
+}
+
 int dsv4g_moe_decode_phase(int phase, float *out, const float *x, const DSV4GLayer *L,
                            const int *token_ids, int n_tokens, void *workspace,
                            size_t workspace_bytes, void *stream) {
   const int fast = (phase & DSV4G_DECODE_FAST) != 0;
   return dec_launch(phase & ~DSV4G_DECODE_FAST, out, x, L, token_ids, n_tokens, workspace,
-                    workspace_bytes, nullptr, nullptr, (hipStream_t)stream, fast);
+                    workspace_bytes, nullptr, nullptr, nullptr, (hipStream_t)stream, fast);
 }
 
 int dsv4g_moe_decode_routing(int *idx_out, float *wt_out, const DSV4GLayer *L, int n_tokens,
                              void *workspace, void *stream) {
   const DecWs w = dec_ws_layout(L, n_tokens, workspace);
   hipStream_t st = (hipStream_t)stream;
+  const size_t row = (size_t)L->topk * 4;  // one token's routing, from its piece
   if (idx_out)
-    DSV4G_HIP(hipMemcpyAsync(idx_out, w.sel_e, (size_t)n_tokens * L->topk * sizeof(int),
-                             hipMemcpyDeviceToDevice, st));
+    DSV4G_HIP(hipMemcpy2DAsync(idx_out, row, w.sel_e, w.tb, row, (size_t)n_tokens,
+                               hipMemcpyDeviceToDevice, st));
   if (wt_out)
-    DSV4G_HIP(hipMemcpyAsync(wt_out, w.sel_w, (size_t)n_tokens * L->topk * sizeof(float),
-                             hipMemcpyDeviceToDevice, st));
+    DSV4G_HIP(hipMemcpy2DAsync(wt_out, row, w.sel_w, w.tb, row, (size_t)n_tokens,
+                               hipMemcpyDeviceToDevice, st));
   return 0;
 }
 
 int dsv4g_moe_forward(float *out, const float *x, const DSV4GLayer *L, const int *token_ids,
                       int n_tokens, void *workspace, size_t workspace_bytes, int *idx_out,
                       float *wt_out, void *stream) {
-  for (int phase = 0; phase < 4; ++phase)
+  for (int phase = 0; phase < 2; ++phase)
     DSV4G_TRY(dec_launch(phase, out, x, L, token_ids, n_tokens, workspace, workspace_bytes,
-                         idx_out, wt_out, (hipStream_t)stream, 0));
+                         idx_out, wt_out, nullptr, (hipStream_t)stream, 0));
   return 0;
 }
 
 int dsv4g_moe_forward_fast(float *out, const float *x, const DSV4GLayer *L,
                            const int *token_ids, int n_tokens, void *workspace,
                            size_t workspace_bytes, int *idx_out, float *wt_out, void *stream) {
-  for (int phase = 0; phase < 4; ++phase)
+  for (int phase = 0; phase < 2; ++phase)
     DSV4G_TRY(dec_launch(phase, out, x, L, token_ids, n_tokens, workspace, workspace_bytes,
-                         idx_out, wt_out, (hipStream_t)stream, 1));
+                         idx_out, wt_out, nullptr, (hipStream_t)stream, 1));
   return 0;
 }
 
-}  // extern "C"
+int dsv4g_moe_forward_routes(float *out, const float *x, const DSV4GLayer *L,
+                             const int *token_ids, int n_tokens, void *workspace,
+                             size_t workspace_bytes, int *idx_out, float *wt_out,
+                             float *route_out, int fast, void *stream) {
+  for (int phase = 0; phase < 2; ++phase)
+    DSV4G_TRY(dec_launch(phase, out, x, L, token_ids, n_tokens, workspace, workspace_bytes,
+                         idx_out, wt_out, route_out, (hipStream_t)stream, fast ? 1 : 0));
+  return 0;
+}
 
-extern "C" int dsv4g_moe_forward_noalloc(float *out, const float *x, const DSV4GLayer *L,
-                                         const int *token_ids, int n_tokens, int *idx_out,
-                                         float *wt_out, void *stream) {
+int dsv4g_moe_forward_noalloc(float *out, const float *x, const DSV4GLayer *L,
+                              const int *token_ids, int n_tokens, int *idx_out, float *wt_out,
+                              void *stream) {
   DSV4G_TRY(dsv4g_layer_ok(L, "moe_noalloc"));
   if (n_tokens <= 0) return dsv4g_fail(DSV4G_EINVAL, "moe_noalloc: n_tokens must be > 0");
   const size_t need = dsv4g_moe_workspace_bytes(L, n_tokens);
@@ -1152,6 +1540,8 @@ extern "C" int dsv4g_moe_forward_noalloc(float *out, const float *x, const DSV4G
                       "than the %zu bytes of the library's scratch; pass fewer tokens per call",
                       n_tokens, need, DEC_SCRATCH_BYTES);
   void *ws = nullptr;
-  DSV4G_TRY(scratch_ptr((hipStream_t)stream, &ws));
+  DSV4G_TRY(scratch_ptr(L, (hipStream_t)stream, &ws));
   return dsv4g_moe_forward(out, x, L, token_ids, n_tokens, ws, need, idx_out, wt_out, stream);
 }
+
+}  // extern "C"

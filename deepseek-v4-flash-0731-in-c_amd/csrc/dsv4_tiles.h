@@ -69,30 +69,31 @@ __device__ __forceinline__ float fp4_group_partial(const uint4 w, const float *x
 }
 
 // acc = fmaf(p, s, acc) over n (p, s) pairs in order (the group chain of
-// one output row). The LDS reads of the next 16 pairs are in flight while the
-// current 16 are chained, so the loop runs at the fma dependency latency.
-// pr: 16-byte aligned.
+// one output row). The LDS reads of the next 2 NB pairs are in flight while
+// the current 2 NB are chained, so the loop runs at the fma dependency
+// latency (NB = 4 holds half the registers of NB = 8). pr: 16-byte aligned.
+template <int NB = 8>
 __device__ __forceinline__ float pair_chain(const float2 *pr, int n) {
   const float4 *p4 = reinterpret_cast<const float4 *>(pr);
-  const int nb = n / 16;
+  const int nb = n / (2 * NB);
   float acc = 0.0f;
-  float4 cur[8];
+  float4 cur[NB];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) cur[j] = nb > 0 ? p4[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int j = 0; j < NB; ++j) cur[j] = nb > 0 ? p4[j] : make_float4(0.f, 0.f, 0.f, 0.f);
   for (int b = 0; b < nb; ++b) {
-    const int nx = (b + 1 < nb ? b + 1 : b) * 8;
-    float4 nxt[8];
+    const int nx = (b + 1 < nb ? b + 1 : b) * NB;
+    float4 nxt[NB];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) nxt[j] = p4[nx + j];
+    for (int j = 0; j < NB; ++j) nxt[j] = p4[nx + j];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < NB; ++j) {
       acc = fmaf(cur[j].x, cur[j].y, acc);
       acc = fmaf(cur[j].z, cur[j].w, acc);
     }
 #pragma unroll
-    for (int j = 0; j < 8; ++j) cur[j] = nxt[j];
+    for (int j = 0; j < NB; ++j) cur[j] = nxt[j];
   }
-  for (int i = nb * 16; i < n; ++i) {
+  for (int i = nb * 2 * NB; i < n; ++i) {
     const float2 v = pr[i];
     acc = fmaf(v.x, v.y, acc);
   }
@@ -410,14 +411,14 @@ __device__ __forceinline__ void fp4_load_w(Fp4RegsT<NP> &R, const uint8_t *__res
   }
 }
 
-// Partials into ps, then one lane per tile row runs the group chain; returns
-// bf16(acc) for lane t < tr (row lr = t), garbage otherwise. cl: 4096 bytes
-// of LDS for the scales, apart from ps. Starts with a barrier: the activation
-// may have been read from LDS that ps overlaps.
+// Partials (group partial, scale) of every tile row into ps, ending with a
+// barrier; R is free afterwards. cl: 4096 bytes of LDS for the scales, apart
+// from ps. Starts with a barrier: the activation may have been read from LDS
+// that ps overlaps.
 template <int NP>
-__device__ __forceinline__ float fp4_tile_rows(const Fp4RegsT<NP> &R, int rows, int r0,
-                                               const Fp4Geom &q, float2 *ps, uint8_t *cl,
-                                               bool pair) {
+__device__ __forceinline__ void fp4_tile_partials(const Fp4RegsT<NP> &R, int rows, int r0,
+                                                  const Fp4Geom &q, float2 *ps, uint8_t *cl,
+                                                  bool pair) {
   const int t = threadIdx.x, g = t % q.gp, rsub = t / q.gp;
   const bool gact = g < q.G;
   const int npass = q.tr / q.rpp, half = q.tr / 2;
@@ -448,9 +449,25 @@ __device__ __forceinline__ float fp4_tile_rows(const Fp4RegsT<NP> &R, int rows, 
     }
   }
   __syncthreads();
+}
+
+// One lane per tile row runs the group chain over ps; returns bf16(acc) for
+// lane t < tr (row lr = t), garbage otherwise. NB: pair_chain's read-ahead.
+template <int NB = 8>
+__device__ __forceinline__ float fp4_tile_chain(const Fp4Geom &q, const float2 *ps) {
+  const int t = threadIdx.x;
   float acc = 0.0f;
-  if (t < q.tr) acc = pair_chain(ps + t * stride, q.G);
+  if (t < q.tr) acc = pair_chain<NB>(ps + t * pair_stride(q.G), q.G);
   return bf16_round(acc);
+}
+
+// Partials, then the chain (fp4_tile_partials, fp4_tile_chain).
+template <int NP>
+__device__ __forceinline__ float fp4_tile_rows(const Fp4RegsT<NP> &R, int rows, int r0,
+                                               const Fp4Geom &q, float2 *ps, uint8_t *cl,
+                                               bool pair) {
+  fp4_tile_partials(R, rows, r0, q, ps, cl, pair);
+  return fp4_tile_chain(q, ps);
 }
 
 // Single matrix: y[r0 + t] for the tile's rows.

@@ -56,6 +56,9 @@ _SIGS = {
     "dsv4g_moe_decode_phase": [_I, _vp, _vp, C.POINTER(DSV4GLayer), _vp, _I, _vp, _Z, _vp],
     "dsv4g_moe_decode_routing": [_vp, _vp, C.POINTER(DSV4GLayer), _I, _vp, _vp],
     "dsv4g_moe_workspace_init": [_vp, _Z, _vp],
+    "dsv4g_moe_decode_status": [_vp, _vp, _vp],
+    "dsv4g_moe_forward_routes": [_vp, _vp, C.POINTER(DSV4GLayer), _vp, _I, _vp, _Z, _vp, _vp,
+                                 _vp, _I, _vp],
     "dsv4g_moe_forward_batch": [_vp, _vp, C.POINTER(DSV4GLayer), _vp, _I, _vp, _Z, _vp, _vp,
                                 _vp],
     "dsv4g_moe_forward_batch_routes": [_vp, _vp, C.POINTER(DSV4GLayer), _vp, _I, _vp, _Z, _vp,
@@ -231,7 +234,11 @@ class GpuLib:
     def moe_workspace_bytes(self, layer, n_tokens):
         return int(self.lib.dsv4g_moe_workspace_bytes(C.byref(layer.struct), n_tokens))
 
-    def moe_forward(self, layer, x, token_ids=None, workspace=None, out=None, fast=False):
+    def moe_forward(self, layer, x, token_ids=None, workspace=None, out=None, fast=False,
+                    route_out=None, check=True):
+        """dsv4g_moe_forward(_fast); with route_out ([n][topk+1][hidden] fp32)
+        dsv4g_moe_forward_routes. check: read the workspace status after the
+        call (synchronises) and raise if a cross-workgroup wait ran out."""
         import torch
         n = x.shape[0]
         L = layer.struct
@@ -241,10 +248,28 @@ class GpuLib:
         out = torch.empty_like(x) if out is None else out
         idx = torch.empty(n, L.topk, dtype=torch.int32, device=x.device)
         wt = torch.empty(n, L.topk, dtype=torch.float32, device=x.device)
-        self._call("dsv4g_moe_forward_fast" if fast else "dsv4g_moe_forward", _ptr(out), _ptr(x),
-                   C.byref(L), _ptr(token_ids), n, _ptr(workspace), workspace.numel(), _ptr(idx),
-                   _ptr(wt), self._stream())
+        if route_out is not None:
+            self._call("dsv4g_moe_forward_routes", _ptr(out), _ptr(x), C.byref(L),
+                       _ptr(token_ids), n, _ptr(workspace), workspace.numel(), _ptr(idx),
+                       _ptr(wt), _ptr(route_out), 1 if fast else 0, self._stream())
+        else:
+            self._call("dsv4g_moe_forward_fast" if fast else "dsv4g_moe_forward", _ptr(out),
+                       _ptr(x), C.byref(L), _ptr(token_ids), n, _ptr(workspace),
+                       workspace.numel(), _ptr(idx), _ptr(wt), self._stream())
+        if check:
+            self.check_decode_status(workspace)
         return out, idx, wt
+
+    def decode_status(self, workspace):
+        """The decode workspace's sticky status word (0: fine), cleared."""
+        st = C.c_uint(0)
+        self._call("dsv4g_moe_decode_status", C.byref(st), _ptr(workspace), self._stream())
+        return st.value
+
+    def check_decode_status(self, workspace):
+        s = self.decode_status(workspace)
+        if s:
+            raise RuntimeError(f"decode: a cross-workgroup wait ran out (status {s:#x})")
 
     def moe_workspace_init(self, workspace):
         """Zero a decode workspace, once, before its first dsv4g_moe_forward."""

@@ -145,13 +145,15 @@ int dsv4g_router_public(int *idx, float *wt, const float *x, const uint16_t *gat
 int dsv4g_swiglu_quant(float *qy, float *qys, const float *gate_up, const float *wt, int K,
                        int n_slots, int inter, float limit, void *stream);
 
-/* Decode MoE layer: moe_forward for each of n_tokens (at most 1023) rows of
+/* Decode MoE layer: moe_forward for each of n_tokens (at most 1020) rows of
  * x (BF16 values in fp32), bit-exact. out [n][hidden]. idx_out/wt_out
  * (optional, device) receive the routing. workspace: 256-byte aligned device
  * memory of at least dsv4g_moe_workspace_bytes(L, n_tokens), zeroed once
  * before its first use (dsv4g_moe_workspace_init, or any zero fill); every
- * call leaves it ready for the next. Calls sharing one workspace must not
- * overlap. */
+ * call leaves it ready for the next, for any token count it holds. A
+ * workspace serves layers of one shape (hidden, inter, n_experts, topk);
+ * zero it again before a call with another shape. Calls sharing one
+ * workspace must not overlap. */
 size_t dsv4g_moe_workspace_bytes(const DSV4GLayer *L, int n_tokens);
 int dsv4g_moe_workspace_init(void *workspace, size_t workspace_bytes, void *stream);
 int dsv4g_moe_forward(float *out, const float *x, const DSV4GLayer *L, const int *token_ids,
@@ -175,24 +177,42 @@ int dsv4g_moe_forward_fast(float *out, const float *x, const DSV4GLayer *L,
  * loops that may not allocate. No counterpart in the reference: for callers
  * that cannot allocate. Same results as dsv4g_moe_forward; EINVAL when
  * dsv4g_moe_workspace_bytes(L, n_tokens) exceeds 16 MiB (about 2.1 MiB per
- * token at the model's shape: up to 7 tokens per call). Every call on one GPU shares that GPU's array: calls that
- * overlap on one GPU (two streams, two threads) race and must not be issued. */
+ * token at the model's shape: up to 7 tokens per call). Every call on one GPU
+ * shares that GPU's array: calls that overlap on one GPU (two streams, two
+ * threads) race and must not be issued. A call with a layer of another shape
+ * than the previous call's on that GPU first clears the array (a fill
+ * kernel). */
 int dsv4g_moe_forward_noalloc(float *out, const float *x, const DSV4GLayer *L,
                               const int *token_ids, int n_tokens, int *idx_out, float *wt_out,
                               void *stream);
-/* The same layer as four ordered phases, for callers that interleave or
- * time them: 0 router logits, candidate experts and activation quant; 1
- * gate/up GEMVs of the candidates and the shared expert, with the exact
- * router chains of the candidates and the exact top-k beside them; 2 SwiGLU
- * requant and down GEMVs; 3 the ordered combine. phase | DSV4G_DECODE_FAST runs the phases of
- * dsv4g_moe_forward_fast. dsv4g_moe_decode_routing copies the routing of
- * the last call. x and out: 16-byte aligned. */
+/* The same layer as two ordered launches, for callers that interleave or
+ * time them: 0 router, candidate experts, exact router chains and top-k, the
+ * shared expert, and the gate/up GEMVs of the candidates; 1 SwiGLU requant,
+ * routed down GEMVs and the ordered combine. phase | DSV4G_DECODE_FAST runs those of
+ * dsv4g_moe_forward_fast. dsv4g_moe_decode_routing copies the routing of the
+ * last call. x and out: 16-byte aligned. */
 #define DSV4G_DECODE_FAST 256
 int dsv4g_moe_decode_phase(int phase, float *out, const float *x, const DSV4GLayer *L,
                            const int *token_ids, int n_tokens, void *workspace,
                            size_t workspace_bytes, void *stream);
 int dsv4g_moe_decode_routing(int *idx_out, float *wt_out, const DSV4GLayer *L, int n_tokens,
                              void *workspace, void *stream);
+/* The decode workspace's sticky status word, read into *status (host) with a
+ * synchronisation of the stream, then cleared: 0 when every cross-workgroup
+ * wait of the calls since the last read completed; nonzero when one ran out
+ * (the outputs of those calls are not valid; re-initialise the workspace with
+ * dsv4g_moe_workspace_init). No counterpart in the reference. */
+int dsv4g_moe_decode_status(unsigned *status, void *workspace, void *stream);
+/* dsv4g_moe_forward (fast = 0) or dsv4g_moe_forward_fast (fast = 1), also
+ * writing each route's expert output before its BF16 rounding to route_out
+ * [n_tokens][topk + 1][hidden] (routes in ascending expert id, slot topk the
+ * shared expert). No counterpart in the reference, which rounds each expert
+ * output to BF16 (src/dsv4/dsv4_model.c:1073): for validating the
+ * accumulation. */
+int dsv4g_moe_forward_routes(float *out, const float *x, const DSV4GLayer *L,
+                             const int *token_ids, int n_tokens, void *workspace,
+                             size_t workspace_bytes, int *idx_out, float *wt_out,
+                             float *route_out, int fast, void *stream);
 
 /* Batched MoE layer: moe_forward_batch (src/dsv4/dsv4_model.c:6812-7117) for
  * n_tokens rows of x (speculative verify, prefill) as grouped GEMMs on the

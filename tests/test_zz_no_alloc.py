@@ -67,3 +67,37 @@ def test_noalloc_matches_workspace_entry():
                                        None, st)
     assert rc != 0
     assert b"scratch" in raw.dsv4g_last_error()
+
+
+def test_noalloc_layers_of_two_shapes():
+    """Calls with layers of two shapes in turn on the one scratch array: a
+    change of shape clears it first, so every call matches the workspace
+    entry bit for bit."""
+    import torch
+    import dsv4_gpu
+    import synth
+    dev = torch.device("cuda:0")
+    lib = dsv4_gpu.lib()
+    raw = lib.lib
+    raw.dsv4g_moe_forward_noalloc.restype = C.c_int
+    raw.dsv4g_moe_forward_noalloc.argtypes = [C.c_void_p, C.c_void_p,
+                                               C.POINTER(dsv4_gpu.DSV4GLayer), C.c_void_p,
+                                               C.c_int, C.c_void_p, C.c_void_p, C.c_void_p]
+    A = synth.device_layer(seed=5, hidden=4096, inter=2048, n_experts=64, device=dev)
+    B = synth.device_layer(seed=6, hidden=4096, inter=512, n_experts=32, topk=4, device=dev)
+    X = synth.bf16_tokens(3, 4096, seed=23, device=dev)
+    st = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+    ptr = lambda t: C.c_void_p(t.data_ptr())
+    for DL, n in ((A, 3), (B, 2), (A, 1), (B, 3)):
+        k = DL.struct.topk
+        out = torch.full((n, 4096), float("nan"), device=dev)
+        idx = torch.full((n, k), -7, dtype=torch.int32, device=dev)
+        wt = torch.zeros(n, k, device=dev)
+        rc = raw.dsv4g_moe_forward_noalloc(ptr(out), ptr(X[:n]), C.byref(DL.struct), None, n,
+                                           ptr(idx), ptr(wt), st)
+        assert rc == 0, raw.dsv4g_last_error()
+        ref, ri, rw = lib.moe_forward(DL, X[:n])
+        torch.cuda.synchronize()
+        assert same_bits(out.cpu().numpy(), ref.cpu().numpy()), (k, n)
+        assert np.array_equal(idx.cpu().numpy(), ri.cpu().numpy()), (k, n)
+        assert same_bits(wt.cpu().numpy(), rw.cpu().numpy()), (k, n)
