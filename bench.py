@@ -62,7 +62,8 @@ def parse():
     p.add_argument("--replays", type=int, default=5)
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--no-cpu", action="store_true")
-    p.add_argument("--workload", choices=("all", "decode", "verify", "prefill"), default="all")
+    p.add_argument("--workload", choices=("all", "decode", "verify", "prefill", "kernels"),
+                   default="all")
     p.add_argument("--zipf-strength", type=float, default=0.15)
     p.add_argument("--copy-calibration", action="store_true",
                    help="after the decode part, copy 1 GiB device-to-device 3 times: the "
@@ -115,7 +116,197 @@ def bench_batch(lib, layer, n_tokens, iters):
         "expert_flops": flops, "iters": iters,
         "mfma": "v_mfma_f32_16x16x32_bf16 (FP4/FP8 weights converted to BF16 x block scale "
                 "in registers; exact products, fp32 accumulate)",
+        "roofline": {"bound": "mfma", "achieved": round(flops / (ms * 1e-3) / 1e12, 2),
+                     "unit": "TFLOP/s", "peak_bf16_mfma": BF16_PEAK_TFLOPS,
+                     "peak_fp8_mfma": FP8_PEAK_TFLOPS,
+                     "frac_bf16": round(flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+                     "frac_fp8": round(flops / (ms * 1e-3) / 1e12 / FP8_PEAK_TFLOPS, 4),
+                     "mfma_busy_fraction_gateup": read_mfma_util(),
+                     "mfma_busy_source": "profiles/prefill_4096_grouped_gemm_mfma_counters.md "
+                                         "(SQ_VALU_MFMA_BUSY_CYCLES / 4 SQ_BUSY_CU_CYCLES)"},
     }
+
+
+def graph_time(fn, iters, replays=5):
+    """ms per call of fn(i), i < iters, captured in one HIP graph (one eager
+    warm-up pass first) and replayed `replays` times."""
+    import torch
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for i in range(iters):
+            fn(i)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(iters):
+            fn(i)
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(replays):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    del g
+    return e0.elapsed_time(e1) / (replays * iters)
+
+
+def cpu_loop(fn, seconds, max_calls=100000):
+    """Seconds per call of fn() on the host: one warm-up call, then calls until
+    `seconds` have elapsed."""
+    fn()
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or n >= max_calls:
+            return el / n, n
+
+
+def bench_fp8_matvec(lib, cpu_seconds):
+    """FP8 E4M3 matvec as the reference's CPU kernel path runs it (dsv4_gemv_fp8,
+    src/dsv4/dsv4_ops.c:176-209): W [2048 x 4096] N(0, 0.02) quantised per
+    128 x 128 block with fp32 absmax scales, x fp32 N(0, 1), seed 0. 48
+    copies of W at distinct addresses rotate so that each call streams its
+    matrix from HBM (48 x 8.4 MB exceeds the 256 MB last-level cache)."""
+    import numpy as np
+    import torch
+    dev = torch.device("cuda:0")
+    rows, cols, copies = 2048, 4096, 48
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    w = torch.randn(rows, cols, generator=g, device=dev) * 0.02
+    x = torch.randn(cols, generator=g, device=dev)
+    codes = torch.empty(copies, rows, cols, dtype=torch.uint8, device=dev)
+    scales = torch.empty(copies, rows // 128, cols // 128, dtype=torch.float32, device=dev)
+    lib.quant_fp8_blocks(w, codes[0], scales[0], mode=1)
+    for i in range(1, copies):
+        codes[i].copy_(codes[0])
+        scales[i].copy_(scales[0])
+    Y = torch.empty(copies, rows, dtype=torch.float32, device=dev)
+    ms = graph_time(lambda i: lib.gemv_fp8_float(x, codes[i % copies], scales[i % copies], cols,
+                                                 rows, 128, 0, y=Y[i % copies]), 4 * copies)
+    nbytes = rows * cols + scales[0].numel() * 4 + cols * 4 + rows * 4
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    r = {"workload": "FP8 E4M3 matvec 2048 x 4096, fp32 absmax 128x128 block scales, fp32 x "
+                     "(dsv4_gemv_fp8; bit-exact unfused sequential chain per row)",
+         "ms_per_call": round(ms, 5), "bytes_per_call": nbytes, "gbs": round(gbs, 1),
+         "roofline": {"bound": "chain latency", "achieved": round(gbs, 1),
+                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                      "frac": round(gbs / HBM_PEAK_GBS, 4)},
+         "note": "one lane per row runs the reference's 4096-step unfused chain (decode, "
+                 "x*s, w*xs, add per column): its VALU issue bounds the call near 20 us "
+                 "whatever the bandwidth; 2048 rows are 32 waves"}
+    if cpu_seconds and cpu_available():
+        ref = cpu_ref()
+        xh, ch, sh = x.cpu().numpy(), codes[0].cpu().numpy(), scales[0].cpu().numpy()
+        y_ref = ref.gemv_fp8_legacy(xh, ch, sh, cols, rows, 128)
+        same = bool(np.array_equal(y_ref.view(np.uint32), Y[0].cpu().numpy().view(np.uint32)))
+        sec, n = cpu_loop(lambda: ref.gemv_fp8_legacy(xh, ch, sh, cols, rows, 128), cpu_seconds)
+        r["cpu_baseline"] = {"value": round(nbytes / sec / 1e9, 3), "unit": "GB/s", "cores": 1,
+                             "kind": "reference", "ms_per_call": round(sec * 1e3, 3),
+                             "gpu_output_bit_exact_vs_reference": same,
+                             "sample": f"{n} calls of the reference dsv4_gemv_fp8 (oracle/_ref, "
+                                       f"single-threaded as the reference kernel is) on the "
+                                       f"same W and x"}
+    return r
+
+
+def bench_fp4_expert(lib, layer, cpu_seconds):
+    """One FP4 expert's SwiGLU at one token (expert_forward,
+    src/dsv4/dsv4_model.c:6289-6345): gate/up [2048 x 4096] and down
+    [4096 x 2048] E2M1 with per-32 E8M0 scales, weights N(0, 0.02), x BF16
+    N(0, 1). Calls rotate over the layer's 256 experts (3.4 GB), so each
+    streams its 13.4 MB from HBM."""
+    import numpy as np
+    import torch
+    import synth
+    dev = torch.device("cuda:0")
+    m = layer.meta
+    stride, srun = m["expert_stride"], m["scale_run"]
+    experts = layer.tensors["experts"]
+    X = synth.bf16_tokens(1, H, seed=5, device=dev)
+    qx, qs = lib.quant_fp8_act(X)
+    iters = E
+    OUT = torch.empty(iters, H, dtype=torch.float32, device=dev)
+    ws = torch.empty(lib.expert_workspace_bytes(I), dtype=torch.uint8, device=dev)
+    ms = graph_time(lambda i: lib.expert_forward(OUT[i], qx[0], qs[0],
+                                                 experts[(i % E) * stride:(i % E + 1) * stride],
+                                                 srun, H, I, m["swiglu_limit"], None, ws), iters)
+    nbytes = EXPERT_BYTES + H * 4 + (H // 128) * 4 + H * 4
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    r = {"workload": "FP4 E2M1 single-expert SwiGLU at 1 token: gate/up 2048 x 4096, down "
+                     "4096 x 2048, per-32 E8M0 scales (expert_forward: paired FP4 GEMV, "
+                     "SwiGLU + FP8 requant, FP4 down GEMV; three launches)",
+         "ms_per_call": round(ms, 5), "bytes_per_call": nbytes, "gbs": round(gbs, 1),
+         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4)}}
+    if cpu_seconds and cpu_available():
+        threads, _ = host_cores()
+        set_omp_threads(threads)
+        ref = cpu_ref()
+        eh = experts[:8 * stride].cpu().numpy()
+        qxh, qsh = qx[0].cpu().numpy(), qs[0].cpu().numpy()
+        outs = OUT[:8].cpu().numpy()
+        same = 0
+        for e in range(8):
+            sl = eh[e * stride:(e + 1) * stride]
+            o = ref.expert_forward(qxh, qsh, sl[:srun], sl[srun:], H, I, m["swiglu_limit"], 1.0)
+            same += int(np.array_equal(o.view(np.uint32), outs[e].view(np.uint32)))
+        k = [0]
+
+        def one():
+            sl = eh[(k[0] % 8) * stride:(k[0] % 8 + 1) * stride]
+            k[0] += 1
+            ref.expert_forward(qxh, qsh, sl[:srun], sl[srun:], H, I, m["swiglu_limit"], 1.0)
+        sec, n = cpu_loop(one, cpu_seconds)
+        r["cpu_baseline"] = {"value": round(nbytes / sec / 1e9, 3), "unit": "GB/s",
+                             "cores": threads, "kind": "reference",
+                             "ms_per_call": round(sec * 1e3, 3),
+                             "gpu_outputs_bit_exact_vs_reference": f"{same}/8",
+                             "sample": f"{n} calls of the reference expert_forward "
+                                       f"(oracle/_ref, OMP_NUM_THREADS={threads}) over 8 "
+                                       f"experts of the same layer and the same token"}
+    return r
+
+
+def cpu_available():
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import pyoracle
+    return pyoracle.ref_available()
+
+
+def cpu_ref():
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import pyoracle
+    return pyoracle.RefLib()
+
+
+def cpu_batch_baseline(layer_host, n_tokens, flops_per_token, seconds):
+    """The reference moe_forward_batch (oracle/_ref) on the host in chunks of 32
+    tokens (its batch limit is 33), on the same Zipf-biased layer: tokens per
+    second and the TFLOP/s that rate is worth."""
+    import numpy as np
+    threads, hw = host_cores()
+    set_omp_threads(threads)
+    ref = cpu_ref()
+    rng = np.random.default_rng(11 + n_tokens)
+    x = rng.standard_normal((32, H)).astype(np.float32)
+    x = (x.view(np.uint32) + 0x7FFF + ((x.view(np.uint32) >> 16) & 1)) & 0xFFFF0000
+    x = x.view(np.float32)
+    sec, n = cpu_loop(lambda: ref.moe_forward_batch(layer_host, x), seconds, max_calls=50)
+    tps = 32 / sec
+    return {"value": round(tps * flops_per_token / 1e12, 5), "unit": "TFLOP/s",
+            "cores": threads, "kind": "reference", "tokens_per_s": round(tps, 1),
+            "host": hw,
+            "sample": f"{n} calls of the reference moe_forward_batch on 32 BF16 tokens "
+                      f"(oracle/_ref, OMP_NUM_THREADS={threads}) of the same layer (256 FP4 "
+                      f"experts + FP8 shared, the same Zipf router bias), after one warm-up "
+                      f"call; the rate stands for the {n_tokens}-token workload"}
 
 
 def host_cores():
@@ -211,6 +402,18 @@ def read_traffic():
             return {"bytes": int(ln.split(":")[1]),
                     "source": "profiles/k_dec_front_hbm_traffic.md (rocprofv3 --pmc "
                               "FETCH_SIZE, WRITE_SIZE; copy-calibrated)"}
+    return None
+
+
+def read_mfma_util():
+    """MFMA-busy fraction of the FP4 grouped gate/up GEMM from the committed
+    rocprofv3 --pmc summary; None if that summary is absent."""
+    p = os.path.join(ROOT, "profiles", "prefill_4096_grouped_gemm_mfma_counters.md")
+    if not os.path.exists(p):
+        return None
+    for ln in open(p):
+        if ln.startswith("mfma_utilisation_k_grouped_gateup_fp4:"):
+            return float(ln.split(":")[1])
     return None
 
 
@@ -339,10 +542,19 @@ def main():
     torch.cuda.synchronize()
     gen_s = time.perf_counter() - t0
 
+    cpu_s = 0.0 if args.no_cpu else min(args.cpu_seconds, 6.0)
+    kernels = {}
+    if wl in ("all", "kernels"):
+        kernels["fp8_matvec_2048x4096"] = bench_fp8_matvec(lib, cpu_s)
+        kernels["fp4_expert_1_token"] = bench_fp4_expert(lib, layers[0], cpu_s)
+        if wl == "kernels":
+            print(json.dumps(kernels))
+            return
+
     batch = {}
     if wl in ("all", "verify", "prefill"):
-        zl = layers[0].with_bias(torch.from_numpy(
-            zipf_bias(E, strength=args.zipf_strength)).to(dev))
+        zb = zipf_bias(E, strength=args.zipf_strength)
+        zl = layers[0].with_bias(torch.from_numpy(zb).to(dev))
         if wl in ("all", "verify"):
             batch["verify_64"] = bench_batch(lib, zl, 64, 50)
         if wl in ("all", "prefill"):
@@ -350,6 +562,14 @@ def main():
         for v in batch.values():
             v["router"] = (f"Zipf(1.2) expert skew: bias {args.zipf_strength} * centred "
                            f"log rank^-1.2 over a seeded expert permutation")
+        if cpu_s and cpu_available():
+            Lh = synth.host_copy(layers[0])
+            Lh["bias"] = zb
+            for v in batch.values():
+                fpt = v["expert_flops"] / v["tokens"]
+                v["cpu_baseline"] = cpu_batch_baseline(Lh, v["tokens"], fpt, 2 * cpu_s)
+                v["speedup_vs_cpu"] = round(v["tflops"] / v["cpu_baseline"]["value"], 1)
+            del Lh
 
     if wl in ("verify", "prefill"):
         key = "verify_64" if wl == "verify" else "prefill_4096"
@@ -365,6 +585,8 @@ def main():
             "roofline": {"bound": "mfma", "achieved": r["tflops"], "peak": BF16_PEAK_TFLOPS,
                          "unit": "TFLOP/s", "frac": r["frac_bf16_mfma_peak"], "traffic": None},
         }
+        if "cpu_baseline" in r:
+            result["cpu_baseline"] = r["cpu_baseline"]
         print(json.dumps(result))
         return
 
@@ -410,6 +632,7 @@ def main():
             "layers_rotated": nl,
             "graph_replay_matches_eager": graph_ok,
             "layer_generation_s": round(gen_s, 2),
+            **kernels,
             **batch,
         },
         "roofline": {

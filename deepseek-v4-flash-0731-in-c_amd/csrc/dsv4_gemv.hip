@@ -75,15 +75,70 @@ __global__ void k_probe_converts(float *__restrict__ fp4_out, float *__restrict_
   fp8_out[t] = b.x;
 }
 
-// grid = (ceil(rows / tr), nvec, nmat). blockIdx.y selects a token vector
-// (batch), blockIdx.z selects matrix 0/1 (pair).
-__global__ __launch_bounds__(256) void k_gemv_fp4(GemvArgs a) {
-  __shared__ float2 ps[FP4_LDS_ENTRIES + 256];
-  const int m = blockIdx.z, b = blockIdx.y;
-  const Fp4Geom q = fp4_geom(a.in);
-  fp4_rows_exact(a.y[m] + (size_t)b * a.y_stride, a.qx + (size_t)b * a.qx_stride,
-                 a.qscale + (size_t)b * a.qs_stride, a.W[m], a.S[m], a.in, a.rows,
-                 blockIdx.x * q.tr, ps);
+// The FP4 GEMVs (dsv4_gemv_fp4_q / _pair_q / _batch_q,
+// src/dsv4/dsv4_model.c:967-1380) on the decode layer's register tiles
+// (dsv4_tiles.h): one (row, 32-column group) partial per lane as a sequential
+// fmaf chain, one lane per row chaining the groups in order; NP
+// passes per tile (paired: NP / 2 of each matrix over the same rows), every
+// pass issued before the first FMA, NP chosen by the host so that one call
+// spans about a thousand workgroups. The token's activation arrives as the
+// E4M3 grid values the activation quant produced (floats): its codes are
+// exact (e4m3_code) and go to LDS with the per-128 scales, loaded ahead of
+// the weights. grid = (tiles, nvec); pair: y[0] / y[1] for W[0] / W[1].
+template <int NP>
+__global__ __launch_bounds__(256) void k_gemv_fp4_t(GemvArgs a, int pair) {
+  extern __shared__ __align__(16) float lds[];
+  __shared__ float s_y[256];
+  const int tid = threadIdx.x, b = blockIdx.y;
+  const Fp4Geom q = fp4_geom_np(a.in, NP);
+  const int in = a.in;
+  const float *qx = a.qx + (size_t)b * a.qx_stride;
+  const float *qs = a.qscale + (size_t)b * a.qs_stride;
+  // this thread's activation values (16 at 16 tid, and 4096 further for
+  // in > 4096), loaded before the weights
+  const BufRsrc rx = buf_rsrc(qx, 4u * (uint32_t)in);
+  uint4 xv[8];
+#pragma unroll
+  for (int k = 0; k < 2; ++k)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      xv[4 * k + i] = buf_load16(rx, 4u * (uint32_t)(16 * tid + 4096 * k) + 16u * i);
+  Fp4RegsT<NP> R;
+  const int half = q.tr / 2;
+  const int r0 = pair ? blockIdx.x * half : blockIdx.x * q.tr;
+  if (pair)
+    fp4_pair_load(R, a.W[0], a.S[0], a.W[1], a.S[1], in, a.rows, r0, q);
+  else
+    fp4_tile_load(R, a.W[0], a.S[0], in, a.rows, r0, q);
+  uint8_t *cl = reinterpret_cast<uint8_t *>(lds) + (size_t)q.tr * pair_stride(q.G) * 8;
+  uint8_t *x8 = cl + 4096;
+  float *xs = reinterpret_cast<float *>(x8 + ((in + 15) & ~15));
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int base = 16 * tid + 4096 * k;
+    if (base < in) {
+      uint32_t c[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint4 v = xv[4 * k + i];
+        c[i] = e4m3_code(u2f(v.x)) | (e4m3_code(u2f(v.y)) << 8) |
+               (e4m3_code(u2f(v.z)) << 16) | (e4m3_code(u2f(v.w)) << 24);
+      }
+      *reinterpret_cast<uint4 *>(x8 + base) = make_uint4(c[0], c[1], c[2], c[3]);
+    }
+  }
+  for (int i = tid; i < (in + 127) / 128; i += 256) xs[i] = qs[i];
+  __syncthreads();
+  fp4_tile_x_lds(R, x8, xs, q);
+  float2 *ps = reinterpret_cast<float2 *>(lds);
+  if (pair) {
+    fp4_pair_finish(R, s_y, a.rows, r0, q, ps, cl);
+    __syncthreads();
+    if (tid < q.tr && r0 + tid % half < a.rows)
+      a.y[tid / half][(size_t)b * a.y_stride + r0 + tid % half] = s_y[tid];
+  } else {
+    fp4_tile_finish(R, a.y[0] + (size_t)b * a.y_stride, a.rows, r0, q, ps, cl);
+  }
 }
 
 __global__ __launch_bounds__(256) void k_gemv_fp8(GemvArgs a) {
@@ -126,6 +181,201 @@ __global__ __launch_bounds__(64) void k_gemv_bf16(float *__restrict__ y,
   }
   for (; c < in; ++c) acc = fmaf(bf16_to_f32(wr[c]), xb[c], acc);
   y[(size_t)b * y_stride + row] = round_out ? bf16_round(acc) : acc;
+}
+
+// ====================================================== row chains =====
+// The same chains, one lane per output row, for rows whose bytes are a
+// multiple of 16: each lane reads its own row straight from HBM 16 bytes at
+// a time through one buffer range over the wave's 64 rows (a row past the
+// matrix reads zeros), 16 loads per chunk and two chunks in turn, so 32
+// loads (512 bytes of the row) are in flight while a chunk is chained; x
+// (every token, at most RC_XBYTES) and the FP8 block scales of the wave's
+// row blocks are staged in LDS once and read as broadcasts. The per-column arithmetic is the reference's, so the results
+// are bit for bit those of the one-load-at-a-time kernels above; they only
+// wait less.
+//   RC_BF16: acc_t = fmaf(bf16(w), x_t[c], acc_t) for MAXB tokens at most
+//            (dsv4_gemv_bf16(_batch), src/dsv4/dsv4_model.c:266-367; the vocab
+//            head's head_logits_block, :7221-7255);
+//   RC_FP8_X: acc += w * (x * s)   (dsv4_gemv_fp8, src/dsv4/dsv4_ops.c:176-209);
+//   RC_FP8_XS: the same when the wave's 64 rows share one row block (block a
+//            multiple of 64): xs = x * s is formed once per column in LDS,
+//            as the reference forms it once per row block;
+//   RC_FP8_T: acc += (w * x) * s   (dsv4_gemv_fp8_tbl, :216-239),
+// unfused as the reference is built; s = wscale[row / block][c / block],
+// block a multiple of 16.
+#define RC_BF16 0
+#define RC_FP8_X 1
+#define RC_FP8_T 2
+#define RC_FP8_XS 3
+#define RC_CHUNK 16           // 16-byte loads per chunk
+#define RC_XBYTES (64 * 1024)  // LDS for x
+
+struct RowChainArgs {
+  float *y;
+  const float *x;
+  const uint8_t *W;
+  const float *wscale;
+  int in, rows, block, batch, round_out;
+  size_t y_stride, x_stride;
+};
+
+// Pieces byte0, byte0 + 16, ... of the lane's row (at row_off in the
+// wave's range; live: the lane has a row). Past the row, or without one:
+// zeros, nothing read.
+__device__ __forceinline__ void rc_load(uint4 (&w)[RC_CHUNK], BufRsrc r, uint32_t row_off,
+                                        bool live, uint32_t byte0, uint32_t rb) {
+#pragma unroll
+  for (int i = 0; i < RC_CHUNK; ++i) {
+    const uint32_t b = byte0 + 16u * i;
+    w[i] = buf_load16(r, live && b < rb ? row_off + b : 0xFFFFFFF0u);
+  }
+}
+
+// One chunk: columns c0 .. of the 16-byte pieces w (8 BF16 or 16 FP8 each);
+// xs: x in LDS, token t at t * in.
+template <int KIND, int MAXB>
+__device__ __forceinline__ void rc_chain(const RowChainArgs &a, const uint4 (&w)[RC_CHUNK],
+                                         int c0, float (&acc)[MAXB], const float *srow,
+                                         const float *xs) {
+  constexpr int CPP = KIND == RC_BF16 ? 8 : 16;  // columns per piece
+#pragma unroll
+  for (int i = 0; i < RC_CHUNK; ++i) {
+    const int c = c0 + CPP * i;
+    if (c >= a.in) break;  // uniform: the chunk's last pieces may lie past the row
+    const uint32_t wd[4] = {w[i].x, w[i].y, w[i].z, w[i].w};
+    if (KIND == RC_BF16) {
+#pragma unroll
+      for (int t = 0; t < MAXB; ++t) {
+        if (t >= a.batch) break;
+        const float4 *xt = reinterpret_cast<const float4 *>(xs + (size_t)t * a.in + c);
+        const float4 x0 = xt[0], x1 = xt[1];
+        const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          acc[t] = fmaf(u2f(wd[d] << 16), xv[2 * d], acc[t]);
+          acc[t] = fmaf(u2f(wd[d] & 0xFFFF0000u), xv[2 * d + 1], acc[t]);
+        }
+      }
+    } else if (KIND == RC_FP8_XS) {
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const float2 lo = fp8x2<false>(wd[d]), hi = fp8x2<true>(wd[d]);
+        const float wv[4] = {lo.x, lo.y, hi.x, hi.y};
+        const float4 x4 = *reinterpret_cast<const float4 *>(xs + c + 4 * d);
+        const float xv[4] = {x4.x, x4.y, x4.z, x4.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[0] += wv[e] * xv[e];
+      }
+    } else {
+      const float s = srow[c / a.block];
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const float2 lo = fp8x2<false>(wd[d]), hi = fp8x2<true>(wd[d]);
+        const float wv[4] = {lo.x, lo.y, hi.x, hi.y};
+        const float4 x4 = *reinterpret_cast<const float4 *>(xs + c + 4 * d);
+        const float xv[4] = {x4.x, x4.y, x4.z, x4.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          acc[0] += KIND == RC_FP8_X ? wv[e] * (xv[e] * s) : (wv[e] * xv[e]) * s;
+      }
+    }
+  }
+}
+
+template <int KIND, int MAXB>
+__global__ __launch_bounds__(64) void k_rowchain(RowChainArgs a) {
+  extern __shared__ __align__(16) float xs[];  // batch * in floats
+  const int r0 = blockIdx.x * 64, lane = threadIdx.x, row = r0 + lane;
+  for (int t = 0; t < a.batch; ++t)
+    for (int i = lane; i < a.in / 4; i += 64)
+      reinterpret_cast<float4 *>(xs + (size_t)t * a.in)[i] =
+          reinterpret_cast<const float4 *>(a.x + (size_t)t * a.x_stride)[i];
+  const uint32_t rb = (uint32_t)a.in * (KIND == RC_BF16 ? 2u : 1u);
+  const int nrow = min(64, a.rows - r0);
+  const BufRsrc r = buf_rsrc(a.W + (size_t)r0 * rb, (uint32_t)nrow * rb);
+  const bool live = lane < nrow;
+  const uint32_t row_off = (uint32_t)lane * rb;
+  const float *srow = nullptr;
+  if (KIND == RC_FP8_XS) {
+    // xs[c] = x[c] * s[row block][c / block], the row block of all 64 rows
+    const int cblocks = (a.in + a.block - 1) / a.block;
+    const float *s = a.wscale + (size_t)(r0 / a.block) * cblocks;
+    __syncthreads();  // x in LDS
+    for (int i = lane; i < a.in; i += 64) xs[i] = xs[i] * s[i / a.block];
+  } else if (KIND != RC_BF16) {
+    // the block scales of the wave's row blocks, after x in LDS
+    const int cblocks = (a.in + a.block - 1) / a.block;
+    const int rb0 = r0 / a.block, nrb = (min(r0 + 63, a.rows - 1)) / a.block - rb0 + 1;
+    float *sc = xs + (size_t)a.batch * a.in;
+    for (int i = lane; i < nrb * cblocks; i += 64)
+      sc[i] = a.wscale[(size_t)rb0 * cblocks + i];
+    srow = sc + (size_t)(min(row, a.rows - 1) / a.block - rb0) * cblocks;
+  }
+  float acc[MAXB];
+#pragma unroll
+  for (int t = 0; t < MAXB; ++t) acc[t] = 0.0f;
+  constexpr uint32_t CB = 16u * RC_CHUNK;  // bytes per chunk
+  constexpr int CPC = (KIND == RC_BF16 ? 8 : 16) * RC_CHUNK;  // columns per chunk
+  uint4 A[RC_CHUNK], B[RC_CHUNK];
+  rc_load(A, r, row_off, live, 0, rb);
+  __syncthreads();  // x in LDS
+  for (uint32_t b0 = 0; b0 < rb; b0 += 2 * CB) {
+    const int c0 = (int)(b0 / CB) * CPC;
+    rc_load(B, r, row_off, live, b0 + CB, rb);
+    rc_chain<KIND, MAXB>(a, A, c0, acc, srow, xs);
+    rc_load(A, r, row_off, live, b0 + 2 * CB, rb);
+    rc_chain<KIND, MAXB>(a, B, c0 + CPC, acc, srow, xs);
+  }
+  if (row >= a.rows) return;
+#pragma unroll
+  for (int t = 0; t < MAXB; ++t) {
+    if (t >= a.batch) break;
+    a.y[(size_t)t * a.y_stride + row] = a.round_out ? bf16_round(acc[t]) : acc[t];
+  }
+}
+
+// ======================================================= greedy pick ===
+// The CLI's greedy token (src/cli/dsv4_run.c:357-359): best = 0, then every
+// v with logits[v] > logits[best] in order; so the first index of the
+// largest value, NaNs never taken, and 0 when logits[0] is NaN. One
+// workgroup per row: each thread keeps its first largest non-NaN value of
+// v = tid, tid + 256, ..., then (value, index) pairs merge with the larger
+// value, or the smaller index on equal values.
+__device__ __forceinline__ void am_merge(float &bv, int &bi, float ov, int oi) {
+  if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) {
+    bv = ov;
+    bi = oi;
+  }
+}
+
+__global__ __launch_bounds__(256) void k_argmax(int *idx, const float *logits, int vocab,
+                                                size_t stride) {
+  __shared__ float s_v[4];
+  __shared__ int s_i[4];
+  const int tid = threadIdx.x;
+  const float *l = logits + (size_t)blockIdx.x * stride;
+  float bv = 0.0f;
+  int bi = -1;
+  for (int v = tid; v < vocab; v += 256) {
+    const float f = l[v];
+    if (f == f && (bi < 0 || f > bv)) {
+      bv = f;
+      bi = v;
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1)
+    am_merge(bv, bi, __shfl_xor(bv, o, 64), __shfl_xor(bi, o, 64));
+  if (tid % 64 == 0) {
+    s_v[tid / 64] = bv;
+    s_i[tid / 64] = bi;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < 4; ++w) am_merge(bv, bi, s_v[w], s_i[w]);
+    const float f0 = l[0];
+    idx[blockIdx.x] = (f0 != f0 || bi < 0) ? 0 : bi;
+  }
 }
 
 // ============================================= public float-scale GEMVs ===
@@ -280,6 +530,16 @@ __global__ __launch_bounds__(256) void k_quant_fp8_blocks(uint8_t *__restrict__ 
 // ============================================================ C-ABI =====
 using namespace dsv4;
 
+template <int NP>
+static void launch_fp4_t(const GemvArgs *a, int nvec, int pair, hipStream_t st) {
+  const Fp4Geom q = fp4_geom_np(a->in, NP);
+  const int span = pair ? q.tr / 2 : q.tr;
+  const dim3 grid((unsigned)((a->rows + span - 1) / span), (unsigned)nvec);
+  const size_t lds = (size_t)q.tr * pair_stride(q.G) * 8 + 4096 + ((a->in + 15) & ~15) +
+                     (size_t)((a->in + 127) / 128) * 4;
+  hipLaunchKernelGGL(k_gemv_fp4_t<NP>, grid, dim3(256), lds, st, *a, pair);
+}
+
 extern "C" {
 
 int dsv4g_quant_fp8_act(float *qx, float *qscale, const float *x, int n, int nvec,
@@ -330,12 +590,23 @@ static int fp8_shape_ok(int in, const char *who) {
 int dsv4g_launch_gemv_fp4(const GemvArgs *a, int nvec, int nmat, void *stream) {
   if (fp4_shape_ok(a->in, "gemv_fp4")) return DSV4G_EINVAL;
   if (a->rows <= 0 || nvec <= 0) return dsv4g_fail(DSV4G_EINVAL, "gemv_fp4: bad size");
-  int G = a->in / 32, gp = 1;
-  while (gp < G) gp <<= 1;
-  int tr = FP4_LDS_ENTRIES / gp;
-  if (tr > 256) tr = 256;
-  dim3 grid((a->rows + tr - 1) / tr, nvec, nmat);
-  hipLaunchKernelGGL(k_gemv_fp4, grid, dim3(256), 0, (hipStream_t)stream, *a);
+  hipStream_t st = (hipStream_t)stream;
+  // passes per tile: the most that still give about 1024 workgroups (paired
+  // tiles hold at least one pass of each matrix)
+  const int pair = nmat == 2;
+  int np = 16;
+  while (np > (pair ? 2 : 1)) {
+    const int tr = fp4_geom_np(a->in, np).tr, span = pair ? tr / 2 : tr;
+    if ((long)((a->rows + span - 1) / span) * nvec >= 1024) break;
+    np /= 2;
+  }
+  switch (np) {
+    case 1: launch_fp4_t<1>(a, nvec, pair, st); break;
+    case 2: launch_fp4_t<2>(a, nvec, pair, st); break;
+    case 4: launch_fp4_t<4>(a, nvec, pair, st); break;
+    case 8: launch_fp4_t<8>(a, nvec, pair, st); break;
+    default: launch_fp4_t<16>(a, nvec, pair, st); break;
+  }
   return dsv4g_check_launch("gemv_fp4");
 }
 
@@ -450,16 +721,70 @@ int dsv4g_gemv_fp8_batch_q(float *y, const float *qx, const float *qscale, int b
 int dsv4g_gemv_bf16(float *y, const float *x, const uint16_t *W, int in, int out,
                     int round_out, int batch, void *stream) {
   if (in <= 0 || out <= 0 || batch <= 0) return dsv4g_fail(DSV4G_EINVAL, "gemv_bf16: bad size");
+  const size_t xb = (size_t)batch * in * 4;
+  if (in % 8 == 0 && xb <= RC_XBYTES && (size_t)64 * in * 2 < 0xFFFF0000u &&
+      ((uintptr_t)x & 15) == 0) {
+    RowChainArgs a = {};
+    a.y = y;
+    a.x = x;
+    a.W = reinterpret_cast<const uint8_t *>(W);
+    a.in = in;
+    a.rows = out;
+    a.batch = batch;
+    a.round_out = round_out;
+    a.y_stride = (size_t)out;
+    a.x_stride = (size_t)in;
+    const dim3 grid((out + 63) / 64);
+    if (batch == 1)
+      hipLaunchKernelGGL((k_rowchain<RC_BF16, 1>), grid, dim3(64), xb, (hipStream_t)stream, a);
+    else if (batch <= 4)
+      hipLaunchKernelGGL((k_rowchain<RC_BF16, 4>), grid, dim3(64), xb, (hipStream_t)stream, a);
+    else if (batch <= 8)
+      hipLaunchKernelGGL((k_rowchain<RC_BF16, 8>), grid, dim3(64), xb, (hipStream_t)stream, a);
+    else
+      hipLaunchKernelGGL((k_rowchain<RC_BF16, 33>), grid, dim3(64), xb, (hipStream_t)stream, a);
+    return dsv4g_check_launch("gemv_bf16");
+  }
   dim3 grid((out + 63) / 64, batch);
   hipLaunchKernelGGL(k_gemv_bf16, grid, dim3(64), 0, (hipStream_t)stream, y, x, W, in, out,
                      round_out, (size_t)out, (size_t)in);
   return dsv4g_check_launch("gemv_bf16");
 }
 
+int dsv4g_argmax(int *idx, const float *logits, int vocab, int n, size_t stride,
+                 void *stream) {
+  if (!idx || !logits || vocab <= 0 || n <= 0 || stride < (size_t)vocab)
+    return dsv4g_fail(DSV4G_EINVAL, "argmax: bad arguments");
+  hipLaunchKernelGGL(k_argmax, dim3((unsigned)n), dim3(256), 0, (hipStream_t)stream, idx,
+                     logits, vocab, stride);
+  return dsv4g_check_launch("argmax");
+}
+
 int dsv4g_gemv_fp8_float(float *y, const float *x, const uint8_t *W, const float *wscale,
                          int in, int rows, int block, int mode, void *stream) {
   if (in <= 0 || rows <= 0 || block <= 0)
     return dsv4g_fail(DSV4G_EINVAL, "gemv_fp8_float: bad size");
+  if (in % 16 == 0 && block % 16 == 0 && (size_t)in * 4 * 2 <= RC_XBYTES &&
+      ((uintptr_t)x & 15) == 0) {
+    RowChainArgs a = {};
+    a.y = y;
+    a.x = x;
+    a.W = W;
+    a.wscale = wscale;
+    a.in = in;
+    a.rows = rows;
+    a.block = block;
+    a.batch = 1;
+    const dim3 grid((rows + 63) / 64);
+    const size_t xb = (size_t)in * 4 + (size_t)(64 / block + 2) * ((in + block - 1) / block) * 4;
+    if (mode == 0 && block % 64 == 0)
+      hipLaunchKernelGGL((k_rowchain<RC_FP8_XS, 1>), grid, dim3(64), xb, (hipStream_t)stream, a);
+    else if (mode == 0)
+      hipLaunchKernelGGL((k_rowchain<RC_FP8_X, 1>), grid, dim3(64), xb, (hipStream_t)stream, a);
+    else
+      hipLaunchKernelGGL((k_rowchain<RC_FP8_T, 1>), grid, dim3(64), xb, (hipStream_t)stream, a);
+    return dsv4g_check_launch("gemv_fp8_float");
+  }
   hipLaunchKernelGGL(k_gemv_fp8_float, dim3((rows + 63) / 64), dim3(64), 0,
                      (hipStream_t)stream, y, x, W, wscale, in, rows, block, mode);
   return dsv4g_check_launch("gemv_fp8_float");

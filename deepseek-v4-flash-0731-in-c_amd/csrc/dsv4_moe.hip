@@ -314,6 +314,37 @@ int dsv4g_router_public(int *idx, float *wt, const float *x, const uint16_t *gat
   return dsv4g_check_launch("router_select");
 }
 
+size_t dsv4g_expert_workspace_bytes(int inter) {
+  return ((size_t)(3 * inter + (inter + 127) / 128) * 4 + 255) & ~(size_t)255;
+}
+
+// expert_forward (src/dsv4/dsv4_model.c:6289-6345) as the reference composes
+// it: the paired FP4 gate/up GEMV, routed_swiglu_quant and the FP4 down GEMV,
+// three launches on the stream; the slot layout of expert_forward_l1/_l2
+// (scales [s1 | s2 | s3] at slot, weights [w1 | w2 | w3] at slot + scale_run).
+int dsv4g_expert_forward(float *out, const float *qx, const float *qscale, const uint8_t *slot,
+                         size_t scale_run, int hidden, int inter, float swiglu_limit,
+                         const float *weight, void *workspace, size_t workspace_bytes,
+                         void *stream) {
+  if (!out || !qx || !qscale || !slot || hidden <= 0 || inter <= 0 || inter % 128 ||
+      hidden % 32)
+    return dsv4g_fail(DSV4G_EINVAL, "expert_forward: bad arguments");
+  if (!workspace || workspace_bytes < dsv4g_expert_workspace_bytes(inter) ||
+      ((uintptr_t)workspace & 255))
+    return dsv4g_fail(DSV4G_EINVAL, "expert_forward: workspace too small or unaligned");
+  const size_t H = (size_t)hidden, I = (size_t)inter;
+  const uint8_t *sc = slot, *wt = slot + scale_run;
+  const uint8_t *w1 = wt, *w2 = wt + I * (H / 2), *w3 = w2 + H * (I / 2);
+  const uint8_t *s1 = sc, *s2 = sc + I * (H / 32), *s3 = s2 + H * (I / 32);
+  float *ws = (float *)workspace;
+  float *gate = ws, *up = ws + I, *qy = ws + 2 * I, *qys = ws + 3 * I;
+  DSV4G_TRY(dsv4g_gemv_fp4_pair_q(gate, up, qx, qscale, w1, s1, w3, s3, hidden, inter, stream));
+  // the reference passes the limit as int (src/dsv4/dsv4_model.c:6297)
+  DSV4G_TRY(dsv4g_swiglu_quant(qy, qys, gate, weight, 0, 1, inter, (float)(int)swiglu_limit,
+                               stream));
+  return dsv4g_gemv_fp4_q(out, qy, qys, w2, s2, inter, hidden, stream);
+}
+
 int dsv4g_swiglu_quant(float *qy, float *qys, const float *gate_up, const float *wt, int K,
                        int n_slots, int inter, float limit, void *stream) {
   if (inter <= 0 || inter % 128 || n_slots <= 0 || K < 0)

@@ -104,76 +104,6 @@ __device__ __forceinline__ float pair_chain(const float2 *pr, int n) {
 // 16-byte reads by consecutive lanes fall in distinct banks.
 __device__ __host__ __forceinline__ int pair_stride(int n) { return (n | 1) + 1; }
 
-// Rows [r0, r0 + tr) of y = bf16(W . qx) (FP4, per-32 E8M0 scales).
-// ps: LDS scratch of FP4_LDS_ENTRIES + tr float2.
-__device__ inline void fp4_rows_exact(float *__restrict__ y, const float *__restrict__ qx,
-                               const float *__restrict__ qscale,
-                               const uint8_t *__restrict__ W, const uint8_t *__restrict__ S,
-                               int in, int rows, int r0, float2 *ps) {
-  const Fp4Geom q = fp4_geom(in);
-  const int t = threadIdx.x;
-  const int g = t % q.gp, rsub = t / q.gp;
-  const bool gact = g < q.G;
-  const size_t pcols = (size_t)in / 2;
-  const int stride = q.G + 1;  // padded LDS row: conflict-free chain reads
-  float xq[32];
-  float as = 0.0f;
-  if (gact) {
-    const float4 *xp = reinterpret_cast<const float4 *>(qx + 32 * g);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float4 v = xp[i];
-      xq[4 * i] = v.x;
-      xq[4 * i + 1] = v.y;
-      xq[4 * i + 2] = v.z;
-      xq[4 * i + 3] = v.w;
-    }
-    as = qscale[g / 4];
-  }
-  const int npass = q.tr / q.rpp;
-  constexpr int U = 4;
-  for (int p0 = 0; p0 < npass; p0 += U) {
-    uint4 w[U];
-    uint32_t code[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int lr = (p0 + u) * q.rpp + rsub;
-      const int row = r0 + lr;
-      if (gact && p0 + u < npass && row < rows) {
-        w[u] = *reinterpret_cast<const uint4 *>(W + (size_t)row * pcols + 16 * g);
-        code[u] = S[(size_t)row * q.G + g];
-      } else {
-        w[u] = make_uint4(0, 0, 0, 0);
-        code[u] = 127;
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int lr = (p0 + u) * q.rpp + rsub;
-      if (gact && p0 + u < npass && r0 + lr < rows) {
-        float part = fp4_group_partial(w[u], xq);
-        float s = as * e8m0(code[u]);
-        if (code[u] == 255u) {  // NaN scale: the reference skips the group
-          part = 0.0f;
-          s = 0.0f;
-        }
-        ps[lr * stride + g] = make_float2(part, s);
-      }
-    }
-  }
-  __syncthreads();
-  if (t < q.tr && r0 + t < rows) {
-    const float2 *pr = ps + t * stride;
-    float acc = 0.0f;
-    for (int gg = 0; gg < q.G; ++gg) {
-      const float2 v = pr[gg];
-      acc = fmaf(v.x, v.y, acc);
-    }
-    y[r0 + t] = bf16_round(acc);
-  }
-}
-
-
 // ===================================================== FP8 exact GEMV ====
 // One workgroup owns FP8_TR rows. Lane t = (row t / 16, block slot t % 16);
 // slot j handles 128-column blocks j, j+16, ... Each block partial is a
@@ -330,10 +260,14 @@ __device__ __forceinline__ void fp4_partials4(const Fp4RegsT<NP> &R, int u0, flo
   const uint32_t *x8 = R.x8;
 #pragma unroll
   for (int i = 0; i < 4; ++i) p[i] = 0.0f;
+  // tiles of fewer than four passes repeat their last pass (its extra
+  // partials are never stored)
+  const int u1 = u0 + 1 < NP ? u0 + 1 : NP - 1, u2 = u0 + 2 < NP ? u0 + 2 : NP - 1;
+  const int u3 = u0 + 3 < NP ? u0 + 3 : NP - 1;
 #pragma unroll
   for (int d = 0; d < 4; ++d) {
-    const uint32_t wd[4] = {u4_word(R.w[u0], d), u4_word(R.w[u0 + 1], d),
-                            u4_word(R.w[u0 + 2], d), u4_word(R.w[u0 + 3], d)};
+    const uint32_t wd[4] = {u4_word(R.w[u0], d), u4_word(R.w[u1], d), u4_word(R.w[u2], d),
+                            u4_word(R.w[u3], d)};
     // columns 8d .. 8d + 7: codes in bytes of x8[2d] and x8[2d + 1]
     const float2 x01 = fp8x2<false>(x8[2 * d]), x23 = fp8x2<true>(x8[2 * d]);
     const float2 x45 = fp8x2<false>(x8[2 * d + 1]), x67 = fp8x2<true>(x8[2 * d + 1]);

@@ -51,6 +51,9 @@ _SIGS = {
     "dsv4g_router_public": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _I, _I, _I, _I, _F, _vp, _vp,
                             _vp],
     "dsv4g_swiglu_quant": [_vp, _vp, _vp, _vp, _I, _I, _I, _F, _vp],
+    "dsv4g_argmax": [_vp, _vp, _I, _I, C.c_size_t, _vp],
+    "dsv4g_expert_forward": [_vp, _vp, _vp, _vp, C.c_size_t, _I, _I, _F, _vp, _vp, C.c_size_t,
+                             _vp],
     "dsv4g_moe_forward": [_vp, _vp, C.POINTER(DSV4GLayer), _vp, _I, _vp, _Z, _vp, _vp, _vp],
     "dsv4g_moe_forward_fast": [_vp, _vp, C.POINTER(DSV4GLayer), _vp, _I, _vp, _Z, _vp, _vp, _vp],
     "dsv4g_moe_decode_phase": [_I, _vp, _vp, C.POINTER(DSV4GLayer), _vp, _I, _vp, _Z, _vp],
@@ -184,6 +187,38 @@ class GpuLib:
         self._call("dsv4g_gemv_bf16", _ptr(y), _ptr(x), _ptr(W), in_, out, round_out, b,
                    self._stream())
         return y
+
+    def gemv_bf16_into(self, y, x, W, in_, out, round_out=0):
+        """dsv4g_gemv_bf16 into a caller's y [batch][out] (no allocation)."""
+        self._call("dsv4g_gemv_bf16", _ptr(y), _ptr(x), _ptr(W), in_, out, round_out,
+                   x.numel() // in_, self._stream())
+        return y
+
+    def argmax(self, logits, idx=None):
+        """dsv4g_argmax over the rows of logits [n][vocab] (int32 [n])."""
+        import torch
+        n, vocab = (1, logits.shape[0]) if logits.dim() == 1 else logits.shape
+        idx = torch.empty(n, dtype=torch.int32, device=logits.device) if idx is None else idx
+        self._call("dsv4g_argmax", _ptr(idx), _ptr(logits), vocab, n, vocab, self._stream())
+        return idx
+
+    def expert_workspace_bytes(self, inter):
+        self.lib.dsv4g_expert_workspace_bytes.restype = C.c_size_t
+        self.lib.dsv4g_expert_workspace_bytes.argtypes = [_I]
+        return int(self.lib.dsv4g_expert_workspace_bytes(inter))
+
+    def expert_forward(self, out, qx, qs, slot, scale_run, hidden, inter, limit, weight=None,
+                       workspace=None):
+        """dsv4g_expert_forward: out [hidden] from one expert slot (uint8, the
+        checkpoint layout) at one token."""
+        import torch
+        need = self.expert_workspace_bytes(inter)
+        if workspace is None:
+            workspace = torch.empty(need, dtype=torch.uint8, device=qx.device)
+        self._call("dsv4g_expert_forward", _ptr(out), _ptr(qx), _ptr(qs), _ptr(slot),
+                   int(scale_run), hidden, inter, float(limit), _ptr(weight), _ptr(workspace),
+                   workspace.numel(), self._stream())
+        return out
 
     def gemv_fp8_float(self, x, W, wscale, in_, rows, block=128, mode=0, y=None):
         import torch

@@ -115,9 +115,18 @@ int dsv4g_gemv_fp8_pair_q(float *y0, float *y1, const float *qx, const float *qs
 int dsv4g_gemv_fp8_batch_q(float *y, const float *qx, const float *qscale, int batch,
                            const uint8_t *W, const uint8_t *S, int in, int out,
                            int round_out, void *stream);
-/* dsv4_gemv_bf16 / _batch (src/dsv4/dsv4_internal.h:256-259); x [batch][in]. */
+/* dsv4_gemv_bf16 / _batch (src/dsv4/dsv4_internal.h:256-259); x [batch][in]
+ * (16-byte aligned for the streaming kernel). The vocabulary head
+ * (head_logits / head_logits_batch, src/dsv4/dsv4_model.c:7314-7445: the same
+ * per-row fmaf chain, logits unrounded) is this call with in = hidden,
+ * out = vocab, round_out = 0. */
 int dsv4g_gemv_bf16(float *y, const float *x, const uint16_t *W, int in, int out,
                     int round_out, int batch, void *stream);
+/* The greedy token of each of n rows of logits (row r at logits + r * stride):
+ * the CLI's first-largest rule (src/cli/dsv4_run.c:357-359), NaN never taken,
+ * 0 when logits[0] is NaN. idx [n], device. */
+int dsv4g_argmax(int *idx, const float *logits, int vocab, int n, size_t stride,
+                 void *stream);
 /* dsv4_gemv_fp8 (mode 0) / dsv4_gemv_fp8_tbl (mode 1) (include/dsv4/dsv4.h:200-206)
  * and dsv4_gemv_fp4 (include/dsv4/dsv4.h:208-211), float block scales. */
 int dsv4g_gemv_fp8_float(float *y, const float *x, const uint8_t *W, const float *wscale,
@@ -138,6 +147,18 @@ int dsv4g_router_public(int *idx, float *wt, const float *x, const uint16_t *gat
                         const float *bias, const int64_t *tid2eid, const int *token_id,
                         int hidden, int n_experts, int topk, int hash_layer,
                         float route_scale, float *z_ws, float *zabs_ws, void *stream);
+/* expert_forward (src/dsv4/dsv4_model.c:6289-6345) for one token: out [hidden]
+ * = the BF16-rounded FP4 down GEMV of routed_swiglu_quant(gate, up) of the
+ * paired FP4 gate/up GEMV of qx / qscale (from dsv4g_quant_fp8_act). slot: one
+ * expert in the checkpoint layout (scales [s1|s2|s3], then scale_run bytes on
+ * the weights [w1|w2|w3]); weight: device pointer to the route weight, NULL
+ * for 1. workspace: dsv4g_expert_workspace_bytes(inter) bytes, 256-aligned.
+ * Three launches on the stream. */
+size_t dsv4g_expert_workspace_bytes(int inter);
+int dsv4g_expert_forward(float *out, const float *qx, const float *qscale, const uint8_t *slot,
+                         size_t scale_run, int hidden, int inter, float swiglu_limit,
+                         const float *weight, void *workspace, size_t workspace_bytes,
+                         void *stream);
 /* routed_swiglu_quant (src/dsv4/dsv4_model.c:6239-6287) over n_slots slots;
  * slot s reads gate at gate_up + 2*s*inter and up right after it. Weights:
  * K > 0: slots are [token][K+1], slot (t,k<K) uses wt[t*K+k], slot K uses 1;
