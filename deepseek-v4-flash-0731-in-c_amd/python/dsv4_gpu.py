@@ -93,6 +93,7 @@ class GpuLib:
             fn = getattr(lib, name)
             fn.argtypes = args
             fn.restype = C.c_int
+        _st_sigs(lib)
 
     # ---- plumbing
     def _call(self, name, *args):
@@ -414,6 +415,151 @@ class DeviceLayer:
         meta = {k: layer[k] for k in ("hidden", "inter", "n_experts", "topk", "route_scale",
                                       "swiglu_limit", "expert_stride", "scale_run")}
         return cls(t, meta)
+
+
+class StTensor(C.Structure):
+    """Mirror of DSV4GTensor (include/dsv4_gpu.h)."""
+
+    _fields_ = [("name", C.c_char_p), ("shard", C.c_int), ("dtype", C.c_int),
+                ("ndim", C.c_int), ("shape", C.c_int64 * 4), ("off", C.c_int64),
+                ("nbytes", C.c_int64)]
+
+    def as_dict(self):
+        return dict(name=self.name.decode("latin-1"), shard=self.shard, dtype=self.dtype,
+                    shape=tuple(self.shape[:self.ndim]), off=self.off, nbytes=self.nbytes)
+
+
+DTYPE_CODES = {"U8": 1, "BF16": 2, "F16": 3, "F32": 4, "I8": 5, "I64": 6, "F8_E4M3": 7,
+               "F8_E8M0": 8}
+
+
+def _st_sigs(lib):
+    sp = C.POINTER(StTensor)
+    for name, res, args in [
+            ("dsv4g_st_open", C.c_int, [C.POINTER(_vp), C.c_char_p]),
+            ("dsv4g_st_close", None, [_vp]),
+            ("dsv4g_st_find", sp, [_vp, C.c_char_p]),
+            ("dsv4g_st_read", C.c_int64, [_vp, sp, _vp]),
+            ("dsv4g_st_read_f32", C.c_int64, [_vp, sp, _vp]),
+            ("dsv4g_st_read_range", C.c_int64, [_vp, C.c_int, C.c_int64, C.c_int64, _vp]),
+            ("dsv4g_st_numel", C.c_int64, [sp]),
+            ("dsv4g_st_elemsize", C.c_int, [C.c_int]),
+            ("dsv4g_st_count", C.c_int, [_vp]),
+            ("dsv4g_st_tensor", sp, [_vp, C.c_int]),
+            ("dsv4g_st_nshard", C.c_int, [_vp]),
+            ("dsv4g_st_shard_path", C.c_char_p, [_vp, C.c_int]),
+            ("dsv4g_st_dtype_name", C.c_char_p, [C.c_int]),
+            ("dsv4g_st_upload", C.c_int, [_vp, sp, _vp, _vp]),
+            ("dsv4g_moe_layer_bytes", C.c_size_t, [C.POINTER(DSV4GLayer), C.c_int, C.c_int]),
+            ("dsv4g_load_moe_layer", C.c_int, [C.POINTER(DSV4GLayer), _vp, C.c_size_t, _vp,
+                                               C.c_char_p, C.c_int, C.c_int, C.c_int, _vp])]:
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+
+
+class Checkpoint:
+    """A safetensors checkpoint directory indexed by dsv4g_st_open (host
+    only: opening, finding and reading touch no GPU)."""
+
+    def __init__(self, directory: str, gpu: "GpuLib | None" = None):
+        self.gl = gpu or lib()
+        self.lib = self.gl.lib
+        h = _vp()
+        rc = self.lib.dsv4g_st_open(C.byref(h), directory.encode())
+        if rc != 0:
+            raise RuntimeError(f"dsv4g_st_open: {self.lib.dsv4g_last_error().decode()}")
+        self.h = h
+
+    def close(self):
+        if self.h:
+            self.lib.dsv4g_st_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __len__(self):
+        return self.lib.dsv4g_st_count(self.h)
+
+    def nshard(self):
+        return self.lib.dsv4g_st_nshard(self.h)
+
+    def shard_path(self, i):
+        p = self.lib.dsv4g_st_shard_path(self.h, i)
+        return None if p is None else p.decode()
+
+    def tensors(self):
+        return [self.lib.dsv4g_st_tensor(self.h, i).contents.as_dict() for i in range(len(self))]
+
+    def _find(self, name):
+        return self.lib.dsv4g_st_find(self.h, name.encode("latin-1"))
+
+    def find(self, name: str):
+        t = self._find(name)
+        return t.contents.as_dict() if t else None
+
+    def read(self, name: str) -> bytes:
+        t = self._find(name)
+        if not t:
+            raise KeyError(name)
+        buf = C.create_string_buffer(max(t.contents.nbytes, 1))
+        got = self.lib.dsv4g_st_read(self.h, t, buf)
+        if got != t.contents.nbytes:
+            raise RuntimeError(f"dsv4g_st_read: {self.lib.dsv4g_last_error().decode()}")
+        return buf.raw[:got]
+
+    def read_f32(self, name: str):
+        import numpy as np
+        t = self._find(name)
+        if not t:
+            raise KeyError(name)
+        n = int(self.lib.dsv4g_st_numel(t))
+        out = np.zeros(max(n, 1), np.float32)
+        got = self.lib.dsv4g_st_read_f32(self.h, t, out.ctypes.data_as(_vp))
+        return out[:got]
+
+    def upload(self, name: str, dst):
+        """One tensor's bytes into the device tensor dst (at least nbytes)."""
+        t = self._find(name)
+        if not t:
+            raise KeyError(name)
+        if dst.numel() * dst.element_size() < t.contents.nbytes:
+            raise ValueError("destination too small")
+        self.gl._call("dsv4g_st_upload", self.h, t, _ptr(dst), self.gl._stream())
+
+    def load_moe_layer(self, meta: dict, scope="layers", layer=0, is_hash=False, vocab=0,
+                       device="cuda"):
+        """dsv4g_load_moe_layer into a fresh device arena: a layer object
+        with .struct, .meta and .arena usable wherever a DeviceLayer is."""
+        import torch
+        L = DSV4GLayer()
+        L.hidden, L.inter = meta["hidden"], meta["inter"]
+        L.n_experts, L.topk = meta["n_experts"], meta["topk"]
+        L.route_scale, L.swiglu_limit = meta["route_scale"], meta["swiglu_limit"]
+        need = int(self.lib.dsv4g_moe_layer_bytes(C.byref(L), int(is_hash), vocab))
+        if need == 0:
+            raise RuntimeError(f"dsv4g_moe_layer_bytes: {self.lib.dsv4g_last_error().decode()}")
+        arena = torch.empty(need, dtype=torch.uint8, device=device)
+        self.gl._call("dsv4g_load_moe_layer", C.byref(L), _ptr(arena), need, self.h,
+                      scope.encode(), layer, int(is_hash), vocab, self.gl._stream())
+        return LoadedLayer(L, arena, dict(meta, expert_stride=L.expert_stride,
+                                          scale_run=L.scale_run))
+
+
+class LoadedLayer:
+    """A DSV4GLayer whose pointers point into one loader arena (kept alive)."""
+
+    def __init__(self, struct, arena, meta):
+        self.struct, self.arena, self.meta = struct, arena, meta
+
+    def offset(self, field: str) -> int:
+        """Byte offset of a DSV4GLayer pointer field inside the arena."""
+        p = getattr(self.struct, field)
+        return None if p is None else p - self.arena.data_ptr()
 
 
 _LIB = None

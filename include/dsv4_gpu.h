@@ -273,6 +273,71 @@ int dsv4g_quant_fp4_rows(uint8_t *packed, uint8_t *scales, const float *w, int r
 int dsv4g_quant_fp8_blocks(uint8_t *codes, void *scales, const float *w, int rows, int cols,
                            int mode, void *stream);
 
+/* ------------------------------------------ checkpoint index + HBM loader
+ * The safetensors index replaces the reference reader K3St
+ * (src/io/k3_st.h:34-103): k3_st_open / close / find / read / read_f32 /
+ * numel / elemsize become dsv4g_st_*, with the same dtype numbering, tensor
+ * record (absolute file offset, byte span) and validation (byte span equal to
+ * numel * elemsize, inside the file; names unique across shards; shards are
+ * the directory's *.safetensors sorted by name). k3_st_read_aligned
+ * (O_DIRECT widening for the expert cache) becomes dsv4g_st_read_range: with
+ * every expert resident in HBM there is no per-token streaming. Index calls
+ * touch no GPU. Errors: DSV4G_EIO with the message in dsv4g_last_error(). */
+#define DSV4G_EIO 3 /* checkpoint file missing, malformed or short */
+
+enum { DSV4G_DT_UNKNOWN = 0, DSV4G_DT_U8, DSV4G_DT_BF16, DSV4G_DT_F16, DSV4G_DT_F32,
+       DSV4G_DT_I8, DSV4G_DT_I64, DSV4G_DT_F8_E4M3, DSV4G_DT_F8_E8M0 };
+
+typedef struct {
+    const char *name;
+    int shard;        /* index into the sorted shard list */
+    int dtype;        /* DSV4G_DT_* */
+    int ndim;         /* 0 (scalar) .. 4 */
+    int64_t shape[4];
+    int64_t off;      /* absolute byte offset in its shard file */
+    int64_t nbytes;
+} DSV4GTensor;
+
+typedef struct DSV4GSt DSV4GSt;
+
+int dsv4g_st_open(DSV4GSt **st, const char *dir);                 /* k3_st.h:67 */
+void dsv4g_st_close(DSV4GSt *st);                                 /* k3_st.h:68 */
+const DSV4GTensor *dsv4g_st_find(const DSV4GSt *st, const char *name); /* k3_st.h:72 */
+int64_t dsv4g_st_read(const DSV4GSt *st, const DSV4GTensor *t, void *buf); /* k3_st.h:75 */
+int64_t dsv4g_st_read_f32(const DSV4GSt *st, const DSV4GTensor *t, float *out); /* k3_st.h:99 */
+int64_t dsv4g_st_numel(const DSV4GTensor *t);                     /* k3_st.h:102 */
+int dsv4g_st_elemsize(int dtype);                                 /* k3_st.h:103 */
+/* [off, off + nbytes) of a shard into buf; returns the bytes read
+ * (k3_st.h:92-93 without the O_DIRECT widening: the payload is at buf[0]). */
+int64_t dsv4g_st_read_range(const DSV4GSt *st, int shard, int64_t off, int64_t nbytes,
+                            void *buf);
+/* Iteration in discovery order (shard, then header order): K3St.t / .nt. */
+int dsv4g_st_count(const DSV4GSt *st);
+const DSV4GTensor *dsv4g_st_tensor(const DSV4GSt *st, int i);
+int dsv4g_st_nshard(const DSV4GSt *st);
+const char *dsv4g_st_shard_path(const DSV4GSt *st, int shard);
+const char *dsv4g_st_dtype_name(int dtype);
+/* One tensor's bytes into device memory dst (pinned staging; returns when
+ * the copy has completed). */
+int dsv4g_st_upload(const DSV4GSt *st, const DSV4GTensor *t, void *dst, void *stream);
+
+/* One layer's MoE weights, read from the checkpoint into one device arena in
+ * the DSV4GLayer layout: the named tensors "<scope>.<layer>.ffn.gate.weight",
+ * ".ffn.gate.bias" (or ".ffn.gate.tid2eid" when is_hash), the shared expert
+ * ".ffn.shared_experts.w{1,3,2}.{weight,scale}" and every routed expert's
+ * ".ffn.experts.<e>.w{1,2,3}.{scale,weight}", bound with the reference's
+ * checks (src/dsv4/dsv4_model.c:1587-1611, 2014-2053, 3063-3136; scope
+ * "layers" or "mtp"). On entry L holds the layer's configuration (hidden,
+ * inter, n_experts, topk, route_scale, swiglu_limit); on success its pointers
+ * point into arena. arena: device memory of at least
+ * dsv4g_moe_layer_bytes(L, is_hash, vocab) bytes (vocab: rows of tid2eid).
+ * Returns when every byte is in place. Routed expert slots are 256-byte
+ * aligned; a checkpoint with each expert's runs stored w1, w2, w3 is read in
+ * long sequential spans. */
+size_t dsv4g_moe_layer_bytes(const DSV4GLayer *shape, int is_hash, int vocab);
+int dsv4g_load_moe_layer(DSV4GLayer *L, void *arena, size_t arena_bytes, const DSV4GSt *st,
+                         const char *scope, int layer, int is_hash, int vocab, void *stream);
+
 /* -------------------------------------------- drop-in (host pointers) ----
  * Same names, argument meaning and error behaviour as the reference. */
 uint16_t dsv4_f32_to_bf16(float f);                                 /* dsv4.h:183 */

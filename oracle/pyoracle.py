@@ -482,5 +482,75 @@ class RefLib(_Base):
         return out
 
 
+class StTensor(C.Structure):
+    """Tensor record of a safetensors index: the reference's K3Tensor
+    (src/io/k3_st.h:37-45) and DSV4GTensor share this layout."""
+
+    _fields_ = [("name", C.c_char_p), ("shard", C.c_int), ("dtype", C.c_int),
+                ("ndim", C.c_int), ("shape", C.c_int64 * 4), ("off", C.c_int64),
+                ("nbytes", C.c_int64)]
+
+    def as_dict(self):
+        return dict(name=self.name.decode("latin-1"), shard=self.shard, dtype=self.dtype,
+                    shape=tuple(self.shape[:self.ndim]), off=self.off, nbytes=self.nbytes)
+
+
+class RefSt:
+    """The reference reader k3_st (compiled in oracle/_ref) over one checkpoint
+    directory: open, iterate, find, read, read_f32."""
+
+    def __init__(self, ref: "RefLib", directory: str):
+        lib = self.lib = ref.lib
+        lib.ref_shim_st_open.restype = C.c_void_p
+        lib.ref_shim_st_open.argtypes = [C.c_char_p]
+        lib.ref_shim_st_close.argtypes = [C.c_void_p]
+        lib.ref_shim_st_count.argtypes = [C.c_void_p]
+        lib.ref_shim_st_nshard.argtypes = [C.c_void_p]
+        lib.ref_shim_st_tensor.restype = C.POINTER(StTensor)
+        lib.ref_shim_st_tensor.argtypes = [C.c_void_p, C.c_int]
+        lib.k3_st_find.restype = C.POINTER(StTensor)
+        lib.k3_st_find.argtypes = [C.c_void_p, C.c_char_p]
+        lib.k3_st_read.restype = C.c_int64
+        lib.k3_st_read.argtypes = [C.c_void_p, C.POINTER(StTensor), C.c_void_p]
+        lib.k3_st_read_f32.restype = C.c_int64
+        lib.k3_st_read_f32.argtypes = [C.c_void_p, C.POINTER(StTensor), C.c_void_p]
+        self.h = lib.ref_shim_st_open(directory.encode())
+        self.ok = bool(self.h)
+
+    def close(self):
+        if self.h:
+            self.lib.ref_shim_st_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def nshard(self):
+        return self.lib.ref_shim_st_nshard(self.h)
+
+    def tensors(self):
+        return [self.lib.ref_shim_st_tensor(self.h, i).contents.as_dict()
+                for i in range(self.lib.ref_shim_st_count(self.h))]
+
+    def find(self, name: str):
+        t = self.lib.k3_st_find(self.h, name.encode("latin-1"))
+        return t.contents.as_dict() if t else None
+
+    def read(self, name: str) -> bytes:
+        t = self.lib.k3_st_find(self.h, name.encode("latin-1"))
+        buf = C.create_string_buffer(max(t.contents.nbytes, 1))
+        got = self.lib.k3_st_read(self.h, t, buf)
+        return buf.raw[:got]
+
+    def read_f32(self, name: str):
+        t = self.lib.k3_st_find(self.h, name.encode("latin-1"))
+        n = 1
+        for d in t.contents.shape[:t.contents.ndim]:
+            n *= d
+        out = np.zeros(max(n, 1), np.float32)
+        got = self.lib.k3_st_read_f32(self.h, t, out.ctypes.data_as(C.c_void_p))
+        return out[:got]
+
+
 def ref_available() -> bool:
     return os.path.exists(REF_SO)

@@ -167,3 +167,23 @@ void ref_shim_moe_forward_batch(const OrcLayer *L, const float *x,
                       NULL, out);
     ref_shim_free(&s);
 }
+
+/* The reference safetensors reader (src/io/k3_st.c:371-602) behind a heap
+ * handle, so the checker can compare the checkpoint index and its reads
+ * with it. NULL when k3_st_open fails. */
+K3St *ref_shim_st_open(const char *dir)
+{
+    K3St *s = (K3St *)calloc(1, sizeof *s);
+    if (!s) return NULL;
+    if (k3_st_open(s, dir) != 0) { free(s); return NULL; }
+    return s;
+}
+
+void ref_shim_st_close(K3St *s)
+{
+    if (s) { k3_st_close(s); free(s); }
+}
+
+int ref_shim_st_count(const K3St *s) { return s->nt; }
+int ref_shim_st_nshard(const K3St *s) { return s->nshard; }
+const K3Tensor *ref_shim_st_tensor(const K3St *s, int i) { return &s->t[i]; }
