@@ -1463,6 +1463,10 @@ int dsv4g_moe_workspace_init(void *workspace, size_t workspace_bytes, void *stre
   return dsv4g_check_launch("moe_workspace_init");
 }
 
+unsigned *dsv4g_decode_status_word(void *workspace) {
+  return (unsigned *)workspace + DEC_ERR;
+}
+
 int dsv4g_moe_decode_status(unsigned *status, void *workspace, void *stream) {
   if (!status || !workspace || ((uintptr_t)workspace & 255))
     return dsv4g_fail(DSV4G_EINVAL, "moe_decode_status: bad arguments");

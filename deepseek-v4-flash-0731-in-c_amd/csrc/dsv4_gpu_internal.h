@@ -36,6 +36,7 @@ int dsv4g_fail(int code, const char *fmt, ...);
 int dsv4g_check_launch(const char *what);
 int dsv4g_launch_gemv_fp4(const GemvArgs *a, int nvec, int nmat, void *stream);
 int dsv4g_launch_gemv_fp8(const GemvArgs *a, int nvec, int nmat, void *stream);
+unsigned *dsv4g_decode_status_word(void *workspace);
 }
 
 #define DSV4G_TRY(expr)            \

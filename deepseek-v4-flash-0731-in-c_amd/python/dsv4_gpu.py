@@ -69,6 +69,12 @@ _SIGS = {
     "dsv4g_probe_mfma": [_I, _vp, _vp, _vp, _vp, _vp, _vp],
     "dsv4g_quant_fp4_rows": [_vp, _vp, _vp, _I, _I, _vp],
     "dsv4g_quant_fp8_blocks": [_vp, _vp, _vp, _I, _I, _I, _vp],
+    "dsv4g_rmsnorm_bf16": [_vp, _vp, _vp, _I, _F, _I, _I, _vp],
+    "dsv4g_hc_split": [_vp, _vp, _vp, _vp, _vp, _vp, _I, _I, _F, _I, _vp],
+    "dsv4g_hc_pre": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _I, _I, _I, _F, _F, _I, _vp, _vp],
+    "dsv4g_hc_post": [_vp, _vp, _vp, _vp, _I, _I, _I, _vp],
+    "dsv4g_ffn_step": [_vp, _vp, _vp, _vp, _vp, C.POINTER(DSV4GLayer), _vp, _I, _I, _I, _F, _F,
+                       _vp, _Z, _vp, _vp, _vp],
 }
 
 
@@ -89,6 +95,8 @@ class GpuLib:
         lib.dsv4g_moe_workspace_bytes.argtypes = [C.POINTER(DSV4GLayer), _I]
         lib.dsv4g_moe_batch_workspace_bytes.restype = C.c_size_t
         lib.dsv4g_moe_batch_workspace_bytes.argtypes = [C.POINTER(DSV4GLayer), _I]
+        lib.dsv4g_ffn_step_workspace_bytes.restype = C.c_size_t
+        lib.dsv4g_ffn_step_workspace_bytes.argtypes = [C.POINTER(DSV4GLayer), _I, _I]
         for name, args in _SIGS.items():
             fn = getattr(lib, name)
             fn.argtypes = args
@@ -376,6 +384,73 @@ class GpuLib:
         rows, cols = w.shape
         self._call("dsv4g_quant_fp8_blocks", _ptr(codes), _ptr(scales), _ptr(w), rows, cols,
                    mode, self._stream())
+
+
+    # ---- caller step around the MoE (RMSNorm, Hyper-Connections)
+    def rmsnorm_bf16(self, x, w=None, eps=1e-6, round_out=1, out=None):
+        """Rows of x [rows][n] (w: BF16 gain bits as int16/uint16 tensor)."""
+        import torch
+        rows, n = x.shape
+        out = torch.empty_like(x) if out is None else out
+        self._call("dsv4g_rmsnorm_bf16", _ptr(out), _ptr(x), _ptr(w), n, C.c_float(eps),
+                   round_out, rows, self._stream())
+        return out
+
+    def hc_split(self, mixes, scale3, base, mult, iters=20, eps=1e-6):
+        import torch
+        n = mixes.shape[0]
+        f = dict(dtype=torch.float32, device=mixes.device)
+        pre, post = torch.empty(n, mult, **f), torch.empty(n, mult, **f)
+        comb = torch.empty(n, mult * mult, **f)
+        self._call("dsv4g_hc_split", _ptr(pre), _ptr(post), _ptr(comb), _ptr(mixes),
+                   _ptr(scale3), _ptr(base), mult, iters, C.c_float(eps), n, self._stream())
+        return pre, post, comb
+
+    def hc_pre(self, state, fn, scale3, base, mult, norm_w=None, iters=20, rms_eps=1e-6,
+               hc_eps=1e-6, status=None):
+        """state [n][mult*hid] -> bin [n][hid] (RMSNormed with norm_w),
+        post [n][mult], comb [n][mult*mult]."""
+        import torch
+        n, K = state.shape
+        hid = K // mult
+        f = dict(dtype=torch.float32, device=state.device)
+        bin_, post = torch.empty(n, hid, **f), torch.empty(n, mult, **f)
+        comb = torch.empty(n, mult * mult, **f)
+        self._call("dsv4g_hc_pre", _ptr(bin_), _ptr(post), _ptr(comb), _ptr(state), _ptr(fn),
+                   _ptr(scale3), _ptr(base), _ptr(norm_w), mult, hid, iters, C.c_float(rms_eps),
+                   C.c_float(hc_eps), n, _ptr(status), self._stream())
+        return bin_, post, comb
+
+    def hc_post(self, state, branch, post, comb, mult):
+        """In place on state [n][mult*hid]."""
+        n, K = state.shape
+        self._call("dsv4g_hc_post", _ptr(state), _ptr(branch), _ptr(post), _ptr(comb), mult,
+                   K // mult, n, self._stream())
+        return state
+
+    def ffn_step_workspace_bytes(self, layer, mult, n_tokens):
+        return int(self.lib.dsv4g_ffn_step_workspace_bytes(C.byref(layer.struct), mult,
+                                                            n_tokens))
+
+    def ffn_step(self, state, hc_fn, hc_scale, hc_base, ffn_norm, layer, mult, token_ids=None,
+                 workspace=None, iters=20, rms_eps=1e-6, hc_eps=1e-6, check=True):
+        """The FFN half of a decoder layer on state [n][mult*hid], in place.
+        Returns (state, idx, wt)."""
+        import torch
+        n = state.shape[0]
+        L = layer.struct
+        need = self.ffn_step_workspace_bytes(layer, mult, n)
+        if workspace is None or workspace.numel() < need:
+            workspace = torch.zeros(need, dtype=torch.uint8, device=state.device)
+        idx = torch.empty(n, L.topk, dtype=torch.int32, device=state.device)
+        wt = torch.empty(n, L.topk, dtype=torch.float32, device=state.device)
+        self._call("dsv4g_ffn_step", _ptr(state), _ptr(hc_fn), _ptr(hc_scale), _ptr(hc_base),
+                   _ptr(ffn_norm), C.byref(L), _ptr(token_ids), n, mult, iters,
+                   C.c_float(rms_eps), C.c_float(hc_eps), _ptr(workspace), workspace.numel(),
+                   _ptr(idx), _ptr(wt), self._stream())
+        if check:
+            self.check_decode_status(workspace)
+        return state, idx, wt
 
 
 class DeviceLayer:

@@ -273,6 +273,50 @@ int dsv4g_quant_fp4_rows(uint8_t *packed, uint8_t *scales, const float *w, int r
 int dsv4g_quant_fp8_blocks(uint8_t *codes, void *scales, const float *w, int rows, int cols,
                            int mode, void *stream);
 
+/* ---------------------------------------- caller step around the MoE ----
+ * The FFN half of forward_loaded_layer (src/dsv4/dsv4_model.c:7549-7559) on
+ * device, bit-exact: Hyper-Connection pre-mix with its Sinkhorn split, the
+ * RMSNorm with BF16 gain, the MoE layer, the post-mix into the residual
+ * state. state: [n_tokens][mult][hidden] fp32 (BF16 values), updated in place
+ * by hc_post; hc_fn [(2+mult)*mult][mult*hidden], hc_scale [3],
+ * hc_base [(2+mult)*mult] (the layer's hc_ffn_fn / _scale / _base, F32);
+ * mult at most 7; hidden a multiple of 4; state and hc_fn 16-byte aligned.
+ * status (optional, device): bit 2 is set if a wait inside hc_pre ran out
+ * (never expected; the outputs are then not valid). */
+/* rmsnorm_bf16 (src/dsv4/dsv4_model.c:4934-4951) over rows of n: y may be x;
+ * w: BF16 gain [n] or NULL. */
+int dsv4g_rmsnorm_bf16(float *y, const float *x, const uint16_t *w, int n, float eps,
+                       int round_out, int rows, void *stream);
+/* dsv4_hc_split (include/dsv4/dsv4.h:236-244) for n rows of mixes
+ * [(2+mult)*mult]: pre, post [n][mult], comb [n][mult*mult]. */
+int dsv4g_hc_split(float *pre, float *post, float *comb, const float *mixes,
+                   const float *scale3, const float *base, int mult, int iters, float eps,
+                   int n, void *stream);
+/* hc_pre (src/dsv4/dsv4_model.c:7123-7156) for n_tokens: bin [n][hidden],
+ * post [n][mult], comb [n][mult*mult]; with norm_w, bin is then
+ * rmsnorm_bf16(bin, bin, norm_w, hidden, rms_eps, 1) as the caller applies
+ * it (src/dsv4/dsv4_model.c:7524, 7553). */
+int dsv4g_hc_pre(float *bin, float *post, float *comb, const float *state, const float *fn,
+                 const float *scale3, const float *base, const uint16_t *norm_w, int mult,
+                 int hidden, int iters, float rms_eps, float hc_eps, int n_tokens,
+                 unsigned *status, void *stream);
+/* hc_post (src/dsv4/dsv4_model.c:7165-7177): state [n][mult][hidden] updated
+ * in place from branch [n][hidden], post, comb. */
+int dsv4g_hc_post(float *state, const float *branch, const float *post, const float *comb,
+                  int mult, int hidden, int n_tokens, void *stream);
+/* hc_pre + rmsnorm_bf16(ffn_norm) -> dsv4g_moe_forward -> hc_post for
+ * n_tokens states (token_ids for hash layers). workspace: 256-byte aligned,
+ * at least dsv4g_ffn_step_workspace_bytes(L, mult, n_tokens), zeroed once
+ * before first use (it begins with the decode MoE workspace, whose status
+ * word dsv4g_moe_decode_status reads; the same shape rules apply).
+ * idx_out / wt_out: optional routing. */
+size_t dsv4g_ffn_step_workspace_bytes(const DSV4GLayer *L, int mult, int n_tokens);
+int dsv4g_ffn_step(float *state, const float *hc_fn, const float *hc_scale,
+                   const float *hc_base, const uint16_t *ffn_norm, const DSV4GLayer *L,
+                   const int *token_ids, int n_tokens, int mult, int iters, float rms_eps,
+                   float hc_eps, void *workspace, size_t workspace_bytes, int *idx_out,
+                   float *wt_out, void *stream);
+
 /* ------------------------------------------ checkpoint index + HBM loader
  * The safetensors index replaces the reference reader K3St
  * (src/io/k3_st.h:34-103): k3_st_open / close / find / read / read_f32 /

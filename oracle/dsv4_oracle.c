@@ -963,3 +963,117 @@ double orc_checksum(const float *v, int n)
     for (int i = 0; i < n; i++) s += (double)v[i] * v[i];
     return sqrt(s);
 }
+
+/* ------------------------------------------- caller step around the MoE ---- */
+
+/* rmsnorm_bf16 (src/dsv4/dsv4_model.c:4934-4951): sum of squares in double,
+ * in index order, each square formed from the widened floats; the scale
+ * 1/sqrtf((float)(ss/n) + eps); y = x * r (* gain) evaluated left to right,
+ * then BF16 when round_out. y may alias x. */
+void orc_rmsnorm_bf16(float *y, const float *x, const uint16_t *w, int n, float eps,
+                      int round_out)
+{
+    double ss = 0.0;
+    for (int i = 0; i < n; i++) {
+        const double d = (double)x[i];
+        ss += d * d;
+    }
+    const float r = 1.0f / sqrtf((float)(ss / n) + eps);
+    for (int i = 0; i < n; i++) {
+        float v = x[i] * r;
+        if (w) v = v * orc_bf16_to_f32(w[i]);
+        y[i] = round_out ? orc_bf16_round(v) : v;
+    }
+}
+
+/* the logistic function in its two overflow-free forms (src/dsv4/dsv4_ops.c:401-409) */
+static float orc_sigmoid(float x)
+{
+    if (x >= 0.0f) return 1.0f / (1.0f + expf(-x));
+    const float e = expf(x);
+    return e / (1.0f + e);
+}
+
+/* dsv4_hc_split (src/dsv4/dsv4_ops.c:415-466): mixes = [pre | post | comb]
+ * sections of mult, mult, mult*mult; pre = sigmoid(m*s0 + b) + eps,
+ * post = 2 sigmoid(m*s1 + b), comb = row softmax + eps, one column pass,
+ * then iters-1 (row, column) passes; each pass divides by (sum + eps). */
+void orc_hc_split(float *pre, float *post, float *comb, const float *mixes,
+                  const float *scale3, const float *base, int mult, int iters, float eps)
+{
+    const int m = mult;
+    for (int i = 0; i < m; i++) {
+        pre[i] = orc_sigmoid(mixes[i] * scale3[0] + base[i]) + eps;
+        post[i] = 2.0f * orc_sigmoid(mixes[m + i] * scale3[1] + base[m + i]);
+    }
+    float *c = comb;
+    for (int k = 0; k < m * m; k++) c[k] = mixes[2 * m + k] * scale3[2] + base[2 * m + k];
+    for (int i = 0; i < m; i++) {
+        float *row = c + i * m;
+        float mx = row[0];
+        for (int j = 1; j < m; j++) mx = row[j] > mx ? row[j] : mx;
+        float s = 0.0f;
+        for (int j = 0; j < m; j++) s += expf(row[j] - mx);
+        for (int j = 0; j < m; j++) row[j] = expf(row[j] - mx) / s + eps;
+    }
+    for (int pass = 0; pass < 2 * iters - 1; pass++) {
+        const int by_col = (pass % 2) == 0; /* column, then (row, column) pairs */
+        for (int a = 0; a < m; a++) {
+            float s = 0.0f;
+            for (int b = 0; b < m; b++) s += by_col ? c[b * m + a] : c[a * m + b];
+            for (int b = 0; b < m; b++) {
+                float *v = by_col ? &c[b * m + a] : &c[a * m + b];
+                *v /= (s + eps);
+            }
+        }
+    }
+}
+
+/* hc_pre (src/dsv4/dsv4_model.c:7123-7156) on the flattened state [mult][hid]:
+ * rsqrt from the double sum of squares over all mult*hid values; mixes[j] =
+ * (fmaf chain of fn row j with the state, index order) * rsqrt; the split;
+ * bin[c] = bf16(fmaf chain over the mult streams of pre[i] * state[i][c]). */
+void orc_hc_pre(float *bin, float *post, float *comb, const float *state, const float *fn,
+                const float *scale3, const float *base, int mult, int hid, int iters,
+                float rms_eps, float hc_eps)
+{
+    const int K = mult * hid, mix_n = (2 + mult) * mult;
+    double ss = 0.0;
+    for (int i = 0; i < K; i++) {
+        const double d = (double)state[i];
+        ss += d * d;
+    }
+    const float rs = 1.0f / sqrtf((float)(ss / K) + rms_eps);
+    float *mixes = (float *)orc_alloc((size_t)mix_n * sizeof(float));
+    for (int j = 0; j < mix_n; j++) {
+        const float *row = fn + (size_t)j * K;
+        float acc = 0.0f;
+        for (int i = 0; i < K; i++) acc = fmaf(row[i], state[i], acc);
+        mixes[j] = acc * rs;
+    }
+    float pre[8];
+    orc_hc_split(pre, post, comb, mixes, scale3, base, mult, iters, hc_eps);
+    free(mixes);
+    for (int c = 0; c < hid; c++) {
+        float acc = 0.0f;
+        for (int i = 0; i < mult; i++) acc = fmaf(pre[i], state[(size_t)i * hid + c], acc);
+        bin[c] = orc_bf16_round(acc);
+    }
+}
+
+/* hc_post (src/dsv4/dsv4_model.c:7165-7177): new[i][c] = post[i] * branch[c],
+ * then fmaf of comb[i][k] * state[k][c] for k in order; state = bf16(new). */
+void orc_hc_post(float *state, const float *branch, const float *post, const float *comb,
+                 int mult, int hid)
+{
+    float *nw = (float *)orc_alloc((size_t)mult * hid * sizeof(float));
+    for (int i = 0; i < mult; i++)
+        for (int c = 0; c < hid; c++) {
+            float y = post[i] * branch[c];
+            for (int k = 0; k < mult; k++)
+                y = fmaf(comb[i * mult + k], state[(size_t)k * hid + c], y);
+            nw[(size_t)i * hid + c] = y;
+        }
+    for (int i = 0; i < mult * hid; i++) state[i] = orc_bf16_round(nw[i]);
+    free(nw);
+}

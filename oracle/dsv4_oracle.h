@@ -127,6 +127,17 @@ void orc_quant_fp8_blocks_absmax(uint8_t *codes, float *scales, const float *w,
 uint8_t orc_e4m3_code(float grid_value);
 
 /* ---- bench-protocol helpers (benchmarks/bench_dsv4_kernels.c) ---- */
+/* ---- caller step around the MoE: RMSNorm and Hyper-Connections ---- */
+void orc_rmsnorm_bf16(float *y, const float *x, const uint16_t *w, int n, float eps,
+                      int round_out);
+void orc_hc_split(float *pre, float *post, float *comb, const float *mixes,
+                  const float *scale3, const float *base, int mult, int iters, float eps);
+void orc_hc_pre(float *bin, float *post, float *comb, const float *state, const float *fn,
+                const float *scale3, const float *base, int mult, int hid, int iters,
+                float rms_eps, float hc_eps);
+void orc_hc_post(float *state, const float *branch, const float *post, const float *comb,
+                 int mult, int hid);
+
 uint64_t orc_xorshift_next(uint64_t *state);
 double orc_checksum(const float *v, int n);
 

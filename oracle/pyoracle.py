@@ -98,9 +98,59 @@ class _Base:
             self._quant(_p(qx[i], _f32p), _p(qs[i], _f32p), _p(x[i], _f32p), n)
         return qx, qs
 
+    # ---- caller step around the MoE (symbol names from _STEP) ----
+    _STEP = {}
+
+    def _step(self, key):
+        return getattr(self.lib, self._STEP[key])
+
+    def rmsnorm_bf16(self, x, w=None, eps=1e-6, round_out=1):
+        """Rows of x [.., n] (w: BF16 gain bits [n] or None)."""
+        x = f32(x)
+        y = np.empty_like(x)
+        n = x.shape[-1]
+        wp = None if w is None else _p(np.ascontiguousarray(w, np.uint16), _u16p)
+        fn = self._step("rmsnorm")
+        for i in np.ndindex(x.shape[:-1]):
+            fn(_p(y[i], _f32p), _p(x[i], _f32p), wp, n, C.c_float(eps), round_out)
+        return y
+
+    def hc_split(self, mixes, scale3, base, mult, iters=20, eps=1e-6):
+        mixes, scale3, base = f32(mixes), f32(scale3), f32(base)
+        pre = np.empty(mult, np.float32)
+        post = np.empty(mult, np.float32)
+        comb = np.empty(mult * mult, np.float32)
+        self._step("split")(_p(pre, _f32p), _p(post, _f32p), _p(comb, _f32p),
+                            _p(mixes, _f32p), _p(scale3, _f32p), _p(base, _f32p), mult, iters,
+                            C.c_float(eps))
+        return pre, post, comb
+
+    def hc_pre(self, state, fn, scale3, base, mult, iters=20, rms_eps=1e-6, hc_eps=1e-6):
+        """One token: state [mult*hid] -> bin [hid], post [mult], comb [mult*mult]."""
+        state, fn, scale3, base = f32(state), f32(fn), f32(scale3), f32(base)
+        hid = state.size // mult
+        bin_ = np.empty(hid, np.float32)
+        post = np.empty(mult, np.float32)
+        comb = np.empty(mult * mult, np.float32)
+        self._step("pre")(_p(bin_, _f32p), _p(post, _f32p), _p(comb, _f32p),
+                          _p(state, _f32p), _p(fn, _f32p), _p(scale3, _f32p), _p(base, _f32p),
+                          mult, hid, iters, C.c_float(rms_eps), C.c_float(hc_eps))
+        return bin_, post, comb
+
+    def hc_post(self, state, branch, post, comb, mult):
+        """One token: the new state [mult*hid] (input not modified)."""
+        st = f32(state).copy()
+        branch, post, comb = f32(branch), f32(post), f32(comb)
+        self._step("post")(_p(st, _f32p), _p(branch, _f32p), _p(post, _f32p), _p(comb, _f32p),
+                           mult, st.size // mult)
+        return st
+
 
 class Oracle(_Base):
     """The C restatement (oracle/dsv4_oracle.c)."""
+
+    _STEP = {"rmsnorm": "orc_rmsnorm_bf16", "split": "orc_hc_split", "pre": "orc_hc_pre",
+             "post": "orc_hc_post"}
 
     def __init__(self, path: str = ORACLE_SO):
         if not os.path.exists(path):
@@ -323,6 +373,9 @@ class Oracle(_Base):
 
 class RefLib(_Base):
     """The reference engine compiled from its sources (oracle/_ref)."""
+
+    _STEP = {"rmsnorm": "ref_shim_rmsnorm_bf16", "split": "dsv4_hc_split",
+             "pre": "ref_shim_hc_pre", "post": "ref_shim_hc_post"}
 
     def __init__(self, path: str = REF_SO):
         if not os.path.exists(path):

@@ -187,3 +187,38 @@ void ref_shim_st_close(K3St *s)
 int ref_shim_st_count(const K3St *s) { return s->nt; }
 int ref_shim_st_nshard(const K3St *s) { return s->nshard; }
 const K3Tensor *ref_shim_st_tensor(const K3St *s, int i) { return &s->t[i]; }
+
+/* The caller step around the MoE: the reference's static rmsnorm_bf16
+ * (src/dsv4/dsv4_model.c:4934), hc_pre_scratch (:7123) and hc_post_scratch
+ * (:7165); hc_pre reads its sizes and epsilons from a bare model config. */
+void ref_shim_rmsnorm_bf16(float *y, const float *x, const uint16_t *w, int n, float eps,
+                           int round_out)
+{
+    rmsnorm_bf16(y, x, w, n, eps, round_out);
+}
+
+void ref_shim_hc_pre(float *bin, float *post, float *comb, const float *state,
+                     const float *fn, const float *scale3, const float *base, int mult,
+                     int hid, int iters, float rms_eps, float hc_eps)
+{
+    DSV4Model *m = (DSV4Model *)calloc(1, sizeof(DSV4Model));
+    float *mixes = (float *)calloc((size_t)(2 + mult) * mult, sizeof(float));
+    if (!m || !mixes) { fprintf(stderr, "ref_shim: OOM\n"); exit(1); }
+    m->cfg.hc_mult = mult;
+    m->cfg.hidden = hid;
+    m->cfg.hc_iters = iters;
+    m->cfg.rms_eps = rms_eps;
+    m->cfg.hc_eps = hc_eps;
+    hc_pre_scratch(m, NULL, state, fn, scale3, base, bin, post, comb, mixes);
+    free(mixes);
+    free(m);
+}
+
+void ref_shim_hc_post(float *state, const float *branch, const float *post,
+                      const float *comb, int mult, int hid)
+{
+    float *nw = (float *)calloc((size_t)mult * hid, sizeof(float));
+    if (!nw) { fprintf(stderr, "ref_shim: OOM\n"); exit(1); }
+    hc_post_scratch(state, branch, post, comb, mult, hid, nw);
+    free(nw);
+}
