@@ -16,6 +16,11 @@ launches on the launch stream. cpu_baseline: the
 reference's own moe_forward (oracle/_ref, compiled from the reference sources)
 on the same layer on the host cores.
 
+The kernels entries (config keys fp8_matvec_2048x4096, fp4_expert_1_token,
+ffn_step_1_token, checkpoint_load) time the standalone FP8 matvec, one FP4
+expert, the FFN half of a decoder layer on device (hyper-connection pre-mix,
+RMSNorm, MoE layer, post-mix) and the checkpoint-to-HBM loader.
+
 The same run also measures the batched path on layer 0 with a Zipf(1.2)
 router bias (config keys "verify_64" and "prefill_4096"): 64 tokens
 (speculative verify) and 4096 tokens (prefill) through the grouped GEMMs,
@@ -272,6 +277,134 @@ def bench_fp4_expert(lib, layer, cpu_seconds):
                                        f"(oracle/_ref, OMP_NUM_THREADS={threads}) over 8 "
                                        f"experts of the same layer and the same token"}
     return r
+
+
+HC_MULT = 4                                   # hyper-connection streams
+HC_MIX = (2 + HC_MULT) * HC_MULT              # 24 mixes per hc_pre
+HC_K = HC_MULT * H                            # 16384 products per mix
+
+
+def bench_ffn_step(lib, layers, cpu_seconds):
+    """The FFN half of a decoder layer at one token (forward_loaded_layer,
+    src/dsv4/dsv4_model.c:7549-7559) on device: hc_pre with its Sinkhorn split
+    and the RMSNorm (24 exact fmaf chains of 16384 steps), the decode MoE
+    layer, hc_post. State [4][4096] BF16 values; per layer its own hc_ffn_fn
+    [24][16384] N(0, 0.01), scale, base and ffn_norm; the calls rotate over
+    the decode layers like the decode benchmark."""
+    import numpy as np
+    import torch
+    dev = torch.device("cuda:0")
+    nl = len(layers)
+    g = torch.Generator(device=dev)
+    g.manual_seed(11)
+
+    def bf16(t):
+        return (t.view(torch.int32) & -65536).view(torch.float32)
+
+    fn = [torch.randn(HC_MIX, HC_K, generator=g, device=dev) * 0.01 for _ in range(nl)]
+    sc = [torch.rand(3, generator=g, device=dev) + 0.5 for _ in range(nl)]
+    base = [torch.randn(HC_MIX, generator=g, device=dev) * 0.5 for _ in range(nl)]
+    norm = [(bf16(1 + 0.1 * torch.randn(H, generator=g, device=dev)).view(torch.int32) >> 16)
+            .to(torch.int16) for _ in range(nl)]
+    state0 = bf16(torch.randn(1, HC_K, generator=g, device=dev) * 0.5)
+    state = state0.clone()
+    ws = torch.zeros(lib.ffn_step_workspace_bytes(layers[0], HC_MULT, 1), dtype=torch.uint8,
+                     device=dev)
+    iters = 8 * nl
+    ms_step = graph_time(lambda i: lib.ffn_step(state, fn[i % nl], sc[i % nl], base[i % nl],
+                                                norm[i % nl], layers[i % nl], HC_MULT,
+                                                workspace=ws, check=False), iters)
+    lib.check_decode_status(ws)
+    b, po, co = lib.hc_pre(state, fn[0], sc[0], base[0], HC_MULT, norm[0])
+    ms_pre = graph_time(lambda i: lib.hc_pre(state, fn[i % nl], sc[i % nl], base[i % nl],
+                                             HC_MULT, norm[i % nl]), iters)
+    st2 = state.clone()
+    ms_post = graph_time(lambda i: lib.hc_post(st2, b, po, co, HC_MULT), iters)
+    pre_bytes = HC_MIX * HC_K * 4 + HC_K * 4 + H * 2 + H * 4
+    r = {"workload": "FFN half of a decoder layer at 1 token: hc_pre (24 mixes, each an exact "
+                     "fmaf chain of 16384 steps) + Sinkhorn split + RMSNorm, the decode MoE "
+                     "layer, hc_post; dsv4g_ffn_step, bit-exact",
+         "ms_per_step": round(ms_step, 5), "ms_hc_pre_rmsnorm": round(ms_pre, 5),
+         "ms_hc_post": round(ms_post, 5),
+         "hc_pre_ns_per_chain_step": round(ms_pre * 1e6 / HC_K, 3),
+         "roofline": {"bound": "fmaf chain latency (hc_pre)",
+                      "achieved": round(pre_bytes / (ms_pre * 1e-3) / 1e9, 1),
+                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                      "frac": round(pre_bytes / (ms_pre * 1e-3) / 1e9 / HBM_PEAK_GBS, 5),
+                      "note": "hc_pre streams 1.6 MB but its 16384-step dependent chains bound "
+                              "it: 2.05-2.4 ns per step for a lone chain from registers on "
+                              "gfx950 (a floor of about 34 us)"}}
+    if cpu_seconds and cpu_available():
+        threads, _ = host_cores()
+        set_omp_threads(threads)
+        ref = cpu_ref()
+        import synth
+        L = synth.host_copy(layers[0])
+        fh, sch, bh = fn[0].cpu().numpy(), sc[0].cpu().numpy(), base[0].cpu().numpy()
+        nh = norm[0].cpu().numpy().view(np.uint16)
+        s0 = state0.cpu().numpy()[0]
+
+        def one(st):
+            x, post, comb = ref.hc_pre(st, fh, sch, bh, HC_MULT)
+            x = ref.rmsnorm_bf16(x[None], nh, 1e-6, 1)[0]
+            out, _, _ = ref.moe_forward(L, x)
+            return ref.hc_post(st, out, post, comb, HC_MULT)
+        want = one(s0)
+        st = state0.clone()
+        lib.ffn_step(st, fn[0], sc[0], base[0], norm[0], layers[0], HC_MULT, workspace=ws)
+        same = bool(np.array_equal(want.view(np.uint32), st.cpu().numpy()[0].view(np.uint32)))
+        sec, n = cpu_loop(lambda: one(s0), cpu_seconds)
+        r["cpu_baseline"] = {"value": round(sec * 1e3, 3), "unit": "ms per step",
+                             "cores": threads, "kind": "reference",
+                             "gpu_output_bit_exact_vs_reference": same,
+                             "sample": f"{n} steps of the reference hc_pre_scratch, "
+                                       f"rmsnorm_bf16, moe_forward and hc_post_scratch "
+                                       f"(oracle/_ref, OMP_NUM_THREADS={threads}) on layer 0 "
+                                       f"and the same state"}
+        del L
+    return r
+
+
+def bench_checkpoint_load(lib, layer):
+    """Checkpoint to HBM (dsv4g_load_moe_layer): 16 full-size routed experts of
+    one layer, its FP8 shared expert, gate and bias, written as three
+    safetensors shards with the checkpoint's tensor names to a temporary
+    directory, then loaded twice; the second load is timed (page cache
+    warm, so the rate is the loader's, not the disk's)."""
+    import shutil
+    import tempfile
+    import numpy as np
+    import torch
+    import dsv4_gpu
+    from st_writer import moe_layer_tensors, write_checkpoint
+    import synth
+    n_exp = 16
+    L = synth.host_copy(layer)
+    stride = L["expert_stride"]
+    L = dict(L, n_experts=n_exp, experts=L["experts"][:n_exp * stride],
+             gate_w=L["gate_w"][:n_exp], bias=np.zeros(n_exp, np.float32))
+    d = tempfile.mkdtemp(prefix="dsv4_ckpt_")
+    try:
+        write_checkpoint(d, moe_layer_tensors(L, "layers", 3), n_shards=3)
+        ck = dsv4_gpu.Checkpoint(d)
+        meta = {k: L[k] for k in ("hidden", "inter", "n_experts", "topk", "route_scale",
+                                  "swiglu_limit")}
+        ck.load_moe_layer(meta, "layers", 3)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        loaded = ck.load_moe_layer(meta, "layers", 3)
+        sec = time.perf_counter() - t0
+        nbytes = sum(t["nbytes"] for t in ck.tensors())
+        same = bool(np.array_equal(loaded.arena[:n_exp * stride].cpu().numpy(), L["experts"]))
+        ck.close()
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
+    return {"workload": f"{n_exp} full-size routed experts + FP8 shared expert + gate/bias of "
+                        f"one layer, 3 safetensors shards -> one HBM arena "
+                        f"(dsv4g_load_moe_layer), page cache warm",
+            "bytes": nbytes, "ms": round(sec * 1e3, 3),
+            "gbs": round(nbytes / sec / 1e9, 2), "arena_experts_match_source": same,
+            "note": "file -> pinned staging -> HBM; a cold load is bound by the disk"}
 
 
 def cpu_available():
@@ -547,6 +680,8 @@ def main():
     if wl in ("all", "kernels"):
         kernels["fp8_matvec_2048x4096"] = bench_fp8_matvec(lib, cpu_s)
         kernels["fp4_expert_1_token"] = bench_fp4_expert(lib, layers[0], cpu_s)
+        kernels["ffn_step_1_token"] = bench_ffn_step(lib, layers, cpu_s)
+        kernels["checkpoint_load"] = bench_checkpoint_load(lib, layers[0])
         if wl == "kernels":
             print(json.dumps(kernels))
             return

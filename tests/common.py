@@ -131,92 +131,4 @@ def bf16_ulp(v):
 
 
 # ------------------------------------------------------------ safetensors
-ST_ITEMSIZE = {"U8": 1, "I8": 1, "I64": 8, "BF16": 2, "F16": 2, "F32": 4, "F8_E4M3": 1,
-               "F8_E8M0": 1}
-
-
-def write_safetensors(path, entries, metadata=None, header_pad=8):
-    """Write one shard: [u64 LE header length][JSON header][data], tensors
-    stored in the order given. entries: (name, dtype, shape, raw bytes).
-    The header is space-padded to a multiple of header_pad bytes."""
-    import json
-    import struct
-    header = {}
-    if metadata is not None:
-        header["__metadata__"] = metadata
-    off = 0
-    for name, dt, shape, raw in entries:
-        n = int(np.prod(shape, dtype=np.int64)) if len(shape) else 1
-        assert len(raw) == n * ST_ITEMSIZE[dt], (name, len(raw), shape, dt)
-        header[name] = {"dtype": dt, "shape": list(shape), "data_offsets": [off, off + len(raw)]}
-        off += len(raw)
-    h = json.dumps(header).encode()
-    h += b" " * ((-len(h)) % header_pad)
-    with open(path, "wb") as f:
-        f.write(struct.pack("<Q", len(h)))
-        f.write(h)
-        for _, _, _, raw in entries:
-            f.write(raw)
-
-
-def moe_layer_tensors(layer, scope="layers", index=0, order="reference", seed=0):
-    """The named tensors of a make_layer() layer, as the checkpoint stores
-    them (src/dsv4/dsv4_model.c:2014-2053, 3063-3136;
-    docs/DSV4_ARCHITECTURE.md:58-113): a list of (name, dtype, shape, bytes).
-    order "reference": each expert's scale run then weight run, w1 w2 w3;
-    "scrambled": each expert's six tensors in a seeded random order and the
-    experts themselves shuffled."""
-    H, I, E = layer["hidden"], layer["inter"], layer["n_experts"]
-    g = expert_geometry(H, I)
-    pre = f"{scope}.{index}."
-    out = [(pre + "ffn.gate.weight", "BF16", (E, H), layer["gate_w"].tobytes())]
-    if layer.get("tid2eid") is not None:
-        t = layer["tid2eid"]
-        out.append((pre + "ffn.gate.tid2eid", "I64", t.shape, t.tobytes()))
-    else:
-        b = layer["bias"] if layer.get("bias") is not None else np.zeros(E, np.float32)
-        out.append((pre + "ffn.gate.bias", "F32", (E,), np.asarray(b, np.float32).tobytes()))
-    bi, bh = (I + 127) // 128, (H + 127) // 128
-    for m, (r, c, sr, sc) in (("w1", (I, H, bi, bh)), ("w3", (I, H, bi, bh)),
-                              ("w2", (H, I, bh, bi))):
-        key = {"w1": "sh1", "w3": "sh3", "w2": "sh2"}[m]
-        out.append((pre + f"ffn.shared_experts.{m}.weight", "F8_E4M3", (r, c),
-                    np.ascontiguousarray(layer[key]).tobytes()))
-        out.append((pre + f"ffn.shared_experts.{m}.scale", "F8_E8M0", (sr, sc),
-                    np.ascontiguousarray(layer[key + "_s"]).tobytes()))
-    rng = np.random.default_rng(seed)
-    experts = list(range(E))
-    if order == "scrambled":
-        rng.shuffle(experts)
-    for e in experts:
-        scales, weights = expert_slot(layer, e)
-        s_sz = (g["s1"], g["s2"], g["s1"])
-        w_sz = (g["w1"], g["w2"], g["w1"])
-        shapes = ((I, H), (H, I), (I, H))
-        items = []
-        so = wo = 0
-        for k in range(3):
-            r, c = shapes[k]
-            items.append((pre + f"ffn.experts.{e}.w{k + 1}.scale", "F8_E8M0", (r, (c + 31) // 32),
-                          scales[so:so + s_sz[k]].tobytes()))
-            so += s_sz[k]
-        for k in range(3):
-            r, c = shapes[k]
-            items.append((pre + f"ffn.experts.{e}.w{k + 1}.weight", "I8", (r, (c + 1) // 2),
-                          weights[wo:wo + w_sz[k]].tobytes()))
-            wo += w_sz[k]
-        if order == "scrambled":
-            items = [items[i] for i in rng.permutation(len(items))]
-        out.extend(items)
-    return out
-
-
-def write_checkpoint(directory, tensors, n_shards=1, prefix="model"):
-    """Split tensors (in order) over n_shards files named like the
-    checkpoint's (model-0000k-of-0000n.safetensors)."""
-    os.makedirs(directory, exist_ok=True)
-    bounds = np.linspace(0, len(tensors), n_shards + 1).astype(int)
-    for k in range(n_shards):
-        write_safetensors(os.path.join(directory, f"{prefix}-{k + 1:05d}-of-{n_shards:05d}"
-                                       ".safetensors"),
-                          tensors[bounds[k]:bounds[k + 1]], metadata={"format": "pt"})
+from st_writer import ST_ITEMSIZE, moe_layer_tensors, write_checkpoint, write_safetensors  # noqa: E402,F401
