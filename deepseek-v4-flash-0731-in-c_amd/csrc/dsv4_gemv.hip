@@ -141,13 +141,158 @@ __global__ __launch_bounds__(256) void k_gemv_fp4_t(GemvArgs a, int pair) {
   }
 }
 
-__global__ __launch_bounds__(256) void k_gemv_fp8(GemvArgs a) {
-  __shared__ __align__(16) float xs[FP8_MAX_IN / 128 * 132];
-  __shared__ float2 ps[FP8_TR * (FP8_MAX_IN / 128 + 1)];
-  const int m = blockIdx.z, b = blockIdx.y;
-  fp8_rows_exact(a.y[m] + (size_t)b * a.y_stride, a.qx + (size_t)b * a.qx_stride,
-                 a.qscale + (size_t)b * a.qs_stride, a.W[m], a.S[m], a.in, a.rows,
-                 blockIdx.x * FP8_TR, a.round_out, xs, ps);
+// ========================================================= FP8 GEMV =====
+// dsv4_gemv_fp8_q / _pair_q / _batch_q (src/dsv4/dsv4_model.c:571-961) for
+// any width up to 8192 and any number of token vectors, bit-exact: per
+// (row, 128-column block) a 128-long sequential fmaf chain, then per row the
+// block chain acc = fmaf(p, qscale * ws, acc) in order (NaN block scale:
+// the block is skipped, as in the reference).
+//
+// Lane t of a workgroup is (row t / SL, slot t % SL) and owns blocks slot
+// and slot + SL; SL (8, 16 or 32 lanes per row) is the smallest that leaves
+// every lane at most two blocks, so a lane's whole weight slice (2 x 128 B)
+// is loaded into registers before any arithmetic and the workgroup's rows
+// stream from HBM in one go. Tokens are taken G at a time: each 16-column
+// piece is decoded once and feeds G chains, and the weights stay in
+// registers across all the token groups, so a batch reads them from HBM
+// once. LDS: the G tokens' activations (padded to 132 floats per block) and
+// their scales, and the (partial, scale) pairs of the block chains.
+template <int SL, int G>
+__global__ __launch_bounds__(256) void k_fp8_proj(GemvArgs a, int nvec, int gpw, int vec4) {
+  constexpr int TR = 256 / SL;
+  extern __shared__ __align__(16) float lds[];
+  const int m = blockIdx.z, t = threadIdx.x, lr = t / SL, slot = t % SL;
+  const int in = a.in, rows = a.rows, r0 = blockIdx.x * TR;
+  const int CB = (in + 127) / 128, stride = pair_stride(CB);
+  float *xs = lds;                                   // [G][CB][132]
+  float *qs = xs + (size_t)G * CB * 132;             // [G][CB]
+  float2 *ps = reinterpret_cast<float2 *>(qs + ((G * CB + 3) & ~3));  // [G][TR][stride]
+
+  // the lane's weights and block-scale codes (zeros past the matrix)
+  const uint32_t nrow = (uint32_t)max(0, min(TR, rows - r0));
+  const BufRsrc rw = buf_rsrc(a.W[m] + (size_t)r0 * in, nrow * (uint32_t)in);
+  const BufRsrc rs = buf_rsrc(a.S[m], (uint32_t)((rows + 127) / 128) * CB);
+  uint4 w[16];
+  uint32_t sc[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const uint32_t cb = (uint32_t)(slot + SL * j);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t c = cb * 128u + 16u * i;
+      w[8 * j + i] = buf_load16(rw, cb < (uint32_t)CB && c < (uint32_t)in
+                                        ? (uint32_t)lr * (uint32_t)in + c
+                                        : 0xFFFFFFF0u);
+    }
+    sc[j] = __builtin_amdgcn_raw_buffer_load_b8(
+        rs, cb < (uint32_t)CB && (uint32_t)lr < nrow ? (uint32_t)((r0 + lr) / 128) * CB + cb
+                                                      : 0xFFFFFFF0u, 0, 0);
+  }
+
+  // this workgroup's token groups: gpw groups of G from blockIdx.y * gpw
+  const int tbeg = blockIdx.y * gpw * G, tend = min(nvec, tbeg + gpw * G);
+  for (int t0 = tbeg; t0 < tend; t0 += G) {
+    // the group's activations and scales into LDS (zeros past the last token)
+    if (vec4) {
+      for (int i = 4 * t; i < G * in; i += 1024) {
+        const int g = i / in, c = i % in;
+        const float4 v = t0 + g < nvec
+                             ? *reinterpret_cast<const float4 *>(
+                                   a.qx + (size_t)(t0 + g) * a.qx_stride + c)
+                             : make_float4(0.f, 0.f, 0.f, 0.f);
+        *reinterpret_cast<float4 *>(xs + (size_t)g * CB * 132 + (c / 128) * 132 + (c % 128)) = v;
+      }
+    } else {
+      for (int i = t; i < G * in; i += 256) {
+        const int g = i / in, c = i % in;
+        xs[(size_t)g * CB * 132 + (c / 128) * 132 + (c % 128)] =
+            t0 + g < nvec ? a.qx[(size_t)(t0 + g) * a.qx_stride + c] : 0.0f;
+      }
+    }
+    for (int i = t; i < G * CB; i += 256) {
+      const int g = i / CB;
+      qs[i] = t0 + g < nvec ? a.qscale[(size_t)(t0 + g) * a.qs_stride + i % CB] : 0.0f;
+    }
+    __syncthreads();
+    if (r0 + lr < rows) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int cb = slot + SL * j;
+        if (cb < CB) {
+          const int len = min(128, in - cb * 128);
+          float part[G];
+#pragma unroll
+          for (int g = 0; g < G; ++g) part[g] = 0.0f;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            if (16 * i < len) {
+              const uint32_t wd[4] = {w[8 * j + i].x, w[8 * j + i].y, w[8 * j + i].z,
+                                      w[8 * j + i].w};
+              float v[16];
+#pragma unroll
+              for (int d = 0; d < 4; ++d) {
+                const float2 lo = fp8x2<false>(wd[d]), hi = fp8x2<true>(wd[d]);
+                v[4 * d] = lo.x;
+                v[4 * d + 1] = lo.y;
+                v[4 * d + 2] = hi.x;
+                v[4 * d + 3] = hi.y;
+              }
+#pragma unroll
+              for (int g = 0; g < G; ++g) {
+                const float *xb = xs + (size_t)g * CB * 132 + cb * 132 + 16 * i;
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                  const float4 xv = *reinterpret_cast<const float4 *>(xb + 4 * d);
+                  part[g] = fmaf(v[4 * d], xv.x, part[g]);
+                  part[g] = fmaf(v[4 * d + 1], xv.y, part[g]);
+                  part[g] = fmaf(v[4 * d + 2], xv.z, part[g]);
+                  part[g] = fmaf(v[4 * d + 3], xv.w, part[g]);
+                }
+              }
+            }
+          }
+#pragma unroll
+          for (int g = 0; g < G; ++g) {
+            float s = qs[g * CB + cb] * e8m0(sc[j]);
+            float p = part[g];
+            if (sc[j] == 255u) {  // NaN scale: the reference skips the block
+              p = 0.0f;
+              s = 0.0f;
+            }
+            ps[(size_t)(g * TR + lr) * stride + cb] = make_float2(p, s);
+          }
+        }
+      }
+    }
+    __syncthreads();
+    if (t < G * TR) {
+      const int g = t / TR, r = t % TR;
+      if (r0 + r < rows && t0 + g < nvec) {
+        const float acc = pair_chain(ps + (size_t)(g * TR + r) * stride, CB);
+        a.y[m][(size_t)(t0 + g) * a.y_stride + r0 + r] = a.round_out ? bf16_round(acc) : acc;
+      }
+    }
+    __syncthreads();  // LDS is refilled by the next group
+  }
+}
+
+// Token groups per workgroup: all of them when the row tiles alone give
+// 1024 or more workgroups (each weight read from HBM once); otherwise the
+// groups are spread so the launch still has about that many (a small
+// matrix's re-reads come from the caches).
+template <int SL, int G>
+static void launch_fp8_proj(const GemvArgs *a, int nvec, int nmat, hipStream_t st) {
+  constexpr int TR = 256 / SL;
+  const int CB = (a->in + 127) / 128;
+  const size_t lds = ((size_t)G * CB * 132 + ((G * CB + 3) & ~3)) * 4 +
+                     (size_t)G * TR * pair_stride(CB) * 8;
+  const int tiles = (a->rows + TR - 1) / TR * nmat, groups = (nvec + G - 1) / G;
+  const int split = min(groups, max(1, 1024 / tiles));
+  const int gpw = (groups + split - 1) / split;
+  const int vec4 = ((uintptr_t)a->qx % 16 == 0) && (a->qx_stride % 4 == 0);
+  hipLaunchKernelGGL((k_fp8_proj<SL, G>),
+                     dim3((a->rows + TR - 1) / TR, (groups + gpw - 1) / gpw, nmat), dim3(256),
+                     lds, st, *a, nvec, gpw, vec4);
 }
 
 // ======================================================== BF16 GEMV =====
@@ -613,8 +758,21 @@ int dsv4g_launch_gemv_fp4(const GemvArgs *a, int nvec, int nmat, void *stream) {
 int dsv4g_launch_gemv_fp8(const GemvArgs *a, int nvec, int nmat, void *stream) {
   if (fp8_shape_ok(a->in, "gemv_fp8")) return DSV4G_EINVAL;
   if (a->rows <= 0 || nvec <= 0) return dsv4g_fail(DSV4G_EINVAL, "gemv_fp8: bad size");
-  dim3 grid((a->rows + FP8_TR - 1) / FP8_TR, nvec, nmat);
-  hipLaunchKernelGGL(k_gemv_fp8, grid, dim3(256), 0, (hipStream_t)stream, *a);
+  hipStream_t st = (hipStream_t)stream;
+  // lanes per row: every lane at most two 128-column blocks
+  // tokens four at a time only when the row tiles alone fill the GPU (a
+  // smaller matrix runs one token per workgroup, all tokens in parallel)
+  const int CB = (a->in + 127) / 128;
+  const int sl = CB <= 16 ? 8 : CB <= 32 ? 16 : 32;
+  const bool many = nvec > 1 && (long)(a->rows + 256 / sl - 1) / (256 / sl) * nmat >= 1024;
+  switch (sl * (many ? 10 : 1)) {
+    case 8: launch_fp8_proj<8, 1>(a, nvec, nmat, st); break;
+    case 16: launch_fp8_proj<16, 1>(a, nvec, nmat, st); break;
+    case 32: launch_fp8_proj<32, 1>(a, nvec, nmat, st); break;
+    case 80: launch_fp8_proj<8, 4>(a, nvec, nmat, st); break;
+    case 160: launch_fp8_proj<16, 4>(a, nvec, nmat, st); break;
+    default: launch_fp8_proj<32, 4>(a, nvec, nmat, st); break;
+  }
   return dsv4g_check_launch("gemv_fp8");
 }
 

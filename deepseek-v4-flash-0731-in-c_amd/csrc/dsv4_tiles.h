@@ -104,67 +104,6 @@ __device__ __forceinline__ float pair_chain(const float2 *pr, int n) {
 // 16-byte reads by consecutive lanes fall in distinct banks.
 __device__ __host__ __forceinline__ int pair_stride(int n) { return (n | 1) + 1; }
 
-// ===================================================== FP8 exact GEMV ====
-// One workgroup owns FP8_TR rows. Lane t = (row t / 16, block slot t % 16);
-// slot j handles 128-column blocks j, j+16, ... Each block partial is a
-// 128-long sequential fmaf chain; qx comes from LDS (padded per block).
-__device__ inline void fp8_rows_exact(float *__restrict__ y, const float *__restrict__ qx,
-                               const float *__restrict__ qscale,
-                               const uint8_t *__restrict__ W, const uint8_t *__restrict__ S,
-                               int in, int rows, int r0, int round_out, float *xs,
-                               float2 *ps) {
-  const int t = threadIdx.x;
-  const int CB = (in + 127) / 128;
-  const int stride = CB + 1;
-  // stage qx into LDS, block-padded by 4 floats
-  for (int i = t; i < in; i += 256) xs[(i / 128) * 132 + (i % 128)] = qx[i];
-  __syncthreads();
-  const int lr = t / 16, slot = t % 16;
-  const int row = r0 + lr;
-  if (row < rows) {
-    const uint8_t *wr = W + (size_t)row * in;
-    const uint8_t *sr = S + (size_t)(row / 128) * CB;
-    for (int cb = slot; cb < CB; cb += 16) {
-      const int c0 = cb * 128;
-      const int len = in - c0 < 128 ? in - c0 : 128;
-      const float *xb = xs + cb * 132;
-      float part = 0.0f;
-      for (int c = 0; c < len; c += 16) {
-        const uint4 w = *reinterpret_cast<const uint4 *>(wr + c0 + c);
-        const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-        for (int d = 0; d < 4; ++d) {
-          const float4 xv = *reinterpret_cast<const float4 *>(xb + c + 4 * d);
-          float2 v = fp8x2<false>(wd[d]);
-          part = fmaf(v.x, xv.x, part);
-          part = fmaf(v.y, xv.y, part);
-          v = fp8x2<true>(wd[d]);
-          part = fmaf(v.x, xv.z, part);
-          part = fmaf(v.y, xv.w, part);
-        }
-      }
-      const uint32_t code = sr[cb];
-      float s = qscale[cb] * e8m0(code);
-      if (code == 255u) {
-        part = 0.0f;
-        s = 0.0f;
-      }
-      ps[lr * stride + cb] = make_float2(part, s);
-    }
-  }
-  __syncthreads();
-  if (t < FP8_TR && r0 + t < rows) {
-    const float2 *pr = ps + t * stride;
-    float acc = 0.0f;
-    for (int cb = 0; cb < CB; ++cb) {
-      const float2 v = pr[cb];
-      acc = fmaf(v.x, v.y, acc);
-    }
-    y[r0 + t] = round_out ? bf16_round(acc) : acc;
-  }
-}
-
-
 // ============================================ two-step tiles (decode) ====
 // The same exact schemes, split so that a kernel issues every weight load
 // of its tile before it has the activation vector: *_load fills registers,
