@@ -17,9 +17,10 @@ reference's own moe_forward (oracle/_ref, compiled from the reference sources)
 on the same layer on the host cores.
 
 The kernels entries (config keys fp8_matvec_2048x4096, fp4_expert_1_token,
-ffn_step_1_token, checkpoint_load) time the standalone FP8 matvec, one FP4
-expert, the FFN half of a decoder layer on device (hyper-connection pre-mix,
-RMSNorm, MoE layer, post-mix) and the checkpoint-to-HBM loader.
+ffn_step_1_token, attention_projections, checkpoint_load) time the
+standalone FP8 matvec, one FP4 expert, the FFN half of a decoder layer on
+device (hyper-connection pre-mix, RMSNorm, MoE layer, post-mix), the four
+attention FP8 projections and the checkpoint-to-HBM loader.
 
 The same run also measures the batched path on layer 0 with a Zipf(1.2)
 router bias (config keys "verify_64" and "prefill_4096"): 64 tokens
@@ -365,6 +366,87 @@ def bench_ffn_step(lib, layers, cpu_seconds):
     return r
 
 
+ATTN_PROJ = (("wq_a", 1024, 4096), ("wq_b", 32768, 1024), ("wkv", 512, 4096),
+             ("wo_b", 4096, 8192))
+
+
+def bench_attn_proj(lib, cpu_seconds):
+    """The attention FP8 projections of one layer (src/dsv4/dsv4_internal.h:57-62)
+    through dsv4_gemv_fp8_q (1 token) and dsv4_gemv_fp8_batch_q (5 tokens, the
+    reference bench's dense batch, benchmarks/bench_dsv4_kernels.c:194-215):
+    E4M3 weights N(0, 0.02) with 128 x 128 E8M0 scales, x BF16 N(0, 1)
+    quantised per 128. Copies of each matrix rotate so that each call streams
+    from HBM."""
+    import numpy as np
+    import torch
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(21)
+    out = {}
+    total_ms = {1: 0.0, 5: 0.0}
+    mats = {}
+    for name, rows, cols in ATTN_PROJ:
+        copies = max(2, min(24, (512 << 20) // (rows * cols)))
+        w = torch.randn(rows, cols, generator=g, device=dev) * 0.02
+        codes = torch.empty(copies, rows, cols, dtype=torch.uint8, device=dev)
+        scales = torch.empty(copies, (rows + 127) // 128, (cols + 127) // 128,
+                             dtype=torch.uint8, device=dev)
+        lib.quant_fp8_blocks(w, codes[0], scales[0], mode=0)
+        for i in range(1, copies):
+            codes[i].copy_(codes[0])
+            scales[i].copy_(scales[0])
+        del w
+        x = (torch.randn(5, cols, generator=g, device=dev).to(torch.bfloat16)
+             .to(torch.float32).contiguous())
+        qx, qs = lib.quant_fp8_act(x)
+        r = {"shape": [rows, cols], "weight_bytes": rows * cols}
+        for n in (1, 5):
+            def call(i, n=n):
+                if n == 1:
+                    lib.gemv_fp8_q(qx[0], qs[0], codes[i % copies], scales[i % copies], cols, rows)
+                else:
+                    lib.gemv_fp8_batch_q(qx[:n], qs[:n], codes[i % copies], scales[i % copies],
+                                         cols, rows)
+            ms = graph_time(call, 4 * copies)
+            total_ms[n] += ms
+            r[f"ms_{n}_token" + ("s" if n > 1 else "")] = round(ms, 5)
+            r[f"gbs_{n}_token" + ("s" if n > 1 else "")] = round(rows * cols / (ms * 1e-3) / 1e9,
+                                                                   1)
+        out[name] = r
+        mats[name] = (codes[0].cpu().numpy(), scales[0].cpu().numpy(), qx.cpu().numpy(),
+                      qs.cpu().numpy(), lib.gemv_fp8_q(qx[0], qs[0], codes[0], scales[0], cols,
+                                                       rows).cpu().numpy())
+        del codes, scales
+    wbytes = sum(r * c for _, r, c in ATTN_PROJ)
+    res = {"workload": "attention FP8 projections wq_a 1024x4096, wq_b 32768x1024, wkv "
+                       "512x4096, wo_b 4096x8192 (dsv4_gemv_fp8_q / _batch_q, bit-exact)",
+           "per_matrix": out, "weight_bytes": wbytes,
+           "ms_1_token": round(total_ms[1], 5), "ms_5_tokens": round(total_ms[5], 5),
+           "roofline": {"bound": "hbm", "achieved": round(wbytes / (total_ms[1] * 1e-3) / 1e9, 1),
+                        "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": round(wbytes / (total_ms[1] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}}
+    if cpu_seconds and cpu_available():
+        threads, _ = host_cores()
+        set_omp_threads(threads)
+        ref = cpu_ref()
+        same = 0
+        sec = 0.0
+        for name, rows, cols in ATTN_PROJ:
+            W, S, qx, qs, y = mats[name]
+            yr = ref.gemv_fp8_q(qx[0], qs[0], W, S, cols, rows)
+            same += int(np.array_equal(yr.view(np.uint32), y.view(np.uint32)))
+            s1, _ = cpu_loop(lambda: ref.gemv_fp8_q(qx[0], qs[0], W, S, cols, rows),
+                             cpu_seconds / 4)
+            sec += s1
+        res["cpu_baseline"] = {"value": round(sec * 1e3, 3), "unit": "ms per token (4 matrices)",
+                               "cores": threads, "kind": "reference",
+                               "gpu_outputs_bit_exact_vs_reference": f"{same}/4",
+                               "sample": f"the reference dsv4_gemv_fp8_q (oracle/_ref, "
+                                         f"OMP_NUM_THREADS={threads}) on each matrix and the "
+                                         f"same token, {cpu_seconds / 4:.1f} s each"}
+    return res
+
+
 def bench_checkpoint_load(lib, layer):
     """Checkpoint to HBM (dsv4g_load_moe_layer): 16 full-size routed experts of
     one layer, its FP8 shared expert, gate and bias, written as three
@@ -681,6 +763,7 @@ def main():
         kernels["fp8_matvec_2048x4096"] = bench_fp8_matvec(lib, cpu_s)
         kernels["fp4_expert_1_token"] = bench_fp4_expert(lib, layers[0], cpu_s)
         kernels["ffn_step_1_token"] = bench_ffn_step(lib, layers, cpu_s)
+        kernels["attention_projections"] = bench_attn_proj(lib, cpu_s)
         kernels["checkpoint_load"] = bench_checkpoint_load(lib, layers[0])
         if wl == "kernels":
             print(json.dumps(kernels))
