@@ -7,12 +7,14 @@
 //      (the reference's activation quant, exact);
 //   2. router: BF16 MFMA logits with sum|g*x| for a rigorous error bound,
 //      candidate experts per token, exact sequential fmaf chains for the
-//      candidates (packed one per lane across tokens), then the reference's
-//      selection and weights - indices and weights identical to the
-//      reference;
+//      candidates, then the reference's selection and weights - indices and
+//      weights identical to the reference (up to 256 tokens: logits,
+//      candidates, and chains with the selection fused into the token's last
+//      chain workgroup - three launches);
 //   3. dispatch: deterministic per-expert position lists (ascending token, as
 //      expert_forward_batch_routes gathers them, src/dsv4/dsv4_model.c:6498-6524)
-//      and a token-tile table; the shared expert is expert number E;
+//      and a token-tile table (one workgroup up to 1024 routes); the shared
+//      expert is expert number E;
 //   4. gate/up grouped GEMM on V_MFMA_F32_16X16X32_BF16: FP4 (routed) or FP8
 //      (shared) weights are converted in registers to BF16 already multiplied
 //      by their E8M0 block scale (V_CVT_SCALEF32_PK_BF16_FP4/FP8, exact: at
@@ -62,11 +64,6 @@ __device__ __forceinline__ v4f mx_mfma(v8i a, v8i b, v4f c, int sa, int sb) {
 
 __device__ __forceinline__ uint32_t scale_code(float s) { return (f2u(s) >> 23) & 0xFFu; }
 
-__global__ void k_fill_zero_i32(int *p, int n) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = 0;
-}
-
 // Operand layouts of V_MFMA_SCALE_F32_16X16X128_F8F6F4 (measured on gfx950 with
 // dsv4g_probe_mfma): lane l serves row/column l%16; with g = l/16,
 //   4-bit operand: nibbles 0..31 (4 VGPRs) = K 32g .. 32g+31, low nibble first;
@@ -113,11 +110,12 @@ __global__ void k_probe_bf16(float *D, const uint16_t *A, const uint16_t *B) {
 
 // ------------------------------------------------------- batch quant ----
 // The reference activation quant per (token, 128-group), stored as the
-// exact BF16 value of each quantised element (E4M3 grid value x scale); flags
-// tokens whose x is not BF16-valued (the router bound then widens for them).
+// exact BF16 value of each quantised element (E4M3 grid value x scale), and
+// per 256-column piece of a token a flag: 1 when a value of x in it is not
+// BF16-valued (the router bound then widens), written either way.
 // 16-byte loads: a half wave per group.
 __global__ __launch_bounds__(256) void k_batch_quant(uint16_t *__restrict__ xb,
-                                                     int *__restrict__ not_bf16,
+                                                     int *__restrict__ off_bf16,
                                                      const float *__restrict__ x, int T, int H) {
   // a wave: 256 columns of one token (two groups, 32 lanes x 4 columns each)
   const size_t w = (blockIdx.x * (size_t)blockDim.x + threadIdx.x) / 64;
@@ -142,7 +140,8 @@ __global__ __launch_bounds__(256) void k_batch_quant(uint16_t *__restrict__ xb,
   if (live) *reinterpret_cast<uint2 *>(xb + t * H + c) = make_uint2(h0 | (h1 << 16), h2 | (h3 << 16));
   const bool exact = bf16_round(v.x) == v.x && bf16_round(v.y) == v.y &&
                      bf16_round(v.z) == v.z && bf16_round(v.w) == v.w;
-  if (__any(!exact) && lane == 0) not_bf16[t] = 1;
+  const bool any_off = __any(!exact);
+  if (lane == 0) off_bf16[w] = any_off ? 1 : 0;  // w = t * pieces + c0 / 256
 }
 
 // ---------------------------------------------------------- router ------
@@ -196,16 +195,12 @@ __device__ __forceinline__ void rl_mfma(v4f (&acc)[4], v4f (&aab)[4], const RlRe
   }
 }
 
-// Split K (few tokens, too few tiles to fill the GPU): block z takes columns
-// [z ncols, (z + 1) ncols) and writes its partial sums at z T E; a second
-// kernel adds the partials in split order. Any summation order of the H
-// products stays within the candidates' any-order bound.
-template <int NS>  // ncols / 128 when known at compile time (fully unrolled K), else 0
+template <int NS>  // H / 128 when known at compile time (fully unrolled K), else 0
 __global__ __launch_bounds__(256) void k_router_logits_mfma(float *__restrict__ z,
                                                             float *__restrict__ zabs,
                                                             const float *__restrict__ x,
                                                             const uint16_t *__restrict__ G,
-                                                            int T, int H, int E, int ncols) {
+                                                            int T, int H, int E) {
   __shared__ __align__(16) uint16_t xs[2][64 * 136];  // [buf][token][128 + 8 pad] bf16
   const int t0 = blockIdx.x * 64, e0 = blockIdx.y * 64;
   const int tid = threadIdx.x, l = tid % 64;
@@ -218,16 +213,13 @@ __global__ __launch_bounds__(256) void k_router_logits_mfma(float *__restrict__ 
   // staging: wave w brings tokens 16 w .. + 15, two 512-byte rows per load
   // (rows past T lie beyond the range and read zeros)
   const BufRsrc rx = buf_rsrc(x + (size_t)t0 * H, 4u * (uint32_t)(min(T - t0, 64) * H));
-  const int kb = blockIdx.z * ncols;
-  z += (size_t)blockIdx.z * T * E;
-  zabs += (size_t)blockIdx.z * T * E;
-  const uint32_t xo = 4u * (uint32_t)((16 * wv + l / 32) * H + 4 * (l % 32) + kb), xstep = 8u * H;
+  const uint32_t xo = 4u * (uint32_t)((16 * wv + l / 32) * H + 4 * (l % 32)), xstep = 8u * H;
   // one range per wave (a per-lane range would serialise the loads); expert
   // rows past E lie beyond it and read zeros
   const int we = e0 + 16 * wv;
   const uint32_t grange = __builtin_amdgcn_readfirstlane(2u * (uint32_t)(max(min(E - we, 16), 0) * H));
   const BufRsrc rg = buf_rsrc(G + (size_t)min(we, E - 1) * H, grange);
-  const uint32_t go = 2u * (uint32_t)((l % 16) * H + 8 * (l / 16) + kb);
+  const uint32_t go = 2u * (uint32_t)((l % 16) * H + 8 * (l / 16));
   RlRegs R[3];
   rl_load(R[0], rx, xo, xstep, rg, go, 0);
   rl_load(R[1], rx, xo, xstep, rg, go, 128);
@@ -248,7 +240,7 @@ __global__ __launch_bounds__(256) void k_router_logits_mfma(float *__restrict__ 
     }
   } else {
     // unrolled by three so that the ring slots are compile-time
-    const int ns = ncols / 128;  // ncols % 128 == 0
+    const int ns = H / 128;  // H % 128 == 0
     for (int s = 0; s < ns; s += 3) {
       rl_load(R[2], rx, xo, xstep, rg, go, 128 * (s + 2));
       rl_mfma(acc, aab, R[0], xs[s & 1], l);
@@ -279,20 +271,6 @@ __global__ __launch_bounds__(256) void k_router_logits_mfma(float *__restrict__ 
   }
 }
 
-__global__ void k_router_logits_sum(float *__restrict__ z, float *__restrict__ zabs,
-                                    const float *__restrict__ zp, const float *__restrict__ ap,
-                                    int S, size_t n) {
-  const size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
-  if (i >= n) return;
-  float a = zp[i], b = ap[i];
-  for (int k = 1; k < S; ++k) {
-    a += zp[k * n + i];
-    b += ap[k * n + i];
-  }
-  z[i] = a;
-  zabs[i] = b;
-}
-
 // Wave argmax with the reference's tie rule (largest value, lowest index).
 __device__ __forceinline__ void wave_argmax(float &v, int &i) {
 #pragma unroll
@@ -313,12 +291,14 @@ __device__ __forceinline__ float gamma_n2(int n) {
 
 // One wave per token: approximate choices, the k-th best, and every expert
 // within the rigorous error margin of it -> candidate list (ascending id).
+// z / zabs: the router logits and sum|g*x| [T][E]; off_bf16: k_batch_quant's
+// flags, np per token.
 template <int PER>  // experts per lane: E <= 64 PER
 __global__ __launch_bounds__(256) void k_router_cand(int *__restrict__ cand,
                                                      int *__restrict__ ncand,
                                                      const float *__restrict__ z,
                                                      const float *__restrict__ zabs,
-                                                     const int *__restrict__ not_bf16,
+                                                     const int *__restrict__ off_bf16, int np,
                                                      const float *__restrict__ bias,
                                                      const int64_t *__restrict__ tid2eid,
                                                      const int *__restrict__ token_ids, int T,
@@ -331,23 +311,26 @@ __global__ __launch_bounds__(256) void k_router_cand(int *__restrict__ cand,
     if (l == 0) ncand[t] = K;
     return;
   }
-  const float *zt = z + (size_t)t * E, *at = zabs + (size_t)t * E;
   float ch[PER];
   float amax = 0.0f;
   for (int j = 0; j < PER; ++j) {
     const int e = l + 64 * j;
     ch[j] = -__builtin_inff();
     if (e < E) {
-      const float c = sqrt_softplus(zt[e]) + (bias ? bias[e] : 0.0f);
+      const size_t i = (size_t)t * E + e;
+      const float c = sqrt_softplus(z[i]) + (bias ? bias[e] : 0.0f);
       ch[j] = c == c ? c : -__builtin_inff();  // NaN is never selected
-      amax = fmaxf(amax, at[e]);
+      amax = fmaxf(amax, zabs[i]);
     }
   }
   amax = wave_max(amax) * 1.001f;
+  // is x of this token BF16-valued (the MFMA logits used its BF16 truncation)?
+  bool off = false;
+  for (int j = l; j < np; j += 64) off |= off_bf16[(size_t)t * np + j] != 0;
   // any-order summation bound, twice (approximate and sequential), plus the
   // BF16 conversion of a non-BF16 input; |d score/dz| <= 1/2; score slack
   float bound_z = 2.0f * gamma_n2(H) * amax;
-  if (not_bf16[t]) bound_z += 0x1p-8f * amax;
+  if (__any(off)) bound_z += 0x1p-8f * amax;
   const float delta = 2.0f * (0.5f * bound_z + 1e-5f);
   unsigned long long used = 0ull;  // bit j: expert l+64j taken
   float kth = -__builtin_inff();
@@ -506,97 +489,27 @@ __global__ __launch_bounds__(256) void k_router_chains(float *__restrict__ cscor
 }
 
 
-// Few tokens (a few hundred chains: a handful of waves of the kernel above,
-// each latency-bound on its x loads): one 64-thread workgroup per chain
-// instead. It stages the token's x and the expert's gate row (widened to
-// fp32) in LDS in one shot, then lane 0 runs the same column-order fmaf
-// chain from LDS at the fma latency (chain_cols). Grid-stride over chains.
-__global__ __launch_bounds__(64) void k_router_chains_small(float *__restrict__ cscore,
-                                                            float *__restrict__ cchoice,
-                                                            const int *__restrict__ cand,
-                                                            const int *__restrict__ chain_off,
-                                                            const float *__restrict__ x,
-                                                            const uint16_t *__restrict__ G,
-                                                            const float *__restrict__ bias,
-                                                            int T, int H, int E) {
-  extern __shared__ __align__(16) float rcs[];  // x, then the gate row: H floats each
-  const int l = threadIdx.x;
-  const int total = chain_off[T];
-  for (int g = blockIdx.x; g < total; g += gridDim.x) {
-    int lo = 0, hi = T;  // chain_off[lo] <= g < chain_off[lo+1]
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) / 2;
-      if (chain_off[mid] <= g) lo = mid;
-      else hi = mid;
-    }
-    const int t = lo, c = g - chain_off[t];
-    int e = cand[(size_t)t * E + c];
-    const bool ok = e >= 0 && e < E;
-    if (!ok) e = 0;
-    const BufRsrc rx = buf_rsrc(x + (size_t)t * H, 4u * (uint32_t)H);
-    const BufRsrc rg = buf_rsrc(G + (size_t)e * H, ok ? 2u * (uint32_t)H : 0u);
-    __syncthreads();  // the previous chain's reads of LDS are done
-    for (int i0 = 0; i0 < H / 4; i0 += 64 * 8) {  // x: 8 pieces of 4 per lane per round
-      uint4 v[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = buf_load16(rx, 16u * (uint32_t)(i0 + l + 64 * j));
-#pragma unroll
-      for (int j = 0; j < 8; ++j)
-        if (i0 + l + 64 * j < H / 4) reinterpret_cast<uint4 *>(rcs)[i0 + l + 64 * j] = v[j];
-    }
-    float *gs = rcs + H;
-    for (int i0 = 0; i0 < H / 8; i0 += 64 * 8) {  // gate: 8 pieces of 8 per lane per round
-      uint4 v[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = buf_load16(rg, 16u * (uint32_t)(i0 + l + 64 * j));
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int i = i0 + l + 64 * j;
-        if (i < H / 8) {
-          float4 *gp = reinterpret_cast<float4 *>(gs) + 2 * i;
-          gp[0] = make_float4(u2f(v[j].x << 16), u2f(v[j].x & 0xFFFF0000u), u2f(v[j].y << 16),
-                              u2f(v[j].y & 0xFFFF0000u));
-          gp[1] = make_float4(u2f(v[j].z << 16), u2f(v[j].z & 0xFFFF0000u), u2f(v[j].w << 16),
-                              u2f(v[j].w & 0xFFFF0000u));
-        }
-      }
-    }
-    const float be = ok && bias ? bias[e] : 0.0f;
-    __syncthreads();
-    if (l == 0) {
-      float acc = 0.0f;
-      const float4 *gp = reinterpret_cast<const float4 *>(gs);
-      const float4 *xp = reinterpret_cast<const float4 *>(rcs);
-      if (H % 256 == 0)
-        for (int cc = 0; cc < H / 4; cc += 64) acc = chain_cols<32>(gp + cc, xp + cc, acc);
-      else
-        for (int cc = 0; cc < H / 4; cc += 32) acc = chain_cols<16>(gp + cc, xp + cc, acc);
-      const float sc = ok ? sqrt_softplus(acc) : 0.0f;
-      cscore[(size_t)t * E + c] = sc;
-      cchoice[(size_t)t * E + c] = ok ? sc + be : -__builtin_inff();
-    }
-  }
-}
-
-// Per token: the reference selection over the candidates (ascending id,
-// strict '>'), weights from the unbiased scores, exchange sort by id
-// (src/dsv4/dsv4_model.c:6866-6906).
-__global__ __launch_bounds__(256) void k_router_finalize(
-    int *__restrict__ idx, float *__restrict__ wt, const int *__restrict__ cand,
-    const int *__restrict__ ncand, const float *__restrict__ cscore,
-    const float *__restrict__ cchoice, int hash, int T, int E, int K, float route_scale) {
-  // one wave per token; lane k carries route k in selection order
-  const int t = blockIdx.x * 4 + threadIdx.x / 64, l = threadIdx.x % 64;
-  if (t >= T) return;
-  const int nc = ncand[t];
-  const int *ct = cand + (size_t)t * E;
-  const float *cs = cscore + (size_t)t * E, *cc = cchoice + (size_t)t * E;
+// The routes of one token (one wave; lane k carries route k in selection
+// order): the reference selection (src/dsv4/dsv4_model.c:6866-6906) over nc
+// scored choices cc[i] of experts ct[i] (ct null: expert i, all of them),
+// strict '>' in ascending position so the lowest id wins a tie; weights from
+// the unbiased scores cs[i]; then an exchange sort by id. Hash layers take
+// the token's tid2eid experts in table order (hash_e: lane k's expert, -1
+// past K) with cs indexed by route (ct given) or by expert (ct null; an
+// expert outside [0, E) scores 0).
+__device__ __forceinline__ void router_finalize_wave(int l, int *__restrict__ idx,
+                                                     float *__restrict__ wt,
+                                                     const int *__restrict__ ct, int nc,
+                                                     const float *__restrict__ cs,
+                                                     const float *__restrict__ cc, bool hash,
+                                                     int hash_e, int E, int K,
+                                                     float route_scale) {
   int my_e = -1;
   float my_sc = 0.0f;
   if (hash) {
     if (l < K) {
-      my_e = ct[l];
-      my_sc = cs[l];
+      my_e = hash_e;
+      my_sc = ct ? cs[l] : (my_e >= 0 && my_e < E ? cs[my_e] : 0.0f);
     }
   } else {
     constexpr int PER = 16;  // nc <= E <= 1024
@@ -608,7 +521,6 @@ __global__ __launch_bounds__(256) void k_router_finalize(
       v[j] = c == c ? c : -__builtin_inff();  // NaN is never selected
     }
     for (int k = 0; k < K; ++k) {
-      // strict '>' in ascending position: the lowest position (id) wins a tie
       float bv = -__builtin_inff();
       int bi = -1;
 #pragma unroll
@@ -625,7 +537,7 @@ __global__ __launch_bounds__(256) void k_router_finalize(
           if (j == bi / 64) v[j] = -__builtin_inff();  // taken
       }
       if (l == k) {
-        my_e = ct[bi];
+        my_e = ct ? ct[bi] : bi;
         my_sc = cs[bi];
       }
     }
@@ -643,9 +555,152 @@ __global__ __launch_bounds__(256) void k_router_finalize(
     rank += (ek < my_e || (ek == my_e && k < l)) ? 1 : 0;
   }
   if (l < K) {
-    idx[(size_t)t * K + rank] = my_e;
-    wt[(size_t)t * K + rank] = my_w;
+    idx[rank] = my_e;
+    wt[rank] = my_w;
   }
+}
+
+// Candidate form (many tokens): the chains of k_router_chains.
+__global__ __launch_bounds__(256) void k_router_finalize(
+    int *__restrict__ idx, float *__restrict__ wt, const int *__restrict__ cand,
+    const int *__restrict__ ncand, const float *__restrict__ cscore,
+    const float *__restrict__ cchoice, int hash, int T, int E, int K, float route_scale) {
+  const int t = blockIdx.x * 4 + threadIdx.x / 64, l = threadIdx.x % 64;
+  if (t >= T) return;
+  const size_t r = (size_t)t * E;
+  router_finalize_wave(l, idx + (size_t)t * K, wt + (size_t)t * K, cand + r, ncand[t],
+                              cscore + r, cchoice + r, hash != 0, l < K ? cand[r + l] : -1, E,
+                              K, route_scale);
+}
+
+// ---- few tokens (T <= 256): every score exact, no candidates.
+// The router logit of (token t, expert e) is the reference's column-order
+// fmaf chain over H (dsv4_gemv_bf16, src/dsv4/dsv4_model.c:298-303, called
+// at src/dsv4/dsv4_model.c:6864-6867). Here every lane runs one whole chain:
+// a one-wave workgroup takes 8 tokens x 8 experts, lane l the token
+// t0 + l % 8 and the expert e0 + l / 8. The columns stream in chunks of 128
+// through a double-buffered LDS tile (x fp32, the gate rows widened to fp32;
+// rows padded by 16 bytes so that the 8 rows a read touches sit in distinct
+// banks), each lane's share of a chunk (four 16-byte x pieces, two of the
+// gate) loaded RX_DEPTH chunks ahead into a register ring, and the lane
+// chains from LDS at the fma latency (chain_cols). One wave per workgroup
+// because the chain reads two 16-byte LDS operands per 4 fmas per lane: the
+// LDS returns 128 bytes a clock per CU, which one wave's chain nearly fills
+// (64 tokens x 256 experts: 256 workgroups, one per CU). Scores go to
+// cscore / cchoice [T][E]; k_router_select then picks the routes.
+#define RX_TOK 8
+#define RX_EXP 8
+#define RX_COLS 128
+#define RX_ROW (RX_COLS * 4 + 16)  // LDS bytes per staged row
+#define RX_DEPTH 6
+#define RX_BUF ((RX_TOK + RX_EXP) * RX_ROW)
+
+struct RxChunk {
+  uint4 x[4], g[2];
+};
+
+// Chunks past the last (ch >= H / 128, the ring's run-out) are loaded too but
+// never used: their offsets stay below 2^31 and either fall inside the range
+// (the next row's columns) or beyond it (zeros). No select on ch: the
+// compiler would branch around the load and drain the ring.
+__device__ __forceinline__ void rx_load(RxChunk &R, BufRsrc rx, BufRsrc rg, int H, int ch) {
+  const int l = threadIdx.x;
+  const uint32_t c0 = (uint32_t)ch * RX_COLS;
+  // x piece p = l + 64 k: row p / 32, columns 4 (p % 32); gate piece p = l +
+  // 64 k: row p / 16, columns 8 (p % 16)
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int p = l + 64 * k;
+    R.x[k] = buf_load16(rx, 4u * ((uint32_t)(p / 32) * H + c0 + 4u * (p % 32)));
+  }
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int p = l + 64 * k;
+    R.g[k] = buf_load16(rg, 2u * ((uint32_t)(p / 16) * H + c0 + 8u * (p % 16)));
+  }
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+__device__ __forceinline__ void rx_store(const RxChunk &R, uint8_t *buf) {
+  const int l = threadIdx.x;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int p = l + 64 * k;
+    *reinterpret_cast<uint4 *>(buf + (p / 32) * RX_ROW + 16 * (p % 32)) = R.x[k];
+  }
+  uint8_t *gs = buf + RX_TOK * RX_ROW;
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int p = l + 64 * k;
+    const uint4 g = R.g[k];
+    float4 *d = reinterpret_cast<float4 *>(gs + (p / 16) * RX_ROW + 32 * (p % 16));
+    d[0] = make_float4(u2f(g.x << 16), u2f(g.x & 0xFFFF0000u), u2f(g.y << 16),
+                       u2f(g.y & 0xFFFF0000u));
+    d[1] = make_float4(u2f(g.z << 16), u2f(g.z & 0xFFFF0000u), u2f(g.w << 16),
+                       u2f(g.w & 0xFFFF0000u));
+  }
+}
+
+__global__ __launch_bounds__(64) void k_router_exact(float *__restrict__ cscore,
+                                                     float *__restrict__ cchoice,
+                                                     const float *__restrict__ x,
+                                                     const uint16_t *__restrict__ G,
+                                                     const float *__restrict__ bias, int T, int H,
+                                                     int E) {
+  __shared__ __align__(16) uint8_t lds[2 * RX_BUF];
+  const int l = threadIdx.x;
+  const int t0 = blockIdx.x * RX_TOK, e0 = blockIdx.y * RX_EXP;
+  const int nch = H / RX_COLS;  // H % 128 == 0
+  // rows past T or E lie beyond the ranges and read zeros
+  const BufRsrc rx = buf_rsrc(x + (size_t)t0 * H, 4u * (uint32_t)(min(T - t0, RX_TOK) * H));
+  const BufRsrc rg = buf_rsrc(G + (size_t)e0 * H, 2u * (uint32_t)(min(E - e0, RX_EXP) * H));
+  RxChunk R[RX_DEPTH];
+#pragma unroll
+  for (int d = 0; d < RX_DEPTH; ++d) rx_load(R[d], rx, rg, H, d);
+  const int tr = l % RX_TOK, er = RX_TOK + l / RX_TOK;  // this lane's LDS rows
+  float acc = 0.0f;
+  // chunk c: its ring slot c % RX_DEPTH is stored into buffer c & 1 (last
+  // read by chunk c - 2) and refilled with chunk c + RX_DEPTH; then the
+  // chain of chunk c. Whole groups of RX_DEPTH chunks, unrolled so the slots
+  // are compile-time, in a loop with one entry and one back edge and no load
+  // under a branch: the compiler's load-count waits then stay exact (each
+  // slot waits only for its own loads). Chunks past the last move run-out
+  // data and skip the chain.
+  int c0 = 0;
+  do {
+#pragma unroll
+    for (int d = 0; d < RX_DEPTH; ++d) {
+      const int c = c0 + d;
+      uint8_t *b = lds + (c & 1) * RX_BUF;
+      rx_store(R[d], b);
+      rx_load(R[d], rx, rg, H, c + RX_DEPTH);
+      __syncthreads();
+      if (c < nch)
+        acc = chain_cols<RX_COLS / 8>(reinterpret_cast<const float4 *>(b + er * RX_ROW),
+                                      reinterpret_cast<const float4 *>(b + tr * RX_ROW), acc);
+    }
+    c0 += RX_DEPTH;
+  } while (c0 < nch);
+  const int t = t0 + tr, e = e0 + l / RX_TOK;
+  if (t < T && e < E) {
+    const float sc = sqrt_softplus(acc);
+    cscore[(size_t)t * E + e] = sc;
+    cchoice[(size_t)t * E + e] = sc + (bias ? bias[e] : 0.0f);
+  }
+}
+
+// One wave per token over every expert's exact score (k_router_exact); hash
+// layers take the token's tid2eid experts.
+__global__ __launch_bounds__(256) void k_router_select(
+    int *__restrict__ idx, float *__restrict__ wt, const float *__restrict__ cscore,
+    const float *__restrict__ cchoice, const int64_t *__restrict__ tid2eid,
+    const int *__restrict__ token_ids, int T, int E, int K, float route_scale) {
+  const int t = blockIdx.x * 4 + threadIdx.x / 64, l = threadIdx.x % 64;
+  if (t >= T) return;
+  const size_t r = (size_t)t * E;
+  const int he = tid2eid && l < K ? (int)tid2eid[(size_t)token_ids[t] * K + l] : -1;
+  router_finalize_wave(l, idx + (size_t)t * K, wt + (size_t)t * K, nullptr, E, cscore + r,
+                              cchoice + r, tid2eid != nullptr, he, E, K, route_scale);
 }
 
 // -------------------------------------------------------- dispatch -------
@@ -755,6 +810,64 @@ __global__ __launch_bounds__(256) void k_dispatch_fill(
   }
 }
 
+// The same placement in one workgroup of 1024 threads for at most 1024
+// routes: expert counts, position and tile offsets, and each route's rank
+// among the earlier routes of its expert counted directly.
+__global__ __launch_bounds__(1024) void k_dispatch_small(
+    int *__restrict__ pos_token, int *__restrict__ pos_route, float *__restrict__ pos_wt,
+    int *__restrict__ pos_off, int *__restrict__ tile_off, const int *__restrict__ idx,
+    const float *__restrict__ wt, int T, int K, int E) {
+  __shared__ __align__(16) int es[1024];
+  __shared__ int sp[1024], st[1024];
+  const int i = threadIdx.x, TK = T * K;
+  int e = i < TK ? idx[i] : -1;
+  if (e >= E) e = -1;
+  es[i] = e;
+  sp[i] = 0;
+  __syncthreads();
+  if (e >= 0) atomicAdd(&sp[e], 1);
+  __syncthreads();
+  const int tot = i < E ? sp[i] : 0;
+  st[i] = (tot + GT_TN - 1) / GT_TN;
+  __syncthreads();
+  for (int o = 1; o < 1024; o <<= 1) {  // inclusive scans over experts
+    const int a = i >= o ? sp[i - o] : 0, c = i >= o ? st[i - o] : 0;
+    __syncthreads();
+    sp[i] += a;
+    st[i] += c;
+    __syncthreads();
+  }
+  if (i < E) {
+    pos_off[i] = sp[i] - tot;
+    tile_off[i] = st[i] - (tot + GT_TN - 1) / GT_TN;
+  }
+  const int P = sp[E - 1], TT = st[E - 1];
+  if (i == 0) {
+    pos_off[E] = P;
+    tile_off[E] = TT;
+    pos_off[E + 1] = P + T;
+    tile_off[E + 1] = TT + (T + GT_TN - 1) / GT_TN;
+  }
+  if (e >= 0) {
+    int rank = 0;  // earlier routes of expert e, four per LDS read
+    const int4 *e4 = reinterpret_cast<const int4 *>(es);
+    for (int k = 0; k < i / 4; ++k) {
+      const int4 v = e4[k];
+      rank += (v.x == e) + (v.y == e) + (v.z == e) + (v.w == e);
+    }
+    for (int k = i & ~3; k < i; ++k) rank += es[k] == e;
+    const int p = (e > 0 ? sp[e - 1] : 0) + rank;  // the exclusive prefix of expert e
+    pos_token[p] = i / K;
+    pos_route[p] = i % K;
+    pos_wt[p] = wt[i];
+  }
+  for (int t = i; t < T; t += 1024) {  // the shared expert: every token, slot K
+    pos_token[P + t] = t;
+    pos_route[P + t] = K;
+    pos_wt[P + t] = 1.0f;
+  }
+}
+
 // ---------------------------------------------------- grouped GEMMs ------
 // BF16 operands over a 128-K super-window. Lane group g = l/16 owns the 32
 // physical columns [32g, 32g+32) of the super-window; MFMA step q (0..3)
@@ -833,6 +946,8 @@ __device__ __forceinline__ void load_b_ops(uint4 (&op)[4], const uint8_t *bt, in
 // past the end read zeros and skip their MFMAs.
 #define GT_CHUNK 12
 #define GT_DEPTH 3
+#define GU_PD_SMALL 3  // FP4 pair slots of the gate/up loop for tiles of <= 32 positions
+#define DN_PD_SMALL 4  // and of the down loop
 #define GT_BT_BYTES (GT_TN * GT_BROW2)
 #define GT_BAD 0x80000000u  // an offset past every range (and its +48)
 
@@ -1124,7 +1239,14 @@ __device__ __forceinline__ void fp8_win_load(Fp8Win<NM> &R, const BufRsrc (&W)[N
 // NSW = in / 128 windows, fully unrolled; NF: token fragments computed (a
 // tile of at most 16 NF positions skips the MFMAs and staging of the rest).
 // FP4 weights come in window pairs, FP8 weights in window slots (above).
-template <int AFMT, int NM, int NSW, int NF>
+// PD: FP4 pair slots. Pair p (windows 2p, 2p + 1) is loaded during window
+// 2 (p - PD + 1) into slot p % PD, and the activations of window w during
+// window w - AD, AD = 2 (PD - 1), into register slot w % AD: weights and
+// activations the same distance ahead, so that the in-order wait for a
+// window's activations never waits on weights loaded for a later window.
+// A tile of one or two token fragments does little MFMA work per window and
+// needs the deeper ring to keep enough weight bytes in flight.
+template <int AFMT, int NM, int NSW, int NF, int PD = 2>
 __device__ __forceinline__ void gemm_k_loop_fast(v4f (&acc)[NM][2][4], const BufRsrc (&W)[NM],
                                                  const BufRsrc (&S)[NM], BufRsrc bsrc, int in,
                                                  int rbase, const int *rows, uint8_t *bt,
@@ -1138,24 +1260,33 @@ __device__ __forceinline__ void gemm_k_loop_fast(v4f (&acc)[NM][2][4], const Buf
   auto code = [&](int m, int f, int sw) -> uint32_t {
     return cs[m * codes_stride(in) + code_offset(rbase % GT_TM + 16 * f + l % 16, sw, l / 16)];
   };
-  Fp4Pair<NM> P[2];
+  static_assert(FP4 || PD == 2, "FP8 windows use two slots");
+  constexpr int AD = 2 * (PD - 1);
+  Fp4Pair<NM> P[PD];
   Fp8Win<NM> R8[2];
-  uint4 B[2][4];
+  uint4 B[AD][4];
   if constexpr (FP4) {
 #pragma unroll
-    for (int m = 0; m < NM; ++m) fp4_pair_load<NM>(P[0], m, W, in, rbase, 0, NSW);
+    for (int p = 0; p + 1 < PD; ++p) {
+#pragma unroll
+      for (int m = 0; m < NM; ++m) fp4_pair_load<NM>(P[p], m, W, in, rbase, 2 * p, NSW);
+      act_load(B[2 * p], 0, bsrc, in, brow, 2 * p, NSW);
+      act_load(B[2 * p], 1, bsrc, in, brow, 2 * p, NSW);
+      act_load(B[2 * p + 1], 0, bsrc, in, brow, 2 * p + 1, NSW);
+      act_load(B[2 * p + 1], 1, bsrc, in, brow, 2 * p + 1, NSW);
+    }
   } else {
     fp8_win_load<NM>(R8[0], W, S, in, rbase, 0, NSW);
     fp8_win_load<NM>(R8[1], W, S, in, rbase, 1, NSW);
+    act_load(B[0], 0, bsrc, in, brow, 0, NSW);
+    act_load(B[0], 1, bsrc, in, brow, 0, NSW);
+    act_load(B[1], 0, bsrc, in, brow, 1, NSW);
+    act_load(B[1], 1, bsrc, in, brow, 1, NSW);
   }
-  act_load(B[0], 0, bsrc, in, brow, 0, NSW);
-  act_load(B[0], 1, bsrc, in, brow, 0, NSW);
-  act_load(B[1], 0, bsrc, in, brow, 1, NSW);
-  act_load(B[1], 1, bsrc, in, brow, 1, NSW);
   // the A operand of (window w, step q): BF16 weights x block scale
   auto a_op = [&](int w, int m, int f, int q, uint32_t c) -> uint4 {
     if constexpr (FP4) {
-      const uint4 r = P[(w / 2) & 1].w[m][f][w & 1];
+      const uint4 r = P[(w / 2) % PD].w[m][f][w & 1];
       return win_op<MX_FP4>(r, r, c, q);
     } else {
       return win_op<MX_FP8>(R8[w & 1].a0[m][f], R8[w & 1].a1[m][f], R8[w & 1].code[m], q);
@@ -1178,7 +1309,7 @@ __device__ __forceinline__ void gemm_k_loop_fast(v4f (&acc)[NM][2][4], const Buf
 #pragma unroll
     for (int k = 0; k < NF; ++k)
       *reinterpret_cast<uint4 *>(bb + (tid / 16 + 16 * k) * GT_BROW2 + 16 * (tid % 16)) =
-          B[sw & 1][k];
+          B[sw % AD][k];
     __syncthreads();
     if (FP4 && sw == 0) {
       // the tile's codes were staged into LDS by every wave's direct-to-LDS
@@ -1195,7 +1326,7 @@ __device__ __forceinline__ void gemm_k_loop_fast(v4f (&acc)[NM][2][4], const Buf
           A[m][f] = a_op(0, m, f, 0, Ac[m][f]);
         }
     }
-    const bool pre = sw + 2 < NSW;
+    const bool pre = sw + AD < NSW;
     const uint8_t *brow_p = bb + (l % 16) * GT_BROW2 + (l / 16) * 64;
     uint4 Bq[2][4];
 #pragma unroll
@@ -1206,11 +1337,11 @@ __device__ __forceinline__ void gemm_k_loop_fast(v4f (&acc)[NM][2][4], const Buf
       if (pre) {
         if constexpr (FP4) {
           if (sw % 2 == 0 && q < NM)
-            fp4_pair_load<NM>(P[(sw / 2 + 1) & 1], q, W, in, rbase, sw + 2, NSW);
+            fp4_pair_load<NM>(P[(sw / 2 + PD - 1) % PD], q, W, in, rbase, sw + AD, NSW);
         } else {
           if (q == 3) fp8_win_load<NM>(R8[sw & 1], W, S, in, rbase, sw + 2, NSW);
         }
-        if (q >= 2) act_load(B[sw & 1], q - 2, bsrc, in, brow, sw + 2, NSW);
+        if (q >= 2) act_load(B[sw % AD], q - 2, bsrc, in, brow, sw + AD, NSW);
       }
       if (q + 1 < 4) {
 #pragma unroll
@@ -1313,9 +1444,11 @@ __device__ __forceinline__ void gateup_tile(const GroupedArgs &a, int e, int rt,
   if constexpr (NSW > 0) {
     const BufRsrc xr = buf_rsrc(a.xb, a.xb_bytes);
     if (AFMT == MX_FP4 && nf <= 1)
-      gemm_k_loop_fast<AFMT, 2, NSW, 1>(acc, W, S, xr, H, rbase, rows_s, bt, cs);
+      gemm_k_loop_fast<AFMT, 2, NSW, 1, AFMT == MX_FP4 ? GU_PD_SMALL : 2>(acc, W, S, xr, H, rbase,
+                                                                          rows_s, bt, cs);
     else if (AFMT == MX_FP4 && nf <= 2)
-      gemm_k_loop_fast<AFMT, 2, NSW, 2>(acc, W, S, xr, H, rbase, rows_s, bt, cs);
+      gemm_k_loop_fast<AFMT, 2, NSW, 2, AFMT == MX_FP4 ? GU_PD_SMALL : 2>(acc, W, S, xr, H, rbase,
+                                                                          rows_s, bt, cs);
     else if (AFMT == MX_FP4 && nf <= 3)
       gemm_k_loop_fast<AFMT, 2, NSW, 3>(acc, W, S, xr, H, rbase, rows_s, bt, cs);
     else
@@ -1394,8 +1527,11 @@ __device__ __forceinline__ void grouped_gateup(const GroupedArgs &a) {
   gateup_tile<AFMT, NSW>(a, e, rt, p0, np, bt, rows_s, wt_s, amax_s, s_tab, codes_s);
 }
 
+// At most 256 registers (two waves per SIMD: the LDS admits two workgroups
+// per CU).
 template <int AFMT, int NSW>
-__global__ __launch_bounds__(256) void k_grouped_gateup(GroupedArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_grouped_gateup(
+    GroupedArgs a) {
   grouped_gateup<AFMT, NSW>(a);
 }
 
@@ -1439,9 +1575,11 @@ __device__ __forceinline__ void down_tile(const GroupedArgs &a, int e, int rt, i
   if constexpr (NSW > 0) {
     const BufRsrc yr = buf_rsrc(a.yb, a.yb_bytes);
     if (AFMT == MX_FP4 && nf <= 1)
-      gemm_k_loop_fast<AFMT, 1, NSW, 1>(acc, W, S, yr, I, rbase, rows_s, bt, cs);
+      gemm_k_loop_fast<AFMT, 1, NSW, 1, AFMT == MX_FP4 ? DN_PD_SMALL : 2>(acc, W, S, yr, I, rbase,
+                                                                          rows_s, bt, cs);
     else if (AFMT == MX_FP4 && nf <= 2)
-      gemm_k_loop_fast<AFMT, 1, NSW, 2>(acc, W, S, yr, I, rbase, rows_s, bt, cs);
+      gemm_k_loop_fast<AFMT, 1, NSW, 2, AFMT == MX_FP4 ? DN_PD_SMALL : 2>(acc, W, S, yr, I, rbase,
+                                                                          rows_s, bt, cs);
     else if (AFMT == MX_FP4 && nf <= 3)
       gemm_k_loop_fast<AFMT, 1, NSW, 3>(acc, W, S, yr, I, rbase, rows_s, bt, cs);
     else
@@ -1473,7 +1611,8 @@ __device__ __forceinline__ void down_tile(const GroupedArgs &a, int e, int rt, i
 }
 
 template <int AFMT, int NSW>
-__global__ __launch_bounds__(256) void k_grouped_down(GroupedArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_grouped_down(
+    GroupedArgs a) {
   __shared__ __align__(16) uint8_t bt[2 * GT_BT_BYTES];
   __shared__ int rows_s[GT_TN];
   extern __shared__ __align__(16) uint8_t codes_s[];  // FP4: codes_stride(I)
@@ -1534,8 +1673,8 @@ using namespace dsv4;
 namespace {
 struct BatchWs {
   uint16_t *xb, *yb;
-  float *z, *zabs, *zpart, *cscore, *cchoice, *wt, *pos_wt;
-  int *not_bf16, *cand, *ncand, *chain_off, *idx, *counts, *bh, *pos_off, *tile_off, *pos_token,
+  float *z, *zabs, *cscore, *cchoice, *wt, *pos_wt;
+  int *off_bf16, *cand, *ncand, *chain_off, *idx, *counts, *bh, *pos_off, *tile_off, *pos_token,
       *pos_route;
   uint16_t *ro;
   size_t bytes;
@@ -1573,10 +1712,9 @@ int side_stream(hipStream_t st, SideStream **out) {
   return 0;
 }
 
-// Router logit K splits: 8 (512 columns each) when the token tiles alone
-// give fewer than 4 x 64 tile blocks' worth of work per 64 experts (T <= 256)
-// and H splits evenly, else 1.
-int rl_splits(int T, int H) { return (T <= 256 && H % 1024 == 0) ? 8 : 1; }
+// Up to this many tokens the router computes every score exactly
+// (k_router_exact); beyond, candidates from approximate logits.
+#define RX_MAX_TOKENS 256
 
 BatchWs batch_ws_layout(const DSV4GLayer *L, int T, void *base) {
   const size_t t = (size_t)T, K = (size_t)L->topk, E = (size_t)L->n_experts;
@@ -1592,10 +1730,9 @@ BatchWs batch_ws_layout(const DSV4GLayer *L, int T, void *base) {
     return r;
   };
   w.xb = (uint16_t *)take(t * H * 2);
-  w.not_bf16 = (int *)take(t * 4);
+  w.off_bf16 = (int *)take(t * ((H + 255) / 256) * 4);
   w.z = (float *)take(t * E * 4);
   w.zabs = (float *)take(t * E * 4);
-  w.zpart = (float *)take(rl_splits(T, (int)H) > 1 ? 2 * (size_t)rl_splits(T, (int)H) * t * E * 4 : 0);
   w.cand = (int *)take(t * E * 4);
   w.ncand = (int *)take(t * 4);
   w.chain_off = (int *)take((t + 1) * 4);
@@ -1664,14 +1801,17 @@ int dsv4g_moe_forward_batch_routes(float *out, const float *x, const DSV4GLayer 
     return dsv4g_fail(DSV4G_EINVAL, "moe_forward_batch: workspace too small (%zu < %zu)",
                       workspace_bytes, dsv4g_moe_batch_workspace_bytes(L, T));
   hipStream_t st = (hipStream_t)stream;
-  const BatchWs w = batch_ws_layout(L, T, workspace);
+  BatchWs w = batch_ws_layout(L, T, workspace);
+  // the routes go straight into the caller's buffers when given
+  if (idx_out) w.idx = idx_out;
+  if (wt_out) w.wt = wt_out;
 
-  // 1. activation quant (+ BF16-valued check for the router bound)
-  hipLaunchKernelGGL(k_fill_zero_i32, dim3((T + 255) / 256), dim3(256), 0, st, w.not_bf16, T);
+  const bool exact_router = T <= RX_MAX_TOKENS;
+  // 1. activation quant (+ BF16-valued flags)
   {
     const size_t waves = (size_t)T * ((H + 255) / 256);
     hipLaunchKernelGGL(k_batch_quant, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st, w.xb,
-                       w.not_bf16, x, T, H);
+                       w.off_bf16, x, T, H);
   }
   DSV4G_TRY(dsv4g_check_launch("batch_quant"));
   GroupedArgs g = {};
@@ -1769,49 +1909,39 @@ int dsv4g_moe_forward_batch_routes(float *out, const float *x, const DSV4GLayer 
   DSV4G_TRY(dsv4g_check_launch("grouped_down_shared"));
   if (side) DSV4G_HIP(hipEventRecord(side->join, sst));
   // 2. router
-  {
-    const int S = rl_splits(T, H);
-    const dim3 grid((T + 63) / 64, (E + 63) / 64, S);
-    float *zo = S > 1 ? w.zpart : w.z, *ao = S > 1 ? w.zpart + (size_t)S * T * E : w.zabs;
-    if (H == 4096 && S == 1)
-      hipLaunchKernelGGL(k_router_logits_mfma<32>, grid, dim3(256), 0, st, zo, ao, x, L->gate_w,
-                         T, H, E, H);
-    else if (H == 4096 && S == 8)
-      hipLaunchKernelGGL(k_router_logits_mfma<4>, grid, dim3(256), 0, st, zo, ao, x, L->gate_w,
-                         T, H, E, H / 8);
+  if (exact_router) {
+    hipLaunchKernelGGL(k_router_exact, dim3((unsigned)((T + RX_TOK - 1) / RX_TOK),
+                                            (unsigned)((E + RX_EXP - 1) / RX_EXP)),
+                       dim3(64), 0, st, w.cscore, w.cchoice, x, L->gate_w, L->bias, T, H, E);
+    hipLaunchKernelGGL(k_router_select, dim3((T + 3) / 4), dim3(256), 0, st, w.idx, w.wt,
+                       w.cscore, w.cchoice, L->tid2eid, token_ids, T, E, K, L->route_scale);
+  } else {
+    const dim3 grid((T + 63) / 64, (E + 63) / 64);
+    if (H == 4096)
+      hipLaunchKernelGGL(k_router_logits_mfma<32>, grid, dim3(256), 0, st, w.z, w.zabs, x,
+                         L->gate_w, T, H, E);
     else
-      hipLaunchKernelGGL(k_router_logits_mfma<0>, grid, dim3(256), 0, st, zo, ao, x, L->gate_w,
-                         T, H, E, H / S);
-    if (S > 1) {
-      const size_t n = (size_t)T * E;
-      hipLaunchKernelGGL(k_router_logits_sum, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
-                         w.z, w.zabs, zo, ao, S, n);
-    }
-  }
-  {
+      hipLaunchKernelGGL(k_router_logits_mfma<0>, grid, dim3(256), 0, st, w.z, w.zabs, x,
+                         L->gate_w, T, H, E);
     auto cand = E <= 64 ? k_router_cand<1> : E <= 128 ? k_router_cand<2> : E <= 256 ? k_router_cand<4>
               : E <= 512 ? k_router_cand<8> : k_router_cand<16>;
     hipLaunchKernelGGL(cand, dim3((T + 3) / 4), dim3(256), 0, st, w.cand, w.ncand, w.z, w.zabs,
-                       w.not_bf16, L->bias, L->tid2eid, token_ids, T, H, E, K);
-  }
-  hipLaunchKernelGGL(k_scan_counts, dim3(1), dim3(1024), 0, st, w.chain_off, w.ncand, T);
-  if (T <= 256) {
-    // about T (K + 2) chains: one workgroup each
-    hipLaunchKernelGGL(k_router_chains_small, dim3((unsigned)(T * (K + 4))), dim3(64),
-                       (size_t)H * 8, st, w.cscore, w.cchoice, w.cand, w.chain_off, x,
-                       L->gate_w, L->bias, T, H, E);
-  } else {
+                       w.off_bf16, (H + 255) / 256, L->bias, L->tid2eid, token_ids, T, H, E, K);
+    hipLaunchKernelGGL(k_scan_counts, dim3(1), dim3(1024), 0, st, w.chain_off, w.ncand, T);
     const long bound = (long)T * (K + 4);
     const int blocks = (int)((bound + 255) / 256 < 4096 ? (bound + 255) / 256 : 4096);
     hipLaunchKernelGGL(k_router_chains, dim3(blocks), dim3(256), 0, st, w.cscore, w.cchoice,
                        w.cand, w.chain_off, x, L->gate_w, L->bias, T, H, E);
+    hipLaunchKernelGGL(k_router_finalize, dim3((T + 3) / 4), dim3(256), 0, st, w.idx, w.wt,
+                       w.cand, w.ncand, w.cscore, w.cchoice, L->tid2eid ? 1 : 0, T, E, K,
+                       L->route_scale);
   }
-  hipLaunchKernelGGL(k_router_finalize, dim3((T + 3) / 4), dim3(256), 0, st, w.idx, w.wt,
-                     w.cand, w.ncand, w.cscore, w.cchoice, L->tid2eid ? 1 : 0, T, E, K,
-                     L->route_scale);
   DSV4G_TRY(dsv4g_check_launch("router"));
   // 3. dispatch
-  {
+  if (T * K <= 1024) {
+    hipLaunchKernelGGL(k_dispatch_small, dim3(1), dim3(1024), 0, st, w.pos_token, w.pos_route,
+                       w.pos_wt, w.pos_off, w.tile_off, w.idx, w.wt, T, K, E);
+  } else {
     const int nb = (T * K + DP_ROUTES - 1) / DP_ROUTES;
     hipLaunchKernelGGL(k_dispatch_hist, dim3(nb), dim3(256), 0, st, w.bh, w.idx, T * K, E);
     hipLaunchKernelGGL(k_dispatch_scan_blocks, dim3(E), dim3(256), 0, st, w.bh, w.counts, nb);
@@ -1836,12 +1966,6 @@ int dsv4g_moe_forward_batch_routes(float *out, const float *x, const DSV4GLayer 
   hipLaunchKernelGGL(k_combine_batch, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st,
                      out, w.ro, w.idx, T, K, H, E);
   DSV4G_TRY(dsv4g_check_launch("combine_batch"));
-  if (idx_out)
-    DSV4G_HIP(hipMemcpyAsync(idx_out, w.idx, (size_t)T * K * sizeof(int),
-                             hipMemcpyDeviceToDevice, st));
-  if (wt_out)
-    DSV4G_HIP(hipMemcpyAsync(wt_out, w.wt, (size_t)T * K * sizeof(float),
-                             hipMemcpyDeviceToDevice, st));
   return 0;
 }
 
