@@ -106,13 +106,20 @@ def bench_batch(lib, layer, n_tokens, iters):
         lib.moe_forward_batch(layer, X, workspace=ws, out=out)
     e1.record()
     torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / iters
+    ms_eager = e0.elapsed_time(e1) / iters
+    # the calls captured in one HIP graph and replayed: the device time without
+    # the host's per-launch cost (eager calls of a few-token batch can be
+    # host-bound)
+    ms = graph_time(lambda i: lib.moe_forward_batch(layer, X, workspace=ws, out=out), iters,
+                    replays=3)
     pairs = int(counts.sum()) + n_tokens              # routed + shared (token, expert) pairs
     flops = 6 * H * I * pairs
     hit = int((counts > 0).sum())
     wbytes = hit * EXPERT_BYTES + SHARED_BYTES + GATE_BYTES
     return {
-        "tokens": n_tokens, "ms_per_layer": round(ms, 4),
+        "tokens": n_tokens, "ms_per_layer": round(ms, 4), "ms_per_layer_eager": round(ms_eager, 4),
+        "timing": "HIP graph of the calls, replayed (ms_per_layer_eager: the same calls launched "
+                  "one by one)",
         "tflops": round(flops / (ms * 1e-3) / 1e12, 2),
         "frac_bf16_mfma_peak": round(flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
         "frac_fp8_mfma_peak": round(flops / (ms * 1e-3) / 1e12 / FP8_PEAK_TFLOPS, 4),

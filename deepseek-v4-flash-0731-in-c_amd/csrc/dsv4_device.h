@@ -294,4 +294,33 @@ __device__ __forceinline__ float chain_cols(const float4 *g, const float4 *x, fl
   return acc;
 }
 
+// chain_cols with the LDS reads of batch j + LA in flight while batch j is
+// chained (ring of LA + 1 batches): for callers whose reads queue behind
+// other lanes' (every lane of the wave chaining), where two batches ahead do
+// not cover the LDS latency.
+template <int NB, int LA>
+__device__ __forceinline__ float chain_cols_deep(const float4 *g, const float4 *x, float acc) {
+  constexpr int R = LA + 1;
+  float4 g0[R], g1[R], x0[R], x1[R];
+#pragma unroll
+  for (int j = 0; j < LA && j < NB; ++j) {
+    g0[j] = g[2 * j];
+    g1[j] = g[2 * j + 1];
+    x0[j] = x[2 * j];
+    x1[j] = x[2 * j + 1];
+  }
+#pragma unroll
+  for (int j = 0; j < NB; ++j) {
+    if (j + LA < NB) {
+      g0[(j + LA) % R] = g[2 * (j + LA)];
+      g1[(j + LA) % R] = g[2 * (j + LA) + 1];
+      x0[(j + LA) % R] = x[2 * (j + LA)];
+      x1[(j + LA) % R] = x[2 * (j + LA) + 1];
+    }
+    acc = chain8(g0[j % R], g1[j % R], x0[j % R], x1[j % R], acc);
+    asm volatile("" : "+v"(acc)::"memory");
+  }
+  return acc;
+}
+
 }  // namespace dsv4

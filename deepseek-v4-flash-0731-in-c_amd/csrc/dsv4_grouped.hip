@@ -583,7 +583,9 @@ __global__ __launch_bounds__(256) void k_router_finalize(
 // rows padded by 16 bytes so that the 8 rows a read touches sit in distinct
 // banks), each lane's share of a chunk (four 16-byte x pieces, two of the
 // gate) loaded RX_DEPTH chunks ahead into a register ring, and the lane
-// chains from LDS at the fma latency (chain_cols). One wave per workgroup
+// chains from LDS at the fma latency (chain_cols_deep: with every lane reading,
+// the LDS is most of a clock per chain step busy and its reads need more
+// than two batches of cover). One wave per workgroup
 // because the chain reads two 16-byte LDS operands per 4 fmas per lane: the
 // LDS returns 128 bytes a clock per CU, which one wave's chain nearly fills
 // (64 tokens x 256 experts: 256 workgroups, one per CU). Scores go to
@@ -593,6 +595,7 @@ __global__ __launch_bounds__(256) void k_router_finalize(
 #define RX_COLS 128
 #define RX_ROW (RX_COLS * 4 + 16)  // LDS bytes per staged row
 #define RX_DEPTH 6
+#define RX_LA 4  // LDS batches of 8 columns read ahead of the chain
 #define RX_BUF ((RX_TOK + RX_EXP) * RX_ROW)
 
 struct RxChunk {
@@ -676,8 +679,9 @@ __global__ __launch_bounds__(64) void k_router_exact(float *__restrict__ cscore,
       rx_load(R[d], rx, rg, H, c + RX_DEPTH);
       __syncthreads();
       if (c < nch)
-        acc = chain_cols<RX_COLS / 8>(reinterpret_cast<const float4 *>(b + er * RX_ROW),
-                                      reinterpret_cast<const float4 *>(b + tr * RX_ROW), acc);
+        acc = chain_cols_deep<RX_COLS / 8, RX_LA>(
+            reinterpret_cast<const float4 *>(b + er * RX_ROW),
+            reinterpret_cast<const float4 *>(b + tr * RX_ROW), acc);
     }
     c0 += RX_DEPTH;
   } while (c0 < nch);
@@ -890,16 +894,16 @@ struct GroupedArgs {
   int H, I, E, K, T, row_tiles;
   float limit;
   int sh_base;  // the shared expert's positions: sh_base + token (yb rows)
+  int sh_wgs;   // with the shared expert folded in: its workgroups, first
 };
 
-// (token tile, row tile) of this workgroup. Workgroups go to the 8 XCDs
+// (token tile, row tile) of workgroup b of nb. Workgroups go to the 8 XCDs
 // round-robin by index and each XCD has its own L2: when the row tiles split
 // evenly, XCD x takes row tiles [x RT/8, (x+1) RT/8) for every token tile,
 // token tile by token tile, so a row tile's weights are read into that L2
 // once and reused by every token tile, and a token tile's activations by
 // the XCD's row tiles. Otherwise row tiles vary fastest.
-__device__ __forceinline__ void tile_coords(int rt_n, int &tt, int &rt) {
-  const int b = blockIdx.x, nb = gridDim.x;
+__device__ __forceinline__ void tile_coords(int b, int nb, int rt_n, int &tt, int &rt) {
   if (rt_n % 8 == 0 && nb % 8 == 0) {
     const int per = rt_n / 8, k = b / 8;
     tt = k / per;
@@ -1177,6 +1181,19 @@ struct Fp4Pair {
   uint4 w[NM][2][2];  // [matrix][fragment][window of the pair]
 };
 
+// The fast loops permute K within each pair of windows (a 128-byte FP4 block
+// of a row, 256 K): lane group g takes the 32 contiguous bytes [32 g, 32 g +
+// 32) of the block, the first 16 as window 2 s and the rest as window
+// 2 s + 1. So window w = 2 s + h holds, for lane group g, the K range
+// 256 s + 64 g + 32 h + [0, 32): E8M0 block 8 s + 2 g + h (fp4k_block), and
+// the activations are staged in the same order (act_load). Each of the two
+// loads then touches every 32-byte sector of the row's 128-byte line; with
+// window w's bytes [64 w, 64 w + 64) per load, each load reads half a line and
+// the row's two halves are fetched apart (about 4.8 against 6.1 TB/s for the
+// same bytes, measured with a probe of the two patterns). Windows come in
+// pairs, so the window count must be even.
+__device__ __forceinline__ int fp4k_block(int sw, int g) { return 8 * (sw / 2) + 2 * g + sw % 2; }
+
 template <int NM>
 __device__ __forceinline__ void fp4_pair_load(Fp4Pair<NM> &P, int m, const BufRsrc (&W)[NM],
                                               int in, int rbase, int pw, int nsw) {
@@ -1184,22 +1201,27 @@ __device__ __forceinline__ void fp4_pair_load(Fp4Pair<NM> &P, int m, const BufRs
 #pragma unroll
   for (int f = 0; f < 2; ++f) {
     const uint32_t row = (uint32_t)(rbase + 16 * f + l % 16);
-    const uint32_t o = row * (uint32_t)(in / 2) + pw * 64u + g * 16u;
+    const uint32_t o = row * (uint32_t)(in / 2) + (pw / 2) * 128u + g * 32u;
     P.w[m][f][0] = buf_load16(W[m], pw < nsw ? o : GT_BAD);
-    P.w[m][f][1] = buf_load16(W[m], pw + 1 < nsw ? o + 64u : GT_BAD);
+    P.w[m][f][1] = buf_load16(W[m], pw + 1 < nsw ? o + 16u : GT_BAD);
   }
   __builtin_amdgcn_sched_barrier(0);
 }
 
 // half h of this thread's activation staging loads of window sw (tile rows
-// tid / 16 + 16 k, k = 2 h, 2 h + 1; 16-byte piece tid % 16)
+// tid / 16 + 16 k, k = 2 h, 2 h + 1; 16-byte piece pc = tid % 16 of the staged
+// row: K 128 sw + 8 pc, or with PERM the FP4 pair order, K 256 (sw / 2) +
+// 64 (pc / 4) + 32 (sw % 2) + 8 (pc % 4))
+template <bool PERM>
 __device__ __forceinline__ void act_load(uint4 (&b)[4], int h, BufRsrc bsrc, int in,
                                          const int (&brow)[4], int sw, int nsw) {
+  const uint32_t pc = threadIdx.x % 16;
+  const uint32_t k0 = PERM ? 256u * (sw / 2) + 32u * (sw % 2) + 64u * (pc / 4) + 8u * (pc % 4)
+                           : 128u * sw + 8u * pc;
 #pragma unroll
   for (int k = 2 * h; k < 2 * h + 2; ++k) {
     const uint32_t bo = (sw < nsw && brow[k] >= 0)
-                            ? 2u * ((uint32_t)brow[k] * (uint32_t)in + sw * 128u) +
-                                  16u * (uint32_t)(threadIdx.x % 16)
+                            ? 2u * ((uint32_t)brow[k] * (uint32_t)in + k0)
                             : GT_BAD;
     b[k] = buf_load16(bsrc, bo);
   }
@@ -1256,9 +1278,14 @@ __device__ __forceinline__ void gemm_k_loop_fast(v4f (&acc)[NM][2][4], const Buf
   int brow[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k) brow[k] = k < NF ? rows[tid / 16 + 16 * k] : -1;
-  // FP4: this lane's codes: row rbase % 128 + 16 f + l % 16, group l / 16
+  // FP4: this lane's codes: row rbase % 128 + 16 f + l % 16, block
+  // fp4k_block(sw, l / 16) (the LDS holds each row's blocks 16 j .. 16 j + 15
+  // in 16 consecutive bytes, as code_offset lays them out)
+  static_assert(!FP4 || NSW % 2 == 0, "FP4 windows come in pairs");
   auto code = [&](int m, int f, int sw) -> uint32_t {
-    return cs[m * codes_stride(in) + code_offset(rbase % GT_TM + 16 * f + l % 16, sw, l / 16)];
+    const int b = fp4k_block(sw, l / 16);
+    return cs[m * codes_stride(in) + (uint32_t)(b / 16) * 16u * GT_TM +
+              16u * (uint32_t)(rbase % GT_TM + 16 * f + l % 16) + (uint32_t)(b % 16)];
   };
   static_assert(FP4 || PD == 2, "FP8 windows use two slots");
   constexpr int AD = 2 * (PD - 1);
@@ -1270,18 +1297,18 @@ __device__ __forceinline__ void gemm_k_loop_fast(v4f (&acc)[NM][2][4], const Buf
     for (int p = 0; p + 1 < PD; ++p) {
 #pragma unroll
       for (int m = 0; m < NM; ++m) fp4_pair_load<NM>(P[p], m, W, in, rbase, 2 * p, NSW);
-      act_load(B[2 * p], 0, bsrc, in, brow, 2 * p, NSW);
-      act_load(B[2 * p], 1, bsrc, in, brow, 2 * p, NSW);
-      act_load(B[2 * p + 1], 0, bsrc, in, brow, 2 * p + 1, NSW);
-      act_load(B[2 * p + 1], 1, bsrc, in, brow, 2 * p + 1, NSW);
+      act_load<FP4>(B[2 * p], 0, bsrc, in, brow, 2 * p, NSW);
+      act_load<FP4>(B[2 * p], 1, bsrc, in, brow, 2 * p, NSW);
+      act_load<FP4>(B[2 * p + 1], 0, bsrc, in, brow, 2 * p + 1, NSW);
+      act_load<FP4>(B[2 * p + 1], 1, bsrc, in, brow, 2 * p + 1, NSW);
     }
   } else {
     fp8_win_load<NM>(R8[0], W, S, in, rbase, 0, NSW);
     fp8_win_load<NM>(R8[1], W, S, in, rbase, 1, NSW);
-    act_load(B[0], 0, bsrc, in, brow, 0, NSW);
-    act_load(B[0], 1, bsrc, in, brow, 0, NSW);
-    act_load(B[1], 0, bsrc, in, brow, 1, NSW);
-    act_load(B[1], 1, bsrc, in, brow, 1, NSW);
+    act_load<FP4>(B[0], 0, bsrc, in, brow, 0, NSW);
+    act_load<FP4>(B[0], 1, bsrc, in, brow, 0, NSW);
+    act_load<FP4>(B[1], 0, bsrc, in, brow, 1, NSW);
+    act_load<FP4>(B[1], 1, bsrc, in, brow, 1, NSW);
   }
   // the A operand of (window w, step q): BF16 weights x block scale
   auto a_op = [&](int w, int m, int f, int q, uint32_t c) -> uint4 {
@@ -1341,7 +1368,7 @@ __device__ __forceinline__ void gemm_k_loop_fast(v4f (&acc)[NM][2][4], const Buf
         } else {
           if (q == 3) fp8_win_load<NM>(R8[sw & 1], W, S, in, rbase, sw + 2, NSW);
         }
-        if (q >= 2) act_load(B[sw % AD], q - 2, bsrc, in, brow, sw + AD, NSW);
+        if (q >= 2) act_load<FP4>(B[sw % AD], q - 2, bsrc, in, brow, sw + AD, NSW);
       }
       if (q + 1 < 4) {
 #pragma unroll
@@ -1499,11 +1526,36 @@ __device__ __forceinline__ void gateup_tile(const GroupedArgs &a, int e, int rt,
   }
 }
 
-// Routed experts (FP4) and the shared expert (FP8) are separate launches,
-// each with the registers of its own format. grid.x = token-tile bound x row
-// tiles (I / 128); FP4: tiles [0, tile_off[E]) (beyond the actual count exit
-// at once); FP8: the shared expert's tiles from tile_off[E].
-template <int AFMT, int NSW>
+// The tile of a routed expert's positions (token tile tt of the dispatch's
+// tile table), or false past the last one.
+__device__ __forceinline__ bool routed_tile(const GroupedArgs &a, int tt, int &e, int &p0,
+                                            int &np) {
+  if (tt >= a.tile_off[a.E]) return false;
+  e = tile_expert(a.tile_off, a.E, tt);
+  p0 = a.pos_off[e] + (tt - a.tile_off[e]) * GT_TN;
+  np = min(GT_TN, a.pos_off[e + 1] - p0);
+  return true;
+}
+
+// The shared expert's tile tt: every token, no routing needed.
+__device__ __forceinline__ bool shared_tile(const GroupedArgs &a, int tt, int &e, int &p0,
+                                            int &np) {
+  if (tt * GT_TN >= a.T) return false;
+  e = a.E;
+  p0 = a.sh_base + tt * GT_TN;
+  np = min(GT_TN, a.T - tt * GT_TN);
+  return true;
+}
+
+// grid.x = token-tile bound x row tiles (I / 128). AFMT FP4: the routed
+// experts' tiles [0, tile_off[E]) (workgroups beyond the actual count exit at
+// once); FP8: the shared expert's tiles. SHNSW >= 0 (FP4 only): the first
+// a.sh_wgs workgroups (0: none) take the shared expert's FP8 tiles (window
+// count SHNSW, 0: generic) in the same launch (few tokens: no second stream
+// and no fork and join, at the cost of the shared expert's bytes in the
+// routed stream). At most 256 registers (two waves per SIMD: the LDS admits
+// two workgroups per CU). The LDS is declared once for both tile kinds.
+template <int AFMT, int NSW, int SHNSW>
 __device__ __forceinline__ void grouped_gateup(const GroupedArgs &a) {
   __shared__ __align__(16) uint8_t bt[2 * GT_BT_BYTES];
   __shared__ int rows_s[GT_TN];
@@ -1511,36 +1563,28 @@ __device__ __forceinline__ void grouped_gateup(const GroupedArgs &a) {
   __shared__ float amax_s[4][GT_TN];
   __shared__ uint64_t s_tab[32];
   extern __shared__ __align__(16) uint8_t codes_s[];  // FP4: 2 x codes_stride(H)
-  int tt, rt, e, p0, np;
-  tile_coords(a.row_tiles, tt, rt);
-  if (AFMT == MX_FP8) {  // the shared expert: every token, no routing needed
-    if (tt * GT_TN >= a.T) return;
-    e = a.E;
-    p0 = a.sh_base + tt * GT_TN;
-    np = min(GT_TN, a.T - tt * GT_TN);
-  } else {
-    if (tt >= a.tile_off[a.E]) return;
-    e = tile_expert(a.tile_off, a.E, tt);
-    p0 = a.pos_off[e] + (tt - a.tile_off[e]) * GT_TN;
-    np = min(GT_TN, a.pos_off[e + 1] - p0);
+  int b = blockIdx.x, nb = gridDim.x, tt, rt, e, p0, np;
+  if constexpr (SHNSW >= 0) {
+    if (b < a.sh_wgs) {
+      tile_coords(b, a.sh_wgs, a.row_tiles, tt, rt);
+      if (shared_tile(a, tt, e, p0, np))
+        gateup_tile<MX_FP8, SHNSW>(a, e, rt, p0, np, bt, rows_s, wt_s, amax_s, s_tab, codes_s);
+      return;
+    }
+    b -= a.sh_wgs;
+    nb -= a.sh_wgs;
   }
-  gateup_tile<AFMT, NSW>(a, e, rt, p0, np, bt, rows_s, wt_s, amax_s, s_tab, codes_s);
+  tile_coords(b, nb, a.row_tiles, tt, rt);
+  bool ok;
+  if constexpr (AFMT == MX_FP8) ok = shared_tile(a, tt, e, p0, np);
+  else ok = routed_tile(a, tt, e, p0, np);
+  if (ok) gateup_tile<AFMT, NSW>(a, e, rt, p0, np, bt, rows_s, wt_s, amax_s, s_tab, codes_s);
 }
 
-// At most 256 registers (two waves per SIMD: the LDS admits two workgroups
-// per CU).
-template <int AFMT, int NSW>
+template <int AFMT, int NSW, int SHNSW = -1>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_grouped_gateup(
     GroupedArgs a) {
-  grouped_gateup<AFMT, NSW>(a);
-}
-
-// The shared expert's FP8 gate/up at hidden 4096, held to 256 registers (two
-// waves per SIMD instead of one): it runs beside the router kernels, whose
-// workgroups otherwise wait for the CU slots it holds.
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void
-k_grouped_gateup_fp8_h4096(GroupedArgs a) {
-  grouped_gateup<MX_FP8, 32>(a);
+  grouped_gateup<AFMT, NSW, SHNSW>(a);
 }
 
 template <int AFMT, int NSW>  // NSW > 0: I = 128 NSW, the unrolled loop
@@ -1610,26 +1654,33 @@ __device__ __forceinline__ void down_tile(const GroupedArgs &a, int e, int rt, i
   }
 }
 
-template <int AFMT, int NSW>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_grouped_down(
-    GroupedArgs a) {
+// As k_grouped_gateup (grid, SHNSW folding, registers).
+template <int AFMT, int NSW, int SHNSW>
+__device__ __forceinline__ void grouped_down(const GroupedArgs &a) {
   __shared__ __align__(16) uint8_t bt[2 * GT_BT_BYTES];
   __shared__ int rows_s[GT_TN];
   extern __shared__ __align__(16) uint8_t codes_s[];  // FP4: codes_stride(I)
-  int tt, rt, e, p0, np;
-  tile_coords(a.row_tiles, tt, rt);
-  if (AFMT == MX_FP8) {  // the shared expert: every token, no routing needed
-    if (tt * GT_TN >= a.T) return;
-    e = a.E;
-    p0 = a.sh_base + tt * GT_TN;
-    np = min(GT_TN, a.T - tt * GT_TN);
-  } else {
-    if (tt >= a.tile_off[a.E]) return;
-    e = tile_expert(a.tile_off, a.E, tt);
-    p0 = a.pos_off[e] + (tt - a.tile_off[e]) * GT_TN;
-    np = min(GT_TN, a.pos_off[e + 1] - p0);
+  int b = blockIdx.x, nb = gridDim.x, tt, rt, e, p0, np;
+  if constexpr (SHNSW >= 0) {
+    if (b < a.sh_wgs) {
+      tile_coords(b, a.sh_wgs, a.row_tiles, tt, rt);
+      if (shared_tile(a, tt, e, p0, np)) down_tile<MX_FP8, SHNSW>(a, e, rt, p0, np, bt, rows_s, codes_s);
+      return;
+    }
+    b -= a.sh_wgs;
+    nb -= a.sh_wgs;
   }
-  down_tile<AFMT, NSW>(a, e, rt, p0, np, bt, rows_s, codes_s);
+  tile_coords(b, nb, a.row_tiles, tt, rt);
+  bool ok;
+  if constexpr (AFMT == MX_FP8) ok = shared_tile(a, tt, e, p0, np);
+  else ok = routed_tile(a, tt, e, p0, np);
+  if (ok) down_tile<AFMT, NSW>(a, e, rt, p0, np, bt, rows_s, codes_s);
+}
+
+template <int AFMT, int NSW, int SHNSW = -1>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_grouped_down(
+    GroupedArgs a) {
+  grouped_down<AFMT, NSW, SHNSW>(a);
 }
 
 // out[t][i] = bf16(((0 + r_0) + ... + r_{K-1}) + shared), routes in
@@ -1715,6 +1766,9 @@ int side_stream(hipStream_t st, SideStream **out) {
 // Up to this many tokens the router computes every score exactly
 // (k_router_exact); beyond, candidates from approximate logits.
 #define RX_MAX_TOKENS 256
+// Up to this many tokens the shared expert's tiles are folded into the
+// routed GEMM launches (one stream); beyond, they run on a second stream.
+#define FOLD_MAX_TOKENS 256
 
 BatchWs batch_ws_layout(const DSV4GLayer *L, int T, void *base) {
   const size_t t = (size_t)T, K = (size_t)L->topk, E = (size_t)L->n_experts;
@@ -1847,16 +1901,16 @@ int dsv4g_moe_forward_batch_routes(float *out, const float *x, const DSV4GLayer 
   const long routed_bound = ((long)T * K + GT_TN - 1) / GT_TN + E;
   const long shared_tiles = (T + GT_TN - 1) / GT_TN;
   const uint32_t gu_codes = 2u * codes_stride(H), dn_codes = codes_stride(I);
-  // the unrolled K loops for the model's widths, else the
-  // per-window loop
-  const void *gu4 = H == 4096 ? (const void *)k_grouped_gateup<MX_FP4, 32>
-                              : (const void *)k_grouped_gateup<MX_FP4, 0>;
-  const void *dn4 = I == 2048 ? (const void *)k_grouped_down<MX_FP4, 16>
-                              : (const void *)k_grouped_down<MX_FP4, 0>;
-  const void *gu8 = H == 4096 ? (const void *)k_grouped_gateup_fp8_h4096
-                              : (const void *)k_grouped_gateup<MX_FP8, 0>;
-  const void *dn8 = I == 2048 ? (const void *)k_grouped_down<MX_FP8, 16>
-                              : (const void *)k_grouped_down<MX_FP8, 0>;
+  // the unrolled K loops for the model's widths, else the per-window loop.
+  // Few tokens: the shared expert's tiles go into the routed launches (its
+  // second stream would cost a fork and a join, several microseconds each,
+  // on a path of a few hundred); many tokens: it runs on the second stream
+  // beside the router, which it then hides behind.
+  const bool fold = T <= FOLD_MAX_TOKENS;
+  const void *gu4 = H == 4096 ? (const void *)k_grouped_gateup<MX_FP4, 32, 32>
+                              : (const void *)k_grouped_gateup<MX_FP4, 0, 0>;
+  const void *dn4 = I == 2048 ? (const void *)k_grouped_down<MX_FP4, 16, 16>
+                              : (const void *)k_grouped_down<MX_FP4, 0, 0>;
   // calls hold this lock while they set up and enqueue: the attribute
   // flags below, and the fork and join events of two calls, cannot interleave
   std::lock_guard<std::mutex> lock(g_side_mu);
@@ -1867,10 +1921,10 @@ int dsv4g_moe_forward_batch_routes(float *out, const float *x, const DSV4GLayer 
     int dev = 0;
     DSV4G_HIP(hipGetDevice(&dev));
     if (dev >= 0 && dev < 64 && !attr_set[dev]) {
-      const void *fs[4] = {(const void *)k_grouped_gateup<MX_FP4, 32>,
-                           (const void *)k_grouped_gateup<MX_FP4, 0>,
-                           (const void *)k_grouped_down<MX_FP4, 16>,
-                           (const void *)k_grouped_down<MX_FP4, 0>};
+      const void *fs[4] = {(const void *)k_grouped_gateup<MX_FP4, 32, 32>,
+                           (const void *)k_grouped_gateup<MX_FP4, 0, 0>,
+                           (const void *)k_grouped_down<MX_FP4, 16, 16>,
+                           (const void *)k_grouped_down<MX_FP4, 0, 0>};
       for (int i = 0; i < 4; ++i)
         DSV4G_HIP(hipFuncSetAttribute(fs[i], hipFuncAttributeMaxDynamicSharedMemorySize, 65536));
       attr_set[dev] = true;
@@ -1881,7 +1935,7 @@ int dsv4g_moe_forward_batch_routes(float *out, const float *x, const DSV4GLayer 
   // GEMMs (joined before the combine). Calls hold a lock while they enqueue,
   // so the fork and join events of two calls cannot interleave.
   SideStream *side = nullptr;
-  DSV4G_TRY(side_stream(st, &side));
+  if (!fold) DSV4G_TRY(side_stream(st, &side));
   if (side) {
     // a capture forked into the side stream stays open there until its
     // caller ends it: a call that is not part of that same capture runs the
@@ -1899,14 +1953,18 @@ int dsv4g_moe_forward_batch_routes(float *out, const float *x, const DSV4GLayer 
     DSV4G_HIP(hipEventRecord(side->fork, st));
     DSV4G_HIP(hipStreamWaitEvent(sst, side->fork, 0));
   }
-  g.row_tiles = I / GT_TM;
-  hipLaunchKernelGGL((void (*)(GroupedArgs))gu8, dim3((unsigned)(shared_tiles * g.row_tiles)),
-                     dim3(256), 0, sst, g);
-  DSV4G_TRY(dsv4g_check_launch("grouped_gateup_shared"));
-  g.row_tiles = H / GT_TM;
-  hipLaunchKernelGGL((void (*)(GroupedArgs))dn8, dim3((unsigned)(shared_tiles * g.row_tiles)),
-                     dim3(256), 0, sst, g);
-  DSV4G_TRY(dsv4g_check_launch("grouped_down_shared"));
+  if (!fold) {
+    // the same kernels with a grid of exactly the shared expert's workgroups
+    // (no routed tiles; the FP8 tiles use no code buffer: no dynamic LDS)
+    g.row_tiles = I / GT_TM;
+    g.sh_wgs = (int)(shared_tiles * g.row_tiles);
+    hipLaunchKernelGGL((void (*)(GroupedArgs))gu4, dim3((unsigned)g.sh_wgs), dim3(256), 0, sst, g);
+    DSV4G_TRY(dsv4g_check_launch("grouped_gateup_shared"));
+    g.row_tiles = H / GT_TM;
+    g.sh_wgs = (int)(shared_tiles * g.row_tiles);
+    hipLaunchKernelGGL((void (*)(GroupedArgs))dn4, dim3((unsigned)g.sh_wgs), dim3(256), 0, sst, g);
+    DSV4G_TRY(dsv4g_check_launch("grouped_down_shared"));
+  }
   if (side) DSV4G_HIP(hipEventRecord(side->join, sst));
   // 2. router
   if (exact_router) {
@@ -1953,12 +2011,16 @@ int dsv4g_moe_forward_batch_routes(float *out, const float *x, const DSV4GLayer 
   DSV4G_TRY(dsv4g_check_launch("dispatch"));
   // 4-5. routed grouped GEMMs
   g.row_tiles = I / GT_TM;
-  hipLaunchKernelGGL((void (*)(GroupedArgs))gu4, dim3((unsigned)(routed_bound * g.row_tiles)),
-                     dim3(256), gu_codes, st, g);
+  g.sh_wgs = fold ? (int)(shared_tiles * g.row_tiles) : 0;
+  hipLaunchKernelGGL((void (*)(GroupedArgs))gu4,
+                     dim3((unsigned)(g.sh_wgs + routed_bound * g.row_tiles)), dim3(256), gu_codes,
+                     st, g);
   DSV4G_TRY(dsv4g_check_launch("grouped_gateup"));
   g.row_tiles = H / GT_TM;
-  hipLaunchKernelGGL((void (*)(GroupedArgs))dn4, dim3((unsigned)(routed_bound * g.row_tiles)),
-                     dim3(256), dn_codes, st, g);
+  g.sh_wgs = fold ? (int)(shared_tiles * g.row_tiles) : 0;
+  hipLaunchKernelGGL((void (*)(GroupedArgs))dn4,
+                     dim3((unsigned)(g.sh_wgs + routed_bound * g.row_tiles)), dim3(256), dn_codes,
+                     st, g);
   DSV4G_TRY(dsv4g_check_launch("grouped_down"));
   // 6. combine, after the shared expert's stream
   if (side) DSV4G_HIP(hipStreamWaitEvent(st, side->join, 0));
