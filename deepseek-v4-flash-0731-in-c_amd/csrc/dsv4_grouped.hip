@@ -112,11 +112,14 @@ __global__ void k_probe_bf16(float *D, const uint16_t *A, const uint16_t *B) {
 // The reference activation quant per (token, 128-group), stored as the
 // exact BF16 value of each quantised element (E4M3 grid value x scale), and
 // per 256-column piece of a token a flag: 1 when a value of x in it is not
-// BF16-valued (the router bound then widens), written either way.
+// BF16-valued (the router bound then widens), written either way; and
+// zeroes *zero (the route placement's counter) for the kernels after it.
 // 16-byte loads: a half wave per group.
 __global__ __launch_bounds__(256) void k_batch_quant(uint16_t *__restrict__ xb,
                                                      int *__restrict__ off_bf16,
+                                                     int *__restrict__ zero,
                                                      const float *__restrict__ x, int T, int H) {
+  if (blockIdx.x == 0 && threadIdx.x == 0) *zero = 0;
   // a wave: 256 columns of one token (two groups, 32 lanes x 4 columns each)
   const size_t w = (blockIdx.x * (size_t)blockDim.x + threadIdx.x) / 64;
   const int lane = threadIdx.x % 64;
@@ -496,7 +499,8 @@ __global__ __launch_bounds__(256) void k_router_chains(float *__restrict__ cscor
 // the unbiased scores cs[i]; then an exchange sort by id. Hash layers take
 // the token's tid2eid experts in table order (hash_e: lane k's expert, -1
 // past K) with cs indexed by route (ct given) or by expert (ct null; an
-// expert outside [0, E) scores 0).
+// expert outside [0, E) scores 0). PER: choices per lane (nc <= 64 PER).
+template <int PER>
 __device__ __forceinline__ void router_finalize_wave(int l, int *__restrict__ idx,
                                                      float *__restrict__ wt,
                                                      const int *__restrict__ ct, int nc,
@@ -512,7 +516,6 @@ __device__ __forceinline__ void router_finalize_wave(int l, int *__restrict__ id
       my_sc = ct ? cs[l] : (my_e >= 0 && my_e < E ? cs[my_e] : 0.0f);
     }
   } else {
-    constexpr int PER = 16;  // nc <= E <= 1024
     float v[PER];
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
@@ -568,7 +571,7 @@ __global__ __launch_bounds__(256) void k_router_finalize(
   const int t = blockIdx.x * 4 + threadIdx.x / 64, l = threadIdx.x % 64;
   if (t >= T) return;
   const size_t r = (size_t)t * E;
-  router_finalize_wave(l, idx + (size_t)t * K, wt + (size_t)t * K, cand + r, ncand[t],
+  router_finalize_wave<16>(l, idx + (size_t)t * K, wt + (size_t)t * K, cand + r, ncand[t],
                               cscore + r, cchoice + r, hash != 0, l < K ? cand[r + l] : -1, E,
                               K, route_scale);
 }
@@ -695,6 +698,7 @@ __global__ __launch_bounds__(64) void k_router_exact(float *__restrict__ cscore,
 
 // One wave per token over every expert's exact score (k_router_exact); hash
 // layers take the token's tid2eid experts.
+template <int PER>  // experts per lane: E <= 64 PER
 __global__ __launch_bounds__(256) void k_router_select(
     int *__restrict__ idx, float *__restrict__ wt, const float *__restrict__ cscore,
     const float *__restrict__ cchoice, const int64_t *__restrict__ tid2eid,
@@ -703,8 +707,8 @@ __global__ __launch_bounds__(256) void k_router_select(
   if (t >= T) return;
   const size_t r = (size_t)t * E;
   const int he = tid2eid && l < K ? (int)tid2eid[(size_t)token_ids[t] * K + l] : -1;
-  router_finalize_wave(l, idx + (size_t)t * K, wt + (size_t)t * K, nullptr, E, cscore + r,
-                              cchoice + r, tid2eid != nullptr, he, E, K, route_scale);
+  router_finalize_wave<PER>(l, idx + (size_t)t * K, wt + (size_t)t * K, nullptr, E, cscore + r,
+                            cchoice + r, tid2eid != nullptr, he, E, K, route_scale);
 }
 
 // -------------------------------------------------------- dispatch -------
@@ -872,6 +876,112 @@ __global__ __launch_bounds__(1024) void k_dispatch_small(
   }
 }
 
+// Few tokens (T K <= 1024, the exact router's scores): the routes of every
+// token and their placement in one launch of ceil(T / 16) workgroups of 1024
+// threads. Wave w of workgroup b selects the routes of token 16 b + w
+// (router_finalize_wave), written through; each workgroup then counts itself
+// done on cnt[0] (zeroed by k_batch_quant) once its stores are complete, and
+// the last one places every route: route i (thread i, in (token, route)
+// order) takes position pos_off[e] + (routes of expert e in earlier waves:
+// per-wave histograms) + (earlier lanes of its own wave with expert e) - the
+// order k_dispatch_fill gives. Expert and tile offsets and the shared
+// expert's positions as there. No workgroup waits for another.
+#define SD_WAVES 16
+template <typename V>
+__device__ __forceinline__ V ld_agent(const V *p) {
+  return __hip_atomic_load(const_cast<V *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename V>
+__device__ __forceinline__ void st_agent(V *p, V v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int PER>  // experts per lane: E <= 64 PER
+__global__ __launch_bounds__(1024) void k_select_dispatch(
+    int *__restrict__ idx, float *__restrict__ wt, int *__restrict__ cnt,
+    int *__restrict__ pos_token, int *__restrict__ pos_route, float *__restrict__ pos_wt,
+    int *__restrict__ pos_off, int *__restrict__ tile_off, const float *__restrict__ cscore,
+    const float *__restrict__ cchoice, const int64_t *__restrict__ tid2eid,
+    const int *__restrict__ token_ids, int T, int E, int K, float route_scale) {
+  __shared__ int es[1024];
+  __shared__ float wsel[1024];
+  __shared__ int hist[SD_WAVES][1024];  // E <= 1024
+  __shared__ int sp[1024], st[1024];
+  __shared__ int s_last;
+  const int i = threadIdx.x, wv = i / 64, l = i % 64, TK = T * K;
+  {
+    const int t = blockIdx.x * SD_WAVES + wv;
+    if (t < T) {
+      const size_t r = (size_t)t * E;
+      const int he = tid2eid && l < K ? (int)tid2eid[(size_t)token_ids[t] * K + l] : -1;
+      router_finalize_wave<PER>(l, es + t % SD_WAVES * K, wsel + t % SD_WAVES * K, nullptr, E,
+                                cscore + r, cchoice + r, tid2eid != nullptr, he, E, K,
+                                route_scale);
+      if (l < K) {
+        st_agent(idx + (size_t)t * K + l, es[t % SD_WAVES * K + l]);
+        st_agent(wt + (size_t)t * K + l, wsel[t % SD_WAVES * K + l]);
+      }
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (i == 0)
+    s_last = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+             (int)gridDim.x - 1;
+  __syncthreads();
+  if (!s_last) return;
+  for (int e = l; e < E; e += 64) hist[wv][e] = 0;
+  int e = i < TK ? ld_agent(idx + i) : -1;
+  const float we = i < TK ? ld_agent(wt + i) : 0.0f;
+  if (e >= E) e = -1;  // never dispatched (its slot adds nothing in the combine)
+  // earlier lanes of this wave with the same expert
+  int r_in = 0;
+  for (int k = 0; k < 64; ++k) {
+    const int ek = __builtin_amdgcn_readlane(e, k);
+    r_in += (k < l && ek == e) ? 1 : 0;
+  }
+  __syncthreads();
+  if (e >= 0) atomicAdd(&hist[wv][e], 1);
+  __syncthreads();
+  int tot = 0;
+  if (i < E)
+    for (int w = 0; w < SD_WAVES; ++w) tot += hist[w][i];
+  sp[i] = tot;
+  st[i] = (tot + GT_TN - 1) / GT_TN;
+  __syncthreads();
+  for (int o = 1; o < 1024; o <<= 1) {  // inclusive scans over experts
+    const int a = i >= o ? sp[i - o] : 0, c = i >= o ? st[i - o] : 0;
+    __syncthreads();
+    sp[i] += a;
+    st[i] += c;
+    __syncthreads();
+  }
+  if (i < E) {
+    pos_off[i] = sp[i] - tot;
+    tile_off[i] = st[i] - (tot + GT_TN - 1) / GT_TN;
+  }
+  const int P = sp[E - 1], TT = st[E - 1];
+  if (i == 0) {
+    pos_off[E] = P;
+    tile_off[E] = TT;
+    pos_off[E + 1] = P + T;
+    tile_off[E + 1] = TT + (T + GT_TN - 1) / GT_TN;
+  }
+  if (e >= 0) {
+    int before = 0;  // routes of expert e in earlier waves
+    for (int w = 0; w < wv; ++w) before += hist[w][e];
+    const int p = (e > 0 ? sp[e - 1] : 0) + before + r_in;
+    pos_token[p] = i / K;
+    pos_route[p] = i % K;
+    pos_wt[p] = we;
+  }
+  for (int t = i; t < T; t += 1024) {  // the shared expert: every token, slot K
+    pos_token[P + t] = t;
+    pos_route[P + t] = K;
+    pos_wt[P + t] = 1.0f;
+  }
+}
+
 // ---------------------------------------------------- grouped GEMMs ------
 // BF16 operands over a 128-K super-window. Lane group g = l/16 owns the 32
 // physical columns [32g, 32g+32) of the super-window; MFMA step q (0..3)
@@ -951,7 +1061,7 @@ __device__ __forceinline__ void load_b_ops(uint4 (&op)[4], const uint8_t *bt, in
 #define GT_CHUNK 12
 #define GT_DEPTH 3
 #define GU_PD_SMALL 3  // FP4 pair slots of the gate/up loop for tiles of <= 32 positions
-#define DN_PD_SMALL 4  // and of the down loop
+#define DN_PD_SMALL 3  // and of the down loop
 #define GT_BT_BYTES (GT_TN * GT_BROW2)
 #define GT_BAD 0x80000000u  // an offset past every range (and its +48)
 
@@ -1654,7 +1764,8 @@ __device__ __forceinline__ void down_tile(const GroupedArgs &a, int e, int rt, i
   }
 }
 
-// As k_grouped_gateup (grid, SHNSW folding, registers).
+// As k_grouped_gateup (grid, SHNSW folding), at most 168 registers: three
+// waves per SIMD, as many as the LDS admits workgroups per CU.
 template <int AFMT, int NSW, int SHNSW>
 __device__ __forceinline__ void grouped_down(const GroupedArgs &a) {
   __shared__ __align__(16) uint8_t bt[2 * GT_BT_BYTES];
@@ -1678,7 +1789,7 @@ __device__ __forceinline__ void grouped_down(const GroupedArgs &a) {
 }
 
 template <int AFMT, int NSW, int SHNSW = -1>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_grouped_down(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k_grouped_down(
     GroupedArgs a) {
   grouped_down<AFMT, NSW, SHNSW>(a);
 }
@@ -1725,7 +1836,7 @@ namespace {
 struct BatchWs {
   uint16_t *xb, *yb;
   float *z, *zabs, *cscore, *cchoice, *wt, *pos_wt;
-  int *off_bf16, *cand, *ncand, *chain_off, *idx, *counts, *bh, *pos_off, *tile_off, *pos_token,
+  int *off_bf16, *rcnt, *cand, *ncand, *chain_off, *idx, *counts, *bh, *pos_off, *tile_off, *pos_token,
       *pos_route;
   uint16_t *ro;
   size_t bytes;
@@ -1785,6 +1896,7 @@ BatchWs batch_ws_layout(const DSV4GLayer *L, int T, void *base) {
   };
   w.xb = (uint16_t *)take(t * H * 2);
   w.off_bf16 = (int *)take(t * ((H + 255) / 256) * 4);
+  w.rcnt = (int *)take(4);
   w.z = (float *)take(t * E * 4);
   w.zabs = (float *)take(t * E * 4);
   w.cand = (int *)take(t * E * 4);
@@ -1865,7 +1977,7 @@ int dsv4g_moe_forward_batch_routes(float *out, const float *x, const DSV4GLayer 
   {
     const size_t waves = (size_t)T * ((H + 255) / 256);
     hipLaunchKernelGGL(k_batch_quant, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st, w.xb,
-                       w.off_bf16, x, T, H);
+                       w.off_bf16, w.rcnt, x, T, H);
   }
   DSV4G_TRY(dsv4g_check_launch("batch_quant"));
   GroupedArgs g = {};
@@ -1971,8 +2083,13 @@ int dsv4g_moe_forward_batch_routes(float *out, const float *x, const DSV4GLayer 
     hipLaunchKernelGGL(k_router_exact, dim3((unsigned)((T + RX_TOK - 1) / RX_TOK),
                                             (unsigned)((E + RX_EXP - 1) / RX_EXP)),
                        dim3(64), 0, st, w.cscore, w.cchoice, x, L->gate_w, L->bias, T, H, E);
-    hipLaunchKernelGGL(k_router_select, dim3((T + 3) / 4), dim3(256), 0, st, w.idx, w.wt,
-                       w.cscore, w.cchoice, L->tid2eid, token_ids, T, E, K, L->route_scale);
+    if (T * K > 1024) {
+      auto sel = E <= 64 ? k_router_select<1> : E <= 128 ? k_router_select<2>
+               : E <= 256 ? k_router_select<4> : E <= 512 ? k_router_select<8>
+                          : k_router_select<16>;
+      hipLaunchKernelGGL(sel, dim3((T + 3) / 4), dim3(256), 0, st, w.idx, w.wt, w.cscore,
+                         w.cchoice, L->tid2eid, token_ids, T, E, K, L->route_scale);
+    }
   } else {
     const dim3 grid((T + 63) / 64, (E + 63) / 64);
     if (H == 4096)
@@ -1996,7 +2113,15 @@ int dsv4g_moe_forward_batch_routes(float *out, const float *x, const DSV4GLayer 
   }
   DSV4G_TRY(dsv4g_check_launch("router"));
   // 3. dispatch
-  if (T * K <= 1024) {
+  if (exact_router && T * K <= 1024) {
+    auto sd = E <= 64 ? k_select_dispatch<1> : E <= 128 ? k_select_dispatch<2>
+            : E <= 256 ? k_select_dispatch<4> : E <= 512 ? k_select_dispatch<8>
+                       : k_select_dispatch<16>;
+    hipLaunchKernelGGL(sd, dim3((unsigned)((T + SD_WAVES - 1) / SD_WAVES)), dim3(1024), 0, st,
+                       w.idx, w.wt, w.rcnt, w.pos_token, w.pos_route, w.pos_wt, w.pos_off,
+                       w.tile_off, w.cscore, w.cchoice, L->tid2eid, token_ids, T, E, K,
+                       L->route_scale);
+  } else if (T * K <= 1024) {
     hipLaunchKernelGGL(k_dispatch_small, dim3(1), dim3(1024), 0, st, w.pos_token, w.pos_route,
                        w.pos_wt, w.pos_off, w.tile_off, w.idx, w.wt, T, K, E);
   } else {
