@@ -1657,15 +1657,16 @@ __device__ __forceinline__ bool shared_tile(const GroupedArgs &a, int tt, int &e
   return true;
 }
 
-// grid.x = token-tile bound x row tiles (I / 128). AFMT FP4: the routed
-// experts' tiles [0, tile_off[E]) (workgroups beyond the actual count exit at
-// once); FP8: the shared expert's tiles. SHNSW >= 0 (FP4 only): the first
-// a.sh_wgs workgroups (0: none) take the shared expert's FP8 tiles (window
-// count SHNSW, 0: generic) in the same launch (few tokens: no second stream
-// and no fork and join, at the cost of the shared expert's bytes in the
-// routed stream). At most 256 registers (two waves per SIMD: the LDS admits
-// two workgroups per CU). The LDS is declared once for both tile kinds.
-template <int AFMT, int NSW, int SHNSW>
+// The first a.sh_wgs workgroups (0: none) take the shared expert's FP8 tiles
+// (K windows SHNSW, 0: the generic loop): up to 256 tokens in the same launch
+// as the routed tiles (no second stream, no fork and join, at the cost of the
+// shared expert's bytes in the routed stream); beyond, as a launch of their
+// own on the second stream with a grid of exactly those workgroups. The
+// others take the routed experts' FP4 tiles (K windows NSW): grid = token-
+// tile bound x row tiles (I / 128), workgroups past tile_off[E] exit at once.
+// At most 256 registers (two waves per SIMD: the LDS admits two workgroups
+// per CU). The LDS is declared once for both tile kinds.
+template <int NSW, int SHNSW>
 __device__ __forceinline__ void grouped_gateup(const GroupedArgs &a) {
   __shared__ __align__(16) uint8_t bt[2 * GT_BT_BYTES];
   __shared__ int rows_s[GT_TN];
@@ -1673,28 +1674,23 @@ __device__ __forceinline__ void grouped_gateup(const GroupedArgs &a) {
   __shared__ float amax_s[4][GT_TN];
   __shared__ uint64_t s_tab[32];
   extern __shared__ __align__(16) uint8_t codes_s[];  // FP4: 2 x codes_stride(H)
-  int b = blockIdx.x, nb = gridDim.x, tt, rt, e, p0, np;
-  if constexpr (SHNSW >= 0) {
-    if (b < a.sh_wgs) {
-      tile_coords(b, a.sh_wgs, a.row_tiles, tt, rt);
-      if (shared_tile(a, tt, e, p0, np))
-        gateup_tile<MX_FP8, SHNSW>(a, e, rt, p0, np, bt, rows_s, wt_s, amax_s, s_tab, codes_s);
-      return;
-    }
-    b -= a.sh_wgs;
-    nb -= a.sh_wgs;
+  int b = blockIdx.x, tt, rt, e, p0, np;
+  if (b < a.sh_wgs) {
+    tile_coords(b, a.sh_wgs, a.row_tiles, tt, rt);
+    if (shared_tile(a, tt, e, p0, np))
+      gateup_tile<MX_FP8, SHNSW>(a, e, rt, p0, np, bt, rows_s, wt_s, amax_s, s_tab, codes_s);
+    return;
   }
-  tile_coords(b, nb, a.row_tiles, tt, rt);
-  bool ok;
-  if constexpr (AFMT == MX_FP8) ok = shared_tile(a, tt, e, p0, np);
-  else ok = routed_tile(a, tt, e, p0, np);
-  if (ok) gateup_tile<AFMT, NSW>(a, e, rt, p0, np, bt, rows_s, wt_s, amax_s, s_tab, codes_s);
+  b -= a.sh_wgs;
+  tile_coords(b, (int)gridDim.x - a.sh_wgs, a.row_tiles, tt, rt);
+  if (routed_tile(a, tt, e, p0, np))
+    gateup_tile<MX_FP4, NSW>(a, e, rt, p0, np, bt, rows_s, wt_s, amax_s, s_tab, codes_s);
 }
 
-template <int AFMT, int NSW, int SHNSW = -1>
+template <int NSW, int SHNSW>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_grouped_gateup(
     GroupedArgs a) {
-  grouped_gateup<AFMT, NSW, SHNSW>(a);
+  grouped_gateup<NSW, SHNSW>(a);
 }
 
 template <int AFMT, int NSW>  // NSW > 0: I = 128 NSW, the unrolled loop
@@ -1764,34 +1760,29 @@ __device__ __forceinline__ void down_tile(const GroupedArgs &a, int e, int rt, i
   }
 }
 
-// As k_grouped_gateup (grid, SHNSW folding), at most 168 registers: three
-// waves per SIMD, as many as the LDS admits workgroups per CU.
-template <int AFMT, int NSW, int SHNSW>
+// As k_grouped_gateup (shared and routed tiles), at most 168 registers:
+// three waves per SIMD, as many as the LDS admits workgroups per CU.
+template <int NSW, int SHNSW>
 __device__ __forceinline__ void grouped_down(const GroupedArgs &a) {
   __shared__ __align__(16) uint8_t bt[2 * GT_BT_BYTES];
   __shared__ int rows_s[GT_TN];
   extern __shared__ __align__(16) uint8_t codes_s[];  // FP4: codes_stride(I)
-  int b = blockIdx.x, nb = gridDim.x, tt, rt, e, p0, np;
-  if constexpr (SHNSW >= 0) {
-    if (b < a.sh_wgs) {
-      tile_coords(b, a.sh_wgs, a.row_tiles, tt, rt);
-      if (shared_tile(a, tt, e, p0, np)) down_tile<MX_FP8, SHNSW>(a, e, rt, p0, np, bt, rows_s, codes_s);
-      return;
-    }
-    b -= a.sh_wgs;
-    nb -= a.sh_wgs;
+  int b = blockIdx.x, tt, rt, e, p0, np;
+  if (b < a.sh_wgs) {
+    tile_coords(b, a.sh_wgs, a.row_tiles, tt, rt);
+    if (shared_tile(a, tt, e, p0, np))
+      down_tile<MX_FP8, SHNSW>(a, e, rt, p0, np, bt, rows_s, codes_s);
+    return;
   }
-  tile_coords(b, nb, a.row_tiles, tt, rt);
-  bool ok;
-  if constexpr (AFMT == MX_FP8) ok = shared_tile(a, tt, e, p0, np);
-  else ok = routed_tile(a, tt, e, p0, np);
-  if (ok) down_tile<AFMT, NSW>(a, e, rt, p0, np, bt, rows_s, codes_s);
+  b -= a.sh_wgs;
+  tile_coords(b, (int)gridDim.x - a.sh_wgs, a.row_tiles, tt, rt);
+  if (routed_tile(a, tt, e, p0, np)) down_tile<MX_FP4, NSW>(a, e, rt, p0, np, bt, rows_s, codes_s);
 }
 
-template <int AFMT, int NSW, int SHNSW = -1>
+template <int NSW, int SHNSW>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k_grouped_down(
     GroupedArgs a) {
-  grouped_down<AFMT, NSW, SHNSW>(a);
+  grouped_down<NSW, SHNSW>(a);
 }
 
 // out[t][i] = bf16(((0 + r_0) + ... + r_{K-1}) + shared), routes in
@@ -2019,10 +2010,10 @@ int dsv4g_moe_forward_batch_routes(float *out, const float *x, const DSV4GLayer 
   // on a path of a few hundred); many tokens: it runs on the second stream
   // beside the router, which it then hides behind.
   const bool fold = T <= FOLD_MAX_TOKENS;
-  const void *gu4 = H == 4096 ? (const void *)k_grouped_gateup<MX_FP4, 32, 32>
-                              : (const void *)k_grouped_gateup<MX_FP4, 0, 0>;
-  const void *dn4 = I == 2048 ? (const void *)k_grouped_down<MX_FP4, 16, 16>
-                              : (const void *)k_grouped_down<MX_FP4, 0, 0>;
+  const void *gu4 = H == 4096 ? (const void *)k_grouped_gateup<32, 32>
+                              : (const void *)k_grouped_gateup<0, 0>;
+  const void *dn4 = I == 2048 ? (const void *)k_grouped_down<16, 16>
+                              : (const void *)k_grouped_down<0, 0>;
   // calls hold this lock while they set up and enqueue: the attribute
   // flags below, and the fork and join events of two calls, cannot interleave
   std::lock_guard<std::mutex> lock(g_side_mu);
@@ -2033,10 +2024,10 @@ int dsv4g_moe_forward_batch_routes(float *out, const float *x, const DSV4GLayer 
     int dev = 0;
     DSV4G_HIP(hipGetDevice(&dev));
     if (dev >= 0 && dev < 64 && !attr_set[dev]) {
-      const void *fs[4] = {(const void *)k_grouped_gateup<MX_FP4, 32, 32>,
-                           (const void *)k_grouped_gateup<MX_FP4, 0, 0>,
-                           (const void *)k_grouped_down<MX_FP4, 16, 16>,
-                           (const void *)k_grouped_down<MX_FP4, 0, 0>};
+      const void *fs[4] = {(const void *)k_grouped_gateup<32, 32>,
+                           (const void *)k_grouped_gateup<0, 0>,
+                           (const void *)k_grouped_down<16, 16>,
+                           (const void *)k_grouped_down<0, 0>};
       for (int i = 0; i < 4; ++i)
         DSV4G_HIP(hipFuncSetAttribute(fs[i], hipFuncAttributeMaxDynamicSharedMemorySize, 65536));
       attr_set[dev] = true;
