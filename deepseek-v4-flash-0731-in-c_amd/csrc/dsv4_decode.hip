@@ -1121,8 +1121,21 @@ __device__ __forceinline__ void dec_route_down(const DecArgs &a, int t, int r0, 
                         s_i))
       return;
     {
-      const uint32_t *src = dec_tok(a.qc, a, t) + (size_t)k0 * (I / 4);
-      for (int i = tid; i < nk * (I / 4); i += 256) qy[i] = ld_dev(src + i);
+      // coherent 8-byte loads, eight in flight per thread before the first
+      // wait (one at a time, each behind its own wait, this copy took most
+      // of the down phase)
+      const uint64_t *src = reinterpret_cast<const uint64_t *>(dec_tok(a.qc, a, t) +
+                                                               (size_t)k0 * (I / 4));
+      uint64_t *dst = reinterpret_cast<uint64_t *>(qy);
+      const int n8 = nk * (I / 8);  // I % 128 == 0: whole 8-byte words
+      for (int i0 = tid; i0 < n8; i0 += 256 * 8) {
+        uint64_t v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = i0 + 256 * j < n8 ? ld_dev(src + i0 + 256 * j) : 0ull;
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          if (i0 + 256 * j < n8) dst[i0 + 256 * j] = v[j];
+      }
       const float *ss = dec_tok(a.qcs, a, t) + (size_t)k0 * (I / 128);
       for (int i = tid; i < nk * (I / 128); i += 256)
         qys[(i / (I / 128)) * 32 + i % (I / 128)] = ld_dev(ss + i);
