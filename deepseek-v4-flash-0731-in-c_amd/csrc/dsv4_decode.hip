@@ -951,12 +951,12 @@ __device__ __forceinline__ void dec_routed_items(const DecArgs &a, int t, int l0
   __syncthreads();  // LDS (candidates, activation) is rewritten by the next token
 }
 
-// Streaming workgroup j of n_stream: token 0's quantised activation into LDS
-// while the router runs, the candidates of token 0 (dec_candidates), its
-// tiles of the shared gate/up (j, j + S, ...), then per token its routed
-// gate/up items from l0 = j rotated past the workgroups with shared tiles
-// (l0, l0 + S, ...), then its tiles of the shared down rows (rotated
-// likewise). Each workgroup holds one item at a time: per unit of work the
+// Streaming workgroup j of n_stream: its tiles of the shared gate/up (js, js
+// + S, ..., js = j - E mod S: the workgroups after the routing ones, from the
+// start, while the router runs), token 0's quantised activation into LDS, the
+// candidates of token 0 (dec_candidates), then per token its routed gate/up
+// items from l0 = js rotated past the workgroups with shared tiles (l0, l0 +
+// S, ...), then its tiles of the shared down rows (rotated likewise). Each workgroup holds one item at a time: per unit of work the
 // latency of a load under full memory traffic, so every workgroup gets about
 // the same number of units (a shared tile counts as two).
 __device__ __forceinline__ void dec_stream_block(const DecArgs &a, int j, float *lds, float *s_y,
@@ -965,18 +965,19 @@ __device__ __forceinline__ void dec_stream_block(const DecArgs &a, int j, float 
   const int S = a.n_stream;
   const uint64_t tabv = libm_table_load();
   const int t8 = (a.I + FP8_TR / 2 - 1) / (FP8_TR / 2), nsh = a.n * t8;
-  const int rot = (j + S - nsh % S) % S;
-  const bool sh = j < nsh;
+  const int js = (j + S - a.E % S) % S;
+  const int rot = (js + S - nsh % S) % S;
+  const bool sh = js < nsh;
   const DecLds L = dec_lds(lds, fp4_geom_np(a.H, DEC_NP), a.H);
   float *s_v = L.aux;  // more than 256 experts: the candidates' choices
-  if (!sh) dec_quant_x(a.x, a.H, L.xq8, nullptr, L.xqs);
   libm_table_store(s_tab, tabv);
-  int nc = dec_candidates(a, 0, s_cand, s_sel, s_v, s_i);
-  if (nc < 0) return;
-  for (int i = j; i < nsh; i += S) {
+  for (int i = js; i < nsh; i += S) {
     __syncthreads();  // LDS of the previous tile
     dec_shared_gu(a, i / t8, i % t8, lds, s_y, s_tab);
   }
+  if (!sh) dec_quant_x(a.x, a.H, L.xq8, nullptr, L.xqs);
+  int nc = dec_candidates(a, 0, s_cand, s_sel, s_v, s_i);
+  if (nc < 0) return;
   for (int t = 0; t < a.n; ++t) {
     if (t > 0 && (nc = dec_candidates(a, t, s_cand, s_sel, s_v, s_i)) < 0) return;
     const int nitems = nc * a.gu_tiles;
