@@ -516,32 +516,51 @@ __device__ __forceinline__ void router_finalize_wave(int l, int *__restrict__ id
       my_sc = ct ? cs[l] : (my_e >= 0 && my_e < E ? cs[my_e] : 0.0f);
     }
   } else {
-    float v[PER];
+    // choices, scores and ids all loaded up front (a score or id fetched
+    // per route would be a dependent memory round trip per route)
+    float v[PER], sv[PER];
+    int ev[PER];
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
       const int i = l + 64 * j;
       const float c = i < nc ? cc[i] : -__builtin_inff();
       v[j] = c == c ? c : -__builtin_inff();  // NaN is never selected
+      sv[j] = i < nc ? cs[i] : 0.0f;
+      ev[j] = ct && i < nc ? ct[i] : i;
     }
     for (int k = 0; k < K; ++k) {
-      float bv = -__builtin_inff();
-      int bi = -1;
+      // the largest choice, the lowest index among equals (the reference's
+      // strict '>' in ascending id): DPP reductions, no LDS round trips
+      float m = -__builtin_inff();
+      int mj = -1;
 #pragma unroll
       for (int j = 0; j < PER; ++j)
-        if (v[j] > bv) {
-          bv = v[j];
-          bi = l + 64 * j;
+        if (v[j] > m) {
+          m = v[j];
+          mj = j;
         }
-      wave_argmax(bv, bi);
-      if (bi < 0 || !(bv > -__builtin_inff())) continue;  // nothing left: route k empty
+      const float wm = wave_max_dpp(m);
+      if (!(wm > -__builtin_inff())) continue;  // nothing left: route k empty
+      const int bi = wave_min_dpp(mj >= 0 && m == wm ? l + 64 * mj : 0x7fffffff);
+      // bi is wave-uniform: its slot j, then the value from its lane
+      float bs = 0.0f;
+      int be = 0;
+#pragma unroll
+      for (int j = 0; j < PER; ++j)
+        if (j == bi / 64) {
+          bs = sv[j];
+          be = ev[j];
+        }
+      bs = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bs), bi % 64));
+      be = __builtin_amdgcn_readlane(be, bi % 64);
       if (bi % 64 == l) {
 #pragma unroll
         for (int j = 0; j < PER; ++j)
           if (j == bi / 64) v[j] = -__builtin_inff();  // taken
       }
       if (l == k) {
-        my_e = ct ? ct[bi] : bi;
-        my_sc = cs[bi];
+        my_e = be;
+        my_sc = bs;
       }
     }
   }
