@@ -940,13 +940,18 @@ __device__ __forceinline__ void dec_routed_items(const DecArgs &a, int t, int l0
   }
   Fp4RegsT<DEC_NP> A;
   fp4_tile_x_lds(A, L.xq8, L.xqs, q);  // the lane's activation group: the same for every item
+  // the next item's loads go out as soon as this item's partials are in LDS
+  // (its weight registers are free then), so they are in flight while this
+  // item's group chains and SwiGLU run
+  int c, r0;
+  bool live;
+  dec_gu_load(a, A, l0, nitems, s_cand, q, c, r0, live);
   for (int l = l0; l < le; l += S) {
-    int c, r0;
-    bool live;
-    dec_gu_load(a, A, l, nitems, s_cand, q, c, r0, live);
-    if (!live) continue;
-    fp4_tile_partials(A, a.I, r0, q, L.ps, L.cl, true);
-    dec_gu_chain(a, t, c, r0, q, L, s_y, s_tab);
+    const int cc = c, rr = r0;
+    const bool lv = live;
+    if (lv) fp4_tile_partials(A, a.I, rr, q, L.ps, L.cl, true);
+    if (l + S < le) dec_gu_load(a, A, l + S, nitems, s_cand, q, c, r0, live);
+    if (lv) dec_gu_chain(a, t, cc, rr, q, L, s_y, s_tab);
   }
   __syncthreads();  // LDS (candidates, activation) is rewritten by the next token
 }
