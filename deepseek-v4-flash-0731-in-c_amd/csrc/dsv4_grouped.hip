@@ -1804,6 +1804,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
   grouped_down<NSW, SHNSW>(a);
 }
 
+#define CB_SLOTS 8  // route slots (K + 1) summed from registers
+
 // out[t][i] = bf16(((0 + r_0) + ... + r_{K-1}) + shared), routes in
 // ascending expert id (src/dsv4/dsv4_model.c:7096-7112).
 // out[t][c .. c + 7]: the routes in ascending expert id, then the shared
@@ -1822,14 +1824,31 @@ __global__ void k_combine_batch(float *__restrict__ out, const uint16_t *__restr
   float acc[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
-  for (int k = 0; k <= K; ++k) {
-    if (k < K && (unsigned)idx[t * K + k] >= (unsigned)E) continue;
-    const uint4 v = *reinterpret_cast<const uint4 *>(r + (size_t)k * H);
+  auto add = [&](const uint4 v) {
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       acc[2 * j] += u2f(w[j] << 16);
       acc[2 * j + 1] += u2f(w[j] & 0xFFFF0000u);
+    }
+  };
+  if (K + 1 <= CB_SLOTS) {
+    // every id and every slot loaded at once (addresses clamped into the
+    // token's K + 1 slots, no branch), then summed in slot order
+    int e[CB_SLOTS];
+    uint4 v[CB_SLOTS];
+#pragma unroll
+    for (int k = 0; k < CB_SLOTS; ++k) e[k] = idx[t * K + min(k, K - 1)];
+#pragma unroll
+    for (int k = 0; k < CB_SLOTS; ++k)
+      v[k] = *reinterpret_cast<const uint4 *>(r + (size_t)min(k, K) * H);
+#pragma unroll
+    for (int k = 0; k < CB_SLOTS; ++k)
+      if (k < K ? (unsigned)e[k] < (unsigned)E : k == K) add(v[k]);
+  } else {
+    for (int k = 0; k <= K; ++k) {
+      if (k < K && (unsigned)idx[t * K + k] >= (unsigned)E) continue;
+      add(*reinterpret_cast<const uint4 *>(r + (size_t)k * H));
     }
   }
   float4 *o = reinterpret_cast<float4 *>(out + t * (size_t)H + c);
