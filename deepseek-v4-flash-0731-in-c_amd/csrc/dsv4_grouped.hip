@@ -314,16 +314,24 @@ __global__ __launch_bounds__(256) void k_router_cand(int *__restrict__ cand,
     if (l == 0) ncand[t] = K;
     return;
   }
-  float ch[PER];
+  // every lane's logits loaded at once (indices clamped into the row, no
+  // branch), then masked past E
+  float ch[PER], zv[PER], av[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const size_t i = (size_t)t * E + min(l + 64 * j, E - 1);
+    zv[j] = z[i];
+    av[j] = zabs[i];
+  }
   float amax = 0.0f;
+#pragma unroll
   for (int j = 0; j < PER; ++j) {
     const int e = l + 64 * j;
     ch[j] = -__builtin_inff();
     if (e < E) {
-      const size_t i = (size_t)t * E + e;
-      const float c = sqrt_softplus(z[i]) + (bias ? bias[e] : 0.0f);
+      const float c = sqrt_softplus(zv[j]) + (bias ? bias[e] : 0.0f);
       ch[j] = c == c ? c : -__builtin_inff();  // NaN is never selected
-      amax = fmaxf(amax, zabs[i]);
+      amax = fmaxf(amax, av[j]);
     }
   }
   amax = wave_max(amax) * 1.001f;
@@ -338,18 +346,20 @@ __global__ __launch_bounds__(256) void k_router_cand(int *__restrict__ cand,
   unsigned long long used = 0ull;  // bit j: expert l+64j taken
   float kth = -__builtin_inff();
   for (int k = 0; k < K; ++k) {
-    float bv = -__builtin_inff();
-    int bi = -1;
-    for (int j = 0; j < PER; ++j) {
-      const int e = l + 64 * j;
-      if (e < E && !((used >> j) & 1ull) && (ch[j] > bv || (ch[j] == bv && bi < 0))) {
-        bv = ch[j];
-        bi = e;
+    // the k-th largest choice: DPP wave maximum, then the lowest index
+    // holding it is taken (no LDS round trips)
+    float m = -__builtin_inff();
+    int mj = -1;
+#pragma unroll
+    for (int j = 0; j < PER; ++j)
+      if (!((used >> j) & 1ull) && ch[j] > m) {
+        m = ch[j];
+        mj = j;
       }
-    }
-    wave_argmax(bv, bi);
-    if (bi >= 0 && (bi % 64) == l) used |= 1ull << (bi / 64);
-    kth = bv;
+    const float wm = wave_max_dpp(m);
+    kth = wm;
+    const int bi = wave_min_dpp(mj >= 0 && m == wm ? l + 64 * mj : 0x7fffffff);
+    if (bi != 0x7fffffff && (bi % 64) == l) used |= 1ull << (bi / 64);
   }
   const float thr = kth - delta;
   // compaction in ascending id: pass j holds ids 64j .. 64j + 63 in lane
