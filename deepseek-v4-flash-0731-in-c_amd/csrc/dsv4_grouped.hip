@@ -502,6 +502,127 @@ __global__ __launch_bounds__(256) void k_router_chains(float *__restrict__ cscor
 }
 
 
+// k_router_chains with x staged in LDS: a wave's 64 consecutive chains
+// belong to at most 63 / K + 2 tokens (every token has at least K
+// candidates), at most RCX_TOK for K >= 5, so per 64-column step the wave
+// stages those tokens' x slices (16-byte pieces, 4 per lane) beside its
+// gate pieces in its own LDS rows, and registers carry both RCX_DEPTH steps
+// ahead (a one-step read-ahead left each step waiting a memory round trip;
+// the x slice per lane alone took 64 VGPRs a step). Loads of steps past the
+// row are range-checked and never used; no load sits under a branch. Same
+// chains, same column order, same outputs.
+#define RCX_TOK 16
+#define RCX_DEPTH 4
+#define RCX_XROW (64 * 4 + 16)  // LDS bytes per staged x slice
+__global__ __launch_bounds__(256) void k_router_chains_x(float *__restrict__ cscore,
+                                                         float *__restrict__ cchoice,
+                                                         const int *__restrict__ cand,
+                                                         const int *__restrict__ chain_off,
+                                                         const float *__restrict__ x,
+                                                         const uint16_t *__restrict__ G,
+                                                         const float *__restrict__ bias, int T,
+                                                         int H, int E) {
+  __shared__ __align__(16) uint8_t gs[4][64 * RC_ROW];
+  __shared__ __align__(16) uint8_t xsh[4][RCX_TOK * RCX_XROW];
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), l = threadIdx.x % 64;
+  const int total = chain_off[T];
+  const BufRsrc rg = buf_rsrc(G, 2u * (uint32_t)E * (uint32_t)H);
+  uint8_t *gbuf = gs[wv], *xbuf = xsh[wv];
+  const int nst = H / 64;  // H % 128 == 0
+  for (int g0 = (blockIdx.x * 4 + wv) * 64; g0 < total; g0 += gridDim.x * 256) {
+    const int g = g0 + l;
+    int t = 0, c = 0, e = -1;
+    if (g < total) {
+      int lo = 0, hi = T;  // chain_off[lo] <= g < chain_off[lo+1]
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) / 2;
+        if (chain_off[mid] <= g) lo = mid;
+        else hi = mid;
+      }
+      t = lo;
+      c = g - chain_off[t];
+      e = cand[(size_t)t * E + c];
+      if (e < 0 || e >= E) e = -1;
+    }
+    const int tf = __builtin_amdgcn_readfirstlane(t);  // lane 0's chain is live
+    const int tt = min(max(t - tf, 0), RCX_TOK - 1);
+    uint32_t srow[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int ek = __shfl(e, 8 * k + l / 8, 64);
+      srow[k] = ek >= 0 ? 2u * (uint32_t)ek * (uint32_t)H + 16u * (l % 8) : RC_BAD;
+    }
+    // x of tokens tf .. tf + RCX_TOK - 1 (rows past T read zeros); piece
+    // p = l + 64 i: token p / 16, columns 4 (p % 16) of the step
+    const BufRsrc rx = buf_rsrc(x + (size_t)tf * H, 4u * (uint32_t)min(T - tf, RCX_TOK) * (uint32_t)H);
+    auto gload = [&](uint4 (&gv)[8], int st) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        gv[k] = buf_load16(rg, srow[k] == RC_BAD ? RC_BAD : srow[k] + 128u * st);
+    };
+    auto xload = [&](uint4 (&xq)[4], int st) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int p = l + 64 * i;
+        xq[i] = buf_load16(rx, 4u * ((uint32_t)(p / 16) * (uint32_t)H + 64u * st + 4u * (p % 16)));
+      }
+    };
+    uint4 gv[RCX_DEPTH][8], xq[RCX_DEPTH][4];
+#pragma unroll
+    for (int d = 0; d < RCX_DEPTH; ++d) {
+      gload(gv[d], d);
+      xload(xq[d], d);
+    }
+    float acc = 0.0f;
+    int s0 = 0;
+    do {
+#pragma unroll
+      for (int d = 0; d < RCX_DEPTH; ++d) {
+        const int st = s0 + d;
+        // the wave's LDS operations run in order: these writes follow the
+        // previous step's reads and precede this step's
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+          *reinterpret_cast<uint4 *>(gbuf + (8 * k + l / 8) * RC_ROW + 16 * (l % 8)) = gv[d][k];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int p = l + 64 * i;
+          *reinterpret_cast<uint4 *>(xbuf + (p / 16) * RCX_XROW + 16 * (p % 16)) = xq[d][i];
+        }
+        gload(gv[d], st + RCX_DEPTH);
+        xload(xq[d], st + RCX_DEPTH);
+        if (st < nst) {
+          const uint8_t *mine = gbuf + l * RC_ROW;
+          const float4 *xr = reinterpret_cast<const float4 *>(xbuf + tt * RCX_XROW);
+#pragma unroll
+          for (int cc = 0; cc < 8; ++cc) {
+            const uint4 w = *reinterpret_cast<const uint4 *>(mine + 16 * cc);
+            const float4 xa = xr[2 * cc], xb = xr[2 * cc + 1];
+            acc = fmaf(u2f(w.x << 16), xa.x, acc);
+            acc = fmaf(u2f(w.x & 0xFFFF0000u), xa.y, acc);
+            acc = fmaf(u2f(w.y << 16), xa.z, acc);
+            acc = fmaf(u2f(w.y & 0xFFFF0000u), xa.w, acc);
+            acc = fmaf(u2f(w.z << 16), xb.x, acc);
+            acc = fmaf(u2f(w.z & 0xFFFF0000u), xb.y, acc);
+            acc = fmaf(u2f(w.w << 16), xb.z, acc);
+            acc = fmaf(u2f(w.w & 0xFFFF0000u), xb.w, acc);
+          }
+        }
+      }
+      s0 += RCX_DEPTH;
+    } while (s0 < nst);
+    if (g < total) {
+      float sc = 0.0f, ch = -__builtin_inff();
+      if (e >= 0) {
+        sc = sqrt_softplus(acc);
+        ch = sc + (bias ? bias[e] : 0.0f);
+      }
+      cscore[(size_t)t * E + c] = sc;
+      cchoice[(size_t)t * E + c] = ch;
+    }
+  }
+}
+
 // The routes of one token (one wave; lane k carries route k in selection
 // order): the reference selection (src/dsv4/dsv4_model.c:6866-6906) over nc
 // scored choices cc[i] of experts ct[i] (ct null: expert i, all of them),
@@ -2144,8 +2265,14 @@ int dsv4g_moe_forward_batch_routes(float *out, const float *x, const DSV4GLayer 
     hipLaunchKernelGGL(k_scan_counts, dim3(1), dim3(1024), 0, st, w.chain_off, w.ncand, T);
     const long bound = (long)T * (K + 4);
     const int blocks = (int)((bound + 255) / 256 < 4096 ? (bound + 255) / 256 : 4096);
-    hipLaunchKernelGGL(k_router_chains, dim3(blocks), dim3(256), 0, st, w.cscore, w.cchoice,
-                       w.cand, w.chain_off, x, L->gate_w, L->bias, T, H, E);
+    // every token has at least K candidates: for K >= 5 a wave's 64 chains
+    // span at most 14 tokens, whose x slices k_router_chains_x stages in LDS
+    if (K >= 5)
+      hipLaunchKernelGGL(k_router_chains_x, dim3(blocks), dim3(256), 0, st, w.cscore, w.cchoice,
+                         w.cand, w.chain_off, x, L->gate_w, L->bias, T, H, E);
+    else
+      hipLaunchKernelGGL(k_router_chains, dim3(blocks), dim3(256), 0, st, w.cscore, w.cchoice,
+                         w.cand, w.chain_off, x, L->gate_w, L->bias, T, H, E);
     hipLaunchKernelGGL(k_router_finalize, dim3((T + 3) / 4), dim3(256), 0, st, w.idx, w.wt,
                        w.cand, w.ncand, w.cscore, w.cchoice, L->tid2eid ? 1 : 0, T, E, K,
                        L->route_scale);
