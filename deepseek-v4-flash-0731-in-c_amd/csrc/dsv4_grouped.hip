@@ -379,27 +379,51 @@ __global__ __launch_bounds__(256) void k_router_cand(int *__restrict__ cand,
 // Exclusive prefix sum of n[0..T) into off[0..T], one workgroup.
 __global__ __launch_bounds__(1024) void k_scan_counts(int *__restrict__ off,
                                                       const int *__restrict__ n, int T) {
-  __shared__ int part[1024];
+  // exclusive prefix of n[0, T) into off, off[T] = the total: 4096 counts a
+  // pass, 4 consecutive per thread, a wave scan by shuffles, the 16 wave
+  // totals scanned by wave 0 (two barriers a pass)
+  __shared__ int wsum[16];
   __shared__ int carry;
-  if (threadIdx.x == 0) carry = 0;
+  const int tid = threadIdx.x, lane = tid % 64, wv = tid / 64;
+  if (tid == 0) carry = 0;
   __syncthreads();
-  for (int b = 0; b < T; b += 1024) {
-    const int i = b + threadIdx.x;
-    int v = i < T ? n[i] : 0;
-    part[threadIdx.x] = v;
-    __syncthreads();
-    for (int o = 1; o < 1024; o <<= 1) {
-      const int add = threadIdx.x >= o ? part[threadIdx.x - o] : 0;
-      __syncthreads();
-      part[threadIdx.x] += add;
-      __syncthreads();
+  for (int b = 0; b < T; b += 4096) {
+    const int i0 = b + 4 * tid;
+    int v[4], run = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[j] = i0 + j < T ? n[i0 + j] : 0;
+      run += v[j];
     }
-    if (i < T) off[i] = carry + part[threadIdx.x] - v;
+    int inc = run;  // inclusive scan of the threads' sums within the wave
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int u = __shfl_up(inc, o, 64);
+      if (lane >= o) inc += u;
+    }
+    if (lane == 63) wsum[wv] = inc;
     __syncthreads();
-    if (threadIdx.x == 1023) carry += part[1023];
+    if (wv == 0) {
+      int ws = lane < 16 ? wsum[lane] : 0;
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) {
+        const int u = __shfl_up(ws, o, 64);
+        if (lane >= o) ws += u;
+      }
+      if (lane < 16) wsum[lane] = ws;  // inclusive over waves
+    }
+    __syncthreads();
+    int x = carry + (wv > 0 ? wsum[wv - 1] : 0) + inc - run;  // exclusive at i0
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (i0 + j < T) off[i0 + j] = x;
+      x += v[j];
+    }
+    __syncthreads();  // every thread has read carry and wsum
+    if (tid == 0) carry += wsum[15];
     __syncthreads();
   }
-  if (threadIdx.x == 0) off[T] = carry;
+  if (tid == 0) off[T] = carry;
 }
 
 // Exact logits of every candidate: the reference's column-order fmaf chain
