@@ -359,7 +359,7 @@ __device__ __forceinline__ int dec_candidates_t(const DecArgs &a, int t, int *ct
   }
   const float sum_abs = wave_max_dpp(amax);
   const float bound_z = a.gamma * sum_abs;
-  const float thr = kth - 2.0f * (0.5f * bound_z + 1e-5f);
+  const float thr = cand_threshold(kth, 2.0f * (0.5f * bound_z + 1e-5f));
   int base = 0;
 #pragma unroll
   for (int j = 0; j < NPER; ++j) {
@@ -425,7 +425,7 @@ __device__ __forceinline__ int dec_candidates_lds(const DecArgs &a, int t, int *
   if (lane < a.K && sel[lane] >= 0) v[sel[lane]] = kth;
   __builtin_amdgcn_wave_barrier();
   const float sum_abs = wave_max_dpp(amax);
-  const float thr = kth - 2.0f * (0.5f * (a.gamma * sum_abs) + 1e-5f);
+  const float thr = cand_threshold(kth, 2.0f * (0.5f * (a.gamma * sum_abs) + 1e-5f));
   int base = 0;
   for (int e0 = 0; e0 < a.E; e0 += 64) {
     const int e = e0 + lane;
@@ -1565,6 +1565,32 @@ int dsv4g_moe_forward_noalloc(float *out, const float *x, const DSV4GLayer *L,
   void *ws = nullptr;
   DSV4G_TRY(scratch_ptr(L, (hipStream_t)stream, &ws));
   return dsv4g_moe_forward(out, x, L, token_ids, n_tokens, ws, need, idx_out, wt_out, stream);
+}
+
+int dsv4g_moe_noalloc_status(unsigned *status, void *stream) {
+  if (!status) return dsv4g_fail(DSV4G_EINVAL, "moe_noalloc_status: status is NULL");
+  *status = 0u;
+  int dev = 0;
+  DSV4G_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= 64) return dsv4g_fail(DSV4G_EINVAL, "moe_noalloc_status: device %d", dev);
+  void *p = nullptr;
+  {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_ptr[dev];
+  }
+  if (!p) return 0;  // no noalloc call on this device yet
+  hipStream_t st = (hipStream_t)stream;
+  DSV4G_HIP(hipMemcpyAsync(status, (const unsigned *)p + DEC_ERR, sizeof(unsigned),
+                           hipMemcpyDeviceToHost, st));
+  DSV4G_HIP(hipStreamSynchronize(st));
+  if (*status) {
+    // a wait that ran out leaves records and flags of its call set
+    const size_t words = DEC_SCRATCH_BYTES / 4;
+    hipLaunchKernelGGL(k_fill_zero_u32, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, st,
+                       (unsigned *)p, words);
+    DSV4G_TRY(dsv4g_check_launch("moe_noalloc_status"));
+  }
+  return 0;
 }
 
 }  // extern "C"

@@ -248,6 +248,16 @@ __device__ __forceinline__ float gamma_n(int n) {
   return (float)(nu / (1.0 - nu));
 }
 
+// Candidate threshold kth - delta of the approximate router. Overflowing
+// logits give kth = +inf with delta = +inf (or a NaN bound): the difference
+// is NaN, every ">= thr" test would fail and no expert would be a candidate.
+// Then every expert is one (-inf), which keeps at least min(K, E) candidates
+// per token, a superset of the exact top-k.
+__device__ __forceinline__ float cand_threshold(float kth, float delta) {
+  const float thr = kth - delta;
+  return thr == thr ? thr : -__builtin_inff();
+}
+
 // ---------------------------------------------------- exact chains ----
 // One 8-column batch of the exact chain acc = fmaf(g[c], x[c], acc), in
 // column order.

@@ -361,7 +361,7 @@ __global__ __launch_bounds__(256) void k_router_cand(int *__restrict__ cand,
     const int bi = wave_min_dpp(mj >= 0 && m == wm ? l + 64 * mj : 0x7fffffff);
     if (bi != 0x7fffffff && (bi % 64) == l) used |= 1ull << (bi / 64);
   }
-  const float thr = kth - delta;
+  const float thr = cand_threshold(kth, delta);
   // compaction in ascending id: pass j holds ids 64j .. 64j + 63 in lane
   // order, and each pass appends after the previous one
   int base = 0;

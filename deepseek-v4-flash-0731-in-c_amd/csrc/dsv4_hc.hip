@@ -543,17 +543,24 @@ int dsv4g_hc_post(float *state, const float *branch, const float *post, const fl
 
 // The FFN half of forward_loaded_layer (src/dsv4/dsv4_model.c:7549-7559) on
 // device: hc_pre + rmsnorm_bf16 -> moe_forward -> hc_post. Workspace: the
-// decode MoE workspace first (its status word also takes hc_pre's), then
-// x [n][hid], out [n][hid], post [n][mult], comb [n][mult*mult].
+// decode MoE workspace at its start (its status word also takes hc_pre's),
+// and x [n][hid], out [n][hid], post [n][mult], comb [n][mult*mult] at its
+// end. The end of the workspace does not move with the call's token count,
+// while the MoE workspace's token pieces grow from its start: a call with
+// fewer tokens than the workspace was sized for never writes over the
+// records and flags of a later call's extra tokens (they must stay zero).
 static size_t ffn_align(size_t v) { return (v + 255) & ~(size_t)255; }
+
+static size_t ffn_tail_bytes(const DSV4GLayer *L, int mult, int n_tokens) {
+  const size_t n = (size_t)n_tokens, H = (size_t)L->hidden, m = (size_t)mult;
+  return 2 * ffn_align(n * H * 4) + ffn_align(n * m * 4) + ffn_align(n * m * m * 4);
+}
 
 size_t dsv4g_ffn_step_workspace_bytes(const DSV4GLayer *L, int mult, int n_tokens) {
   if (!L || n_tokens <= 0 || mult < 1 || mult > HC_MAX_MULT) return 0;
   const size_t moe = dsv4g_moe_workspace_bytes(L, n_tokens);
   if (!moe) return 0;
-  const size_t n = (size_t)n_tokens, H = (size_t)L->hidden, m = (size_t)mult;
-  return ffn_align(moe) + 2 * ffn_align(n * H * 4) + ffn_align(n * m * 4) +
-         ffn_align(n * m * m * 4);
+  return ffn_align(moe) + ffn_tail_bytes(L, mult, n_tokens);
 }
 
 int dsv4g_ffn_step(float *state, const float *hc_fn, const float *hc_scale,
@@ -570,7 +577,10 @@ int dsv4g_ffn_step(float *state, const float *hc_fn, const float *hc_scale,
   const size_t n = (size_t)n_tokens, H = (size_t)L->hidden, m = (size_t)mult;
   const size_t moe = dsv4g_moe_workspace_bytes(L, n_tokens);
   uint8_t *p = (uint8_t *)workspace;
-  float *x = (float *)(p + ffn_align(moe));
+  // 256-byte aligned start of the tail; at or past ffn_align(moe) since
+  // workspace_bytes >= need
+  const size_t tail0 = (workspace_bytes - ffn_tail_bytes(L, mult, n_tokens)) & ~(size_t)255;
+  float *x = (float *)(p + tail0);
   float *out = x + ffn_align(n * H * 4) / 4;
   float *post = out + ffn_align(n * H * 4) / 4;
   float *comb = post + ffn_align(n * m * 4) / 4;

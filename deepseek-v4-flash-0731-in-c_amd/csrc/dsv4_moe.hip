@@ -116,7 +116,7 @@ __global__ __launch_bounds__(256) void k_router_select(
         kth = bv;
       }
       int n = 0;
-      const float thr = kth - delta;
+      const float thr = cand_threshold(kth, delta);
       for (int e = 0; e < E; ++e)
         if (choice_a[e] >= thr) cand[n++] = e;
       ncand_s = n;

@@ -60,6 +60,7 @@ _SIGS = {
     "dsv4g_moe_decode_routing": [_vp, _vp, C.POINTER(DSV4GLayer), _I, _vp, _vp],
     "dsv4g_moe_workspace_init": [_vp, _Z, _vp],
     "dsv4g_moe_decode_status": [_vp, _vp, _vp],
+    "dsv4g_moe_noalloc_status": [_vp, _vp],
     "dsv4g_moe_forward_routes": [_vp, _vp, C.POINTER(DSV4GLayer), _vp, _I, _vp, _Z, _vp, _vp,
                                  _vp, _I, _vp],
     "dsv4g_moe_forward_batch": [_vp, _vp, C.POINTER(DSV4GLayer), _vp, _I, _vp, _Z, _vp, _vp,
@@ -311,9 +312,20 @@ class GpuLib:
         return st.value
 
     def check_decode_status(self, workspace):
+        """Raise if a cross-workgroup wait of the calls on this workspace ran
+        out; the workspace is zeroed again first (that call's records and
+        flags may be left set), so it serves the next call."""
         s = self.decode_status(workspace)
         if s:
+            self.moe_workspace_init(workspace)
             raise RuntimeError(f"decode: a cross-workgroup wait ran out (status {s:#x})")
+
+    def noalloc_status(self):
+        """Status word of dsv4g_moe_forward_noalloc's device array (0: fine);
+        a nonzero status also clears the array."""
+        st = C.c_uint(0)
+        self._call("dsv4g_moe_noalloc_status", C.byref(st), self._stream())
+        return st.value
 
     def moe_workspace_init(self, workspace):
         """Zero a decode workspace, once, before its first dsv4g_moe_forward."""

@@ -202,10 +202,21 @@ int dsv4g_moe_forward_fast(float *out, const float *x, const DSV4GLayer *L,
  * shares that GPU's array: calls that overlap on one GPU (two streams, two
  * threads) race and must not be issued. A call with a layer of another shape
  * than the previous call's on that GPU first clears the array (a fill
- * kernel). */
+ * kernel). That decision is taken on the host when the call is enqueued: a
+ * captured call replays without it, so a graph holding noalloc calls must
+ * not be replayed after a noalloc call of another layer shape on that GPU
+ * (all MoE layers of the model share one shape). */
 int dsv4g_moe_forward_noalloc(float *out, const float *x, const DSV4GLayer *L,
                               const int *token_ids, int n_tokens, int *idx_out, float *wt_out,
                               void *stream);
+/* The status word of the current GPU's no-allocation array, read into
+ * *status (host) with a synchronisation of the stream: 0 when every
+ * cross-workgroup wait of the noalloc calls since the last read completed,
+ * nonzero when one ran out (their outputs are not valid). A nonzero status
+ * also clears the whole array (a fill kernel on the stream), so the next
+ * call starts from zeroed records and flags. No counterpart in the
+ * reference: the status query of dsv4g_moe_forward_noalloc. */
+int dsv4g_moe_noalloc_status(unsigned *status, void *stream);
 /* The same layer as two ordered launches, for callers that interleave or
  * time them: 0 router, candidate experts, exact router chains and top-k, the
  * shared expert, and the gate/up GEMVs of the candidates; 1 SwiGLU requant,
@@ -308,8 +319,12 @@ int dsv4g_hc_post(float *state, const float *branch, const float *post, const fl
  * n_tokens states (token_ids for hash layers). workspace: 256-byte aligned,
  * at least dsv4g_ffn_step_workspace_bytes(L, mult, n_tokens), zeroed once
  * before first use (it begins with the decode MoE workspace, whose status
- * word dsv4g_moe_decode_status reads; the same shape rules apply).
- * idx_out / wt_out: optional routing. */
+ * word dsv4g_moe_decode_status reads; the same shape rules apply; the step's
+ * own buffers sit at its end, so a workspace sized for N tokens serves every
+ * call with at most N). idx_out / wt_out: optional routing. Asynchronous:
+ * the caller reads dsv4g_moe_decode_status at its next synchronisation
+ * (the sticky word covers hc_pre's and the MoE layer's waits of every step
+ * since the last read) and treats a nonzero status as fatal. */
 size_t dsv4g_ffn_step_workspace_bytes(const DSV4GLayer *L, int mult, int n_tokens);
 int dsv4g_ffn_step(float *state, const float *hc_fn, const float *hc_scale,
                    const float *hc_base, const uint16_t *ffn_norm, const DSV4GLayer *L,

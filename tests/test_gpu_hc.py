@@ -174,18 +174,18 @@ def test_tiny_checkpoint_hc_weights(env):
             assert same_bits(b[t], orc.rmsnorm_bf16(ob[None], norm, 1e-6, 1)[0])
 
 
-def run_ffn_step(env, L, mult, n, seed, token_ids=None):
+def run_ffn_step(env, L, mult, n, seed, token_ids=None, DL=None, workspace=None):
     orc, lib, dg, torch = env["orc"], env["lib"], env["dg"], env["torch"]
     rng = np.random.default_rng(seed)
     hid = L["hidden"]
     S = bf16_values((rng.standard_normal((n, mult * hid)) * 0.5).astype(np.float32))
     _, fn, sc, base = hc_inputs(rng, mult, hid, fn_sigma=0.005)
     norm = bf16_bits((1.0 + 0.1 * rng.standard_normal(hid)).astype(np.float32))
-    DL = dg.DeviceLayer.from_host(L, env["dev"])
+    DL = dg.DeviceLayer.from_host(L, env["dev"]) if DL is None else DL
     st = T(env, S)
     tok = None if token_ids is None else torch.from_numpy(token_ids).to(env["dev"])
     _, idx, wt = lib.ffn_step(st, T(env, fn), T(env, sc), T(env, base), T(env, norm), DL, mult,
-                              token_ids=tok)
+                              token_ids=tok, workspace=workspace)
     got, idx, wt = H(st), H(idx), H(wt)
     for t in range(n):
         x, post, comb = orc.hc_pre(S[t], fn, sc, base, mult)
@@ -202,6 +202,21 @@ def test_ffn_step_bit_exact(env):
     synthetic layer, against the oracle's composition of the same steps."""
     L = make_layer(env["orc"], 256, 128, 16, 6, seed=31, bias=True)
     run_ffn_step(env, L, 4, 3, seed=32)
+
+
+def test_ffn_step_workspace_reused_across_token_counts(env):
+    """One workspace sized for 4 tokens serves steps of 4, 1, 3 and 4 tokens
+    in a row, each bit-exact: a step with fewer tokens must not write its
+    own buffers over the decode records and flags of the tokens it does not
+    use (a later step with more tokens needs them zero)."""
+    torch, lib, dg = env["torch"], env["lib"], env["dg"]
+    L = make_layer(env["orc"], 256, 128, 16, 6, seed=37, bias=True)
+    DL = dg.DeviceLayer.from_host(L, env["dev"])
+    ws = torch.zeros(lib.ffn_step_workspace_bytes(DL, 4, 4), dtype=torch.uint8,
+                     device=env["dev"])
+    for i, n in enumerate((4, 1, 3, 4)):
+        print(f"ffn_step on a 4-token workspace: {n} tokens", flush=True)
+        run_ffn_step(env, L, 4, n, seed=38 + i, DL=DL, workspace=ws)
 
 
 def test_ffn_step_hash_layer(env):
