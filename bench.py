@@ -10,9 +10,10 @@ serve the weights; each step has its own token. The K timed steps are
 captured in a HIP graph and replayed, so the time is the GPU's, not Python's.
 
 Prints ONE JSON line. value = algorithmic HBM bytes per step / time per step.
-roofline: the dominant kernel (the front launch: router, shared expert and the
-routed gate/up GEMVs), timed live with HIP events around a graph of its
-launches on the launch stream. cpu_baseline: the
+roofline: the dominant kernel (the front launch, the second of three: exact
+router chains, the routed gate/up GEMVs and the shared expert's down GEMV),
+timed live with HIP events around a graph of its launches on the launch
+stream. cpu_baseline: the
 reference's own moe_forward (oracle/_ref, compiled from the reference sources)
 on the same layer on the host cores.
 
@@ -53,10 +54,10 @@ GATE_BYTES = E * H * 2                        # BF16 router gate
 # the router gate, the BF16 input and the BF16 output
 DECODE_BYTES = K * EXPERT_BYTES + SHARED_BYTES + GATE_BYTES + H * 2 + H * 2
 DECODE_FLOPS = 7 * 2 * 3 * I * H + 2 * E * H
-# the front launch (dominant kernel): the router gate, w1 and w3 of the 6
-# routed experts with their scales, the whole shared expert with its scales,
-# and the BF16 input
-FRONT_BYTES = GATE_BYTES + K * 2 * (4_194_304 + 262_144) + SHARED_BYTES + H * 2
+# the front launch (dominant kernel, phase 1 of three): w1 and w3 of the 6
+# routed experts with their scales, the shared expert's down matrix w2 with
+# its scales, and the BF16 input
+FRONT_BYTES = K * 2 * (4_194_304 + 262_144) + (8_388_608 + 512) + H * 2
 
 
 def parse():
@@ -692,7 +693,7 @@ def bench_decode(args, lib, layers):
     chk = torch.empty_like(OUT[:4])
     for i in range(4):
         L = layers[i % nl]
-        for ph in range(2):  # the two launches in order
+        for ph in range(3):  # the three launches in order
             lib.moe_decode_phase(ph, L, X[i:i + 1], chk[i:i + 1], WS[i])
     torch.cuda.synchronize()
     eager_ok = bool(torch.equal(chk, ref_out[:4]))
@@ -716,29 +717,29 @@ def bench_decode(args, lib, layers):
         step(i)
     torch.cuda.synchronize()
 
-    # dominant kernel: the front launch of every step. Its hand-off flags are
-    # cleared by the back launch, which this graph leaves out, so the
-    # workspaces are re-initialised (untimed) before each replay.
-    def reset_workspaces():
-        for i in range(nsteps):
-            lib.moe_workspace_init(WS[i])
-
+    # dominant kernel: the front launch (phase 1) of every step, timed in a
+    # graph of its own. It reads what the route launch (phase 0) left in each
+    # step's workspace, which only the back launch (phase 2) clears, so
+    # phase 0 runs once for every step first and the front graph replays
+    # on those records; phase 2 then cleans every workspace.
+    for i in range(nsteps):
+        step(i, phases=(0,))
     g2 = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g2):
         for i in range(nsteps):
-            step(i, phases=(0,))
-    reset_workspaces()
+            step(i, phases=(1,))
     g2.replay()
+    torch.cuda.synchronize()
     ms_front = 0.0
     for _ in range(args.replays):
-        reset_workspaces()
         ev0.record()
         g2.replay()
         ev1.record()
         torch.cuda.synchronize()
         ms_front += ev0.elapsed_time(ev1)
     ms_front /= args.replays * nsteps
-    reset_workspaces()
+    for i in range(nsteps):
+        step(i, phases=(2,))
     torch.cuda.synchronize()
     status = sum(lib.decode_status(WS[i]) for i in range(nsteps))
     del graph, g2
@@ -862,8 +863,8 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "k_dec_front (router logits, candidates, exact router chains, shared FP8 "
-                      "expert gate/up + down, 6 routed FP4 gate/up pairs with the SwiGLU epilogue)",
+            "kernel": "k_dec_front (candidates, exact router chains and top-k, 6 routed FP4 "
+                      "gate/up pairs with the SwiGLU epilogue, the shared FP8 expert's down)",
             "achieved": round(achieved, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

@@ -75,6 +75,7 @@ namespace dsv4 {
 // about a microsecond: on the order of a second)
 #define DEC_SPIN_LIMIT (1u << 20)
 #define DB_RC 6  // routes per chunk of k_dec_back
+#define DEC_PHASES 3  // launches per layer: route, front, back
 // set in the high word of a router record once it is written (the low 31
 // bits hold sum|w*x|, whose sign bit is always clear)
 #define DEC_REC_SET 0x80000000u
@@ -94,11 +95,12 @@ struct DecArgs {
   // token 0's (dec_tok)
   uint64_t *rec;   // [E] router record: choice | (sum|w*x| + DEC_REC_SET) << 32
   uint64_t *zrec;  // [E] router logit z | DEC_REC_SET << 32
-  unsigned *sf;    // [I/8] shared gate/up tile flags (DEC_FS words apart)
   unsigned *cf;    // [E] exact chain done flags per candidate position
   unsigned *qf;    // [K] route requant done flags (DEC_FS apart)
   uint32_t *qc;    // [K][I/4] E4M3 codes of the requantised routes
   float *qcs;      // [K][I/128] their scales
+  uint8_t *xq;     // [H] E4M3 codes of the token's activation (route launch)
+  float *xqs;      // [H/128] their per-128 scales
   float *zx, *zc;  // [E] exact score sqrt_softplus(z) and choice score + bias per
                    // candidate position
   int *sel_e;      // [K] routing, ascending id (moe_forward's idx)
@@ -214,10 +216,71 @@ __device__ __forceinline__ void expert_mat(const DecArgs &a, int e, int m, const
 __device__ __host__ __forceinline__ int dec_par_depth(int H) { return 8 * ((H / 4 + 511) / 512) + 11; }
 
 // ------------------------------------------------------- activation ----
-// quant_fp8_act (src/dsv4/dsv4_ops.c:96-121) of token row xt into LDS: E4M3
-// codes into q8 (H bytes) and/or grid values into xf (padded to 132 floats
-// per 128-group), per-128 scales into qs. Thread i takes 16 consecutive
-// values; a group's 8 threads are neighbouring lanes of one wave.
+// quant_fp8_act (src/dsv4/dsv4_ops.c:96-121) of 16 consecutive values v of a
+// token row, columns [base, base + 16), into LDS: E4M3 codes into q8 (H
+// bytes) and/or grid values into xf (padded to 132 floats per 128-group),
+// the per-128 scale into qs. A group's 8 threads are neighbouring lanes of
+// one wave (all threads of the wave call it; base past H stores nothing).
+__device__ __forceinline__ void dec_quant16(const float (&v)[16], int base, int H, uint8_t *q8,
+                                            float *xf, float *qs) {
+  float m = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) m = fmaxf(m, fabsf(v[i]));
+  m = fmaxf(m, __shfl_xor(m, 1, 64));
+  m = fmaxf(m, __shfl_xor(m, 2, 64));
+  m = fmaxf(m, __shfl_xor(m, 4, 64));
+  if (base < H) {
+    const float scale = act_scale(m);
+    const float inv = 1.0f / scale;
+    float g[16];
+    uint32_t k[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) g[i] = quant_e4m3_code(v[i], inv, k[i]);
+    if (q8) {
+      uint32_t c[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        c[i] = k[4 * i] | (k[4 * i + 1] << 8) | (k[4 * i + 2] << 16) | (k[4 * i + 3] << 24);
+      *reinterpret_cast<uint4 *>(q8 + base) = make_uint4(c[0], c[1], c[2], c[3]);
+    }
+    if (xf) {
+      float *d = xf + (base / 128) * 132 + base % 128;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        *reinterpret_cast<float4 *>(d + 4 * i) =
+            make_float4(g[4 * i], g[4 * i + 1], g[4 * i + 2], g[4 * i + 3]);
+    }
+    if ((threadIdx.x & 7) == 0) qs[base / 128] = scale;
+  }
+}
+
+// Thread i's 16 values of token row xt (columns 16 i .. 16 i + 15; zeros past
+// H), for rows of at most 4096: loaded once, at the start of a workgroup,
+// before any weight load, so that they return first (loads complete in
+// order) and the quantisation never waits on a memory round trip under the
+// weight stream.
+struct XRegs {
+  uint4 v[4];
+};
+__device__ __forceinline__ void dec_x_load(XRegs &X, const float *xt, int H) {
+  const BufRsrc rx = buf_rsrc(xt, H <= 4096 ? 4u * (uint32_t)H : 0u);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) X.v[i] = buf_load16(rx, 4u * (uint32_t)(16 * threadIdx.x + 4 * i));
+}
+__device__ __forceinline__ void dec_quant_regs(const XRegs &X, int H, uint8_t *q8, float *xf,
+                                               float *qs) {
+  float v[16];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[4 * i] = u2f(X.v[i].x);
+    v[4 * i + 1] = u2f(X.v[i].y);
+    v[4 * i + 2] = u2f(X.v[i].z);
+    v[4 * i + 3] = u2f(X.v[i].w);
+  }
+  dec_quant16(v, 16 * threadIdx.x, H, q8, xf, qs);
+}
+
+// The same straight from memory, for any row width (all threads).
 __device__ __forceinline__ void dec_quant_x(const float *xt, int H, uint8_t *q8, float *xf,
                                             float *qs) {
   const int tid = threadIdx.x;
@@ -233,36 +296,28 @@ __device__ __forceinline__ void dec_quant_x(const float *xt, int H, uint8_t *q8,
       v[4 * i + 2] = u2f(u.z);
       v[4 * i + 3] = u2f(u.w);
     }
-    float m = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) m = fmaxf(m, fabsf(v[i]));
-    m = fmaxf(m, __shfl_xor(m, 1, 64));
-    m = fmaxf(m, __shfl_xor(m, 2, 64));
-    m = fmaxf(m, __shfl_xor(m, 4, 64));
-    if (base < H) {
-      const float scale = act_scale(m);
-      const float inv = 1.0f / scale;
-      float g[16];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) g[i] = quant_e4m3(v[i], inv);
-      if (q8) {
-        uint32_t c[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          c[i] = e4m3_code(g[4 * i]) | (e4m3_code(g[4 * i + 1]) << 8) |
-                 (e4m3_code(g[4 * i + 2]) << 16) | (e4m3_code(g[4 * i + 3]) << 24);
-        *reinterpret_cast<uint4 *>(q8 + base) = make_uint4(c[0], c[1], c[2], c[3]);
-      }
-      if (xf) {
-        float *d = xf + (base / 128) * 132 + base % 128;
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          *reinterpret_cast<float4 *>(d + 4 * i) =
-              make_float4(g[4 * i], g[4 * i + 1], g[4 * i + 2], g[4 * i + 3]);
-      }
-      if ((tid & 7) == 0) qs[base / 128] = scale;
-    }
+    dec_quant16(v, base, H, q8, xf, qs);
   }
+}
+
+// Token 0's quantised activation: from X when it holds the row (H <= 4096),
+// else loaded.
+__device__ __forceinline__ void dec_quant_t0(const DecArgs &a, const XRegs &X, uint8_t *q8,
+                                             float *xf, float *qs) {
+  if (a.H <= 4096)
+    dec_quant_regs(X, a.H, q8, xf, qs);
+  else
+    dec_quant_x(a.x, a.H, q8, xf, qs);
+}
+
+// Token t's activation codes and per-128 scales (written by the route launch)
+// into LDS (all threads; read after the caller's next barrier).
+__device__ __forceinline__ void dec_x_codes(const DecArgs &a, int t, uint8_t *q8, float *qs) {
+  const int H = a.H;
+  const uint4 *gq = reinterpret_cast<const uint4 *>(dec_tok(a.xq, a, t));
+  const float *gs = dec_tok(a.xqs, a, t);
+  for (int i = threadIdx.x; i < H / 16; i += 256) reinterpret_cast<uint4 *>(q8)[i] = gq[i];
+  for (int i = threadIdx.x; i < (H + 127) / 128; i += 256) qs[i] = gs[i];
 }
 
 // ------------------------------------------------------------ routing ----
@@ -302,7 +357,10 @@ __device__ __forceinline__ void dec_select_finish(const DecArgs &a, int t, int m
 // choices in selection order (-1 past the selectable experts), both in LDS.
 // Returns nc, or -1 if the wait for the records ran out. Every workgroup that
 // calls it for a token derives the same candidates from the same records.
-// NPER = experts per lane (E <= 64 * NPER).
+// The records come from the previous launch (k_dec_route), so plain cached
+// loads see them (agent-scope loads of 256 records by every workgroup cost
+// microseconds of fabric round trips); the mark check stays as a bounded
+// guard. NPER = experts per lane (E <= 64 * NPER).
 template <int NPER>
 __device__ __forceinline__ int dec_candidates_t(const DecArgs &a, int t, int *ct, int *sel) {
   const int lane = threadIdx.x % 64;
@@ -316,7 +374,7 @@ __device__ __forceinline__ int dec_candidates_t(const DecArgs &a, int t, int *ct
 #pragma unroll
     for (int j = 0; j < NPER; ++j) {
       const int e = lane + 64 * j;
-      r[j] = e < a.E ? ld_dev(rec + e) : ((uint64_t)DEC_REC_SET << 32);
+      r[j] = e < a.E ? rec[e] : ((uint64_t)DEC_REC_SET << 32);
     }
     amax = 0.0f;
 #pragma unroll
@@ -387,7 +445,7 @@ __device__ __forceinline__ int dec_candidates_lds(const DecArgs &a, int t, int *
     int ready = 1;
     amax = 0.0f;
     for (int e = lane; e < a.E; e += 64) {
-      const uint64_t r = ld_dev(rec + e);
+      const uint64_t r = rec[e];
       const float c = __uint_as_float((uint32_t)r);
       ready &= (int)(r >> 63);
       v[e] = c == c ? c : ninf;
@@ -491,7 +549,7 @@ __device__ __forceinline__ bool dec_route_direct(const DecArgs &a, int t, const 
   const uint64_t *zr = dec_tok(a.zrec, a, t) + (use ? e : 0);
   uint64_t r = (uint64_t)DEC_REC_SET << 32;
   for (unsigned it = 0;; ++it) {
-    if (use) r = ld_dev(zr);
+    if (use) r = *zr;
     if (__all((int)(r >> 63))) break;
     if (!dec_spin(it, a.ctl)) return false;
   }
@@ -623,8 +681,8 @@ __device__ __forceinline__ void dec_select(const DecArgs &a, int t, int nc, cons
 // bias with sum|w*x| (rounding depth: dec_par_depth) and z, each published as
 // one 64-bit record that carries its own DEC_REC_SET mark. Workgroup 0 also
 // clears the previous call's requant flags.
-__device__ __forceinline__ void dec_router_block(const DecArgs &a, int e, uint64_t *s_tab,
-                                                 float *s_part) {
+__device__ __forceinline__ void dec_router_block(const DecArgs &a, int e, uint64_t tabv,
+                                                 uint64_t *s_tab, float *s_part) {
   const int tid = threadIdx.x, wv = tid / 64, lane = tid % 64;
   const int H = a.H, Q = H / 4;
   if (e == 0)
@@ -634,7 +692,6 @@ __device__ __forceinline__ void dec_router_block(const DecArgs &a, int e, uint64
   uint4 w[4];  // Q <= 2048: at most 4 pieces per lane; pieces past Q read zeros
 #pragma unroll
   for (int i = 0; i < 4; ++i) w[i] = buf_load16(rg, 16u * (uint32_t)(lane + 64 * i));
-  const uint64_t tabv = libm_table_load();
   const float be = a.bias ? a.bias[e] : 0.0f;
   for (int t = 0; t < a.n; ++t) {
     const BufRsrc rx = buf_rsrc(a.x + (size_t)t * H + (size_t)wv * Q, 4u * (uint32_t)Q);
@@ -681,6 +738,204 @@ __device__ __forceinline__ void dec_router_block(const DecArgs &a, int e, uint64
 }
 
 // ------------------------------------------------------------ chains ----
+// The exact logit z = ((0 + g0 x0) + g1 x1) + ... (one fmaf per column,
+// dsv4_gemv_bf16's order, src/dsv4/dsv4_model.c:298-303) is a 4096-step
+// dependent chain, about 20 us under the weight stream. When every product
+// g[c] x[c] is exact in fp32 (BF16 gate times the BF16-valued activation:
+// at most 16 significant bits; checked per column as fmaf(g, x, -p) == 0),
+// each step is acc = fl(acc + p[c]), so the chain can be cut:
+//  * the prefix sums P_b (fp64) locate, near H/4, H/2 and 3H/4, the
+//    boundary b where |P_b| is largest (there the fp32 running sum s_b has
+//    the coarsest spacing, so it lies fewest floats from fl(P_b); sampled
+//    over random gates and activations: within 75 floats, mostly a few);
+//  * wave 0 runs the first segment from +0; wave k runs segment k from the
+//    64 consecutive floats around fl(P_b) (lane j: 32 below to 31 above),
+//    all in parallel;
+//  * the true start of segment k is the end of segment k - 1 from its true
+//    start: one lane of wave k started there (bit-equal), and its end is
+//    the true end; otherwise the rest runs sequentially from the true start.
+// Every step is the reference's own addition in the reference's order, so
+// the result is the sequential chain's, bit for bit. Needs H a multiple of
+// 256, at least 1024; gs (fp32 gate row) is overwritten with the products.
+#define SPLIT_SEGS 4
+struct SplitLds {
+  double wtot[4];                  // per-wave prefix totals
+  double wmax[SPLIT_SEGS - 1][4];  // per-wave window maxima of |P_b|
+  int widx[SPLIT_SEGS - 1][4];
+  int b[SPLIT_SEGS + 1];           // segment boundaries
+  float p0[SPLIT_SEGS];            // fl(P_b) of each boundary
+  float st[SPLIT_SEGS][64], en[SPLIT_SEGS][64];  // starts and ends per lane
+  int exact;
+};
+
+__device__ __forceinline__ int ord_f(float f) {
+  const int b = (int)f2u(f);
+  return b >= 0 ? b : -(b & 0x7FFFFFFF);
+}
+__device__ __forceinline__ float ord_inv(int o) {
+  return o >= 0 ? u2f((uint32_t)o) : u2f((uint32_t)(-o) | 0x80000000u);
+}
+
+// acc + p[lo] + ... + p[hi - 1] in order (fp32 adds; p in LDS, read as a
+// broadcast by every lane). The main loop takes 64 columns an iteration in two
+// halves of 8 float4 reads, each half's reads issued a half ahead, with no
+// condition on a read: the last reads may pass hi by up to 64 floats, which
+// stay inside the workgroup's LDS (the callers' arrays past p), and are not
+// added.
+__device__ __forceinline__ float split_run(const float *p, int lo, int hi, float acc) {
+  int c = lo;
+  for (; c < hi && (c & 3); ++c) acc = acc + p[c];
+  const float4 *q = reinterpret_cast<const float4 *>(p + c);
+  const int nb = (hi - c) / 64;  // whole 64-column iterations
+  float4 ra[8], rb[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) ra[k] = q[k];
+  for (int it = 0; it < nb; ++it) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) rb[k] = q[16 * it + 8 + k];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      acc = acc + ra[k].x;
+      acc = acc + ra[k].y;
+      acc = acc + ra[k].z;
+      acc = acc + ra[k].w;
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) ra[k] = q[16 * it + 16 + k];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      acc = acc + rb[k].x;
+      acc = acc + rb[k].y;
+      acc = acc + rb[k].z;
+      acc = acc + rb[k].w;
+    }
+  }
+  for (c += 64 * nb; c < hi; ++c) acc = acc + p[c];
+  return acc;
+}
+
+// z for every thread, or NaN-free false in *ok when a product is inexact (then
+// nothing is computed and the caller runs the fmaf chain).
+__device__ __forceinline__ float dec_chain_split(float *gs, const float *xs, int H, SplitLds *L,
+                                                 bool *ok) {
+  const int tid = threadIdx.x, wv = tid / 64, lane = tid % 64;
+  const int npt = H / 256, c0 = tid * npt;
+  if (tid == 0) L->exact = 1;
+  __syncthreads();
+  // products in place, their exactness, and the thread's fp64 sum
+  double tsum = 0.0;
+  int ex = 1;
+  for (int i = 0; i < npt; ++i) {
+    const float g = gs[c0 + i], x = xs[c0 + i];
+    const float pr = g * x;
+    ex &= fmaf(g, x, -pr) == 0.0f;
+    gs[c0 + i] = pr;
+    tsum += (double)pr;
+  }
+  if (!__all(ex) && lane == 0) L->exact = 0;
+  // exclusive prefix of the thread sums (wave scan, then the wave totals)
+  double inc = tsum;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const double u = __shfl_up(inc, o, 64);
+    if (lane >= o) inc += u;
+  }
+  if (lane == 63) L->wtot[wv] = inc;
+  __syncthreads();
+  *ok = L->exact != 0;
+  if (!*ok) return 0.0f;
+  double pre = inc - tsum;
+  for (int w = 0; w < wv; ++w) pre += L->wtot[w];
+  // in each window, the boundary b (the chain's value before column b is
+  // P_b) with the largest |P_b|, lowest b on ties
+  const int wd = min(128, H / 16);
+  double bm[SPLIT_SEGS - 1];
+  int bi[SPLIT_SEGS - 1];
+#pragma unroll
+  for (int k = 0; k < SPLIT_SEGS - 1; ++k) {
+    bm[k] = -1.0;
+    bi[k] = 0x7FFFFFFF;
+  }
+  double run = pre;
+  for (int i = 0; i < npt; ++i) {
+    const int c = c0 + i;  // run = P_c
+#pragma unroll
+    for (int k = 0; k < SPLIT_SEGS - 1; ++k) {
+      const int nom = (k + 1) * (H / SPLIT_SEGS);
+      if (c >= nom - wd && c <= nom + wd && fabs(run) > bm[k]) {
+        bm[k] = fabs(run);
+        bi[k] = c;
+      }
+    }
+    run += (double)gs[c];
+  }
+#pragma unroll
+  for (int k = 0; k < SPLIT_SEGS - 1; ++k) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const double om = __shfl_xor(bm[k], o, 64);
+      const int oi = __shfl_xor(bi[k], o, 64);
+      if (om > bm[k] || (om == bm[k] && oi < bi[k])) {
+        bm[k] = om;
+        bi[k] = oi;
+      }
+    }
+    if (lane == 0) {
+      L->wmax[k][wv] = bm[k];
+      L->widx[k][wv] = bi[k];
+    }
+  }
+  __syncthreads();
+  if (tid < SPLIT_SEGS - 1) {
+    double m = -1.0;
+    int b = 0x7FFFFFFF;
+    for (int w = 0; w < 4; ++w)
+      if (L->wmax[tid][w] > m || (L->wmax[tid][w] == m && L->widx[tid][w] < b)) {
+        m = L->wmax[tid][w];
+        b = L->widx[tid][w];
+      }
+    L->b[tid + 1] = b;
+  }
+  if (tid == 0) {
+    L->b[0] = 0;
+    L->b[SPLIT_SEGS] = H;
+  }
+  __syncthreads();
+  // fl(P_b): the thread whose columns hold b recomputes P_b in fp64
+  for (int k = 1; k < SPLIT_SEGS; ++k) {
+    const int b = L->b[k];
+    if (b >= c0 && b < c0 + npt) {
+      double pb = pre;
+      for (int c = c0; c < b; ++c) pb += (double)gs[c];
+      L->p0[k] = (float)pb;
+    }
+  }
+  __syncthreads();
+  // the segments, all at once: wave k takes segment k
+  if (wv < SPLIT_SEGS) {
+    __builtin_amdgcn_s_setprio(3);
+    const float st = wv == 0 ? 0.0f : ord_inv(ord_f(L->p0[wv]) + lane - 32);
+    const float en = split_run(gs, L->b[wv], L->b[wv + 1], st);
+    __builtin_amdgcn_s_setprio(0);
+    L->st[wv][lane] = st;
+    L->en[wv][lane] = en;
+  }
+  __syncthreads();
+  // the true chain through the segments (every wave, from LDS)
+  float cur = L->en[0][0];
+  for (int k = 1; k < SPLIT_SEGS; ++k) {
+    const unsigned long long m = __ballot(f2u(L->st[k][lane]) == f2u(cur));
+    if (m) {
+      cur = L->en[k][__builtin_ctzll(m)];
+    } else {  // not covered: the rest in order from the true start
+      cur = split_run(gs, L->b[k], H, cur);
+      break;
+    }
+  }
+  return cur;
+}
+
+
 // Exact logits of candidate positions c, c + maxc, ... of token t: x and the
 // candidate's gate row widened to fp32 in LDS, then lane 0 of wave 0 runs
 // the reference's fmaf chain in column order (dsv4_gemv_bf16,
@@ -696,6 +951,8 @@ __device__ __forceinline__ void dec_chain_block(const DecArgs &a, int t, int c, 
   const int H = a.H;
   float *s_v = lds + 2 * H;  // more than 256 experts: the candidates' choices
   float *xs = lds, *gs = lds + H;
+  // the split chain's scratch, past x, the gate row and the E choices
+  SplitLds *sl = reinterpret_cast<SplitLds *>(lds + 2 * H + ((a.E + 3) & ~3));
   const uint64_t tabv = libm_table_load();
   // x is staged before the candidates are known
   const BufRsrc rx = buf_rsrc(a.x + (size_t)t * H, 4u * (uint32_t)H);
@@ -731,16 +988,22 @@ __device__ __forceinline__ void dec_chain_block(const DecArgs &a, int t, int c, 
       }
     }
     __syncthreads();
+    bool split = false;
+    float zsplit = 0.0f;
+    if (H % 256 == 0 && H >= 1024) zsplit = dec_chain_split(gs, xs, H, sl, &split);
     if (wv == 0 && lane == 0) {
-      __builtin_amdgcn_s_setprio(3);
-      float acc = 0.0f;
-      const float4 *g = reinterpret_cast<const float4 *>(gs);
-      const float4 *x = reinterpret_cast<const float4 *>(xs);
-      if (H % 256 == 0)
-        for (int cc = 0; cc < H / 4; cc += 64) acc = chain_cols<32>(g + cc, x + cc, acc);
-      else
-        for (int cc = 0; cc < H / 4; cc += 32) acc = chain_cols<16>(g + cc, x + cc, acc);
-      __builtin_amdgcn_s_setprio(0);
+      float acc = zsplit;
+      if (!split) {
+        __builtin_amdgcn_s_setprio(3);
+        acc = 0.0f;
+        const float4 *g = reinterpret_cast<const float4 *>(gs);
+        const float4 *x = reinterpret_cast<const float4 *>(xs);
+        if (H % 256 == 0)
+          for (int cc = 0; cc < H / 4; cc += 64) acc = chain_cols<32>(g + cc, x + cc, acc);
+        else
+          for (int cc = 0; cc < H / 4; cc += 32) acc = chain_cols<16>(g + cc, x + cc, acc);
+        __builtin_amdgcn_s_setprio(0);
+      }
       // the reference's score and choice (src/dsv4/dsv4_model.c:5827-5831,
       // 6627-6634)
       const float sc = sqrt_softplus(acc, s_tab);
@@ -765,25 +1028,86 @@ __device__ __forceinline__ void dec_chain_block(const DecArgs &a, int t, int c, 
 }
 
 // ---------------------------------------------------- shared expert ----
-// Shared expert gate/up, rows [r0, r0 + 8) of both, from the quantised x
-// (grid values in LDS, padded to 132 per group): t for the 8 rows into the
-// shared slot of sv, then the tile's flag.
+// Rows of each shared matrix per gate/up tile: a staged FP8 tile holds
+// fp8s_rows(H) / 2 rows of gate and of up, a register tile FP8_TR / 2.
+__device__ __host__ __forceinline__ bool dec_sh_gu_staged(int H) {
+  return fp8s_ok(H) && H >= 1024 && H <= 4096;
+}
+__device__ __host__ __forceinline__ int dec_sh_gu_rows(int H) {
+  return dec_sh_gu_staged(H) ? fp8s_rows(H) / 2 : FP8_TR / 2;
+}
+__device__ __host__ __forceinline__ int dec_sh_dn_rows(int I) {
+  return fp8s_ok(I) ? fp8s_rows(I) : FP8_TR;
+}
+
+// Shared expert gate/up tile `tile` of token t (rows [r0, r0 + dec_sh_gu_rows)
+// of both matrices), from the quantised x (grid values in LDS, padded to 132
+// per group): t for its rows into the shared slot of sv (read by the next
+// launch). ST (dec_sh_gu_staged(H)): the token's x row and the weights come
+// by direct-to-LDS loads, x first, so the quantisation runs while the
+// weights stream; otherwise a register tile, and x loaded here.
+template <bool ST>
 __device__ __forceinline__ void dec_shared_gu(const DecArgs &a, int t, int tile, float *lds,
-                                              float *s_y, const uint64_t *s_tab) {
+                                              float *s_y, uint64_t *s_tab) {
   const int tid = threadIdx.x;
-  const int H = a.H, I = a.I, r0 = tile * (FP8_TR / 2);
-  Fp8Regs R;
-  fp8_pair_load(R, a.sh[0], a.sh_s[0], a.sh[1], a.sh_s[1], H, I, r0);
-  float *xs = lds, *qs = lds + (H / 128) * 132;
-  float2 *ps = reinterpret_cast<float2 *>(qs + ((H / 128 + 3) & ~3));
-  dec_quant_x(a.x + (size_t)t * H, H, nullptr, xs, qs);
+  const int H = a.H, I = a.I, hr = dec_sh_gu_rows(H), r0 = tile * hr;
+  const uint64_t tabv = libm_table_load();
+  if (ST) {
+    // [32 KB tile][x: H raw floats, then 132 floats per group][scales]
+    // [pairs]; the scale codes in s_y (free until the rows are chained), so
+    // that three workgroups fit a CU's LDS. Every load below is a
+    // direct-to-LDS load the compiler does not track, so its only wait (for
+    // tabv) comes after fp8s_wait().
+    uint8_t *tl = reinterpret_cast<uint8_t *>(lds);
+    float *xs = lds + 8192, *qs = xs + (H / 128) * 132;
+    float2 *ps = reinterpret_cast<float2 *>(qs + ((H / 128 + 3) & ~3));
+    uint32_t *codes = reinterpret_cast<uint32_t *>(s_y);
+    fp8s_code_dma(codes, a.sh_s[0], a.sh_s[1], H, I, r0, true);
+    {
+      // the row: H / 256 pieces of 1 KB, a quarter per wave
+      const int l = tid % 64, wv = __builtin_amdgcn_readfirstlane(tid / 64);
+      const int nd = H / 1024;
+      const DmaRsrc rx = dma_rsrc(a.x + (size_t)t * H, 4u * (uint32_t)H);
+      const uint32_t wb = (uint32_t)(wv * nd) * 1024u;
+      for (int d = 0; d < nd; ++d)
+        dma_load16(rx, wb + (uint32_t)d * 1024u + 16u * (uint32_t)l,
+                   lds_addr(xs) + wb + (uint32_t)d * 1024u);
+    }
+    fp8s_dma(tl, a.sh[0], a.sh[1], H, I, r0, true);
+    vm_wait_n<8>();  // codes and x have landed (the tile's 8 loads may be in flight)
+    __syncthreads();
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float4 f = 16 * tid < H ? reinterpret_cast<const float4 *>(xs)[4 * tid + i]
+                                    : make_float4(0.f, 0.f, 0.f, 0.f);
+      v[4 * i] = f.x;
+      v[4 * i + 1] = f.y;
+      v[4 * i + 2] = f.z;
+      v[4 * i + 3] = f.w;
+    }
+    __syncthreads();  // every raw value read before the padded rows overwrite them
+    dec_quant16(v, 16 * tid, H, nullptr, xs, qs);
+    const uint32_t code = fp8s_code(codes, H, I, r0, true);
+    fp8s_wait();
+    __syncthreads();  // also: every code read before s_y takes the rows
+    libm_table_store(s_tab, tabv);
+    const float y = fp8s_rows_dot(tl, xs, qs, code, H, ps);
+    if (tid < 2 * hr) s_y[tid] = bf16_round(y);
+  } else {
+    Fp8Regs R;
+    fp8_pair_load(R, a.sh[0], a.sh_s[0], a.sh[1], a.sh_s[1], H, I, r0);
+    float *xs = lds, *qs = lds + (H / 128) * 132;
+    float2 *ps = reinterpret_cast<float2 *>(qs + ((H / 128 + 3) & ~3));
+    libm_table_store(s_tab, tabv);  // after the weight loads are issued
+    dec_quant_x(a.x + (size_t)t * H, H, nullptr, xs, qs);
+    __syncthreads();
+    fp8_pair_finish(R, s_y, xs, qs, a.sh[0], a.sh_s[0], a.sh[1], a.sh_s[1], H, I, r0, ps);
+  }
   __syncthreads();
-  fp8_pair_finish(R, s_y, xs, qs, a.sh[0], a.sh_s[0], a.sh[1], a.sh_s[1], H, I, r0, ps);
-  __syncthreads();
-  if (tid < FP8_TR / 2 && r0 + tid < I)
-    st_dev(dec_tok(a.sv, a, t) + (size_t)a.E * I + r0 + tid,
-           swiglu_t(s_y[tid], s_y[tid + FP8_TR / 2], a.limit, s_tab));
-  dec_signal(dec_tok(a.sf, a, t) + (size_t)tile * DEC_FS);
+  if (tid < hr && r0 + tid < I)
+    dec_tok(a.sv, a, t)[(size_t)a.E * I + r0 + tid] =
+        swiglu_t(s_y[tid], s_y[tid + hr], a.limit, s_tab);
 }
 
 // y = bf16(t * w), then per-128 E4M3 requant into LDS (all threads):
@@ -828,27 +1152,73 @@ __device__ void dec_requant_f(float *qy, float *qys, const TvRegs &T, const floa
   __syncthreads();
 }
 
-// Shared expert down, rows [16 tile, 16 tile + 16): the weights are issued
-// first, then (unless the caller has seen them) the wait for the token's
-// shared gate/up tiles, then t (weight 1) requantised into LDS and the FP8
-// tile into ro (fp32; k_dec_back rounds it). False if the wait ran out.
-__device__ __forceinline__ bool dec_shared_dn(const DecArgs &a, int t, int tile, bool wait,
-                                              float *lds, int *s_i) {
-  const int H = a.H, I = a.I;
-  Fp8Regs R;
-  fp8_tile_load(R, a.sh[2], a.sh_s[2], I, H, tile * FP8_TR);
-  if (wait && !dec_wait_flags(dec_tok(a.sf, a, t), (I + FP8_TR / 2 - 1) / (FP8_TR / 2), DEC_FS,
-                              nullptr, a.ctl, s_i))
-    return false;
+// Shared expert down tile `tile` of token t (rows [r0, r0 + dec_sh_dn_rows)):
+// the token's shared t (written by the route launch) is loaded first, then
+// the weights, so t returns first and is requantised (weight 1) into LDS
+// while the weights stream; then the FP8 rows into ro (fp32; k_dec_back
+// rounds them). ST: the tile is staged (fp8s_ok(I)).
+template <bool ST>
+__device__ __forceinline__ void dec_shared_dn(const DecArgs &a, int t, int tile, float *lds) {
+  const int H = a.H, I = a.I, nr = dec_sh_dn_rows(I), r0 = tile * nr;
   const float *tv = dec_tok(a.sv, a, t) + (size_t)a.E * I;
-  TvRegs T;
-  dec_tv_load_dev(T, tv, I);
-  float *xs = lds, *qys = lds + (I / 128) * 132;
-  float2 *ps = reinterpret_cast<float2 *>(qys + ((I / 128 + 3) & ~3));
-  dec_requant_f(xs, qys, T, tv, 1.0f, I);
-  fp8_tile_finish(R, dec_tok(a.ro, a, t), xs, qys, a.sh[2], a.sh_s[2], I, H, tile * FP8_TR, 0,
-                  ps);
-  return true;
+  if (ST) {
+    // [32 KB tile][t: I raw floats, then 132 floats per group][scales]
+    // [pairs][scale codes], all by direct-to-LDS loads (none the compiler
+    // tracks): t and the codes first, so they land while the weights stream
+    uint8_t *tl = reinterpret_cast<uint8_t *>(lds);
+    float *xs = lds + 8192, *qys = xs + (I / 128) * 132;
+    float2 *ps = reinterpret_cast<float2 *>(qys + ((I / 128 + 3) & ~3));
+    uint32_t *codes = reinterpret_cast<uint32_t *>(ps + fp8s_rows(I) * pair_stride(I / 128));
+    const int tid = threadIdx.x, l = tid % 64, wv = __builtin_amdgcn_readfirstlane(tid / 64);
+    fp8s_code_dma(codes, a.sh_s[2], a.sh_s[2], I, H, r0, false);
+    {
+      const int nd = I / 1024;  // 1 KB pieces per wave
+      const DmaRsrc rt = dma_rsrc(tv, 4u * (uint32_t)I);
+      const uint32_t wb = (uint32_t)(wv * nd) * 1024u;
+      for (int d = 0; d < nd; ++d)
+        dma_load16(rt, wb + (uint32_t)d * 1024u + 16u * (uint32_t)l,
+                   lds_addr(xs) + wb + (uint32_t)d * 1024u);
+    }
+    fp8s_dma(tl, a.sh[2], a.sh[2], I, H, r0, false);
+    vm_wait_n<8>();  // codes and t have landed
+    __syncthreads();
+    // requant (weight 1, src/dsv4/dsv4_model.c:6268-6287) of the raw t in
+    // place: wave w takes groups w, w + 4, ..., lane l columns l, l + 64
+    float tvv[2 * 16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int g = wv + 4 * j;
+      tvv[2 * j] = g * 128 < I ? xs[g * 128 + l] : 0.0f;
+      tvv[2 * j + 1] = g * 128 < I ? xs[g * 128 + 64 + l] : 0.0f;
+    }
+    __syncthreads();  // every raw value read before the padded rows overwrite them
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int g = wv + 4 * j;
+      if (g >= I / 128) break;
+      const float y0 = bf16_round(tvv[2 * j]), y1 = bf16_round(tvv[2 * j + 1]);
+      const float amax = wave_max_dpp(fmaxf(fabsf(y0), fabsf(y1)));
+      const float scale = act_scale(amax);
+      const float inv = 1.0f / scale;
+      xs[g * 132 + l] = quant_e4m3(y0, inv);
+      xs[g * 132 + 64 + l] = quant_e4m3(y1, inv);
+      if (l == 0) qys[g] = scale;
+    }
+    const uint32_t code = fp8s_code(codes, I, H, r0, false);
+    fp8s_wait();
+    __syncthreads();
+    const float v = fp8s_rows_dot(tl, xs, qys, code, I, ps);
+    if (tid < nr && r0 + tid < H) dec_tok(a.ro, a, t)[r0 + tid] = v;
+  } else {
+    TvRegs T;
+    dec_tv_load_dev(T, tv, I);
+    Fp8Regs R;
+    fp8_tile_load(R, a.sh[2], a.sh_s[2], I, H, r0);
+    float *xs = lds, *qys = lds + (I / 128) * 132;
+    float2 *ps = reinterpret_cast<float2 *>(qys + ((I / 128 + 3) & ~3));
+    dec_requant_f(xs, qys, T, tv, 1.0f, I);
+    fp8_tile_finish(R, dec_tok(a.ro, a, t), xs, qys, a.sh[2], a.sh_s[2], I, H, r0, 0, ps);
+  }
 }
 
 // --------------------------------------------------- routed gate/up ----
@@ -956,73 +1326,102 @@ __device__ __forceinline__ void dec_routed_items(const DecArgs &a, int t, int l0
   __syncthreads();  // LDS (candidates, activation) is rewritten by the next token
 }
 
-// Streaming workgroup j of n_stream: its tiles of the shared gate/up (js, js
-// + S, ..., js = j - E mod S: the workgroups after the routing ones, from the
-// start, while the router runs), token 0's quantised activation into LDS, the
-// candidates of token 0 (dec_candidates), then per token its routed gate/up
-// items from l0 = js rotated past the workgroups with shared tiles (l0, l0 +
-// S, ...), then its tiles of the shared down rows (rotated likewise). Each workgroup holds one item at a time: per unit of work the
-// latency of a load under full memory traffic, so every workgroup gets about
-// the same number of units (a shared tile counts as two).
-__device__ __forceinline__ void dec_stream_block(const DecArgs &a, int j, float *lds, float *s_y,
-                                                 uint64_t *s_tab, int *s_cand, int *s_sel,
-                                                 int *s_i) {
+// Streaming workgroup j of n_stream (k_dec_front): per token, its quantised
+// activation (codes and per-128 scales, written by the route launch) into
+// LDS, the candidates (dec_candidates: the route launch has written every
+// router record, so the first poll finds them) and its routed gate/up items,
+// then its tiles of the shared down rows. The units (a routed item: 16 FP4
+// rows, 32 KB; a shared down tile: 16 FP8 rows, 32 KB) are dealt round-robin
+// over the streaming workgroups in the order [token 0's items, token 1's
+// items, ..., the shared down tiles], so no workgroup has more than one unit
+// above the mean. ST: the shared down tiles are staged (fp8s_ok(I)).
+template <bool ST>
+__device__ __forceinline__ void dec_stream_block(const DecArgs &a, int j, float *lds, float *s_y, uint64_t *s_tab,
+                                                 int *s_cand, int *s_sel, int *s_i) {
   const int S = a.n_stream;
-  const uint64_t tabv = libm_table_load();
-  const int t8 = (a.I + FP8_TR / 2 - 1) / (FP8_TR / 2), nsh = a.n * t8;
-  const int js = (j + S - a.E % S) % S;
-  const int rot = (js + S - nsh % S) % S;
-  const bool sh = js < nsh;
   const DecLds L = dec_lds(lds, fp4_geom_np(a.H, DEC_NP), a.H);
   float *s_v = L.aux;  // more than 256 experts: the candidates' choices
-  libm_table_store(s_tab, tabv);
-  for (int i = js; i < nsh; i += S) {
-    __syncthreads();  // LDS of the previous tile
-    dec_shared_gu(a, i / t8, i % t8, lds, s_y, s_tab);
-  }
-  if (!sh) dec_quant_x(a.x, a.H, L.xq8, nullptr, L.xqs);
-  int nc = dec_candidates(a, 0, s_cand, s_sel, s_v, s_i);
-  if (nc < 0) return;
+  int done = 0;  // units dealt so far
   for (int t = 0; t < a.n; ++t) {
-    if (t > 0 && (nc = dec_candidates(a, t, s_cand, s_sel, s_v, s_i)) < 0) return;
+    dec_x_codes(a, t, L.xq8, L.xqs);  // read after dec_candidates' first barrier
+    const int nc = dec_candidates(a, t, s_cand, s_sel, s_v, s_i);
+    if (nc < 0) return;
     const int nitems = nc * a.gu_tiles;
-    if (rot < nitems) {
-      dec_routed_items(a, t, rot, nitems, nc, t == 0 && !sh, L, s_y, s_tab, s_cand);
-    }
+    const int l0 = (j + S - done % S) % S;
+    if (l0 < nitems) dec_routed_items(a, t, l0, nitems, nc, true, L, s_y, s_tab, s_cand);
+    done += nitems;
   }
-  const int t16 = (a.H + FP8_TR - 1) / FP8_TR;
-  int seen = -1;  // the token whose shared gate/up tiles are known written
-  for (int i = rot; i < a.n * t16; i += S) {
-    __syncthreads();
-    const int t = i / t16;
-    if (!dec_shared_dn(a, t, i % t16, t != seen, lds, s_i)) return;
-    seen = t;
+  const int t16 = (a.H + dec_sh_dn_rows(a.I) - 1) / dec_sh_dn_rows(a.I);
+  for (int i = (j + S - done % S) % S; i < a.n * t16; i += S) {
+    __syncthreads();  // LDS of the previous unit
+    dec_shared_dn<ST>(a, i / t16, i % t16, lds);
   }
 }
 
-// Blocks: [E streaming that first route expert j][n maxc chain][n_stream - E
-// streaming]: every streaming workgroup is resident from the start where the
-// device holds them all, so each learns the candidates before the weight
-// streams load the memory system.
-__global__ __launch_bounds__(256) void k_dec_front(DecArgs a) {
+// Token t's activation quantised once (quant_fp8_act,
+// src/dsv4/dsv4_model.c:5580-5606) into the workspace: E4M3 codes and
+// per-128 scales, read by every streaming workgroup of the next launch.
+__device__ __forceinline__ void dec_quant_block(const DecArgs &a, int t, float *lds) {
+  const int H = a.H;
+  uint8_t *q8 = reinterpret_cast<uint8_t *>(lds);
+  float *qs = reinterpret_cast<float *>(q8 + ((H + 15) & ~15));
+  dec_quant_x(a.x + (size_t)t * H, H, q8, nullptr, qs);
+  __syncthreads();
+  uint8_t *gq = dec_tok(a.xq, a, t);
+  float *gs = dec_tok(a.xqs, a, t);
+  for (int i = threadIdx.x; i < H / 16; i += 256)
+    reinterpret_cast<uint4 *>(gq)[i] = reinterpret_cast<const uint4 *>(q8)[i];
+  for (int i = threadIdx.x; i < (H + 127) / 128; i += 256) gs[i] = qs[i];
+}
+
+// Route launch: blocks [n quant][E router][n * (I / rows) shared gate/up
+// tiles]. Quant workgroup t: token t's activation codes (dec_quant_block).
+// Router workgroup e: the approximate logits of expert e for every token,
+// published as records (dec_router_block). Shared workgroup: one tile of the
+// shared expert's gate/up for one token. Nothing here waits on another
+// workgroup: the next launch reads all three results. ST:
+// dec_sh_gu_staged(H).
+template <bool ST>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k_dec_route(
+    DecArgs a) {
   extern __shared__ __align__(16) float lds[];
   __shared__ uint64_t s_tab[32];
   __shared__ float s_y[256];
   __shared__ float s_part[8];
+  int b = blockIdx.x;
+  if (b < a.n) return dec_quant_block(a, b, lds);
+  b -= a.n;
+  if (b < a.E) {
+    const uint64_t tabv = libm_table_load();
+    return dec_router_block(a, b, tabv, s_tab, s_part);
+  }
+  const int hr = dec_sh_gu_rows(a.H), t8 = (a.I + hr - 1) / hr, i = b - a.E;
+  if (i >= a.n * t8) return;
+  dec_shared_gu<ST>(a, i / t8, i % t8, lds, s_y, s_tab);
+}
+
+// Front launch: blocks [n maxc chain][n_stream streaming]. The chain
+// workgroups come first, so their loads (x and the candidates' gate rows)
+// are ahead of the weight streams; the token's last chain workgroup waits
+// only on the token's other chain workgroups, dispatched before it. A
+// streaming workgroup's first loads are token 0's activation and the expf
+// table. ST: fp8s_ok(I).
+template <bool ST>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k_dec_front(
+    DecArgs a) {
+  extern __shared__ __align__(16) float lds[];
+  __shared__ uint64_t s_tab[32];
+  __shared__ float s_y[256];
   __shared__ int s_cand[ROUTER_MAX_EXPERTS];
   __shared__ int s_sel[32];
   __shared__ int s_i;
-  int b = blockIdx.x;
-  if (b < a.E) {
-    dec_router_block(a, b, s_tab, s_part);
-    return dec_stream_block(a, b, lds, s_y, s_tab, s_cand, s_sel, &s_i);
-  }
-  b -= a.E;
+  const int b = blockIdx.x;
   if (b < a.n * a.maxc)
     return dec_chain_block(a, b / a.maxc, b % a.maxc, lds, s_tab, s_cand, s_sel, &s_i);
-  b -= a.n * a.maxc;
-  if (a.E + b < a.n_stream)
-    dec_stream_block(a, a.E + b, lds, s_y, s_tab, s_cand, s_sel, &s_i);
+  const int j = b - a.n * a.maxc;
+  if (j >= a.n_stream) return;
+  libm_table_store(s_tab, libm_table_load());
+  dec_stream_block<ST>(a, j, lds, s_y, s_tab, s_cand, s_sel, &s_i);
 }
 
 // ------------------------------------------------------- down + combine ----
@@ -1063,11 +1462,12 @@ __device__ __forceinline__ void dec_route_requant(const DecArgs &a, int t, int k
       const float inv = 1.0f / scale;
       uint32_t c[2];
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
-        c[h] = e4m3_code(quant_e4m3(y[4 * h], inv)) |
-               (e4m3_code(quant_e4m3(y[4 * h + 1], inv)) << 8) |
-               (e4m3_code(quant_e4m3(y[4 * h + 2], inv)) << 16) |
-               (e4m3_code(quant_e4m3(y[4 * h + 3], inv)) << 24);
+      for (int h = 0; h < 2; ++h) {
+        uint32_t k[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) quant_e4m3_code(y[4 * h + i], inv, k[i]);
+        c[h] = k[0] | (k[1] << 8) | (k[2] << 16) | (k[3] << 24);
+      }
       st_dev(qc + base / 4, c[0]);
       st_dev(qc + base / 4 + 1, c[1]);
       if ((tid & 15) == 0) st_dev(qcs + base / 128, scale);
@@ -1213,13 +1613,10 @@ __global__ __launch_bounds__(256) void k_dec_back(DecArgs a) {
   int b = blockIdx.x;
   if (b < nq) {
     if (b == 0) {
-      const int t8 = (a.I + FP8_TR / 2 - 1) / (FP8_TR / 2);
       for (int i = threadIdx.x; i < a.n * a.E; i += 256) {
         dec_tok(a.rec, a, i / a.E)[i % a.E] = 0ull;
         dec_tok(a.zrec, a, i / a.E)[i % a.E] = 0ull;
       }
-      for (int i = threadIdx.x; i < a.n * t8; i += 256)
-        dec_tok(a.sf, a, i / t8)[(size_t)(i % t8) * DEC_FS] = 0u;
     }
     return dec_route_requant(a, b / a.K, b % a.K);
   }
@@ -1241,10 +1638,11 @@ using namespace dsv4;
 namespace {
 
 struct DecWs {
-  unsigned *ctl, *sf, *cf, *qf;
+  unsigned *ctl, *cf, *qf;
   uint64_t *rec, *zrec;
   uint32_t *qc;
-  float *qcs, *zx, *zc, *sel_w, *sv, *ro;
+  float *qcs, *zx, *zc, *sel_w, *sv, *ro, *xqs;
+  uint8_t *xq;
   int *sel_e, *sel_pos;
   size_t tb;  // bytes of one token's piece
   size_t bytes;
@@ -1257,7 +1655,6 @@ struct DecWs {
 DecWs dec_ws_layout(const DSV4GLayer *L, int n_tokens, void *base) {
   const size_t K = (size_t)L->topk, E = (size_t)L->n_experts;
   const size_t H = (size_t)L->hidden, I = (size_t)L->inter;
-  const size_t t8 = (I + FP8_TR / 2 - 1) / (FP8_TR / 2);
   DecWs w = {};
   uintptr_t p = (uintptr_t)base;
   auto take = [&](size_t bytes) {
@@ -1269,7 +1666,6 @@ DecWs dec_ws_layout(const DSV4GLayer *L, int n_tokens, void *base) {
   const uintptr_t t0 = p;
   w.rec = (uint64_t *)take(E * 8);
   w.zrec = (uint64_t *)take(E * 8);
-  w.sf = (unsigned *)take(t8 * DEC_FS * 4);
   w.cf = (unsigned *)take(E * 4);
   w.qf = (unsigned *)take(K * DEC_FS * 4);
   w.zx = (float *)take(E * 4);
@@ -1281,6 +1677,8 @@ DecWs dec_ws_layout(const DSV4GLayer *L, int n_tokens, void *base) {
   w.ro = (float *)take(H * 4);
   w.qc = (uint32_t *)take(K * I);
   w.qcs = (float *)take(K * (I / 128) * 4);
+  w.xq = (uint8_t *)take(H);
+  w.xqs = (float *)take(((H + 127) / 128) * 4);
   w.tb = (size_t)(p - t0);
   w.bytes = DEC_CTL_BYTES + (size_t)n_tokens * w.tb;
   return w;
@@ -1290,7 +1688,7 @@ size_t max_sz(size_t a, size_t b) { return a > b ? a : b; }
 
 // Workgroups of k_dec_front resident at once on the current device (its
 // occupancy times the CU count), cached per device and LDS size.
-int front_slots(size_t lds, int *slots) {
+int front_slots(size_t lds, bool st, int *slots) {
   static std::mutex mu;
   static int cache_slots[64];
   static size_t cache_lds[64];
@@ -1298,17 +1696,19 @@ int front_slots(size_t lds, int *slots) {
   if (hipGetDevice(&dev) != hipSuccess || dev < 0)
     return dsv4g_fail(DSV4G_EHIP, "moe_decode: hipGetDevice failed");
   std::lock_guard<std::mutex> lock(mu);
-  if (dev < 64 && cache_slots[dev] > 0 && cache_lds[dev] == lds) {
+  const size_t key = 2 * lds + (st ? 1 : 0);  // the kernel variant and its LDS
+  if (dev < 64 && cache_slots[dev] > 0 && cache_lds[dev] == key) {
     *slots = cache_slots[dev];
     return DSV4G_OK;
   }
   int per_cu = 0, cus = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_dec_front, 256, lds) != hipSuccess ||
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+          &per_cu, st ? k_dec_front<true> : k_dec_front<false>, 256, lds) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
     return dsv4g_fail(DSV4G_EHIP, "moe_decode: occupancy query failed");
   *slots = max(1, per_cu) * max(1, cus);
   if (dev < 64) {
-    cache_lds[dev] = lds;
+    cache_lds[dev] = key;
     cache_slots[dev] = *slots;
   }
   return DSV4G_OK;
@@ -1351,11 +1751,12 @@ int dec_launch(int phase, float *out, const float *x, const DSV4GLayer *L, const
   a.ctl = w.ctl;
   a.rec = w.rec;
   a.zrec = w.zrec;
-  a.sf = w.sf;
   a.cf = w.cf;
   a.qf = w.qf;
   a.qc = w.qc;
   a.qcs = w.qcs;
+  a.xq = w.xq;
+  a.xqs = w.xqs;
   a.tb = w.tb;
   a.zx = w.zx;
   a.zc = w.zc;
@@ -1382,33 +1783,48 @@ int dec_launch(int phase, float *out, const float *x, const DSV4GLayer *L, const
   a.limit = (float)(int)L->swiglu_limit;  // the reference passes the limit as int
   a.fast = fast;
   const int n = n_tokens, H = a.H, I = a.I;
-  if (phase == 0) {
-    // streaming: routed pairs and their scales, the activation codes and
-    // scales; the shared FP8 tiles; chains: x and the gate row in fp32, then
-    // nc ints or 2 nc floats
-    const size_t lds_fp4 = dec_lds_fp4(qg, H, a.E);
-    const size_t lds_fp8_gu = (size_t)(H / 128) * 132 * 4 + (size_t)((H / 128 + 3) & ~3) * 4 +
-                              (size_t)FP8_TR * pair_stride(H / 128) * 8;
-    const size_t lds_fp8_dn = (size_t)(I / 128) * 132 * 4 + (size_t)((I / 128 + 3) & ~3) * 4 +
-                              (size_t)FP8_TR * pair_stride(I / 128) * 8;
-    const size_t lds = max_sz(max_sz(lds_fp4, (size_t)8 * H + (size_t)8 * a.E),
-                              max_sz(lds_fp8_gu, lds_fp8_dn));
-    int slots = 0;
-    DSV4G_TRY(front_slots(lds, &slots));
-    // the routing workgroups wait for each other's records: all must be
-    // resident
-    if (a.E > slots)
-      return dsv4g_fail(DSV4G_EINVAL, "moe_decode: %d experts exceed this device's resident "
-                        "workgroups (%d)", a.E, slots);
-    a.maxc = min(max(a.K + 10, 16), a.E);
-    // streaming workgroups: the resident slots beside the chains, at least
-    // one per expert (the first E of them route first)
-    a.n_stream = max(a.E, slots - n * a.maxc);
-    const long blocks = (long)n * a.maxc + a.n_stream;
-    hipLaunchKernelGGL(k_dec_front, dim3((unsigned)blocks), dim3(256), lds, st, a);
-    return dsv4g_check_launch("dec_front");
+  // a shared FP8 tile: staged (32 KB of weights, then the activation, its
+  // scales and the pairs) or in registers (the activation, scales, pairs)
+  auto lds_fp8 = [](int in) {
+    const size_t CB = (size_t)(in + 127) / 128;
+    const size_t act = CB * 132 * 4 + ((CB + 3) & ~(size_t)3) * 4;
+    return fp8s_ok(in) ? 32768 + act + (size_t)fp8s_rows(in) * pair_stride((int)CB) * 8 + 1024
+                       : act + (size_t)FP8_TR * pair_stride((int)CB) * 8;
+  };
+  // the staged gate/up tile keeps its scale codes in static LDS
+  const size_t lds_fp8_gu = max_sz(lds_fp8(H) - (dec_sh_gu_staged(H) ? 1024 : 0),
+                                   (size_t)H + 16 + (size_t)(H / 128) * 4);
+  if (phase == 0) {  // activation codes, router records and the shared expert's gate/up
+    const int t8 = (I + dec_sh_gu_rows(H) - 1) / dec_sh_gu_rows(H);
+    const dim3 grid((unsigned)((long)n + (long)a.E + (long)n * t8));
+    if (dec_sh_gu_staged(H))
+      hipLaunchKernelGGL(k_dec_route<true>, grid, dim3(256), lds_fp8_gu, st, a);
+    else
+      hipLaunchKernelGGL(k_dec_route<false>, grid, dim3(256), lds_fp8_gu, st, a);
+    return dsv4g_check_launch("dec_route");
   }
   if (phase == 1) {
+    // streaming: routed pairs and their scales, the activation codes and
+    // scales, or a shared FP8 down tile; chains: x and the gate row in fp32,
+    // then nc ints or 2 nc floats
+    const size_t lds_fp4 = dec_lds_fp4(qg, H, a.E);
+    const size_t lds_fp8_dn = lds_fp8(I);
+    const size_t lds_chain = (size_t)8 * H + (size_t)4 * ((a.E + 3) & ~3) + sizeof(SplitLds);
+    const size_t lds = max_sz(max_sz(lds_fp4, max_sz(lds_chain, (size_t)8 * H + (size_t)8 * a.E)),
+                              lds_fp8_dn);
+    int slots = 0;
+    DSV4G_TRY(front_slots(lds, fp8s_ok(I), &slots));
+    a.maxc = min(max(a.K + 10, 16), a.E);
+    // streaming workgroups: the resident slots beside the chains
+    a.n_stream = max(64, slots - n * a.maxc);
+    const long blocks = (long)n * a.maxc + a.n_stream;
+    if (fp8s_ok(I))
+      hipLaunchKernelGGL(k_dec_front<true>, dim3((unsigned)blocks), dim3(256), lds, st, a);
+    else
+      hipLaunchKernelGGL(k_dec_front<false>, dim3((unsigned)blocks), dim3(256), lds, st, a);
+    return dsv4g_check_launch("dec_front");
+  }
+  if (phase == 2) {
     const int G = I / 32;
     const size_t lds =
         (size_t)DB_RC * I + DB_RC * 32 * 4 + (size_t)DB_RC * 8 * pair_stride(G) * 8;
@@ -1526,7 +1942,7 @@ int dsv4g_moe_decode_routing(int *idx_out, float *wt_out, const DSV4GLayer *L, i
 int dsv4g_moe_forward(float *out, const float *x, const DSV4GLayer *L, const int *token_ids,
                       int n_tokens, void *workspace, size_t workspace_bytes, int *idx_out,
                       float *wt_out, void *stream) {
-  for (int phase = 0; phase < 2; ++phase)
+  for (int phase = 0; phase < DEC_PHASES; ++phase)
     DSV4G_TRY(dec_launch(phase, out, x, L, token_ids, n_tokens, workspace, workspace_bytes,
                          idx_out, wt_out, nullptr, (hipStream_t)stream, 0));
   return 0;
@@ -1535,7 +1951,7 @@ int dsv4g_moe_forward(float *out, const float *x, const DSV4GLayer *L, const int
 int dsv4g_moe_forward_fast(float *out, const float *x, const DSV4GLayer *L,
                            const int *token_ids, int n_tokens, void *workspace,
                            size_t workspace_bytes, int *idx_out, float *wt_out, void *stream) {
-  for (int phase = 0; phase < 2; ++phase)
+  for (int phase = 0; phase < DEC_PHASES; ++phase)
     DSV4G_TRY(dec_launch(phase, out, x, L, token_ids, n_tokens, workspace, workspace_bytes,
                          idx_out, wt_out, nullptr, (hipStream_t)stream, 1));
   return 0;
@@ -1545,7 +1961,7 @@ int dsv4g_moe_forward_routes(float *out, const float *x, const DSV4GLayer *L,
                              const int *token_ids, int n_tokens, void *workspace,
                              size_t workspace_bytes, int *idx_out, float *wt_out,
                              float *route_out, int fast, void *stream) {
-  for (int phase = 0; phase < 2; ++phase)
+  for (int phase = 0; phase < DEC_PHASES; ++phase)
     DSV4G_TRY(dec_launch(phase, out, x, L, token_ids, n_tokens, workspace, workspace_bytes,
                          idx_out, wt_out, route_out, (hipStream_t)stream, fast ? 1 : 0));
   return 0;

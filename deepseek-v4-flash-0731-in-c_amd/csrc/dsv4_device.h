@@ -94,10 +94,11 @@ __device__ __forceinline__ float2 fp8x2(uint32_t w) {
   return make_float2(v[0], v[1]);
 }
 
-// Nearest E4M3 grid value, ties to even (src/dsv4/dsv4_ops.c:81-109). rintf
-// is round-half-even, identical to the reference's floor-based helper for the
-// magnitudes used here (< 16).
-__device__ __forceinline__ float round_e4m3(float v) {
+// Nearest E4M3 grid value, ties to even (src/dsv4/dsv4_ops.c:81-109): the
+// reference's frexp form, kept for magnitudes above 448 and NaN (its
+// overflow and infinity quirks). rintf is round-half-even, identical to the
+// reference's floor-based helper for the magnitudes used here (< 16).
+__device__ __forceinline__ float round_e4m3_frexp(float v) {
   if (v == 0.0f) return 0.0f;
   const float s = v < 0.0f ? -1.0f : 1.0f;
   const float a = fabsf(v);
@@ -115,17 +116,63 @@ __device__ __forceinline__ float round_e4m3(float v) {
   return s * (rintf(a * 512.0f) / 512.0f);
 }
 
-// 2^ceil(log2(max(amax,1e-4)/448)) (src/dsv4/dsv4_model.c:5590-5596).
+// The same for |v| <= 448 by bit operations, with the grid value's E4M3 code:
+// at or above 2^-6 (an E4M3 normal) the fp32 significand is rounded to
+// 3 bits, ties to even, by adding 0x7FFFF plus the kept lowest bit at bit 20
+// (a carry moves to the exponent, as the reference's mr >= 1 step does), and
+// the code is the kept bits rebiased (exponent 127 - 7); below it the value
+// is rint(|v| 512) / 512 and the code that integer (8 is the smallest normal,
+// code 0x08). The sign is copied, so a negative value that rounds to zero
+// gives -0 as the reference's s * 0 does; v = +-0 gives +0 (code 0).
+// Checked against the reference's dsv4_round_e4m3 for every float with
+// |v| <= 448, both signs, values and decoded codes.
+__device__ __forceinline__ float round_e4m3_small(float v, uint32_t &code) {
+  const uint32_t u = f2u(v), a = u & 0x7FFFFFFFu;
+  uint32_t r, c;
+  if (a >= 0x3C800000u) {  // 2^-6
+    r = (a + 0x7FFFFu + ((a >> 20) & 1u)) & 0xFFF00000u;
+    c = (r >> 20) - (120u << 3);
+  } else {
+    const float q = rintf(u2f(a) * 512.0f);
+    r = f2u(q * (1.0f / 512.0f));
+    c = (uint32_t)q;
+  }
+  if (a == 0u) {
+    code = 0u;
+    return 0.0f;
+  }
+  code = c | ((u >> 24) & 0x80u);
+  return u2f(r | (u & 0x80000000u));
+}
+
+__device__ __forceinline__ float round_e4m3(float v) {
+  if (!(fabsf(v) <= 448.0f)) return round_e4m3_frexp(v);
+  uint32_t c;
+  return round_e4m3_small(v, c);
+}
+
+// 2^ceil(log2(max(amax,1e-4)/448)) (src/dsv4/dsv4_model.c:5590-5596): for a
+// normal r = 1.f 2^E the reference's frexp gives e = E + 1, less one when
+// f = 0, so the scale is r itself when its mantissa is zero and 2^(E+1)
+// otherwise (checked against the reference over every amax below 2^-11 and
+// above 2^125 and a dense sample between). r is normal for every finite
+// amax >= 1e-4; infinity and NaN take the frexp form.
 __device__ __forceinline__ float act_scale(float amax) {
   if (amax < 1e-4f) amax = 1e-4f;
   const float r = amax * (1.0f / 448.0f);
-  int e;
-  const float m = frexpf(r, &e);
-  if (m == 0.5f) e--;
-  return ldexpf(1.0f, e);
+  const uint32_t ur = f2u(r);
+  if (ur >= 0x7F800000u) {
+    int e;
+    const float m = frexpf(r, &e);
+    if (m == 0.5f) e--;
+    return ldexpf(1.0f, e);
+  }
+  const uint32_t ex = ur & 0x7F800000u;
+  return u2f((ur & 0x007FFFFFu) ? ex + 0x00800000u : ex);
 }
 
 // q = round_e4m3(clamp(x * inv, +-448)) (src/dsv4/dsv4_model.c:5598-5604).
+// A NaN x stays NaN through the clamp and takes the frexp form.
 __device__ __forceinline__ float quant_e4m3(float x, float inv) {
   float q = x * inv;
   if (q > 448.0f) q = 448.0f;
@@ -141,6 +188,19 @@ __device__ __forceinline__ uint32_t e4m3_code(float v) {
   const uint32_t b = f2u(a);
   const uint32_t ef = ((b >> 23) & 0xFFu) - 120u;  // fp32 exp -> E4M3 field
   return sign | (ef << 3) | ((b >> 20) & 7u);
+}
+
+// quant_e4m3 with the value's E4M3 code (a NaN x: NaN, coded by e4m3_code).
+__device__ __forceinline__ float quant_e4m3_code(float x, float inv, uint32_t &code) {
+  float q = x * inv;
+  if (q > 448.0f) q = 448.0f;
+  else if (q < -448.0f) q = -448.0f;
+  if (!(fabsf(q) <= 448.0f)) {
+    const float g = round_e4m3_frexp(q);
+    code = e4m3_code(g);
+    return g;
+  }
+  return round_e4m3_small(q, code);
 }
 
 // ---- glibc 2.35 libm, restated bit-exactly (dsv4_libm.h) ------------------

@@ -536,4 +536,169 @@ __device__ __forceinline__ void fp8_pair_finish(const Fp8Regs &R, float *yl, con
   }
 }
 
+// ================================ FP8 tiles staged by direct-to-LDS loads ====
+// The same exact FP8 scheme (lane = one 128-column block of one row, its
+// partial a sequential fmaf chain in column order, then one lane per row
+// chains the blocks), with the tile's weights moved into LDS by
+// buffer_load_dwordx4 ... lds instead of registers. A register tile gives
+// every lane its own block, 128 contiguous bytes, so each of its loads
+// touches 64 different cache lines; here each load instruction moves 1 KB
+// of consecutive bytes (coalesced), and the 16-byte pieces are permuted
+// within each block on the way so that the compute's block reads are free of
+// LDS bank conflicts: piece p of block cb sits at slot (p + cb / 2) mod 8 of
+// the block, so the 16 lanes of one read phase (16 consecutive blocks, the
+// same piece) hit 16 distinct 16-byte bank groups.
+//
+// Tile: NR = 32768 / in rows (a power of two), 32 KB; lane t owns row t / CB,
+// block t % CB (CB = in / 128). Supported when in is a power of two between
+// 1024 and 8192 (fp8s_ok): every wave's 8 KB covers whole rows, and a wave's
+// 64 lanes cover whole rows of blocks.
+// Paired tiles hold NR / 2 rows of W0 then the same rows of W1.
+//
+// The loads are issued by inline assembly: the compiler does not see them,
+// so it never inserts a wait for them (its own conservative wait before any
+// LDS read after a direct-to-LDS load would drain every load in flight), and
+// fp8s_wait() waits for all of the calling wave's loads before the barrier
+// that publishes the tile.
+typedef int DmaRsrc __attribute__((ext_vector_type(4)));
+
+// Raw buffer descriptor in scalar registers (wave-uniform): base, no stride,
+// num_records = bytes (reads at or past it return zeros and touch nothing).
+__device__ __forceinline__ DmaRsrc dma_rsrc(const void *p, uint32_t bytes) {
+  const uint64_t ad = (uint64_t)(uintptr_t)p;
+  DmaRsrc r;
+  r[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)ad);
+  r[1] = __builtin_amdgcn_readfirstlane((int)((uint32_t)(ad >> 32) & 0xFFFFu));
+  r[2] = __builtin_amdgcn_readfirstlane((int)bytes);
+  r[3] = 0x00020000;
+  return r;
+}
+
+// LDS byte address of a __shared__ pointer.
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+  return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void *)p;
+}
+
+// 16 bytes per lane from voff of r into LDS [lds + 16 lane] (lds
+// wave-uniform). M0 carries the LDS base; one wait state after writing it.
+__device__ __forceinline__ void dma_load16(DmaRsrc r, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(lds), "v"(voff), "s"(r)
+               : "memory");
+}
+
+__device__ __forceinline__ void fp8s_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// Waits until at most N vector memory operations of the wave are
+// outstanding (they complete in order: everything issued before the last N
+// has landed).
+template <int N>
+__device__ __forceinline__ void vm_wait_n() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+__device__ __host__ __forceinline__ bool fp8s_ok(int in) {
+  return in >= 1024 && in <= 8192 && (in & (in - 1)) == 0;
+}
+__device__ __host__ __forceinline__ int fp8s_rows(int in) { return 32768 / in; }
+
+// 4 bytes per lane from voff of r into LDS [lds + 4 lane] (lds wave-uniform).
+__device__ __forceinline__ void dma_load4(DmaRsrc r, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+               :
+               : "s"(lds), "v"(voff), "s"(r)
+               : "memory");
+}
+
+// Issues the load of the scale-code dword holding the calling lane's block
+// scale (lane t: tile row t / CB, block t % CB; the tile at rows r0 of W,
+// paired: NR / 2 rows of W0, then of W1) into codes[t] (LDS, 4 bytes per
+// lane). fp8s_code() extracts the byte once it has landed. The scale array
+// of a matrix with CB >= 8 blocks per row is a multiple of 8 bytes, so the
+// dword never leaves it.
+__device__ __forceinline__ void fp8s_code_dma(uint32_t *codes, const uint8_t *__restrict__ S0,
+                                              const uint8_t *__restrict__ S1, int in, int rows,
+                                              int r0, bool pair) {
+  const int t = threadIdx.x;
+  const int wv = __builtin_amdgcn_readfirstlane(t / 64);
+  const int CB = in / 128, half = fp8s_rows(in) / 2;
+  const int lr = t / CB, cb = t % CB;
+  // a wave's lanes cover 64 / CB whole rows: one matrix per wave
+  const bool m1 = pair && (wv * 64) / CB >= half;
+  const int row = r0 + (m1 ? lr - half : lr);
+  const DmaRsrc rs = dma_rsrc(m1 ? S1 : S0, (uint32_t)((rows + 127) / 128) * (uint32_t)CB);
+  const uint32_t byte = row < rows ? (uint32_t)((row / 128) * CB + cb) : 0xFFFFFFF0u;
+  dma_load4(rs, byte & ~3u, lds_addr(codes) + (uint32_t)wv * 256u);
+}
+__device__ __forceinline__ uint32_t fp8s_code(const uint32_t *codes, int in, int rows, int r0,
+                                              bool pair) {
+  const int t = threadIdx.x;
+  const int CB = in / 128, half = fp8s_rows(in) / 2;
+  const int lr = t / CB, cb = t % CB;
+  const int row = r0 + ((pair && lr >= half) ? lr - half : lr);
+  const uint32_t byte = (uint32_t)((row / 128) * CB + cb);
+  return (codes[t] >> (8u * (byte & 3u))) & 0xFFu;
+}
+
+// Issues the tile's loads (8 per wave): rows [r0, r0 + NR) of W (or, paired,
+// rows [r0, r0 + NR / 2) of W0 and of W1) into tile (32 KB of LDS, 16-byte
+// aligned); rows at or past `rows` read zeros.
+__device__ __forceinline__ void fp8s_dma(uint8_t *tile, const uint8_t *__restrict__ W0,
+                                         const uint8_t *__restrict__ W1, int in, int rows,
+                                         int r0, bool pair) {
+  const int l = threadIdx.x % 64;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+  const int half = fp8s_rows(in) / 2;
+  const int wrows = 8192 / in;  // rows per wave
+  const int lr0 = wv * wrows;   // the wave's first tile row
+  const bool m1 = pair && lr0 >= half;
+  const int mrow = r0 + (m1 ? lr0 - half : lr0);  // its row in the matrix
+  const uint8_t *W = m1 ? W1 : W0;
+  const int nrow = max(0, min(wrows, rows - mrow));
+  const DmaRsrc rw = dma_rsrc(W + (size_t)mrow * in, (uint32_t)(nrow * in));
+  const uint32_t base = lds_addr(tile) + (uint32_t)wv * 8192u;
+#pragma unroll
+  for (int d = 0; d < 8; ++d) {
+    const uint32_t q = (uint32_t)d * 1024u + 16u * (uint32_t)l;  // byte in the wave's 8 KB
+    const uint32_t o = q % (uint32_t)in, cb = o / 128u, slot = (o % 128u) / 16u;
+    const uint32_t piece = (slot - cb / 2u) & 7u;
+    dma_load16(rw, (q / (uint32_t)in) * (uint32_t)in + cb * 128u + 16u * piece,
+               base + (uint32_t)d * 1024u);
+  }
+}
+
+// After fp8s_wait() and a barrier: the lane's block partial from the staged
+// tile and the activation xs (LDS, 132 floats per 128-block), paired with
+// its scale qscale[cb] * e8m0(code) into ps[lr * stride + cb] (a NaN scale
+// skips the block), then a barrier and one lane per row chains the blocks;
+// returns the row's fp32 sum for lanes t < NR (rows past `rows` give 0).
+__device__ __forceinline__ float fp8s_rows_dot(const uint8_t *tile, const float *xs,
+                                               const float *qscale, uint32_t code, int in,
+                                               float2 *ps) {
+  const int t = threadIdx.x;
+  const int CB = in / 128, NR = fp8s_rows(in), stride = pair_stride(CB);
+  const int lr = t / CB, cb = t % CB;
+  const uint8_t *blk = tile + (size_t)lr * in + cb * 128;
+  const float *xb = xs + cb * 132;
+  float part = 0.0f;
+  // one piece ahead: its weight read is in flight while a piece is chained
+  // (the chain is sequential; reading further ahead only costs registers)
+  uint4 w = *reinterpret_cast<const uint4 *>(blk + 16 * ((cb / 2) & 7));
+#pragma unroll
+  for (int p = 0; p < 8; ++p) {
+    const uint4 wn = *reinterpret_cast<const uint4 *>(blk + 16 * ((p + 1 + cb / 2) & 7));
+    part = fp8_piece(w, xb + 16 * p, part);
+    w = wn;
+    asm volatile("" : "+v"(part)::"memory");  // keeps later pieces' reads below
+  }
+  float s = qscale[cb] * e8m0(code);
+  if (code == 255u) {  // NaN scale: the reference skips the block
+    part = 0.0f;
+    s = 0.0f;
+  }
+  ps[lr * stride + cb] = make_float2(part, s);
+  __syncthreads();
+  return t < NR ? pair_chain(ps + t * stride, CB) : 0.0f;
+}
+
 }  // namespace dsv4

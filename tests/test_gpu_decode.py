@@ -351,7 +351,7 @@ def test_moe_forward_more_than_256_candidates(env, winners):
 
 
 def test_moe_phases_and_graph_replay_match_fused(env):
-    """The two launches in order on one stream, and a captured graph of the
+    """The three launches in order on one stream, and a captured graph of the
     fused entry replayed several times with eager calls on the same
     workspace between the replays: every result has the fused call's bits,
     which match the oracle."""
@@ -368,7 +368,7 @@ def test_moe_phases_and_graph_replay_match_fused(env):
         assert same_bits(H(ref)[t], o), t
     ws = lib.new_moe_workspace(DL, 3, env["dev"])
     out = torch.zeros_like(X)
-    for ph in range(2):
+    for ph in range(3):
         lib.moe_decode_phase(ph, DL, X, out, ws)
     torch.cuda.synchronize()
     assert torch.equal(out, ref)

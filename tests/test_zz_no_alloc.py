@@ -62,8 +62,14 @@ def test_noalloc_matches_workspace_entry():
     o, i, w = orc.moe_forward(L, X[1].cpu().numpy())
     assert same_bits(outs[2][1].cpu().numpy(), o)
     # beyond the scratch: a clear error, nothing launched
-    big = torch.zeros(64, 4096, device=dev)
-    rc = raw.dsv4g_moe_forward_noalloc(ptr(big), ptr(big), C.byref(DL.struct), None, 64, None,
+    raw.dsv4g_moe_workspace_bytes.restype = C.c_size_t
+    raw.dsv4g_moe_workspace_bytes.argtypes = [C.POINTER(dsv4_gpu.DSV4GLayer), C.c_int]
+    nbig = 1
+    while raw.dsv4g_moe_workspace_bytes(C.byref(DL.struct), nbig) <= 16 << 20:
+        nbig += 1
+    assert nbig <= 1020  # the decode entry's own token limit is not what fails
+    big = torch.zeros(nbig, DL.struct.hidden, device=dev)
+    rc = raw.dsv4g_moe_forward_noalloc(ptr(big), ptr(big), C.byref(DL.struct), None, nbig, None,
                                        None, st)
     assert rc != 0
     assert b"scratch" in raw.dsv4g_last_error()
