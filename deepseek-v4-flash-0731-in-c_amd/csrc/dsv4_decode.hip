@@ -1041,9 +1041,11 @@ __device__ __host__ __forceinline__ int dec_sh_dn_rows(int I) {
 }
 
 // Shared expert gate/up tile `tile` of token t (rows [r0, r0 + dec_sh_gu_rows)
-// of both matrices), from the quantised x (grid values in LDS, padded to 132
-// per group): t for its rows into the shared slot of sv (read by the next
-// launch). ST (dec_sh_gu_staged(H)): the token's x row and the weights come
+// of both matrices), from the quantised x (quant_fp8_act,
+// src/dsv4/dsv4_model.c:5580-5606; grid values in LDS, padded to 132 per
+// group): t for its rows into the shared slot of sv (read by the next
+// launch). Tile 0 also writes the token's activation codes and per-128
+// scales (xq, xqs) for the next launch's routed items. ST (dec_sh_gu_staged(H)): the token's x row and the weights come
 // by direct-to-LDS loads, x first, so the quantisation runs while the
 // weights stream; otherwise a register tile, and x loaded here.
 template <bool ST>
@@ -1087,10 +1089,11 @@ __device__ __forceinline__ void dec_shared_gu(const DecArgs &a, int t, int tile,
       v[4 * i + 3] = f.w;
     }
     __syncthreads();  // every raw value read before the padded rows overwrite them
-    dec_quant16(v, 16 * tid, H, nullptr, xs, qs);
+    dec_quant16(v, 16 * tid, H, tile == 0 ? dec_tok(a.xq, a, t) : nullptr, xs, qs);
     const uint32_t code = fp8s_code(codes, H, I, r0, true);
     fp8s_wait();
     __syncthreads();  // also: every code read before s_y takes the rows
+    if (tile == 0 && tid < H / 128) dec_tok(a.xqs, a, t)[tid] = qs[tid];
     libm_table_store(s_tab, tabv);
     const float y = fp8s_rows_dot(tl, xs, qs, code, H, ps);
     if (tid < 2 * hr) s_y[tid] = bf16_round(y);
@@ -1100,8 +1103,10 @@ __device__ __forceinline__ void dec_shared_gu(const DecArgs &a, int t, int tile,
     float *xs = lds, *qs = lds + (H / 128) * 132;
     float2 *ps = reinterpret_cast<float2 *>(qs + ((H / 128 + 3) & ~3));
     libm_table_store(s_tab, tabv);  // after the weight loads are issued
-    dec_quant_x(a.x + (size_t)t * H, H, nullptr, xs, qs);
+    dec_quant_x(a.x + (size_t)t * H, H, tile == 0 ? dec_tok(a.xq, a, t) : nullptr, xs, qs);
     __syncthreads();
+    if (tile == 0)
+      for (int i = tid; i < H / 128; i += 256) dec_tok(a.xqs, a, t)[i] = qs[i];
     fp8_pair_finish(R, s_y, xs, qs, a.sh[0], a.sh_s[0], a.sh[1], a.sh_s[1], H, I, r0, ps);
   }
   __syncthreads();
@@ -1358,29 +1363,13 @@ __device__ __forceinline__ void dec_stream_block(const DecArgs &a, int j, float 
   }
 }
 
-// Token t's activation quantised once (quant_fp8_act,
-// src/dsv4/dsv4_model.c:5580-5606) into the workspace: E4M3 codes and
-// per-128 scales, read by every streaming workgroup of the next launch.
-__device__ __forceinline__ void dec_quant_block(const DecArgs &a, int t, float *lds) {
-  const int H = a.H;
-  uint8_t *q8 = reinterpret_cast<uint8_t *>(lds);
-  float *qs = reinterpret_cast<float *>(q8 + ((H + 15) & ~15));
-  dec_quant_x(a.x + (size_t)t * H, H, q8, nullptr, qs);
-  __syncthreads();
-  uint8_t *gq = dec_tok(a.xq, a, t);
-  float *gs = dec_tok(a.xqs, a, t);
-  for (int i = threadIdx.x; i < H / 16; i += 256)
-    reinterpret_cast<uint4 *>(gq)[i] = reinterpret_cast<const uint4 *>(q8)[i];
-  for (int i = threadIdx.x; i < (H + 127) / 128; i += 256) gs[i] = qs[i];
-}
-
-// Route launch: blocks [n quant][E router][n * (I / rows) shared gate/up
-// tiles]. Quant workgroup t: token t's activation codes (dec_quant_block).
-// Router workgroup e: the approximate logits of expert e for every token,
-// published as records (dec_router_block). Shared workgroup: one tile of the
-// shared expert's gate/up for one token. Nothing here waits on another
-// workgroup: the next launch reads all three results. ST:
-// dec_sh_gu_staged(H).
+// Route launch: blocks [E router][n * (I / rows) shared gate/up tiles]
+// (768 at the model's shape: one round of resident workgroups). Router
+// workgroup e: the approximate logits of expert e for every token, published
+// as records (dec_router_block). Shared workgroup: one tile of the shared
+// expert's gate/up for one token (tile 0 also the token's activation codes).
+// Nothing here waits on another workgroup: the next launch reads both
+// results. ST: dec_sh_gu_staged(H).
 template <bool ST>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k_dec_route(
     DecArgs a) {
@@ -1388,9 +1377,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
   __shared__ uint64_t s_tab[32];
   __shared__ float s_y[256];
   __shared__ float s_part[8];
-  int b = blockIdx.x;
-  if (b < a.n) return dec_quant_block(a, b, lds);
-  b -= a.n;
+  const int b = blockIdx.x;
   if (b < a.E) {
     const uint64_t tabv = libm_table_load();
     return dec_router_block(a, b, tabv, s_tab, s_part);
@@ -1425,6 +1412,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
 }
 
 // ------------------------------------------------------- down + combine ----
+// E4M3 codes of four values already scaled and clamped to +-448 (quant_e4m3's
+// q, src/dsv4/dsv4_model.c:5598-5604), packed little-endian: the hardware
+// conversion (v_cvt_pk_fp8_f32, OCP E4M3, round to nearest even) equals
+// round_e4m3's code for every |q| <= 448 of either sign except q = -0, which
+// the reference codes as +0 (q + 0 gives +0 there and changes nothing
+// else); checked exhaustively on the device. A NaN q takes the frexp form.
+__device__ __forceinline__ uint32_t e4m3_codes4(const float (&q)[4]) {
+  uint32_t c = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q[0] + 0.0f, q[1] + 0.0f, 0, false);
+  c = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q[2] + 0.0f, q[3] + 0.0f, (int)c, true);
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (!(fabsf(q[i]) <= 448.0f))
+      c = (c & ~(0xFFu << (8 * i))) | (e4m3_code(round_e4m3_frexp(q[i])) << (8 * i));
+  return c;
+}
+
 // Requant workgroup of route (t, k): y = bf16(t * w) and the per-128 E4M3
 // requant (src/dsv4/dsv4_model.c:6261-6287), published as codes and scales,
 // then its flag. Thread i takes 8 consecutive values; a 128-group is 16
@@ -1463,10 +1466,14 @@ __device__ __forceinline__ void dec_route_requant(const DecArgs &a, int t, int k
       uint32_t c[2];
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        uint32_t k[4];
+        float q[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) quant_e4m3_code(y[4 * h + i], inv, k[i]);
-        c[h] = k[0] | (k[1] << 8) | (k[2] << 16) | (k[3] << 24);
+        for (int i = 0; i < 4; ++i) {
+          q[i] = y[4 * h + i] * inv;
+          if (q[i] > 448.0f) q[i] = 448.0f;
+          else if (q[i] < -448.0f) q[i] = -448.0f;
+        }
+        c[h] = e4m3_codes4(q);
       }
       st_dev(qc + base / 4, c[0]);
       st_dev(qc + base / 4 + 1, c[1]);
@@ -1792,11 +1799,10 @@ int dec_launch(int phase, float *out, const float *x, const DSV4GLayer *L, const
                        : act + (size_t)FP8_TR * pair_stride((int)CB) * 8;
   };
   // the staged gate/up tile keeps its scale codes in static LDS
-  const size_t lds_fp8_gu = max_sz(lds_fp8(H) - (dec_sh_gu_staged(H) ? 1024 : 0),
-                                   (size_t)H + 16 + (size_t)(H / 128) * 4);
+  const size_t lds_fp8_gu = lds_fp8(H) - (dec_sh_gu_staged(H) ? 1024 : 0);
   if (phase == 0) {  // activation codes, router records and the shared expert's gate/up
     const int t8 = (I + dec_sh_gu_rows(H) - 1) / dec_sh_gu_rows(H);
-    const dim3 grid((unsigned)((long)n + (long)a.E + (long)n * t8));
+    const dim3 grid((unsigned)((long)a.E + (long)n * t8));
     if (dec_sh_gu_staged(H))
       hipLaunchKernelGGL(k_dec_route<true>, grid, dim3(256), lds_fp8_gu, st, a);
     else
