@@ -740,30 +740,31 @@ __device__ __forceinline__ void dec_router_block(const DecArgs &a, int e, uint64
 // ------------------------------------------------------------ chains ----
 // The exact logit z = ((0 + g0 x0) + g1 x1) + ... (one fmaf per column,
 // dsv4_gemv_bf16's order, src/dsv4/dsv4_model.c:298-303) is a 4096-step
-// dependent chain, about 20 us under the weight stream. When every product
-// g[c] x[c] is exact in fp32 (BF16 gate times the BF16-valued activation:
-// at most 16 significant bits; checked per column as fmaf(g, x, -p) == 0),
-// each step is acc = fl(acc + p[c]), so the chain can be cut:
-//  * the prefix sums P_b (fp64) locate, near H/4, H/2 and 3H/4, the
-//    boundary b where |P_b| is largest (there the fp32 running sum s_b has
-//    the coarsest spacing, so it lies fewest floats from fl(P_b); sampled
-//    over random gates and activations: within 75 floats, mostly a few);
+// dependent chain, about 20 us under the weight stream. When every product g[c] x[c] is exact in fp32 (BF16 gate
+// times the BF16-valued activation: at most 16 significant bits; checked per
+// column as fmaf(g, x, -p) == 0), each step is acc = fl(acc + p[c]), so the
+// chain can be cut:
+//  * the prefix sums P_b (fp32 partial sums: only a guess) locate, near H/4,
+//    H/2 and 3H/4, the boundary b where |P_b| is largest (there the fp32
+//    running sum s_b has the coarsest spacing, so it lies fewest floats from
+//    fl(P_b); sampled over random gates and activations: within 75 floats,
+//    mostly a few);
 //  * wave 0 runs the first segment from +0; wave k runs segment k from the
-//    64 consecutive floats around fl(P_b) (lane j: 32 below to 31 above),
-//    all in parallel;
+//    64 consecutive floats around the guess of P_b (lane j: 32 below to 31
+//    above), all in parallel;
 //  * the true start of segment k is the end of segment k - 1 from its true
 //    start: one lane of wave k started there (bit-equal), and its end is
-//    the true end; otherwise the rest runs sequentially from the true start.
+//    the true end; otherwise segment k runs again from the true start.
 // Every step is the reference's own addition in the reference's order, so
-// the result is the sequential chain's, bit for bit. Needs H a multiple of
-// 256, at least 1024; gs (fp32 gate row) is overwritten with the products.
+// the result is the sequential chain's, bit for bit, however good the
+// guesses. Needs H a multiple of 256, at least 1024; gs (fp32 gate row) is
+// overwritten with the products.
 #define SPLIT_SEGS 4
 struct SplitLds {
-  double wtot[4];                  // per-wave prefix totals
-  double wmax[SPLIT_SEGS - 1][4];  // per-wave window maxima of |P_b|
-  int widx[SPLIT_SEGS - 1][4];
-  int b[SPLIT_SEGS + 1];           // segment boundaries
-  float p0[SPLIT_SEGS];            // fl(P_b) of each boundary
+  float wtot[4];                        // per-wave sums
+  unsigned long long key[SPLIT_SEGS];   // per window: |P_b| bits, then ~b
+  int b[SPLIT_SEGS + 1];                // segment boundaries
+  float p0[SPLIT_SEGS];                 // the guess of P_b at each boundary
   float st[SPLIT_SEGS][64], en[SPLIT_SEGS][64];  // starts and ends per lane
   int exact;
 };
@@ -814,127 +815,97 @@ __device__ __forceinline__ float split_run(const float *p, int lo, int hi, float
   return acc;
 }
 
-// z for every thread, or NaN-free false in *ok when a product is inexact (then
-// nothing is computed and the caller runs the fmaf chain).
+// z in wave 0 (the other waves return an unspecified value), or false in
+// *ok when a product is inexact (then nothing is computed and the caller
+// runs the fmaf chain).
 __device__ __forceinline__ float dec_chain_split(float *gs, const float *xs, int H, SplitLds *L,
                                                  bool *ok) {
   const int tid = threadIdx.x, wv = tid / 64, lane = tid % 64;
-  const int npt = H / 256, c0 = tid * npt;
+  const int npt = H / 256, c0 = tid * npt, seg = H / SPLIT_SEGS;
   if (tid == 0) L->exact = 1;
+  if (tid < SPLIT_SEGS) L->key[tid] = 0ull;
   __syncthreads();
-  // products in place, their exactness, and the thread's fp64 sum
-  double tsum = 0.0;
+  // products in place, their exactness, and the thread's sum
+  float tsum = 0.0f;
   int ex = 1;
   for (int i = 0; i < npt; ++i) {
     const float g = gs[c0 + i], x = xs[c0 + i];
     const float pr = g * x;
     ex &= fmaf(g, x, -pr) == 0.0f;
     gs[c0 + i] = pr;
-    tsum += (double)pr;
+    tsum += pr;
   }
   if (!__all(ex) && lane == 0) L->exact = 0;
-  // exclusive prefix of the thread sums (wave scan, then the wave totals)
-  double inc = tsum;
+  // exclusive prefix of the thread sums (wave scan, then the wave sums)
+  float inc = tsum;
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
-    const double u = __shfl_up(inc, o, 64);
+    const float u = __shfl_up(inc, o, 64);
     if (lane >= o) inc += u;
   }
   if (lane == 63) L->wtot[wv] = inc;
   __syncthreads();
   *ok = L->exact != 0;
   if (!*ok) return 0.0f;
-  double pre = inc - tsum;
+  float pre = inc - tsum;
   for (int w = 0; w < wv; ++w) pre += L->wtot[w];
-  // in each window, the boundary b (the chain's value before column b is
-  // P_b) with the largest |P_b|, lowest b on ties
+  // the window [nom - wd, nom + wd] around boundary k's nominal column nom
+  // (wd <= seg / 4 and npt <= seg / 4: only the window nearest c0 can meet a
+  // thread's columns): the column b with the largest |P_b|, lowest b on
+  // ties, by a 64-bit LDS max over (|P_b| bits, ~b)
   const int wd = min(128, H / 16);
-  double bm[SPLIT_SEGS - 1];
-  int bi[SPLIT_SEGS - 1];
-#pragma unroll
-  for (int k = 0; k < SPLIT_SEGS - 1; ++k) {
-    bm[k] = -1.0;
-    bi[k] = 0x7FFFFFFF;
-  }
-  double run = pre;
-  for (int i = 0; i < npt; ++i) {
-    const int c = c0 + i;  // run = P_c
-#pragma unroll
-    for (int k = 0; k < SPLIT_SEGS - 1; ++k) {
-      const int nom = (k + 1) * (H / SPLIT_SEGS);
-      if (c >= nom - wd && c <= nom + wd && fabs(run) > bm[k]) {
-        bm[k] = fabs(run);
-        bi[k] = c;
+  const int k = (c0 + seg / 2) / seg, nom = k * seg;
+  float pb = 0.0f;
+  unsigned long long best = 0ull;
+  if (k >= 1 && k < SPLIT_SEGS && c0 <= nom + wd && c0 + npt > nom - wd) {
+    float run = pre;
+    for (int i = 0; i < npt; ++i) {
+      const int c = c0 + i;  // run = P_c
+      if (c >= nom - wd && c <= nom + wd) {
+        const unsigned long long key =
+            ((unsigned long long)f2u(fabsf(run)) << 32) | (uint32_t)~(uint32_t)c;
+        if (key > best) {
+          best = key;
+          pb = run;
+        }
       }
+      run += gs[c];
     }
-    run += (double)gs[c];
-  }
-#pragma unroll
-  for (int k = 0; k < SPLIT_SEGS - 1; ++k) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const double om = __shfl_xor(bm[k], o, 64);
-      const int oi = __shfl_xor(bi[k], o, 64);
-      if (om > bm[k] || (om == bm[k] && oi < bi[k])) {
-        bm[k] = om;
-        bi[k] = oi;
-      }
-    }
-    if (lane == 0) {
-      L->wmax[k][wv] = bm[k];
-      L->widx[k][wv] = bi[k];
-    }
-  }
-  __syncthreads();
-  if (tid < SPLIT_SEGS - 1) {
-    double m = -1.0;
-    int b = 0x7FFFFFFF;
-    for (int w = 0; w < 4; ++w)
-      if (L->wmax[tid][w] > m || (L->wmax[tid][w] == m && L->widx[tid][w] < b)) {
-        m = L->wmax[tid][w];
-        b = L->widx[tid][w];
-      }
-    L->b[tid + 1] = b;
+    if (best) atomicMax(&L->key[k], best);
   }
   if (tid == 0) {
     L->b[0] = 0;
     L->b[SPLIT_SEGS] = H;
+    L->p0[0] = 0.0f;
   }
   __syncthreads();
-  // fl(P_b): the thread whose columns hold b recomputes P_b in fp64
-  for (int k = 1; k < SPLIT_SEGS; ++k) {
-    const int b = L->b[k];
-    if (b >= c0 && b < c0 + npt) {
-      double pb = pre;
-      for (int c = c0; c < b; ++c) pb += (double)gs[c];
-      L->p0[k] = (float)pb;
-    }
+  if (best && L->key[k] == best) {  // this thread holds the boundary
+    L->b[k] = (int)~(uint32_t)best;
+    L->p0[k] = pb;
   }
   __syncthreads();
   // the segments, all at once: wave k takes segment k
   if (wv < SPLIT_SEGS) {
-    __builtin_amdgcn_s_setprio(3);
     const float st = wv == 0 ? 0.0f : ord_inv(ord_f(L->p0[wv]) + lane - 32);
     const float en = split_run(gs, L->b[wv], L->b[wv + 1], st);
-    __builtin_amdgcn_s_setprio(0);
     L->st[wv][lane] = st;
     L->en[wv][lane] = en;
   }
   __syncthreads();
-  // the true chain through the segments (every wave, from LDS)
-  float cur = L->en[0][0];
-  for (int k = 1; k < SPLIT_SEGS; ++k) {
-    const unsigned long long m = __ballot(f2u(L->st[k][lane]) == f2u(cur));
-    if (m) {
-      cur = L->en[k][__builtin_ctzll(m)];
-    } else {  // not covered: the rest in order from the true start
-      cur = split_run(gs, L->b[k], H, cur);
-      break;
+  // the true chain through the segments (wave 0, from LDS)
+  float cur = 0.0f;
+  if (wv == 0) {
+    cur = L->en[0][0];
+    for (int s = 1; s < SPLIT_SEGS; ++s) {
+      const unsigned long long m = __ballot(f2u(L->st[s][lane]) == f2u(cur));
+      if (m)
+        cur = L->en[s][__builtin_ctzll(m)];
+      else  // not covered: the segment again from the true start
+        cur = split_run(gs, L->b[s], L->b[s + 1], cur);
     }
   }
   return cur;
 }
-
 
 // Exact logits of candidate positions c, c + maxc, ... of token t: x and the
 // candidate's gate row widened to fp32 in LDS, then lane 0 of wave 0 runs
@@ -990,7 +961,13 @@ __device__ __forceinline__ void dec_chain_block(const DecArgs &a, int t, int c, 
     __syncthreads();
     bool split = false;
     float zsplit = 0.0f;
-    if (H % 256 == 0 && H >= 1024) zsplit = dec_chain_split(gs, xs, H, sl, &split);
+    if (H % 256 == 0 && H >= 1024) {
+      // the token's critical path: ahead of the streaming workgroups' VALU
+      // work on the SIMD
+      __builtin_amdgcn_s_setprio(3);
+      zsplit = dec_chain_split(gs, xs, H, sl, &split);
+      __builtin_amdgcn_s_setprio(0);
+    }
     if (wv == 0 && lane == 0) {
       float acc = zsplit;
       if (!split) {
