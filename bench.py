@@ -644,6 +644,7 @@ def bench_decode(args, lib, layers):
     """Graph-replayed decode steps over the rotated layers; returns the
     per-step and gate/up-pass times and the graph/eager agreement."""
     import torch
+    import dsv4_gpu
     import synth
     dev = torch.device("cuda:0")
     nl = len(layers)
@@ -693,7 +694,7 @@ def bench_decode(args, lib, layers):
     chk = torch.empty_like(OUT[:4])
     for i in range(4):
         L = layers[i % nl]
-        for ph in range(3):  # the three launches in order
+        for ph in range(dsv4_gpu.DECODE_PHASES):  # the launches in order
             lib.moe_decode_phase(ph, L, X[i:i + 1], chk[i:i + 1], WS[i])
     torch.cuda.synchronize()
     eager_ok = bool(torch.equal(chk, ref_out[:4]))
@@ -739,7 +740,7 @@ def bench_decode(args, lib, layers):
         ms_front += ev0.elapsed_time(ev1)
     ms_front /= args.replays * nsteps
     for i in range(nsteps):
-        step(i, phases=(2,))
+        step(i, phases=tuple(range(2, dsv4_gpu.DECODE_PHASES)))
     torch.cuda.synchronize()
     status = sum(lib.decode_status(WS[i]) for i in range(nsteps))
     del graph, g2

@@ -1,34 +1,37 @@
 // dsv4_decode.hip - the decode MoE layer on gfx950: moe_forward
-// (src/dsv4/dsv4_model.c:6599-6807) for a few tokens, bit for bit, as two
-// kernels per layer.
+// (src/dsv4/dsv4_model.c:6599-6807) for a few tokens, bit for bit, as four
+// kernels per layer (workgroups are dispatched in index order; a wait inside
+// a launch only ever holds a workgroup whose producers were dispatched
+// before it and never wait on it):
 //
-//   k_dec_front  one launch with two kinds of workgroups, in this index
-//                order (workgroups are dispatched in index order; a wait
-//                only ever holds a workgroup whose producers were
-//                dispatched before it and never wait on it):
-//                * streaming (the first E of them first route expert j:
-//                  approximate router logits z and sum|w*x| for every token
-//                  and the approximate choice sqrt_softplus(z) + bias,
-//                  published as self-marked 64-bit records): each derives
-//                  every token's candidate experts (below) from the records
-//                  itself, then streams, one register tile at a time, its
-//                  tiles of the shared FP8 expert's gate/up, its FP4 gate/up
-//                  items of the candidates, t = silu(bf16 gate) * bf16 up
-//                  into the candidate's slot (src/dsv4/dsv4_model.c:
-//                  6264-6268), and its tiles of the shared expert's down rows;
-//                * chain, a few per token (between the first E streaming
-//                  workgroups and the rest): for the candidate positions c,
-//                  c + maxc, ... the reference's exact sequential logit chain
-//                  (dsv4_gemv_bf16, src/dsv4/dsv4_model.c:298-303); the last
-//                  of them waits for the others and takes the exact top-k and
-//                  route weights (src/dsv4/dsv4_model.c:6615-6676).
-//   k_dec_back   one workgroup per route: the route weight scales t, the
-//                per-128 FP8 requant (src/dsv4/dsv4_model.c:6239-6287),
-//                published as codes; then one workgroup per 8 output rows:
-//                the FP4 down rows of every route (weights loaded while the
-//                requant runs), then the routes in ascending expert id and the
-//                shared expert, rounded to BF16
-//                (src/dsv4/dsv4_model.c:6795-6805).
+//   k_dec_route    E router workgroups (expert e: the approximate logits z
+//                  and sum|w*x| of every token and the approximate choice
+//                  sqrt_softplus(z) + bias, published as self-marked 64-bit
+//                  records); the shared FP8 expert's gate/up tiles (tile 0
+//                  also writes the token's E4M3 activation codes); last, one
+//                  candidate workgroup per token, which waits for the
+//                  records and writes the token's candidate list (below).
+//   k_dec_front    chain workgroups, a few per token: for the candidate
+//                  positions c, c + maxc, ... the reference's exact
+//                  sequential logit chain (dsv4_gemv_bf16,
+//                  src/dsv4/dsv4_model.c:298-303); the last of them waits
+//                  for the others and takes the exact top-k and route
+//                  weights (src/dsv4/dsv4_model.c:6615-6676). Then the
+//                  streaming workgroups: one register tile at a time, the
+//                  FP4 gate/up items of the candidates, t = silu(bf16 gate)
+//                  * bf16 up into the candidate's slot
+//                  (src/dsv4/dsv4_model.c:6264-6268), then the shared
+//                  expert's down rows.
+//   k_dec_requant  one workgroup per route: y = bf16(t * w) and the per-128
+//                  E4M3 requant (src/dsv4/dsv4_model.c:6239-6287), as codes.
+//   k_dec_back     one workgroup per 8 output rows: the FP4 down rows of
+//                  every route, then the routes in ascending expert id and
+//                  the shared expert, rounded to BF16
+//                  (src/dsv4/dsv4_model.c:6795-6805).
+//
+// Memory round trips that one launch's workgroups need before their weights
+// can stream (the candidates, the route ids) are cut to one each: under the
+// weight stream every dependent round trip queues behind the whole stream.
 //
 // Candidates. A parallel logit differs from the sequential fmaf chain by at
 // most gamma_d + gamma_H times sum|w*x| (d: the parallel sum's rounding
@@ -57,6 +60,7 @@
 // call leaves them zero. Data that crosses the launch boundary uses plain
 // loads and stores.
 #include <mutex>
+#include <type_traits>
 
 #include "dsv4_device.h"
 #include "dsv4_gpu_internal.h"
@@ -75,7 +79,7 @@ namespace dsv4 {
 // about a microsecond: on the order of a second)
 #define DEC_SPIN_LIMIT (1u << 20)
 #define DB_RC 6  // routes per chunk of k_dec_back
-#define DEC_PHASES 3  // launches per layer: route, front, back
+#define DEC_PHASES 4  // launches per layer: route, front, requant, down
 // set in the high word of a router record once it is written (the low 31
 // bits hold sum|w*x|, whose sign bit is always clear)
 #define DEC_REC_SET 0x80000000u
@@ -96,13 +100,14 @@ struct DecArgs {
   uint64_t *rec;   // [E] router record: choice | (sum|w*x| + DEC_REC_SET) << 32
   uint64_t *zrec;  // [E] router logit z | DEC_REC_SET << 32
   unsigned *cf;    // [E] exact chain done flags per candidate position
-  unsigned *qf;    // [K] route requant done flags (DEC_FS apart)
   uint32_t *qc;    // [K][I/4] E4M3 codes of the requantised routes
   float *qcs;      // [K][I/128] their scales
   uint8_t *xq;     // [H] E4M3 codes of the token's activation (route launch)
   float *xqs;      // [H/128] their per-128 scales
   float *zx, *zc;  // [E] exact score sqrt_softplus(z) and choice score + bias per
                    // candidate position
+  int *cl;         // [1 + E + K] the candidates (route launch): count, ids, then the
+                   // K best approximate choices in selection order
   int *sel_e;      // [K] routing, ascending id (moe_forward's idx)
   int *sel_pos;    // [K] candidate position of each route
   float *sel_w;    // [K] route weights (moe_forward's wt)
@@ -122,19 +127,29 @@ struct DecArgs {
 };
 
 // Token t's piece of a per-token workspace array.
+// (Byte-pointer arithmetic, not an integer round trip: the compiler then
+// still sees a pointer into device memory and emits global loads and
+// stores, not FLAT ones, whose pending state makes it drain every load.)
 template <typename T>
 __device__ __forceinline__ T *dec_tok(T *p, const DecArgs &a, int t) {
-  return reinterpret_cast<T *>(reinterpret_cast<uintptr_t>(p) + (size_t)t * a.tb);
+  using B = typename std::conditional<std::is_const<T>::value, const char, char>::type;
+  return reinterpret_cast<T *>(reinterpret_cast<B *>(p) + (size_t)t * a.tb);
 }
 
 // ------------------------------------------------- agent-scope hand-off ----
+// Through global-address-space pointers (every hand-off word lives in device
+// memory): a generic pointer would make these FLAT operations, and one FLAT
+// operation in flight makes the compiler wait for every load of the wave
+// before any later use (it cannot order FLAT against other loads).
 template <typename T>
 __device__ __forceinline__ T ld_dev(const T *p) {
-  return __hip_atomic_load(const_cast<T *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return __hip_atomic_load((__attribute__((address_space(1))) T *)(const_cast<T *>(p)),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 template <typename T>
 __device__ __forceinline__ void st_dev(T *p, T v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store((__attribute__((address_space(1))) T *)p, v, __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Sets the calling workgroup's flag once every thread's agent-scope stores
@@ -361,7 +376,7 @@ __device__ __forceinline__ void dec_select_finish(const DecArgs &a, int t, int m
 // loads see them (agent-scope loads of 256 records by every workgroup cost
 // microseconds of fabric round trips); the mark check stays as a bounded
 // guard. NPER = experts per lane (E <= 64 * NPER).
-template <int NPER>
+template <int NPER, bool COH>
 __device__ __forceinline__ int dec_candidates_t(const DecArgs &a, int t, int *ct, int *sel) {
   const int lane = threadIdx.x % 64;
   const float ninf = -__builtin_inff();
@@ -374,7 +389,7 @@ __device__ __forceinline__ int dec_candidates_t(const DecArgs &a, int t, int *ct
 #pragma unroll
     for (int j = 0; j < NPER; ++j) {
       const int e = lane + 64 * j;
-      r[j] = e < a.E ? rec[e] : ((uint64_t)DEC_REC_SET << 32);
+      r[j] = e < a.E ? (COH ? ld_dev(rec + e) : rec[e]) : ((uint64_t)DEC_REC_SET << 32);
     }
     amax = 0.0f;
 #pragma unroll
@@ -435,6 +450,7 @@ __device__ __forceinline__ int dec_candidates_t(const DecArgs &a, int t, int *ct
 // that every step takes the same expert as dec_candidates_t; a taken expert
 // is marked -inf in v (no strict '>' takes it again) and set back to the
 // k-th best choice afterwards (it is a candidate either way).
+template <bool COH>
 __device__ __forceinline__ int dec_candidates_lds(const DecArgs &a, int t, int *ct, int *sel,
                                                float *v) {
   const int lane = threadIdx.x % 64;
@@ -445,7 +461,7 @@ __device__ __forceinline__ int dec_candidates_lds(const DecArgs &a, int t, int *
     int ready = 1;
     amax = 0.0f;
     for (int e = lane; e < a.E; e += 64) {
-      const uint64_t r = rec[e];
+      const uint64_t r = COH ? ld_dev(rec + e) : rec[e];
       const float c = __uint_as_float((uint32_t)r);
       ready &= (int)(r >> 63);
       v[e] = c == c ? c : ninf;
@@ -500,6 +516,7 @@ __device__ __forceinline__ int dec_candidates_lds(const DecArgs &a, int t, int *
 // deriving them while the others wait (s_v: E floats of LDS for more than 256
 // experts). Returns nc (all threads), -1 if the wait for the router records
 // ran out.
+template <bool COH>
 __device__ __forceinline__ int dec_candidates(const DecArgs &a, int t, int *ct, int *sel,
                                               float *s_v, int *s_i) {
   __syncthreads();  // ct, sel and s_i of the previous token have been read
@@ -511,16 +528,59 @@ __device__ __forceinline__ int dec_candidates(const DecArgs &a, int t, int *ct, 
       if (lane < a.K) ct[lane] = sel[lane] = (int)row[lane];
       nc = a.K;
     } else if (a.E <= 64) {
-      nc = dec_candidates_t<1>(a, t, ct, sel);
+      nc = dec_candidates_t<1, COH>(a, t, ct, sel);
     } else if (a.E <= 128) {
-      nc = dec_candidates_t<2>(a, t, ct, sel);
+      nc = dec_candidates_t<2, COH>(a, t, ct, sel);
     } else if (a.E <= 256) {
-      nc = dec_candidates_t<4>(a, t, ct, sel);
+      nc = dec_candidates_t<4, COH>(a, t, ct, sel);
     } else {
-      nc = dec_candidates_lds(a, t, ct, sel, s_v);
+      nc = dec_candidates_lds<COH>(a, t, ct, sel, s_v);
     }
     if (threadIdx.x == 0) *s_i = nc;
   }
+  __syncthreads();
+  return *s_i;
+}
+
+// Candidate workgroup of token t in the route launch (dispatched after every
+// router workgroup, whose records it waits for: coherent loads, since they
+// are written in this launch): the candidates, once, into the token's list
+// for the next launch, whose workgroups read it in one memory round trip
+// instead of each deriving it from the 256 records (about 4 us of every
+// front workgroup's start, with no weight in flight). A wait that runs out
+// writes a count of -1.
+__device__ __forceinline__ void dec_cand_block(const DecArgs &a, int t, float *lds) {
+  int *ct = reinterpret_cast<int *>(lds), *sel = ct + ROUTER_MAX_EXPERTS;
+  float *sv = reinterpret_cast<float *>(sel + 32);
+  int *si = reinterpret_cast<int *>(sv + ROUTER_MAX_EXPERTS);
+  const int nc = dec_candidates<true>(a, t, ct, sel, sv, si);
+  int *cl = dec_tok(a.cl, a, t);
+  if (threadIdx.x == 0) cl[0] = nc;
+  for (int i = threadIdx.x; i < nc; i += 256) cl[1 + i] = ct[i];
+  if (threadIdx.x < a.K) cl[1 + a.E + threadIdx.x] = sel[threadIdx.x];
+}
+
+// The token's candidates from the route launch's list into LDS (all
+// threads): ct[0, nc) the candidate ids in ascending order, sel[0, K) the K
+// best approximate choices in selection order; returns nc (-1: the route
+// launch's wait ran out). Every entry is loaded at once (entries past nc
+// unused), one memory round trip.
+__device__ __forceinline__ int dec_candidates_read(const DecArgs &a, int t, int *ct, int *sel,
+                                                   int *s_i) {
+  __syncthreads();  // ct, sel and s_i of the previous token have been read
+  const int *cl = dec_tok(a.cl, a, t);
+  const int tid = threadIdx.x, E = a.E;
+  int v[ROUTER_MAX_EXPERTS / 256];
+#pragma unroll
+  for (int j = 0; j < ROUTER_MAX_EXPERTS / 256; ++j)
+    v[j] = tid + 256 * j < E ? cl[1 + tid + 256 * j] : 0;
+  const int sv = tid < a.K ? cl[1 + E + tid] : 0;
+  const int nc = tid == 0 ? cl[0] : 0;
+#pragma unroll
+  for (int j = 0; j < ROUTER_MAX_EXPERTS / 256; ++j)
+    if (tid + 256 * j < E) ct[tid + 256 * j] = v[j];
+  if (tid < a.K) sel[tid] = sv;
+  if (tid == 0) *s_i = nc;
   __syncthreads();
   return *s_i;
 }
@@ -679,15 +739,11 @@ __device__ __forceinline__ void dec_select(const DecArgs &a, int t, int nc, cons
 // (wv + 1) H/4), lane l its 8-column pieces l, l + 64, ... (gate row and x
 // read directly); for every token the approximate choice sqrt_softplus(z) +
 // bias with sum|w*x| (rounding depth: dec_par_depth) and z, each published as
-// one 64-bit record that carries its own DEC_REC_SET mark. Workgroup 0 also
-// clears the previous call's requant flags.
+// one 64-bit record that carries its own DEC_REC_SET mark.
 __device__ __forceinline__ void dec_router_block(const DecArgs &a, int e, uint64_t tabv,
                                                  uint64_t *s_tab, float *s_part) {
   const int tid = threadIdx.x, wv = tid / 64, lane = tid % 64;
   const int H = a.H, Q = H / 4;
-  if (e == 0)
-    for (int i = tid; i < a.n * a.K; i += 256)
-      st_dev(dec_tok(a.qf, a, i / a.K) + (size_t)(i % a.K) * DEC_FS, 0u);
   const BufRsrc rg = buf_rsrc(a.gate + (size_t)e * H + (size_t)wv * Q, 2u * (uint32_t)Q);
   uint4 w[4];  // Q <= 2048: at most 4 pieces per lane; pieces past Q read zeros
 #pragma unroll
@@ -920,7 +976,6 @@ __device__ __forceinline__ void dec_chain_block(const DecArgs &a, int t, int c, 
                                                 int *s_i) {
   const int tid = threadIdx.x, wv = tid / 64, lane = tid % 64;
   const int H = a.H;
-  float *s_v = lds + 2 * H;  // more than 256 experts: the candidates' choices
   float *xs = lds, *gs = lds + H;
   // the split chain's scratch, past x, the gate row and the E choices
   SplitLds *sl = reinterpret_cast<SplitLds *>(lds + 2 * H + ((a.E + 3) & ~3));
@@ -933,7 +988,7 @@ __device__ __forceinline__ void dec_chain_block(const DecArgs &a, int t, int c, 
     if (4u * i4 < (uint32_t)H) reinterpret_cast<uint4 *>(xs)[i4] = buf_load16(rx, 16u * i4);
   }
   libm_table_store(s_tab, tabv);
-  const int nc = dec_candidates(a, t, s_cand, s_sel, s_v, s_i);
+  const int nc = dec_candidates_read(a, t, s_cand, s_sel, s_i);
   if (nc < 0) return;
   if (!dec_need_chain(a, nc, s_cand)) {
     if (c == a.maxc - 1 && wv == 0) dec_route_direct(a, t, s_sel, s_tab);
@@ -1322,11 +1377,10 @@ __device__ __forceinline__ void dec_stream_block(const DecArgs &a, int j, float 
                                                  int *s_cand, int *s_sel, int *s_i) {
   const int S = a.n_stream;
   const DecLds L = dec_lds(lds, fp4_geom_np(a.H, DEC_NP), a.H);
-  float *s_v = L.aux;  // more than 256 experts: the candidates' choices
   int done = 0;  // units dealt so far
   for (int t = 0; t < a.n; ++t) {
     dec_x_codes(a, t, L.xq8, L.xqs);  // read after dec_candidates' first barrier
-    const int nc = dec_candidates(a, t, s_cand, s_sel, s_v, s_i);
+    const int nc = dec_candidates_read(a, t, s_cand, s_sel, s_i);
     if (nc < 0) return;
     const int nitems = nc * a.gu_tiles;
     const int l0 = (j + S - done % S) % S;
@@ -1360,7 +1414,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
     return dec_router_block(a, b, tabv, s_tab, s_part);
   }
   const int hr = dec_sh_gu_rows(a.H), t8 = (a.I + hr - 1) / hr, i = b - a.E;
-  if (i >= a.n * t8) return;
+  if (i >= a.n * t8) {
+    if (i - a.n * t8 < a.n) dec_cand_block(a, i - a.n * t8, lds);
+    return;
+  }
   dec_shared_gu<ST>(a, i / t8, i % t8, lds, s_y, s_tab);
 }
 
@@ -1405,17 +1462,22 @@ __device__ __forceinline__ uint32_t e4m3_codes4(const float (&q)[4]) {
   return c;
 }
 
-// Requant workgroup of route (t, k): y = bf16(t * w) and the per-128 E4M3
-// requant (src/dsv4/dsv4_model.c:6261-6287), published as codes and scales,
-// then its flag. Thread i takes 8 consecutive values; a 128-group is 16
-// neighbouring lanes. t comes from the front launch (plain loads); a route
-// without an expert, or with a position outside the candidate slots (the
-// routing of a front launch whose waits ran out), reads zeros.
+// Requant workgroup of route (t, k) (its own launch, ahead of the down
+// launch): y = bf16(t * w) and the per-128 E4M3 requant
+// (src/dsv4/dsv4_model.c:6261-6287), written as codes and scales for the
+// next launch. Thread i takes 8 consecutive values; a 128-group is 16
+// neighbouring lanes. t comes from the front launch; a route without an
+// expert, or with a position outside the candidate slots (the routing of a
+// front launch whose waits ran out), reads zeros. A launch of its own
+// because every memory round trip inside the down launch queues behind its
+// whole weight stream: the requant's t loads there took about as long as
+// the weights (and every down workgroup reading t itself made 48 KB of t a
+// hot spot for 512 readers).
 __device__ __forceinline__ void dec_route_requant(const DecArgs &a, int t, int k) {
   const int tid = threadIdx.x;
   const int I = a.I, E = a.E;
-  const int e = dec_tok(a.sel_e, a, t)[k], pos = dec_tok(a.sel_pos, a, t)[k];
-  const float w = dec_tok(a.sel_w, a, t)[k];
+  const int e = ldg(dec_tok(a.sel_e, a, t) + k), pos = ldg(dec_tok(a.sel_pos, a, t) + k);
+  const float w = ldg(dec_tok(a.sel_w, a, t) + k);
   const bool ok = e >= 0 && e < E && pos >= 0 && pos < E;
   const BufRsrc rt = buf_rsrc(dec_tok(a.sv, a, t) + (size_t)(ok ? pos : 0) * I,
                               ok ? 4u * (uint32_t)I : 0u);
@@ -1452,51 +1514,74 @@ __device__ __forceinline__ void dec_route_requant(const DecArgs &a, int t, int k
         }
         c[h] = e4m3_codes4(q);
       }
-      st_dev(qc + base / 4, c[0]);
-      st_dev(qc + base / 4 + 1, c[1]);
-      if ((tid & 15) == 0) st_dev(qcs + base / 128, scale);
+      stg(qc + base / 4, c[0]);
+      stg(qc + base / 4 + 1, c[1]);
+      if ((tid & 15) == 0) stg(qcs + base / 128, scale);
     }
   }
-  dec_signal(dec_tok(a.qf, a, t) + (size_t)k * DEC_FS);
 }
 
-// Down workgroup (token t, rows [r0, r0 + 8)): the FP4 down rows of every
-// route (routes in chunks of DB_RC; weights issued before the wait for the
-// routes' codes), lane: group g of 32 columns of tile row h rpp + lane / GP,
-// a sequential fmaf partial per group, then one lane per (route, row) chains
-// the groups in order (src/dsv4/dsv4_model.c:1049-1074), y_route =
-// bf16(acc); then out = bf16(((0 + y_0) + ... + y_{K-1}) + shared) in
-// ascending expert id (src/dsv4/dsv4_model.c:6795-6805). NPR: passes per
-// route (inter <= 1024 NPR).
+// Down workgroup (token t, rows [r0, r0 + 8)): the routes' ids first; then,
+// all in flight together, every route's E4M3 codes and scales (written by
+// the requant launch) and behind them the FP4 down rows of every route; the
+// codes into LDS as soon as they land, then the partials route by route as
+// its rows land: lane: group g of 32 columns of tile row h rpp + lane / GP,
+// a sequential fmaf partial per group; one lane per (route, row) chains the
+// groups in order (src/dsv4/dsv4_model.c:1049-1074), y_route = bf16(acc);
+// then out = bf16(((0 + y_0) + ... + y_{K-1}) + shared) in ascending expert id
+// (src/dsv4/dsv4_model.c:6795-6805). A route without an expert adds zeros.
+// NPR: passes per route (inter <= 1024 NPR); routes go in chunks of RC.
 template <int NPR>
 __device__ __forceinline__ void dec_route_down(const DecArgs &a, int t, int r0, float *lds,
-                                               int *s_e, float *s_r, int *s_i) {
+                                               int *s_e, float *s_r) {
+  constexpr int RC = NPR <= 2 ? DB_RC : DB_RC / 2;  // routes per chunk
   const int tid = threadIdx.x;
   const int H = a.H, I = a.I, K = a.K, E = a.E;
   const int G = I / 32;
   int GP = 1;
   while (GP < G) GP <<= 1;
   const int rpp = 256 / GP, g = tid % GP, rsub = tid / GP;
-  if (tid < K) s_e[tid] = dec_tok(a.sel_e, a, t)[tid];
-  const float ysh = tid < 8 ? dec_tok(a.ro, a, t)[r0 + tid] : 0.0f;
+  if (tid < K) s_e[tid] = ldg(dec_tok(a.sel_e, a, t) + tid);
+  const float ysh = tid < 8 ? ldg(dec_tok(a.ro, a, t) + r0 + tid) : 0.0f;
   __syncthreads();
   uint32_t *qy = reinterpret_cast<uint32_t *>(lds);      // [DB_RC][I / 4] codes
   float *qys = reinterpret_cast<float *>(qy + DB_RC * (I / 4));  // [DB_RC][32]
   float2 *ps = reinterpret_cast<float2 *>(qys + DB_RC * 32);       // [DB_RC * 8][stride]
   const int stride = pair_stride(G);
-  for (int k0 = 0; k0 < K; k0 += DB_RC) {
-    const int nk = min(DB_RC, K - k0);
-    uint4 w[DB_RC][NPR];
-    uint32_t code[DB_RC][NPR];
-    bool ok[DB_RC];
+  // one chunk of routes (k0 .. k0 + nk - 1)
+  auto chunk = [&](int k0) {
+    const int nk = min(RC, K - k0);
+    // every route id of the chunk before the first load (an LDS read between
+    // two routes' loads made the compiler drain the earlier loads first)
+    int es[RC];
+    bool ok[RC];
 #pragma unroll
-    for (int kk = 0; kk < DB_RC; ++kk) {
-      const int e = kk < nk ? s_e[k0 + kk] : -1;
-      ok[kk] = e >= 0 && e < E;
+    for (int kk = 0; kk < RC; ++kk) {
+      es[kk] = __builtin_amdgcn_readfirstlane(s_e[min(k0 + kk, K - 1)]);
+      ok[kk] = kk < nk && es[kk] >= 0 && es[kk] < E;
+    }
+    // the chunk's codes: nk I bytes as 16-byte pieces (at most 4 per thread
+    // for inter <= 1024 NPR) and nk I / 128 scales (at most one per thread)
+    const uint32_t nb = (uint32_t)nk * (uint32_t)I;
+    const BufRsrc rq = buf_rsrc(uptr(dec_tok(a.qc, a, t) + (size_t)k0 * (I / 4)), nb);
+    const BufRsrc rqs =
+        buf_rsrc(uptr(dec_tok(a.qcs, a, t) + (size_t)k0 * (I / 128)), 4u * (uint32_t)(nk * (I / 128)));
+    constexpr int NC = (RC * 1024 * NPR + 4095) / 4096;
+    uint4 cv[NC];
+#pragma unroll
+    for (int j = 0; j < NC; ++j) cv[j] = buf_load16(rq, 4096u * (uint32_t)j + 16u * (uint32_t)tid);
+    const float sc = buf_loadf(rqs, 4u * (uint32_t)tid);
+    // the codes are issued ahead of the rows (loads return in order)
+    __builtin_amdgcn_sched_barrier(0);
+    uint4 w[RC][NPR];
+    uint32_t code[RC][NPR];
+#pragma unroll
+    for (int kk = 0; kk < RC; ++kk) {
       const uint8_t *W, *S;
-      expert_mat(a, ok[kk] ? e : 0, 2, W, S);
-      const BufRsrc rw = buf_rsrc(W + (size_t)r0 * (I / 2), ok[kk] ? 8u * (uint32_t)(I / 2) : 0u);
-      const BufRsrc rs = buf_rsrc(S + (size_t)r0 * G, ok[kk] ? 8u * (uint32_t)G : 0u);
+      expert_mat(a, ok[kk] ? es[kk] : 0, 2, W, S);
+      const BufRsrc rw =
+          buf_rsrc(uptr(W + (size_t)r0 * (I / 2)), ok[kk] ? 8u * (uint32_t)(I / 2) : 0u);
+      const BufRsrc rs = buf_rsrc(uptr(S + (size_t)r0 * G), ok[kk] ? 8u * (uint32_t)G : 0u);
 #pragma unroll
       for (int h = 0; h < NPR; ++h) {
         const int lr = h * rpp + rsub;
@@ -1506,34 +1591,16 @@ __device__ __forceinline__ void dec_route_down(const DecArgs &a, int t, int r0, 
             rs, in ? (uint32_t)(lr * G + g) : 0xFFFFFFF0u, 0, 0);
       }
     }
-    // the chunk's routes requantised: codes and scales into LDS
-    if (!dec_wait_flags(dec_tok(a.qf, a, t) + (size_t)k0 * DEC_FS, nk, DEC_FS, nullptr, a.ctl,
-                        s_i))
-      return;
-    {
-      // coherent 8-byte loads, eight in flight per thread before the first
-      // wait (one at a time, each behind its own wait, this copy took most
-      // of the down phase)
-      const uint64_t *src = reinterpret_cast<const uint64_t *>(dec_tok(a.qc, a, t) +
-                                                               (size_t)k0 * (I / 4));
-      uint64_t *dst = reinterpret_cast<uint64_t *>(qy);
-      const int n8 = nk * (I / 8);  // I % 128 == 0: whole 8-byte words
-      for (int i0 = tid; i0 < n8; i0 += 256 * 8) {
-        uint64_t v[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = i0 + 256 * j < n8 ? ld_dev(src + i0 + 256 * j) : 0ull;
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-          if (i0 + 256 * j < n8) dst[i0 + 256 * j] = v[j];
-      }
-      const float *ss = dec_tok(a.qcs, a, t) + (size_t)k0 * (I / 128);
-      for (int i = tid; i < nk * (I / 128); i += 256)
-        qys[(i / (I / 128)) * 32 + i % (I / 128)] = ld_dev(ss + i);
+    for (int j = 0; j < NC; ++j) {
+      const uint32_t o = 4096u * (uint32_t)j + 16u * (uint32_t)tid;
+      if (o < nb) reinterpret_cast<uint4 *>(qy)[o / 16] = cv[j];
     }
+    if (tid < nk * (I / 128)) qys[(tid / (I / 128)) * 32 + tid % (I / 128)] = sc;
     __syncthreads();
     // partials: a route's passes share the lane's activation group
 #pragma unroll
-    for (int kk = 0; kk < DB_RC; ++kk) {
+    for (int kk = 0; kk < RC; ++kk) {
       if (kk >= nk) break;
       const int gc = min(g, G - 1);
       const uint4 c0 = *reinterpret_cast<const uint4 *>(qy + kk * (I / 4) + 8 * gc);
@@ -1564,49 +1631,52 @@ __device__ __forceinline__ void dec_route_down(const DecArgs &a, int t, int r0, 
       }
     }
     __syncthreads();
-    if (tid < DB_RC * 8) {
+    if (tid < RC * 8) {
       const int kk = tid / 8, lr = tid % 8, k = k0 + kk;
       if (kk < nk) {
         const float acc = ok[kk] ? pair_chain(ps + tid * stride, G) : 0.0f;
         s_r[k * 8 + lr] = bf16_round(acc);  // no expert: the route adds zeros
-        if (a.route_out) a.route_out[((size_t)t * (K + 1) + k) * H + r0 + lr] = acc;
+        if (a.route_out) stg(a.route_out + ((size_t)t * (K + 1) + k) * H + r0 + lr, acc);
       }
     }
     __syncthreads();  // qy, qys and ps are rewritten by the next chunk
-  }
+  };
+  // the model's top-k fits one chunk: no loop, so no loads that the compiler
+  // sees carried across a back edge (it drains every load at such a loop's
+  // head, the shared expert's row among them, before the first code load)
+  if (K <= RC)
+    chunk(0);
+  else
+    for (int k0 = 0; k0 < K; k0 += RC) chunk(k0);
   if (tid < 8) {
     float acc = 0.0f;
     for (int k = 0; k < K; ++k) acc += s_r[k * 8 + tid];
     acc += bf16_round(ysh);
-    a.out[(size_t)t * H + r0 + tid] = bf16_round(acc);
-    if (a.route_out) a.route_out[((size_t)t * (K + 1) + K) * H + r0 + tid] = ysh;
+    stg(a.out + (size_t)t * H + r0 + tid, bf16_round(acc));
+    if (a.route_out) stg(a.route_out + ((size_t)t * (K + 1) + K) * H + r0 + tid, ysh);
   }
 }
 
-// Blocks: [n K route requants][n (H / 8) down row tiles]. The requant
-// workgroups come first in dispatch order: the down workgroups wait for
-// them. Workgroup 0 also clears the front launch's records and flags (that
-// launch has ended).
+// Requant launch: one workgroup per route (n K). Workgroup 0 also clears the
+// front launch's records (that launch has ended).
+__global__ __launch_bounds__(256) void k_dec_requant(DecArgs a) {
+  const int b = blockIdx.x;
+  if (b == 0)
+    for (int i = threadIdx.x; i < a.n * a.E; i += 256) {
+      stg(dec_tok(a.rec, a, i / a.E) + i % a.E, (uint64_t)0);
+      stg(dec_tok(a.zrec, a, i / a.E) + i % a.E, (uint64_t)0);
+    }
+  dec_route_requant(a, b / a.K, b % a.K);
+}
+
+// Down launch: n (H / 8) row tiles, all resident at once at the model's shape.
 template <int NPR>
 __global__ __launch_bounds__(256) void k_dec_back(DecArgs a) {
   extern __shared__ __align__(16) float lds[];
   __shared__ int s_e[32];
   __shared__ float s_r[32 * 8];
-  __shared__ int s_i;
-  const int nq = a.n * a.K;
-  int b = blockIdx.x;
-  if (b < nq) {
-    if (b == 0) {
-      for (int i = threadIdx.x; i < a.n * a.E; i += 256) {
-        dec_tok(a.rec, a, i / a.E)[i % a.E] = 0ull;
-        dec_tok(a.zrec, a, i / a.E)[i % a.E] = 0ull;
-      }
-    }
-    return dec_route_requant(a, b / a.K, b % a.K);
-  }
-  b -= nq;
-  const int nt = a.H / 8;
-  dec_route_down<NPR>(a, b / nt, (b % nt) * 8, lds, s_e, s_r, &s_i);
+  const int b = blockIdx.x, nt = a.H / 8;
+  dec_route_down<NPR>(a, b / nt, (b % nt) * 8, lds, s_e, s_r);
 }
 
 __global__ void k_fill_zero_u32(unsigned *p, size_t n) {
@@ -1622,12 +1692,12 @@ using namespace dsv4;
 namespace {
 
 struct DecWs {
-  unsigned *ctl, *cf, *qf;
+  unsigned *ctl, *cf;
   uint64_t *rec, *zrec;
   uint32_t *qc;
   float *qcs, *zx, *zc, *sel_w, *sv, *ro, *xqs;
   uint8_t *xq;
-  int *sel_e, *sel_pos;
+  int *sel_e, *sel_pos, *cl;
   size_t tb;  // bytes of one token's piece
   size_t bytes;
 };
@@ -1651,9 +1721,9 @@ DecWs dec_ws_layout(const DSV4GLayer *L, int n_tokens, void *base) {
   w.rec = (uint64_t *)take(E * 8);
   w.zrec = (uint64_t *)take(E * 8);
   w.cf = (unsigned *)take(E * 4);
-  w.qf = (unsigned *)take(K * DEC_FS * 4);
   w.zx = (float *)take(E * 4);
   w.zc = (float *)take(E * 4);
+  w.cl = (int *)take((1 + E + K) * 4);
   w.sel_e = (int *)take(K * 4);
   w.sel_w = (float *)take(K * 4);
   w.sel_pos = (int *)take(K * 4);
@@ -1736,7 +1806,6 @@ int dec_launch(int phase, float *out, const float *x, const DSV4GLayer *L, const
   a.rec = w.rec;
   a.zrec = w.zrec;
   a.cf = w.cf;
-  a.qf = w.qf;
   a.qc = w.qc;
   a.qcs = w.qcs;
   a.xq = w.xq;
@@ -1744,6 +1813,7 @@ int dec_launch(int phase, float *out, const float *x, const DSV4GLayer *L, const
   a.tb = w.tb;
   a.zx = w.zx;
   a.zc = w.zc;
+  a.cl = w.cl;
   a.sel_e = w.sel_e;
   a.sel_w = w.sel_w;
   a.sel_pos = w.sel_pos;
@@ -1777,13 +1847,15 @@ int dec_launch(int phase, float *out, const float *x, const DSV4GLayer *L, const
   };
   // the staged gate/up tile keeps its scale codes in static LDS
   const size_t lds_fp8_gu = lds_fp8(H) - (dec_sh_gu_staged(H) ? 1024 : 0);
+  // the route launch's candidate workgroups: ids, choices and flags in LDS
+  const size_t lds_cand = 4 * (2 * (size_t)ROUTER_MAX_EXPERTS + 40);
   if (phase == 0) {  // activation codes, router records and the shared expert's gate/up
     const int t8 = (I + dec_sh_gu_rows(H) - 1) / dec_sh_gu_rows(H);
-    const dim3 grid((unsigned)((long)a.E + (long)n * t8));
+    const dim3 grid((unsigned)((long)a.E + (long)n * t8 + n));  // + candidate workgroups
     if (dec_sh_gu_staged(H))
-      hipLaunchKernelGGL(k_dec_route<true>, grid, dim3(256), lds_fp8_gu, st, a);
+      hipLaunchKernelGGL(k_dec_route<true>, grid, dim3(256), max_sz(lds_fp8_gu, lds_cand), st, a);
     else
-      hipLaunchKernelGGL(k_dec_route<false>, grid, dim3(256), lds_fp8_gu, st, a);
+      hipLaunchKernelGGL(k_dec_route<false>, grid, dim3(256), max_sz(lds_fp8_gu, lds_cand), st, a);
     return dsv4g_check_launch("dec_route");
   }
   if (phase == 1) {
@@ -1808,10 +1880,14 @@ int dec_launch(int phase, float *out, const float *x, const DSV4GLayer *L, const
     return dsv4g_check_launch("dec_front");
   }
   if (phase == 2) {
+    hipLaunchKernelGGL(k_dec_requant, dim3((unsigned)((long)n * a.K)), dim3(256), 0, st, a);
+    return dsv4g_check_launch("dec_requant");
+  }
+  if (phase == 3) {
     const int G = I / 32;
     const size_t lds =
         (size_t)DB_RC * I + DB_RC * 32 * 4 + (size_t)DB_RC * 8 * pair_stride(G) * 8;
-    const dim3 grid((unsigned)((long)n * a.K + (long)n * (H / 8)));
+    const dim3 grid((unsigned)((long)n * (H / 8)));
     if (I <= 1024)
       hipLaunchKernelGGL(k_dec_back<1>, grid, dim3(256), lds, st, a);
     else if (I <= 2048)

@@ -15,6 +15,29 @@
 
 namespace dsv4 {
 
+// Loads and stores through global-address-space pointers: a generic pointer
+// gives a FLAT operation, and while one is in flight the compiler can only
+// wait for every load of the wave (it cannot order FLAT against other loads),
+// so a pending generic load ahead of a weight stream serialises the stream.
+template <typename T>
+__device__ __forceinline__ T ldg(const T *p) {
+  return *(const __attribute__((address_space(1))) T *)p;
+}
+template <typename T>
+__device__ __forceinline__ void stg(T *p, T v) {
+  *(__attribute__((address_space(1))) T *)p = v;
+}
+
+// A wave-uniform pointer made visibly uniform (scalar registers), so that a
+// buffer descriptor built from it needs no per-lane waterfall loop.
+template <typename T>
+__device__ __forceinline__ T *uptr(T *p) {
+  const uint64_t v = (uint64_t)(uintptr_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return (T *)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+
 __device__ __forceinline__ uint32_t f2u(float f) { return __float_as_uint(f); }
 __device__ __forceinline__ float u2f(uint32_t u) { return __uint_as_float(u); }
 

@@ -368,7 +368,7 @@ def test_moe_phases_and_graph_replay_match_fused(env):
         assert same_bits(H(ref)[t], o), t
     ws = lib.new_moe_workspace(DL, 3, env["dev"])
     out = torch.zeros_like(X)
-    for ph in range(3):
+    for ph in range(dg.DECODE_PHASES):
         lib.moe_decode_phase(ph, DL, X, out, ws)
     torch.cuda.synchronize()
     assert torch.equal(out, ref)
