@@ -1320,7 +1320,11 @@ __device__ __forceinline__ void dec_gu_chain(const DecArgs &a, int t, int c, int
                                              const Fp4Geom &q, const DecLds &L, float *s_y,
                                              const uint64_t *s_tab) {
   const int tid = threadIdx.x, I = a.I, half = q.tr / 2;
+  // the chain lanes' wave ahead of the other waves' partials on its SIMD:
+  // at the usual priority its 128 dependent steps took about 2 us
+  __builtin_amdgcn_s_setprio(3);
   const float v = fp4_tile_chain(q, L.ps);
+  __builtin_amdgcn_s_setprio(0);
   if (tid < q.tr) s_y[tid] = v;
   __syncthreads();
   if (tid < half && r0 + tid < I)
@@ -1363,34 +1367,37 @@ __device__ __forceinline__ void dec_routed_items(const DecArgs &a, int t, int l0
   __syncthreads();  // LDS (candidates, activation) is rewritten by the next token
 }
 
-// Streaming workgroup j of n_stream (k_dec_front): per token, its quantised
-// activation (codes and per-128 scales, written by the route launch) into
-// LDS, the candidates (dec_candidates: the route launch has written every
-// router record, so the first poll finds them) and its routed gate/up items,
-// then its tiles of the shared down rows. The units (a routed item: 16 FP4
-// rows, 32 KB; a shared down tile: 16 FP8 rows, 32 KB) are dealt round-robin
-// over the streaming workgroups in the order [token 0's items, token 1's
-// items, ..., the shared down tiles], so no workgroup has more than one unit
-// above the mean. ST: the shared down tiles are staged (fp8s_ok(I)).
+// Streaming workgroup j of n_stream (k_dec_front): first its tiles of the
+// shared expert's down rows (their input, the shared t, is complete when the
+// launch starts, so their loads fill the time the candidates take to
+// arrive), then per token its quantised activation (codes and per-128
+// scales, written by the route launch) into LDS, the candidates
+// (dec_candidates_read) and its routed gate/up items. The units (a shared
+// down tile: 16 FP8 rows, 32 KB; a routed item: 16 FP4 rows, 32 KB) are
+// dealt round-robin over the streaming workgroups in the order [the shared
+// down tiles, token 0's items, token 1's items, ...], so no workgroup has
+// more than one unit above the mean. ST: the shared down tiles are staged
+// (fp8s_ok(I)).
 template <bool ST>
 __device__ __forceinline__ void dec_stream_block(const DecArgs &a, int j, float *lds, float *s_y, uint64_t *s_tab,
                                                  int *s_cand, int *s_sel, int *s_i) {
   const int S = a.n_stream;
   const DecLds L = dec_lds(lds, fp4_geom_np(a.H, DEC_NP), a.H);
-  int done = 0;  // units dealt so far
+  const int t16 = (a.H + dec_sh_dn_rows(a.I) - 1) / dec_sh_dn_rows(a.I);
+  int done = a.n * t16;  // units dealt so far: the shared down tiles first
+  for (int i = j; i < done; i += S) {
+    __syncthreads();  // LDS of the previous unit
+    dec_shared_dn<ST>(a, i / t16, i % t16, lds);
+  }
+  __syncthreads();  // the tiles' LDS before the activation codes take it
   for (int t = 0; t < a.n; ++t) {
-    dec_x_codes(a, t, L.xq8, L.xqs);  // read after dec_candidates' first barrier
+    dec_x_codes(a, t, L.xq8, L.xqs);  // read after dec_candidates_read's first barrier
     const int nc = dec_candidates_read(a, t, s_cand, s_sel, s_i);
     if (nc < 0) return;
     const int nitems = nc * a.gu_tiles;
     const int l0 = (j + S - done % S) % S;
     if (l0 < nitems) dec_routed_items(a, t, l0, nitems, nc, true, L, s_y, s_tab, s_cand);
     done += nitems;
-  }
-  const int t16 = (a.H + dec_sh_dn_rows(a.I) - 1) / dec_sh_dn_rows(a.I);
-  for (int i = (j + S - done % S) % S; i < a.n * t16; i += S) {
-    __syncthreads();  // LDS of the previous unit
-    dec_shared_dn<ST>(a, i / t16, i % t16, lds);
   }
 }
 
