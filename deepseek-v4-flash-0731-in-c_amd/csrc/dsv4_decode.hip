@@ -1,5 +1,5 @@
 // dsv4_decode.hip - the decode MoE layer on gfx950: moe_forward
-// (src/dsv4/dsv4_model.c:6599-6807) for a few tokens, bit for bit, as four
+// (src/dsv4/dsv4_model.c:6599-6807) for a few tokens, bit for bit, as three
 // kernels per layer (workgroups are dispatched in index order; a wait inside
 // a launch only ever holds a workgroup whose producers were dispatched
 // before it and never wait on it):
@@ -22,11 +22,13 @@
 //                  * bf16 up into the candidate's slot
 //                  (src/dsv4/dsv4_model.c:6264-6268), then the shared
 //                  expert's down rows.
-//   k_dec_requant  one workgroup per route: y = bf16(t * w) and the per-128
-//                  E4M3 requant (src/dsv4/dsv4_model.c:6239-6287), as codes.
-//   k_dec_back     one workgroup per 8 output rows: the FP4 down rows of
-//                  every route, then the routes in ascending expert id and
-//                  the shared expert, rounded to BF16
+//   k_dec_back     one requant workgroup per route first: y = bf16(t * w)
+//                  and the per-128 E4M3 requant
+//                  (src/dsv4/dsv4_model.c:6239-6287), published as codes and
+//                  a flag; then one workgroup per 8 output rows: the FP4 down
+//                  rows of every route (issued before the wait for the
+//                  codes), then the routes in ascending expert id and the
+//                  shared expert, rounded to BF16
 //                  (src/dsv4/dsv4_model.c:6795-6805).
 //
 // Memory round trips that one launch's workgroups need before their weights
@@ -79,7 +81,7 @@ namespace dsv4 {
 // about a microsecond: on the order of a second)
 #define DEC_SPIN_LIMIT (1u << 20)
 #define DB_RC 6  // routes per chunk of k_dec_back
-#define DEC_PHASES 4  // launches per layer: route, front, requant, down
+#define DEC_PHASES 3  // launches per layer: route, front, back
 // set in the high word of a router record once it is written (the low 31
 // bits hold sum|w*x|, whose sign bit is always clear)
 #define DEC_REC_SET 0x80000000u
@@ -106,6 +108,7 @@ struct DecArgs {
   float *xqs;      // [H/128] their per-128 scales
   float *zx, *zc;  // [E] exact score sqrt_softplus(z) and choice score + bias per
                    // candidate position
+  unsigned *qf;    // [K] route requant done flags (DEC_FS apart)
   int *cl;         // [1 + E + K] the candidates (route launch): count, ids, then the
                    // K best approximate choices in selection order
   int *sel_e;      // [K] routing, ascending id (moe_forward's idx)
@@ -739,11 +742,15 @@ __device__ __forceinline__ void dec_select(const DecArgs &a, int t, int nc, cons
 // (wv + 1) H/4), lane l its 8-column pieces l, l + 64, ... (gate row and x
 // read directly); for every token the approximate choice sqrt_softplus(z) +
 // bias with sum|w*x| (rounding depth: dec_par_depth) and z, each published as
-// one 64-bit record that carries its own DEC_REC_SET mark.
+// one 64-bit record that carries its own DEC_REC_SET mark. Workgroup 0 also
+// clears the previous call's requant flags.
 __device__ __forceinline__ void dec_router_block(const DecArgs &a, int e, uint64_t tabv,
                                                  uint64_t *s_tab, float *s_part) {
   const int tid = threadIdx.x, wv = tid / 64, lane = tid % 64;
   const int H = a.H, Q = H / 4;
+  if (e == 0)
+    for (int i = tid; i < a.n * a.K; i += 256)
+      stg(dec_tok(a.qf, a, i / a.K) + (size_t)(i % a.K) * DEC_FS, 0u);
   const BufRsrc rg = buf_rsrc(a.gate + (size_t)e * H + (size_t)wv * Q, 2u * (uint32_t)Q);
   uint4 w[4];  // Q <= 2048: at most 4 pieces per lane; pieces past Q read zeros
 #pragma unroll
@@ -1469,17 +1476,24 @@ __device__ __forceinline__ uint32_t e4m3_codes4(const float (&q)[4]) {
   return c;
 }
 
-// Requant workgroup of route (t, k) (its own launch, ahead of the down
+// 16 bytes of a buffer with the agent-scope coherent load (sc1: data written
+// by another workgroup of the launch through st_dev, as ld_dev reads it;
+// past the range: zeros).
+__device__ __forceinline__ uint4 buf_load16_dev(BufRsrc r, uint32_t off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 16);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
+// Requant workgroup of route (t, k) (the first n K workgroups of the back
 // launch): y = bf16(t * w) and the per-128 E4M3 requant
-// (src/dsv4/dsv4_model.c:6261-6287), written as codes and scales for the
-// next launch. Thread i takes 8 consecutive values; a 128-group is 16
-// neighbouring lanes. t comes from the front launch; a route without an
-// expert, or with a position outside the candidate slots (the routing of a
-// front launch whose waits ran out), reads zeros. A launch of its own
-// because every memory round trip inside the down launch queues behind its
-// whole weight stream: the requant's t loads there took about as long as
-// the weights (and every down workgroup reading t itself made 48 KB of t a
-// hot spot for 512 readers).
+// (src/dsv4/dsv4_model.c:6261-6287), published as codes and scales
+// (write-through stores), then its flag. Thread i takes 8 consecutive
+// values; a 128-group is 16 neighbouring lanes. t comes from the front
+// launch; a route without an expert, or with a position outside the
+// candidate slots (the routing of a front launch whose waits ran out), reads
+// zeros. (Every down workgroup requantising for itself made the routes' t,
+// 48 KB read by 512 workgroups, an L2 hot spot; a launch of its own cost a
+// launch gap more than the flag hand-off.)
 __device__ __forceinline__ void dec_route_requant(const DecArgs &a, int t, int k) {
   const int tid = threadIdx.x;
   const int I = a.I, E = a.E;
@@ -1521,18 +1535,22 @@ __device__ __forceinline__ void dec_route_requant(const DecArgs &a, int t, int k
         }
         c[h] = e4m3_codes4(q);
       }
-      stg(qc + base / 4, c[0]);
-      stg(qc + base / 4 + 1, c[1]);
-      if ((tid & 15) == 0) stg(qcs + base / 128, scale);
+      st_dev(qc + base / 4, c[0]);
+      st_dev(qc + base / 4 + 1, c[1]);
+      if ((tid & 15) == 0) st_dev(qcs + base / 128, scale);
     }
   }
+  dec_signal(dec_tok(a.qf, a, t) + (size_t)k * DEC_FS);
 }
 
-// Down workgroup (token t, rows [r0, r0 + 8)): the routes' ids first; then,
-// all in flight together, every route's E4M3 codes and scales (written by
-// the requant launch) and behind them the FP4 down rows of every route; the
-// codes into LDS as soon as they land, then the partials route by route as
-// its rows land: lane: group g of 32 columns of tile row h rpp + lane / GP,
+// Down workgroup (token t, rows [r0, r0 + 8)): the routes' ids first; then
+// the FP4 down rows of every route, all in flight together; then wave 0
+// polls the chunk's requant flags (its first poll returns behind its own rows,
+// when the requant has normally long finished, so hundreds of workgroups do
+// not keep polling the flag lines while the weights stream) and every thread
+// copies the routes' E4M3 codes and scales with coherent loads (one memory
+// round trip); then the partials route by route: lane: group g of 32
+// columns of tile row h rpp + lane / GP,
 // a sequential fmaf partial per group; one lane per (route, row) chains the
 // groups in order (src/dsv4/dsv4_model.c:1049-1074), y_route = bf16(acc);
 // then out = bf16(((0 + y_0) + ... + y_{K-1}) + shared) in ascending expert id
@@ -1540,7 +1558,7 @@ __device__ __forceinline__ void dec_route_requant(const DecArgs &a, int t, int k
 // NPR: passes per route (inter <= 1024 NPR); routes go in chunks of RC.
 template <int NPR>
 __device__ __forceinline__ void dec_route_down(const DecArgs &a, int t, int r0, float *lds,
-                                               int *s_e, float *s_r) {
+                                               int *s_e, float *s_r, int *s_i) {
   constexpr int RC = NPR <= 2 ? DB_RC : DB_RC / 2;  // routes per chunk
   const int tid = threadIdx.x;
   const int H = a.H, I = a.I, K = a.K, E = a.E;
@@ -1567,19 +1585,6 @@ __device__ __forceinline__ void dec_route_down(const DecArgs &a, int t, int r0, 
       es[kk] = __builtin_amdgcn_readfirstlane(s_e[min(k0 + kk, K - 1)]);
       ok[kk] = kk < nk && es[kk] >= 0 && es[kk] < E;
     }
-    // the chunk's codes: nk I bytes as 16-byte pieces (at most 4 per thread
-    // for inter <= 1024 NPR) and nk I / 128 scales (at most one per thread)
-    const uint32_t nb = (uint32_t)nk * (uint32_t)I;
-    const BufRsrc rq = buf_rsrc(uptr(dec_tok(a.qc, a, t) + (size_t)k0 * (I / 4)), nb);
-    const BufRsrc rqs =
-        buf_rsrc(uptr(dec_tok(a.qcs, a, t) + (size_t)k0 * (I / 128)), 4u * (uint32_t)(nk * (I / 128)));
-    constexpr int NC = (RC * 1024 * NPR + 4095) / 4096;
-    uint4 cv[NC];
-#pragma unroll
-    for (int j = 0; j < NC; ++j) cv[j] = buf_load16(rq, 4096u * (uint32_t)j + 16u * (uint32_t)tid);
-    const float sc = buf_loadf(rqs, 4u * (uint32_t)tid);
-    // the codes are issued ahead of the rows (loads return in order)
-    __builtin_amdgcn_sched_barrier(0);
     uint4 w[RC][NPR];
     uint32_t code[RC][NPR];
 #pragma unroll
@@ -1598,12 +1603,31 @@ __device__ __forceinline__ void dec_route_down(const DecArgs &a, int t, int r0, 
             rs, in ? (uint32_t)(lr * G + g) : 0xFFFFFFF0u, 0, 0);
       }
     }
+    __builtin_amdgcn_sched_barrier(0);  // the rows are issued before the poll
+    if (!dec_wait_flags(dec_tok(a.qf, a, t) + (size_t)k0 * DEC_FS, nk, DEC_FS, nullptr, a.ctl,
+                        s_i))
+      return;
+    {
+      // the chunk's codes: nk I bytes as 16-byte pieces (at most 3 per
+      // thread for inter <= 1024 NPR) and nk I / 128 scales (at most one per
+      // thread), coherent loads (written in this launch)
+      const uint32_t nb = (uint32_t)nk * (uint32_t)I;
+      const BufRsrc rq = buf_rsrc(uptr(dec_tok(a.qc, a, t) + (size_t)k0 * (I / 4)), nb);
+      const BufRsrc rqs = buf_rsrc(uptr(dec_tok(a.qcs, a, t) + (size_t)k0 * (I / 128)),
+                                   4u * (uint32_t)(nk * (I / 128)));
+      constexpr int NC = (RC * 1024 * NPR + 4095) / 4096;
+      uint4 cv[NC];
 #pragma unroll
-    for (int j = 0; j < NC; ++j) {
-      const uint32_t o = 4096u * (uint32_t)j + 16u * (uint32_t)tid;
-      if (o < nb) reinterpret_cast<uint4 *>(qy)[o / 16] = cv[j];
+      for (int j = 0; j < NC; ++j)
+        cv[j] = buf_load16_dev(rq, 4096u * (uint32_t)j + 16u * (uint32_t)tid);
+      const float sc = u2f(__builtin_amdgcn_raw_buffer_load_b32(rqs, 4u * (uint32_t)tid, 0, 16));
+#pragma unroll
+      for (int j = 0; j < NC; ++j) {
+        const uint32_t o = 4096u * (uint32_t)j + 16u * (uint32_t)tid;
+        if (o < nb) reinterpret_cast<uint4 *>(qy)[o / 16] = cv[j];
+      }
+      if (tid < nk * (I / 128)) qys[(tid / (I / 128)) * 32 + tid % (I / 128)] = sc;
     }
-    if (tid < nk * (I / 128)) qys[(tid / (I / 128)) * 32 + tid % (I / 128)] = sc;
     __syncthreads();
     // partials: a route's passes share the lane's activation group
 #pragma unroll
@@ -1664,26 +1688,28 @@ __device__ __forceinline__ void dec_route_down(const DecArgs &a, int t, int r0, 
   }
 }
 
-// Requant launch: one workgroup per route (n K). Workgroup 0 also clears the
-// front launch's records (that launch has ended).
-__global__ __launch_bounds__(256) void k_dec_requant(DecArgs a) {
-  const int b = blockIdx.x;
-  if (b == 0)
-    for (int i = threadIdx.x; i < a.n * a.E; i += 256) {
-      stg(dec_tok(a.rec, a, i / a.E) + i % a.E, (uint64_t)0);
-      stg(dec_tok(a.zrec, a, i / a.E) + i % a.E, (uint64_t)0);
-    }
-  dec_route_requant(a, b / a.K, b % a.K);
-}
-
-// Down launch: n (H / 8) row tiles, all resident at once at the model's shape.
+// Back launch: [n K requant workgroups][n (H / 8) down row tiles], all
+// resident at once at the model's shape; the requant workgroups come first in
+// dispatch order (the down workgroups wait for them). Requant workgroup 0
+// also clears the front launch's records (that launch has ended).
 template <int NPR>
 __global__ __launch_bounds__(256) void k_dec_back(DecArgs a) {
   extern __shared__ __align__(16) float lds[];
   __shared__ int s_e[32];
   __shared__ float s_r[32 * 8];
-  const int b = blockIdx.x, nt = a.H / 8;
-  dec_route_down<NPR>(a, b / nt, (b % nt) * 8, lds, s_e, s_r);
+  __shared__ int s_i;
+  const int nq = a.n * a.K, nt = a.H / 8;
+  int b = blockIdx.x;
+  if (b < nq) {
+    if (b == 0)
+      for (int i = threadIdx.x; i < a.n * a.E; i += 256) {
+        stg(dec_tok(a.rec, a, i / a.E) + i % a.E, (uint64_t)0);
+        stg(dec_tok(a.zrec, a, i / a.E) + i % a.E, (uint64_t)0);
+      }
+    return dec_route_requant(a, b / a.K, b % a.K);
+  }
+  b -= nq;
+  dec_route_down<NPR>(a, b / nt, (b % nt) * 8, lds, s_e, s_r, &s_i);
 }
 
 __global__ void k_fill_zero_u32(unsigned *p, size_t n) {
@@ -1699,7 +1725,7 @@ using namespace dsv4;
 namespace {
 
 struct DecWs {
-  unsigned *ctl, *cf;
+  unsigned *ctl, *cf, *qf;
   uint64_t *rec, *zrec;
   uint32_t *qc;
   float *qcs, *zx, *zc, *sel_w, *sv, *ro, *xqs;
@@ -1728,6 +1754,7 @@ DecWs dec_ws_layout(const DSV4GLayer *L, int n_tokens, void *base) {
   w.rec = (uint64_t *)take(E * 8);
   w.zrec = (uint64_t *)take(E * 8);
   w.cf = (unsigned *)take(E * 4);
+  w.qf = (unsigned *)take(K * DEC_FS * 4);
   w.zx = (float *)take(E * 4);
   w.zc = (float *)take(E * 4);
   w.cl = (int *)take((1 + E + K) * 4);
@@ -1813,6 +1840,7 @@ int dec_launch(int phase, float *out, const float *x, const DSV4GLayer *L, const
   a.rec = w.rec;
   a.zrec = w.zrec;
   a.cf = w.cf;
+  a.qf = w.qf;
   a.qc = w.qc;
   a.qcs = w.qcs;
   a.xq = w.xq;
@@ -1887,14 +1915,10 @@ int dec_launch(int phase, float *out, const float *x, const DSV4GLayer *L, const
     return dsv4g_check_launch("dec_front");
   }
   if (phase == 2) {
-    hipLaunchKernelGGL(k_dec_requant, dim3((unsigned)((long)n * a.K)), dim3(256), 0, st, a);
-    return dsv4g_check_launch("dec_requant");
-  }
-  if (phase == 3) {
     const int G = I / 32;
     const size_t lds =
         (size_t)DB_RC * I + DB_RC * 32 * 4 + (size_t)DB_RC * 8 * pair_stride(G) * 8;
-    const dim3 grid((unsigned)((long)n * (H / 8)));
+    const dim3 grid((unsigned)((long)n * a.K + (long)n * (H / 8)));
     if (I <= 1024)
       hipLaunchKernelGGL(k_dec_back<1>, grid, dim3(256), lds, st, a);
     else if (I <= 2048)

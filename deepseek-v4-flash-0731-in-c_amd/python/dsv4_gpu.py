@@ -14,7 +14,7 @@ import os
 HERE = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.dirname(HERE)
 LIB_PATH = os.path.join(PKG, "lib", "libdsv4_gpu.so")
-DECODE_PHASES = 4  # DSV4G_DECODE_PHASES: ordered launches of one decode layer
+DECODE_PHASES = 3  # DSV4G_DECODE_PHASES: ordered launches of one decode layer
 
 _vp = C.c_void_p
 

@@ -219,15 +219,15 @@ int dsv4g_moe_forward_noalloc(float *out, const float *x, const DSV4GLayer *L,
 int dsv4g_moe_noalloc_status(unsigned *status, void *stream);
 /* The same layer as DSV4G_DECODE_PHASES ordered launches, for callers that
  * interleave or time them: 0 the activation's E4M3 codes, the approximate
- * router logits and the shared expert's gate/up; 1 the candidate experts,
- * exact router chains and top-k, the candidates' gate/up GEMVs and the
- * shared expert's down GEMV; 2 the routes' SwiGLU requant; 3 the routed down
+ * router logits, the candidate experts and the shared expert's gate/up; 1
+ * the exact router chains and top-k, the candidates' gate/up GEMVs and the
+ * shared expert's down GEMV; 2 the routes' SwiGLU requant, the routed down
  * GEMVs and the ordered combine. Phases 0 .. DSV4G_DECODE_PHASES - 1 in
  * order equal one fused call (the workspace is left as the fused call
  * leaves it only after the last). phase | DSV4G_DECODE_FAST runs those of
  * dsv4g_moe_forward_fast. dsv4g_moe_decode_routing copies the routing of the
  * last call. x and out: 16-byte aligned. */
-#define DSV4G_DECODE_PHASES 4
+#define DSV4G_DECODE_PHASES 3
 #define DSV4G_DECODE_FAST 256
 int dsv4g_moe_decode_phase(int phase, float *out, const float *x, const DSV4GLayer *L,
                            const int *token_ids, int n_tokens, void *workspace,
