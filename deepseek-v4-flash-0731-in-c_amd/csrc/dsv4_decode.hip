@@ -1347,7 +1347,8 @@ __device__ __forceinline__ void dec_gu_chain(const DecArgs &a, int t, int c, int
 // more bandwidth than two tiles in turn in fewer workgroups).
 __device__ __forceinline__ void dec_routed_items(const DecArgs &a, int t, int l0, int le, int nc,
                                                  bool have_x, const DecLds &L, float *s_y,
-                                                 const uint64_t *s_tab, const int *s_cand) {
+                                                 uint64_t *s_tab, uint64_t tabv,
+                                                 const int *s_cand) {
   const int H = a.H, S = a.n_stream;
   const Fp4Geom q = fp4_geom_np(H, DEC_NP);
   const int nitems = nc * a.gu_tiles;
@@ -1358,6 +1359,9 @@ __device__ __forceinline__ void dec_routed_items(const DecArgs &a, int t, int l0
   }
   Fp4RegsT<DEC_NP> A;
   fp4_tile_x_lds(A, L.xq8, L.xqs, q);  // the lane's activation group: the same for every item
+  // the expf table for SwiGLU (loaded at the workgroup's start; read after
+  // the first chain's barrier)
+  libm_table_store(s_tab, tabv);
   // the next item's loads go out as soon as this item's partials are in LDS
   // (its weight registers are free then), so they are in flight while this
   // item's group chains and SwiGLU run
@@ -1387,7 +1391,7 @@ __device__ __forceinline__ void dec_routed_items(const DecArgs &a, int t, int l0
 // (fp8s_ok(I)).
 template <bool ST>
 __device__ __forceinline__ void dec_stream_block(const DecArgs &a, int j, float *lds, float *s_y, uint64_t *s_tab,
-                                                 int *s_cand, int *s_sel, int *s_i) {
+                                                 uint64_t tabv, int *s_cand, int *s_sel, int *s_i) {
   const int S = a.n_stream;
   const DecLds L = dec_lds(lds, fp4_geom_np(a.H, DEC_NP), a.H);
   const int t16 = (a.H + dec_sh_dn_rows(a.I) - 1) / dec_sh_dn_rows(a.I);
@@ -1403,7 +1407,7 @@ __device__ __forceinline__ void dec_stream_block(const DecArgs &a, int j, float 
     if (nc < 0) return;
     const int nitems = nc * a.gu_tiles;
     const int l0 = (j + S - done % S) % S;
-    if (l0 < nitems) dec_routed_items(a, t, l0, nitems, nc, true, L, s_y, s_tab, s_cand);
+    if (l0 < nitems) dec_routed_items(a, t, l0, nitems, nc, true, L, s_y, s_tab, tabv, s_cand);
     done += nitems;
   }
 }
@@ -1455,8 +1459,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
     return dec_chain_block(a, b / a.maxc, b % a.maxc, lds, s_tab, s_cand, s_sel, &s_i);
   const int j = b - a.n * a.maxc;
   if (j >= a.n_stream) return;
-  libm_table_store(s_tab, libm_table_load());
-  dec_stream_block<ST>(a, j, lds, s_y, s_tab, s_cand, s_sel, &s_i);
+  // the expf table's load goes first, but its LDS store (which waits for
+  // it) only when the first routed item needs it, not ahead of the first
+  // weight loads: a memory round trip at the start of every workgroup
+  const uint64_t tabv = libm_table_load();
+  dec_stream_block<ST>(a, j, lds, s_y, s_tab, tabv, s_cand, s_sel, &s_i);
 }
 
 // ------------------------------------------------------- down + combine ----

@@ -479,6 +479,155 @@ __global__ __launch_bounds__(64) void k_rowchain(RowChainArgs a) {
   }
 }
 
+// ================================================ product chains (FP8) ===
+// dsv4_gemv_fp8 / dsv4_gemv_fp8_tbl with the products formed apart from the
+// chain. The reference's per-row loop acc += p[c] (p[c] = w[c] * xs[c] with
+// xs = x * s, or (w[c] * x[c]) * s; each product rounded on its own, the
+// build unfused; src/dsv4/dsv4_ops.c:176-239) adds products that do not
+// depend on acc. So all four waves of a workgroup form its PC_ROWS rows'
+// products into LDS (rows padded by 16 bytes, so that the chain lanes'
+// reads of one column fall in distinct banks), and then one lane per row
+// runs only the dependent adds, in column order, four products per LDS read
+// and the next 32 products' reads in flight while 32 are added. (One lane
+// per row decoding, scaling, multiplying and adding every column ran at
+// about 23 cycles per column; an add chain alone runs at its dependency
+// latency.) The rows of a workgroup share one row block (block a multiple of
+// 16); in a multiple of 32, at most PC_MAXIN.
+#define PC_ROWS 8
+#define PC_MAXIN 4096
+
+// acc + p[0] + ... + p[4 N4 - 1] in order, p in LDS (16-byte aligned): fully
+// unrolled, so every read is one instruction with an immediate offset and
+// the lane's instruction stream holds nothing but reads and the dependent
+// adds (in a single wave every other instruction delays the chain by its
+// issue time); the compiler places the reads ahead within its register
+// budget.
+template <int N4>
+__device__ __forceinline__ float pc_chain_fixed(const float4 *p4, float acc) {
+#pragma unroll
+  for (int j = 0; j < N4; ++j) {
+    const float4 v = p4[j];
+    acc = acc + v.x;
+    acc = acc + v.y;
+    acc = acc + v.z;
+    acc = acc + v.w;
+  }
+  return acc;
+}
+
+// The products of piece k of the calling thread (16 columns of one row) into
+// the row's LDS products: p = w * xs (MODE 0) or (w * x) * s (MODE 1).
+template <int MODE>
+__device__ __forceinline__ void pc_products(const uint4 w, int r, int c, const float *xs,
+                                            const float *srow, int block, int ps, float *pr) {
+  const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+  const float sc = MODE == 1 ? srow[c / block] : 1.0f;
+  float4 *dst = reinterpret_cast<float4 *>(pr + (size_t)r * ps + c);
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const float2 lo = fp8x2<false>(wd[d]), hi = fp8x2<true>(wd[d]);
+    const float4 xv = *reinterpret_cast<const float4 *>(xs + c + 4 * d);
+    float4 p;
+    if (MODE == 0) {
+      p = make_float4(lo.x * xv.x, lo.y * xv.y, hi.x * xv.z, hi.y * xv.w);
+    } else {
+      p = make_float4((lo.x * xv.x) * sc, (lo.y * xv.y) * sc, (hi.x * xv.z) * sc,
+                      (hi.y * xv.w) * sc);
+    }
+    dst[d] = p;
+  }
+}
+
+// Two halves of the columns: every thread loads and forms pieces of the first
+// half; waves 1-3 alone load the second half. After the first half's
+// products (a barrier), wave 0's chain lanes add it while waves 1-3 form the
+// second half's products and then raise an LDS flag, which the chain lanes
+// wait for at the half's boundary; so the chain starts once half the weights
+// have landed.
+template <int MODE>
+__global__ __launch_bounds__(256) void k_fp8_prodchain(float *__restrict__ y,
+                                                       const float *__restrict__ x,
+                                                       const uint8_t *__restrict__ W,
+                                                       const float *__restrict__ wscale, int in,
+                                                       int rows, int block) {
+  extern __shared__ __align__(16) float lds[];
+  __shared__ int s_half;
+  const int tid = threadIdx.x, r0 = blockIdx.x * PC_ROWS;
+  const int cblocks = (in + block - 1) / block;
+  const int ps = in + 4;             // product row stride (floats)
+  float *xs = lds;                   // [in] x (MODE 1) or x * s (MODE 0)
+  float *pr = lds + in;              // [PC_ROWS][ps] products
+  const float *srow = wscale + (size_t)(r0 / block) * cblocks;
+  const int hp = in / 32;            // 16-byte pieces per half row
+  const int nrow = min(PC_ROWS, rows - r0);
+  // first half: piece i of PC_ROWS * hp (row i / hp, columns 16 (i % hp) ..),
+  // two per thread at most; second half: PC_ROWS * hp pieces over the 192
+  // threads of waves 1-3, six per thread at most (in <= PC_MAXIN)
+  constexpr int P0 = PC_ROWS * PC_MAXIN / 32 / 256, P1 = (PC_ROWS * PC_MAXIN / 32 + 191) / 192;
+  const BufRsrc rw = buf_rsrc(W + (size_t)r0 * in, (uint32_t)(nrow * in));
+  auto off = [&](int i, int half) {  // byte offset of piece i of a half
+    return i < PC_ROWS * hp
+               ? (uint32_t)(i / hp) * (uint32_t)in + 16u * (uint32_t)(half * hp + i % hp)
+               : 0xFFFFFFF0u;
+  };
+  uint4 w0[P0], w1[P1];
+#pragma unroll
+  for (int k = 0; k < P0; ++k) w0[k] = buf_load16(rw, off(tid + 256 * k, 0));
+  if (tid >= 64) {
+#pragma unroll
+    for (int k = 0; k < P1; ++k) w1[k] = buf_load16(rw, off(tid - 64 + 192 * k, 1));
+  }
+  if (tid == 0) s_half = 0;
+  for (int i = tid; i < in / 4; i += 256) {
+    float4 v = reinterpret_cast<const float4 *>(x)[i];
+    if (MODE == 0) {  // xs = x * s of the row block (the 4 columns share a column block)
+      const float sc = srow[(4 * i) / block];
+      v = make_float4(v.x * sc, v.y * sc, v.z * sc, v.w * sc);
+    }
+    reinterpret_cast<float4 *>(xs)[i] = v;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < P0; ++k) {
+    const int i = tid + 256 * k;
+    if (i < PC_ROWS * hp) pc_products<MODE>(w0[k], i / hp, 16 * (i % hp), xs, srow, block, ps, pr);
+  }
+  __syncthreads();
+  if (tid >= 64) {
+#pragma unroll
+    for (int k = 0; k < P1; ++k) {
+      const int i = tid - 64 + 192 * k;
+      if (i < PC_ROWS * hp)
+        pc_products<MODE>(w1[k], i / hp, 16 * (hp + i % hp), xs, srow, block, ps, pr);
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's product stores done
+    if (tid % 64 == 0) atomicAdd(&s_half, 1);
+    return;
+  }
+  if (tid >= PC_ROWS || tid >= nrow) return;
+  const float4 *p4 = reinterpret_cast<const float4 *>(pr + (size_t)tid * ps);
+  const int n4 = in / 4, h4 = n4 / 2;  // a multiple of 4 each
+  float acc = 0.0f;
+  auto chain = [&](int b0, int b1) {
+    if (h4 == 512) {  // the model's width: 8 fixed blocks of 64 float4 a half
+#pragma unroll 1
+      for (int b = b0; b < b1; b += 64) acc = pc_chain_fixed<64>(p4 + b, acc);
+    } else {
+      int b = b0;
+      for (; b + 16 <= b1; b += 16) acc = pc_chain_fixed<16>(p4 + b, acc);
+      for (; b < b1; ++b) acc = pc_chain_fixed<1>(p4 + b, acc);
+    }
+  };
+  chain(0, h4);
+  // the second half's products: every wave of 1-3 has raised the flag (a
+  // bounded wait: they finish their products long before the first half's
+  // chain ends; volatile reads of the LDS counter)
+  for (unsigned it = 0; *(volatile int *)&s_half < 3 && it < (1u << 24); ++it)
+    __builtin_amdgcn_s_sleep(1);
+  chain(h4, n4);
+  y[r0 + tid] = acc;
+}
+
 // ======================================================= greedy pick ===
 // The CLI's greedy token (src/cli/dsv4_run.c:357-359): best = 0, then every
 // v with logits[v] > logits[best] in order; so the first index of the
@@ -922,6 +1071,21 @@ int dsv4g_gemv_fp8_float(float *y, const float *x, const uint8_t *W, const float
                          int in, int rows, int block, int mode, void *stream) {
   if (in <= 0 || rows <= 0 || block <= 0)
     return dsv4g_fail(DSV4G_EINVAL, "gemv_fp8_float: bad size");
+  if (in % 32 == 0 && in <= PC_MAXIN && block % 16 == 0 && ((uintptr_t)x & 15) == 0) {
+    const size_t lds = ((size_t)in + (size_t)PC_ROWS * (in + 4)) * 4;
+    const void *fn = mode == 0 ? (const void *)k_fp8_prodchain<0> : (const void *)k_fp8_prodchain<1>;
+    // more than the default 64 KB of LDS (a host-side setting of the kernel)
+    DSV4G_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  (int)(((size_t)PC_MAXIN + (size_t)PC_ROWS * (PC_MAXIN + 4)) * 4)));
+    const dim3 grid((unsigned)((rows + PC_ROWS - 1) / PC_ROWS));
+    if (mode == 0)
+      hipLaunchKernelGGL(k_fp8_prodchain<0>, grid, dim3(256), lds, (hipStream_t)stream, y, x, W,
+                         wscale, in, rows, block);
+    else
+      hipLaunchKernelGGL(k_fp8_prodchain<1>, grid, dim3(256), lds, (hipStream_t)stream, y, x, W,
+                         wscale, in, rows, block);
+    return dsv4g_check_launch("gemv_fp8_float");
+  }
   if (in % 16 == 0 && block % 16 == 0 && (size_t)in * 4 * 2 <= RC_XBYTES &&
       ((uintptr_t)x & 15) == 0) {
     RowChainArgs a = {};

@@ -153,7 +153,8 @@ def test_fp8_gemv_full_size_bit_exact(env, rows, in_):
                      orc.gemv_fp8_batch_q(qx, qs, W, S, in_, rows, 1))
 
 
-@pytest.mark.parametrize("rows,in_", [(256, 4096), (2048, 4096), (37, 200)])
+@pytest.mark.parametrize("rows,in_", [(256, 4096), (2048, 4096), (37, 200), (37, 4096),
+                                     (300, 2048)])
 def test_bf16_and_float_gemvs_full_size_bit_exact(env, rows, in_):
     """The standalone BF16 GEMV (batch of 3, with and without BF16 output
     rounding) and the float-scale FP8 / FP4 GEMVs against the oracle's
@@ -467,3 +468,23 @@ def test_moe_forward_fast_tolerance(env, shape, kw):
         bound = bf16_ulp(o) + 1e-3 * np.max(np.abs(o))
         assert np.all(np.abs(d) <= bound), (t, float(np.max(np.abs(d) / bound)))
     print(f"\n  fast decode: max norm-relative error {worst:.2e}")
+
+
+@pytest.mark.parametrize("block", [16, 64, 256])
+def test_fp8_float_gemv_block_sizes(env, block):
+    """dsv4_gemv_fp8 / _tbl with other block sizes than the model's 128: the
+    product-chain kernel's rows share one row block for every block size that
+    is a multiple of 16; 44 rows leave a partial last workgroup."""
+    orc, lib = env["orc"], env["lib"]
+    rows, in_ = 44, 1024
+    rng = np.random.default_rng(block)
+    x = rng.standard_normal(in_).astype(np.float32)
+    codes = rng.integers(0, 256, (rows, in_), dtype=np.uint8)
+    codes[(codes & 0x7F) == 0x7F] = 0x35
+    fsc = (rng.random(((rows + block - 1) // block, (in_ + block - 1) // block)) * 0.01
+           + 1e-4).astype(np.float32)
+    gx, gc, gs = T(env, x), T(env, codes), T(env, fsc)
+    assert same_bits(H(lib.gemv_fp8_float(gx, gc, gs, in_, rows, block, 0)),
+                     orc.gemv_fp8_legacy(x, codes, fsc, in_, rows, block))
+    assert same_bits(H(lib.gemv_fp8_float(gx, gc, gs, in_, rows, block, 1)),
+                     orc.gemv_fp8_tbl(x, codes, fsc, in_, rows, block))
