@@ -256,8 +256,9 @@ def bench_fp4_expert(lib, layer, cpu_seconds):
     nbytes = EXPERT_BYTES + H * 4 + (H // 128) * 4 + H * 4
     gbs = nbytes / (ms * 1e-3) / 1e9
     r = {"workload": "FP4 E2M1 single-expert SwiGLU at 1 token: gate/up 2048 x 4096, down "
-                     "4096 x 2048, per-32 E8M0 scales (expert_forward: paired FP4 GEMV, "
-                     "SwiGLU + FP8 requant, FP4 down GEMV; three launches)",
+                     "4096 x 2048, per-32 E8M0 scales (expert_forward: paired FP4 GEMV "
+                     "with the SwiGLU epilogue, then the FP4 down GEMV with the per-128 "
+                     "FP8 requant folded in; two launches)",
          "ms_per_call": round(ms, 5), "bytes_per_call": nbytes, "gbs": round(gbs, 1),
          "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
                       "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4)}}

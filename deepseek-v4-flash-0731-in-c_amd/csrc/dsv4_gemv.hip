@@ -134,8 +134,14 @@ __global__ __launch_bounds__(256) void k_gemv_fp4_t(GemvArgs a, int pair) {
   if (pair) {
     fp4_pair_finish(R, s_y, a.rows, r0, q, ps, cl);
     __syncthreads();
-    if (tid < q.tr && r0 + tid % half < a.rows)
+    if (a.swi_y) {  // routed_swiglu_quant's y (src/dsv4/dsv4_model.c:6258-6268)
+      if (tid < half && r0 + tid < a.rows)
+        a.swi_y[(size_t)b * a.y_stride + r0 + tid] =
+            bf16_round(swiglu_t(s_y[tid], s_y[tid + half], a.swi_limit) *
+                       (a.swi_w ? *a.swi_w : 1.0f));
+    } else if (tid < q.tr && r0 + tid % half < a.rows) {
       a.y[tid / half][(size_t)b * a.y_stride + r0 + tid % half] = s_y[tid];
+    }
   } else {
     fp4_tile_finish(R, a.y[0] + (size_t)b * a.y_stride, a.rows, r0, q, ps, cl);
   }
@@ -894,6 +900,7 @@ int dsv4g_launch_gemv_fp4(const GemvArgs *a, int nvec, int nmat, void *stream) {
     if ((long)((a->rows + span - 1) / span) * nvec >= 1024) break;
     np /= 2;
   }
+  if (a->np) np = a->np;
   switch (np) {
     case 1: launch_fp4_t<1>(a, nvec, pair, st); break;
     case 2: launch_fp4_t<2>(a, nvec, pair, st); break;

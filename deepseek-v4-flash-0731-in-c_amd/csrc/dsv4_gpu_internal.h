@@ -25,6 +25,12 @@ struct GemvArgs {
   const float *qscale;
   size_t y_stride, qx_stride, qs_stride;
   int in, rows, round_out;
+  // paired FP4 tiles with the SwiGLU epilogue (swi_y set): swi_y[r] =
+  // bf16(swiglu(gate[r], up[r]) * swi_w) instead of the two rows
+  float *swi_y;
+  const float *swi_w;  // device pointer to the route weight (null: 1)
+  float swi_limit;
+  int np;  // FP4 passes per tile (0: chosen by the launcher)
 };
 
 // Largest expert count of the router kernels.

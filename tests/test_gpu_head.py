@@ -139,3 +139,23 @@ def test_expert_forward_full_size(env):
         ref = orc.expert_forward(qx[0], qs[0], scales, weights, 4096, 2048, 10,
                                  1.0 if w is None else w)
         assert same_bits(H(out), ref), w
+
+
+@pytest.mark.parametrize("hidden,inter", [(256, 128), (1024, 384), (2048, 4096)])
+def test_expert_forward_shapes(env, hidden, inter):
+    """The two-launch expert_forward (gate/up with the SwiGLU epilogue, then the
+    down rows with the requant folded in) at other shapes: an inter that is not
+    a multiple of 512 and the widest inter the fused path takes."""
+    orc, lib, torch = env["orc"], env["lib"], env["torch"]
+    L = make_layer(orc, hidden, inter, 2, 1, seed=hidden + inter)
+    scales, weights = expert_slot(L, 0)
+    slot = np.concatenate([scales, weights])
+    rng = np.random.default_rng(inter)
+    x = bf16_input(rng, (1, hidden))
+    qx, qs = orc.quant_fp8_act(x)
+    out = torch.empty(hidden, dtype=torch.float32, device=env["dev"])
+    gw = torch.tensor([0.618], dtype=torch.float32, device=env["dev"])
+    lib.expert_forward(out, T(env, qx[0]), T(env, qs[0]), T(env, slot), L["scale_run"], hidden,
+                       inter, 10.0, gw)
+    ref = orc.expert_forward(qx[0], qs[0], scales, weights, hidden, inter, 10, 0.618)
+    assert same_bits(H(out), ref)
