@@ -44,6 +44,11 @@ sys.path.insert(0, os.path.join(ROOT, "deepseek-v4-flash-0731-in-c_amd", "python
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0   # dense MFMA peaks of one MI355X
 FP8_PEAK_TFLOPS = 5000.0
+# fp32 vector FMA: 256 CUs x 64 lanes x 2 flops x 2.4 GHz issued one FMA per
+# lane per clock; the published 157.3 TFLOP/s is the packed (two-wide) rate,
+# which this build does not emit
+FP32_FMA_PEAK_TFLOPS = 78.6
+VOCAB = 129280
 METRIC = "MoE layer decode GB/s (% HBM peak); prefill grouped-GEMM TFLOPS (% MFMA)"
 
 H, I, E, K = 4096, 2048, 256, 6
@@ -69,7 +74,8 @@ def parse():
     p.add_argument("--replays", type=int, default=5)
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--no-cpu", action="store_true")
-    p.add_argument("--workload", choices=("all", "decode", "verify", "prefill", "kernels"),
+    p.add_argument("--workload", choices=("all", "decode", "verify", "prefill", "kernels",
+                                          "head"),
                    default="all")
     p.add_argument("--zipf-strength", type=float, default=0.15)
     p.add_argument("--copy-calibration", action="store_true",
@@ -458,6 +464,76 @@ def bench_attn_proj(lib, cpu_seconds):
     return res
 
 
+def bench_vocab_head(lib, cpu_seconds):
+    """The vocabulary head (head_logits / head_logits_batch,
+    src/dsv4/dsv4_model.c:7313-7445) through dsv4_gemv_bf16: BF16 rows
+    [129280][4096] N(0, 0.02), hidden states N(0, 1) rounded to BF16 values
+    and held as fp32, fp32 logits; 1 token (decode) and 64 tokens (a verify
+    batch). The 1.06 GB head exceeds every cache, so each call streams it
+    from HBM. Bit-exact per-row fmaf chains in column order."""
+    import numpy as np
+    import torch
+    import synth
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(33)
+    W = torch.empty(VOCAB, H, dtype=torch.bfloat16, device=dev)
+    for r0 in range(0, VOCAB, 16384):
+        r1 = min(VOCAB, r0 + 16384)
+        W[r0:r1] = (torch.randn(r1 - r0, H, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    Wu = W.view(torch.int16)
+    X = synth.bf16_tokens(64, H, seed=9, device=dev)
+    Y = torch.empty(64, VOCAB, dtype=torch.float32, device=dev)
+    wbytes = VOCAB * H * 2
+    res = {"workload": "vocabulary head 129280 x 4096 BF16, fp32 logits (dsv4_gemv_bf16; "
+                       "1 token: coalesced 64 x 64 tiles transposed through LDS, a lane per "
+                       "row, HBM-bound; 64 tokens: 4 rows x 16 tokens of chains per lane, x "
+                       "from LDS, fp32-FMA-bound)", "weight_bytes": wbytes}
+    for n in (1, 64):
+        ms = graph_time(lambda i, n=n: lib.gemv_bf16_into(Y[:n], X[:n], Wu, H, VOCAB, 0),
+                        8 if n == 1 else 2)
+        nbytes = wbytes + n * H * 4 + n * VOCAB * 4
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        tf = 2.0 * VOCAB * H * n / (ms * 1e-3) / 1e12
+        r = {"ms_per_call": round(ms, 5), "bytes_per_call": nbytes, "gbs": round(gbs, 1),
+             "tflops": round(tf, 2)}
+        if n == 1:
+            r["roofline"] = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                             "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4)}
+        else:
+            r["roofline"] = {"bound": "fp32 fma issue (the per-row chains are fmaf in column "
+                                      "order, so no matrix-core form is exact)",
+                             "achieved": round(tf, 2), "peak": FP32_FMA_PEAK_TFLOPS,
+                             "unit": "TFLOP/s", "frac": round(tf / FP32_FMA_PEAK_TFLOPS, 4),
+                             "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+        res[f"{n}_token" + ("s" if n > 1 else "")] = r
+    if cpu_seconds and cpu_available():
+        threads, _ = host_cores()
+        set_omp_threads(threads)
+        ref = cpu_ref()
+        Wh = Wu.cpu().numpy().view(np.uint16)
+        Xh = X.cpu().numpy()
+        for n in (1, 64):
+            lib.gemv_bf16_into(Y[:n], X[:n], Wu, H, VOCAB, 0)
+            got = Y[:n].cpu().numpy()
+            yr = ref.head_logits(Xh[:n], Wh, threads)
+            same = bool(np.array_equal(yr.view(np.uint32), got.view(np.uint32)))
+            sec, calls = cpu_loop(lambda n=n: ref.head_logits(Xh[:n], Wh, threads),
+                                  cpu_seconds / 2, max_calls=50)
+            key = f"{n}_token" + ("s" if n > 1 else "")
+            nbytes = res[key]["bytes_per_call"]
+            res[key]["cpu_baseline"] = {
+                "value": round(nbytes / sec / 1e9, 3), "unit": "GB/s", "cores": threads,
+                "kind": "reference", "ms_per_call": round(sec * 1e3, 3),
+                "gpu_output_bit_exact_vs_reference": same,
+                "sample": f"{calls} calls of the reference "
+                          f"{'head_logits' if n == 1 else 'head_logits_batch'} (oracle/_ref, "
+                          f"AVX2, OMP_NUM_THREADS={threads}) on the same head and tokens"}
+        del Wh
+    del W, Wu, Y
+    return res
+
+
 def bench_checkpoint_load(lib, layer):
     """Checkpoint to HBM (dsv4g_load_moe_layer): 16 full-size routed experts of
     one layer, its FP8 shared expert, gate and bias, written as three
@@ -763,19 +839,23 @@ def main():
     dev = torch.device("cuda:0")
     lib = dsv4_gpu.lib()
     wl = args.workload
+    cpu_s = 0.0 if args.no_cpu else min(args.cpu_seconds, 6.0)
+    if wl == "head":
+        print(json.dumps({"vocab_head": bench_vocab_head(lib, cpu_s)}))
+        return
     nl = args.layers if wl in ("all", "decode") else 1
     t0 = time.perf_counter()
     layers = [synth.device_layer(seed=100 + l, device=dev) for l in range(nl)]
     torch.cuda.synchronize()
     gen_s = time.perf_counter() - t0
 
-    cpu_s = 0.0 if args.no_cpu else min(args.cpu_seconds, 6.0)
     kernels = {}
     if wl in ("all", "kernels"):
         kernels["fp8_matvec_2048x4096"] = bench_fp8_matvec(lib, cpu_s)
         kernels["fp4_expert_1_token"] = bench_fp4_expert(lib, layers[0], cpu_s)
         kernels["ffn_step_1_token"] = bench_ffn_step(lib, layers, cpu_s)
         kernels["attention_projections"] = bench_attn_proj(lib, cpu_s)
+        kernels["vocab_head"] = bench_vocab_head(lib, cpu_s)
         kernels["checkpoint_load"] = bench_checkpoint_load(lib, layers[0])
         if wl == "kernels":
             print(json.dumps(kernels))

@@ -634,6 +634,214 @@ __global__ __launch_bounds__(256) void k_fp8_prodchain(float *__restrict__ y,
   y[r0 + tid] = acc;
 }
 
+// ================================================ batched BF16 rows ====
+// dsv4_gemv_bf16_batch / head_logits_batch (src/dsv4/dsv4_model.c:266-367,
+// 7371-7445) for many tokens, where the fp32 FMA issue rate, not HBM, is the
+// bound (64 tokens through the 129280 x 4096 head: 34 G dependent-chain
+// fmaf). Register blocking: lane = (row group rg = lane / 4, token group
+// tg = lane % 4) keeps 4 rows x KT tokens of chains, so each weight is read
+// and widened once for KT tokens and each x value read from LDS feeds 4 rows.
+// x moves through LDS in blocks of 8 columns (double-buffered, the next
+// block's weights and x in flight while the current block is chained); the
+// four token groups' rows sit 4 floats apart in LDS so that one 16-byte read
+// of all four hits distinct banks. Per (row, token) the fmaf chain runs in
+// column order, as the reference's. The reads of token k + 1 are issued
+// while token k is chained: an empty asm on token k's accumulators pins that
+// order, or the compiler hoists all reads of a block and runs out of
+// registers. in a multiple of 8, x 16-byte aligned; tokens [t0, t0 + 4 KT)
+// all present.
+template <int KT>
+__global__ __launch_bounds__(64) void k_bf16_rows_blocked(float *__restrict__ y,
+                                                          const float *__restrict__ x,
+                                                          const uint16_t *__restrict__ W, int in,
+                                                          int rows, int round_out, int t0) {
+  constexpr int NT = 4 * KT;            // tokens of this launch
+  constexpr int XS = NT * 8 + 16;       // one block: token t at 8 t + 4 (t / KT)
+  constexpr int NQ = (2 * NT + 63) / 64;  // 16-byte x pieces per lane per block
+  __shared__ __align__(16) float xs[2][XS];
+  const int lane = threadIdx.x, rg = lane >> 2, tg = lane & 3;
+  const int r0 = blockIdx.x * 64, rr = 4 * rg;
+  const int nrow = min(64, rows - r0);
+  const uint32_t rb = 2u * (uint32_t)in;
+  const BufRsrc rw = buf_rsrc(W + (size_t)r0 * in, (uint32_t)nrow * rb);
+  // rows past the tile's end read row 0 (in bounds) and are not stored
+  const uint32_t ro0 = rr < nrow ? (uint32_t)rr * rb : 0u;
+  const uint32_t ro1 = rr + 1 < nrow ? (uint32_t)(rr + 1) * rb : 0u;
+  const uint32_t ro2 = rr + 2 < nrow ? (uint32_t)(rr + 2) * rb : 0u;
+  const uint32_t ro3 = rr + 3 < nrow ? (uint32_t)(rr + 3) * rb : 0u;
+  const float *xb = x + (size_t)t0 * in;
+  // x staging: piece p = lane + 64 q (q < NQ <= 2) is token p / 2, columns
+  // 4 (p % 2) .. + 3; a lane past the last piece re-reads it and stores nothing
+  static_assert(NQ <= 2, "x staging holds two pieces per lane");
+  const int p0 = min(lane, 2 * NT - 1), p1 = min(lane + 64, 2 * NT - 1);
+  const float *xp0 = xb + (size_t)(p0 >> 1) * in + 4 * (p0 & 1);
+  const float *xp1 = xb + (size_t)(p1 >> 1) * in + 4 * (p1 & 1);
+  const int so0 = 4 * p0 + 4 * ((p0 >> 1) / KT);  // 8 t + 4 (p % 2) + 4 (t / KT)
+  const int so1 = 4 * p1 + 4 * ((p1 >> 1) / KT);
+  const bool st0 = lane < 2 * NT, st1 = NQ > 1 && lane + 64 < 2 * NT;
+  float acc[4][KT];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int k = 0; k < KT; ++k) acc[j][k] = 0.0f;
+  uint4 w0 = buf_load16(rw, ro0), w1 = buf_load16(rw, ro1), w2 = buf_load16(rw, ro2),
+        w3 = buf_load16(rw, ro3);
+  float4 xr0 = *reinterpret_cast<const float4 *>(xp0), xr1 = xr0;
+  if (NQ > 1) xr1 = *reinterpret_cast<const float4 *>(xp1);
+  if (st0) *reinterpret_cast<float4 *>(&xs[0][so0]) = xr0;
+  if (st1) *reinterpret_cast<float4 *>(&xs[0][so1]) = xr1;
+  __syncthreads();
+  const int rd = 8 * KT * tg + 4 * tg;  // token KT tg of this lane's group
+  int b = 0;
+  for (int c0 = 0; c0 < in; c0 += 8) {
+    const bool more = c0 + 8 < in;
+    uint4 n0, n1, n2, n3;
+    if (more) {
+      const uint32_t o = 2u * (uint32_t)(c0 + 8);
+      n0 = buf_load16(rw, ro0 + o);
+      n1 = buf_load16(rw, ro1 + o);
+      n2 = buf_load16(rw, ro2 + o);
+      n3 = buf_load16(rw, ro3 + o);
+      xr0 = *reinterpret_cast<const float4 *>(xp0 + c0 + 8);
+      if (NQ > 1) xr1 = *reinterpret_cast<const float4 *>(xp1 + c0 + 8);
+    }
+    float wv[4][8];
+    const uint4 wq[4] = {w0, w1, w2, w3};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t wd[4] = {wq[j].x, wq[j].y, wq[j].z, wq[j].w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        wv[j][2 * k] = u2f(wd[k] << 16);
+        wv[j][2 * k + 1] = u2f(wd[k] & 0xFFFF0000u);
+      }
+    }
+    const float *xl = &xs[b][rd];
+    float4 na = *reinterpret_cast<const float4 *>(xl);
+    float4 nb = *reinterpret_cast<const float4 *>(xl + 4);
+#pragma unroll
+    for (int k = 0; k < KT; ++k) {
+      const float4 xa = na, xc = nb;
+      if (k + 1 < KT) {
+        na = *reinterpret_cast<const float4 *>(xl + 8 * (k + 1));
+        nb = *reinterpret_cast<const float4 *>(xl + 8 * (k + 1) + 4);
+      }
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float a = acc[j][k];
+        a = fmaf(wv[j][0], xa.x, a);
+        a = fmaf(wv[j][1], xa.y, a);
+        a = fmaf(wv[j][2], xa.z, a);
+        a = fmaf(wv[j][3], xa.w, a);
+        a = fmaf(wv[j][4], xc.x, a);
+        a = fmaf(wv[j][5], xc.y, a);
+        a = fmaf(wv[j][6], xc.z, a);
+        a = fmaf(wv[j][7], xc.w, a);
+        acc[j][k] = a;
+      }
+      asm volatile("" : "+v"(acc[0][k]), "+v"(acc[1][k]), "+v"(acc[2][k]), "+v"(acc[3][k]));
+    }
+    if (more) {
+      if (st0) *reinterpret_cast<float4 *>(&xs[b ^ 1][so0]) = xr0;
+      if (st1) *reinterpret_cast<float4 *>(&xs[b ^ 1][so1]) = xr1;
+      w0 = n0;
+      w1 = n1;
+      w2 = n2;
+      w3 = n3;
+    }
+    __syncthreads();
+    b ^= 1;
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int row = r0 + rr + j;
+    if (row < rows) {
+#pragma unroll
+      for (int k = 0; k < KT; ++k) {
+        const float v = acc[j][k];
+        y[(size_t)(t0 + KT * tg + k) * rows + row] = round_out ? bf16_round(v) : v;
+      }
+    }
+  }
+}
+
+// The same chains for 1 to 3 tokens (decode, and the remainder of a batch
+// split into runs of 4 KT), where HBM is the bound: a lane per output row
+// reading its own row would touch 64 cache lines per load, so the wave loads
+// tiles of 64 rows x 64 columns coalesced (lane l: rows 8 i + l / 8, 16
+// bytes at column 8 (l % 8)), writes them to LDS (rows 144 bytes apart, so
+// that the lanes' row reads hit distinct banks) and reads back its own row's
+// 64 columns. Two tiles are in flight while one is chained; x enters each
+// fmaf as a scalar operand. LDS holds one tile: the wave's LDS accesses run
+// in order, and the empty asms keep the compiler from moving them across
+// each other. in a multiple of 64; tokens [t0, t0 + TB) present.
+#define RT_DEPTH 2
+template <int TB>
+__global__ __launch_bounds__(64) void k_bf16_rows_tiled(float *__restrict__ y,
+                                                        const float *__restrict__ x,
+                                                        const uint16_t *__restrict__ W, int in,
+                                                        int rows, int round_out, int t0) {
+  __shared__ __align__(16) uint4 tl[64 * 9];
+  const int lane = threadIdx.x, r0 = blockIdx.x * 64;
+  const int nrow = min(64, rows - r0);
+  const uint32_t rb = 2u * (uint32_t)in;
+  const BufRsrc rw = buf_rsrc(W + (size_t)r0 * in, (uint32_t)nrow * rb);
+  const int lr = lane >> 3, lp = lane & 7;
+  const uint32_t lo = (uint32_t)lr * rb + 16u * lp;  // tile t, rows 8 i + lr: + 8 rb i + 128 t
+  const int nt = in / 64;
+  typedef const __attribute__((address_space(4))) float cfloat;
+  cfloat *xc = (cfloat *)(x + (size_t)t0 * in);
+  uint4 T[RT_DEPTH][8];
+#pragma unroll
+  for (int d = 0; d < RT_DEPTH; ++d)
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      T[d][i] = buf_load16(rw, d < nt ? lo + 8u * rb * i + 128u * d : 0xFFFFFFF0u);
+  float acc[TB];
+#pragma unroll
+  for (int t = 0; t < TB; ++t) acc[t] = 0.0f;
+  for (int tb = 0; tb < nt; tb += RT_DEPTH) {
+#pragma unroll
+    for (int d = 0; d < RT_DEPTH; ++d) {
+      const int t = tb + d;
+      if (t >= nt) break;  // uniform
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for (int i = 0; i < 8; ++i) tl[(8 * i + lr) * 9 + lp] = T[d][i];
+      if (t + RT_DEPTH < nt) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          T[d][i] = buf_load16(rw, lo + 8u * rb * i + 128u * (t + RT_DEPTH));
+      }
+      asm volatile("" ::: "memory");
+      uint4 m[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) m[k] = tl[lane * 9 + k];
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const uint32_t wd[4] = {m[k].x, m[k].y, m[k].z, m[k].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int c = 64 * t + 8 * k + 2 * e;
+          const float wl = u2f(wd[e] << 16), wh = u2f(wd[e] & 0xFFFF0000u);
+#pragma unroll
+          for (int u = 0; u < TB; ++u) {
+            acc[u] = fmaf(wl, xc[(size_t)u * in + c], acc[u]);
+            acc[u] = fmaf(wh, xc[(size_t)u * in + c + 1], acc[u]);
+          }
+        }
+      }
+    }
+  }
+  if (lane >= nrow) return;
+#pragma unroll
+  for (int u = 0; u < TB; ++u)
+    y[(size_t)(t0 + u) * rows + r0 + lane] = round_out ? bf16_round(acc[u]) : acc[u];
+}
+
 // ======================================================= greedy pick ===
 // The CLI's greedy token (src/cli/dsv4_run.c:357-359): best = 0, then every
 // v with logits[v] > logits[best] in order; so the first index of the
@@ -1036,6 +1244,25 @@ int dsv4g_gemv_bf16(float *y, const float *x, const uint16_t *W, int in, int out
                     int round_out, int batch, void *stream) {
   if (in <= 0 || out <= 0 || batch <= 0) return dsv4g_fail(DSV4G_EINVAL, "gemv_bf16: bad size");
   const size_t xb = (size_t)batch * in * 4;
+  if (in % 64 == 0 && ((uintptr_t)x & 15) == 0 && (size_t)64 * in * 2 < 0xFFFF0000u) {
+    // runs of 64, 32, 16, 8 or 4 tokens through the register-blocked chains,
+    // a remainder of 1 to 3 through the tiled chains
+    const dim3 grid((out + 63) / 64);
+    for (int t0 = 0; t0 < batch;) {
+      const int rem = batch - t0;
+      const int tb = rem >= 64 ? 64 : rem >= 32 ? 32 : rem >= 16 ? 16 : rem >= 8 ? 8 : rem >= 4 ? 4
+                                                                                      : rem;
+      auto k = tb == 64 ? k_bf16_rows_blocked<16> : tb == 32 ? k_bf16_rows_blocked<8>
+               : tb == 16 ? k_bf16_rows_blocked<4> : tb == 8 ? k_bf16_rows_blocked<2>
+               : tb == 4 ? k_bf16_rows_blocked<1> : tb == 3 ? k_bf16_rows_tiled<3>
+               : tb == 2 ? k_bf16_rows_tiled<2> : k_bf16_rows_tiled<1>;
+      hipLaunchKernelGGL(k, grid, dim3(64), 0, (hipStream_t)stream, y, x, W, in, out, round_out,
+                         t0);
+      DSV4G_TRY(dsv4g_check_launch("gemv_bf16"));
+      t0 += tb;
+    }
+    return 0;
+  }
   if (in % 8 == 0 && xb <= RC_XBYTES && (size_t)64 * in * 2 < 0xFFFF0000u &&
       ((uintptr_t)x & 15) == 0) {
     RowChainArgs a = {};

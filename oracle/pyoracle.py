@@ -417,6 +417,17 @@ class RefLib(_Base):
                                 round_out)
         return y
 
+    def head_logits(self, h, W, threads):
+        """head_logits (1 token) / head_logits_batch (more) of the reference
+        engine on BF16 head rows W [vocab][hid]: fp32 logits [n][vocab]."""
+        h = f32(np.atleast_2d(h))
+        n, hid = h.shape
+        vocab = W.shape[0]
+        y = np.empty((n, vocab), np.float32)
+        self.lib.ref_shim_head_logits(_p(y, _f32p), _p(h, _f32p), _p(W, _u16p), hid, vocab, n,
+                                      int(threads))
+        return y
+
     def gemv_fp8_q(self, qx, qs, W, S, in_, out, round_out=1):
         y = np.empty(out, np.float32)
         self.lib.dsv4_gemv_fp8_q(_p(y, _f32p), _p(f32(qx), _f32p), _p(f32(qs), _f32p),

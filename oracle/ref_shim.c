@@ -10,6 +10,8 @@
  *   moe_forward              src/dsv4/dsv4_model.c:6599
  *   moe_forward_batch        src/dsv4/dsv4_model.c:6812
  *   sqrt_softplus            src/dsv4/dsv4_model.c:5827
+ *   head_logits              src/dsv4/dsv4_model.c:7313
+ *   head_logits_batch        src/dsv4/dsv4_model.c:7373
  * The MoE entries run on a hand-built DSV4Model whose expert cache holds every
  * expert of layer 0, so every expert lookup is a hit and no I/O path runs
  * (expert_get_many, src/dsv4/dsv4_model.c:3642-3663).
@@ -221,4 +223,24 @@ void ref_shim_hc_post(float *state, const float *branch, const float *post,
     if (!nw) { fprintf(stderr, "ref_shim: OOM\n"); exit(1); }
     hc_post_scratch(state, branch, post, comb, mult, hid, nw);
     free(nw);
+}
+
+/* The vocabulary head on a DSV4Model whose head tensor is the given BF16 rows
+ * [vocab][hid] in memory, as for a mapped checkpoint (head_map_rows), on
+ * `threads` OpenMP threads: one token through head_logits, more through
+ * head_logits_batch. */
+void ref_shim_head_logits(float *logits, const float *h, const uint16_t *rows, int hid,
+                          int vocab, int n_tokens, int threads)
+{
+    DSV4Model *m = (DSV4Model *)calloc(1, sizeof(DSV4Model));
+    if (!m) { fprintf(stderr, "ref_shim: OOM\n"); exit(1); }
+    m->cfg.hidden = hid;
+    m->cfg.vocab = vocab;
+    m->threads = threads > 0 ? threads : 1;
+    m->head_map_rows = rows;
+    if (n_tokens == 1)
+        head_logits(m, h, logits);
+    else
+        head_logits_batch(m, h, n_tokens, logits);
+    free(m);
 }

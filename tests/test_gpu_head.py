@@ -3,9 +3,9 @@ the oracle on identical inputs, bit for bit:
 
 * the vocabulary head, the reference's per-row fmaf chain
   (head_logits_block, src/dsv4/dsv4_model.c:7221-7255), at its full shape
-  (129280 x 4096 BF16, about 1 GiB) for one token and for a 3-token verify
-  batch (head_logits_block_batch, :7257-7308), then the greedy token of
-  every row (src/cli/dsv4_run.c:357-359, NaN and tie edges included);
+  (129280 x 4096 BF16, about 1 GiB) for one token and for 3- and 64-token
+  verify batches (head_logits_block_batch, :7257-7308), then the greedy token
+  of every row (src/cli/dsv4_run.c:357-359, NaN and tie edges included);
 * dsv4_gemv_bf16_batch at the batch sizes of each kernel instance;
 * dsv4_gemv_fp8 / _tbl at the FP8 matvec benchmark's shape (2048 x 4096,
   fp32 absmax block scales, fp32 x);
@@ -72,6 +72,15 @@ def test_vocab_head_full_size_and_greedy(env):
     idx = H(lib.argmax(torch.from_numpy(three).to(env["dev"])))
     for t in range(3):
         assert idx[t] == cli_greedy_fast(three[t]), t
+    # 64 tokens (a verify batch; the batched row chains): every token equal to
+    # its own one-token head, three of them to the oracle
+    h64 = bf16_input(rng, (64, hid))
+    h64d = T(env, h64)
+    b64 = H(lib.gemv_bf16(h64d, Wd, hid, vocab, 0))
+    for t in range(64):
+        assert same_bits(b64[t], H(lib.gemv_bf16(h64d[t:t + 1], Wd, hid, vocab, 0))[0]), t
+    for t in (0, 37, 63):
+        assert same_bits(b64[t], orc.gemv_bf16(h64[t], W, hid, vocab, 0)), t
     del Wd
 
 
@@ -95,8 +104,15 @@ def test_greedy_edges(env):
 
 
 @pytest.mark.parametrize("rows,in_,batch", [(300, 1024, 5), (300, 1024, 9), (1000, 256, 33),
-                                            (64, 4096, 2)])
+                                            (64, 4096, 2), (200, 4096, 5), (130, 4096, 71),
+                                            (64, 2048, 40), (100, 1024, 20), (77, 4096, 3),
+                                            (300, 1000, 3), (50, 2056, 9)])
 def test_bf16_batch_instances(env, rows, in_, batch):
+    """Every kernel form: for in a multiple of 64, the register-blocked chains
+    in runs of 64/32/16/8/4 tokens and the tiled chains for a remainder of 1
+    to 3 (5 = 4 + 1, 71 = 64 + 4 + 3, 40 = 32 + 8, ragged last row tiles);
+    for other in, the x-in-LDS row chains (x up to 64 KB) and the
+    one-row-per-(row, token) fallback."""
     orc, lib = env["orc"], env["lib"]
     rng = np.random.default_rng(rows + batch)
     W = bf16_bits(rng.standard_normal((rows, in_), dtype=np.float32) * 0.05)

@@ -362,6 +362,23 @@ def test_oracle_matches_compiled_reference_full_size(orc):
     assert same_bits(orc.sqrt_softplus(z), ref.sqrt_softplus(z))
 
 
+@pytest.mark.skipif(not pyoracle.ref_available(), reason="oracle/_ref not built")
+@pytest.mark.parametrize("vocab,n", [(1003, 1), (1003, 7), (517, 40)])
+def test_oracle_gemv_bf16_is_the_reference_head(orc, vocab, n):
+    """head_logits (AVX2 8-row blocks plus a scalar tail block) and
+    head_logits_batch (tokens in runs of DSV4_MAX_TOPK + 1) of the compiled
+    reference equal the oracle's per-row BF16 chain, token by token: the GPU
+    head is checked against the latter."""
+    ref = pyoracle.RefLib()
+    rng = np.random.default_rng(vocab + n)
+    hid = 768
+    W = bf16_bits(rng.standard_normal((vocab, hid), dtype=np.float32) * 0.02)
+    h = rng.standard_normal((n, hid)).astype(np.float32)
+    y = ref.head_logits(h, W, 4)
+    for t in range(n):
+        assert same_bits(y[t], orc.gemv_bf16(h[t], W, hid, vocab, 0)), t
+
+
 # ---------------------------------------------------------- libm restatement
 def test_libm_restatement_matches_host_libm(tmp_path):
     """The GPU's expf/log1pf source (dsv4_libm.h) is bit-identical to the host
