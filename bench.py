@@ -75,7 +75,7 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--workload", choices=("all", "decode", "verify", "prefill", "kernels",
-                                          "head"),
+                                          "head", "dropin"),
                    default="all")
     p.add_argument("--zipf-strength", type=float, default=0.15)
     p.add_argument("--copy-calibration", action="store_true",
@@ -534,6 +534,107 @@ def bench_vocab_head(lib, cpu_seconds):
     return res
 
 
+def bench_dropin(cpu_seconds):
+    """The reference-named entry points on host buffers, called through the C
+    ABI as a reference caller would (src/dsv4/dsv4_internal.h:261-272):
+    dsv4_gemv_fp8_q at 2048 x 4096 (E4M3, 128 x 128 E8M0 scales) and
+    dsv4_gemv_fp4_pair_q at one expert's gate/up shape (two 2048 x 4096 E2M1
+    matrices, per-32 E8M0 scales), weights N(0, 0.02), x BF16 N(0, 1)
+    quantised per 128. Every call copies its activations in and its outputs
+    back and synchronises; unregistered weights are also copied from pageable
+    host memory on every call, registered ones (dsv4_gpu_register_weights)
+    stay in HBM. Host wall clock per call."""
+    import ctypes as C
+    import numpy as np
+    import torch
+    import dsv4_gpu
+    dev = torch.device("cuda:0")
+    glib = dsv4_gpu.lib()
+    lib = C.CDLL(dsv4_gpu.LIB_PATH)
+    f32p, u8p = C.POINTER(C.c_float), C.POINTER(C.c_uint8)
+    lib.dsv4_gpu_register_weights.restype = C.c_int
+    lib.dsv4_gpu_register_weights.argtypes = [C.c_void_p, C.c_size_t]
+    lib.dsv4_gpu_forget_weights.argtypes = [C.c_void_p]
+    P = lambda a, t: a.ctypes.data_as(t)
+    g = torch.Generator(device=dev)
+    g.manual_seed(41)
+    rows, cols = 2048, 4096
+    w = torch.randn(rows, cols, generator=g, device=dev) * 0.02
+    c8 = torch.empty(rows, cols, dtype=torch.uint8, device=dev)
+    s8 = torch.empty(rows // 128, cols // 128, dtype=torch.uint8, device=dev)
+    glib.quant_fp8_blocks(w, c8, s8, mode=0)
+    fp4 = []
+    for _ in range(2):
+        torch.randn(rows, cols, generator=g, device=dev, out=w)
+        w.mul_(0.02)
+        pk = torch.empty(rows, cols // 2, dtype=torch.uint8, device=dev)
+        sc = torch.empty(rows, cols // 32, dtype=torch.uint8, device=dev)
+        glib.quant_fp4_rows(w, pk, sc)
+        fp4.append((pk.cpu().numpy(), sc.cpu().numpy()))
+    W8, S8 = c8.cpu().numpy(), s8.cpu().numpy()
+    x = synth_tokens(1, cols, 43)
+    qx, qs = glib.quant_fp8_act(x)
+    qx, qs = qx[0].cpu().numpy().copy(), qs[0].cpu().numpy().copy()
+    del w, c8, s8
+    y8 = np.empty(rows, np.float32)
+    y0, y1 = np.empty(rows, np.float32), np.empty(rows, np.float32)
+    (W0, S0), (W1, S1) = fp4
+
+    def fp8():
+        lib.dsv4_gemv_fp8_q(P(y8, f32p), P(qx, f32p), P(qs, f32p), P(W8, u8p), P(S8, u8p),
+                            cols, rows, 1)
+
+    def pair():
+        lib.dsv4_gemv_fp4_pair_q(P(y0, f32p), P(y1, f32p), P(qx, f32p), P(qs, f32p),
+                                 P(W0, u8p), P(S0, u8p), P(W1, u8p), P(S1, u8p), cols, rows)
+
+    res = {"workload": "drop-in entry points on host buffers: dsv4_gemv_fp8_q 2048 x 4096 "
+                       "E4M3 (8.4 MB) and dsv4_gemv_fp4_pair_q 2 x 2048 x 4096 E2M1 (8.9 MB), "
+                       "activations in and outputs out through pageable host memory, one "
+                       "synchronising call at a time"}
+    wts = {"fp8_q": [W8, S8], "fp4_pair_q": [W0, S0, W1, S1]}
+    fns = {"fp8_q": fp8, "fp4_pair_q": pair}
+    outs = {}
+    for name in ("fp8_q", "fp4_pair_q"):
+        fn = fns[name]
+        r = {"weight_bytes": int(sum(a.nbytes for a in wts[name]))}
+        sec, n = cpu_loop(fn, 1.0, max_calls=2000)
+        r["unregistered_ms"] = round(sec * 1e3, 4)
+        for a in wts[name]:
+            assert lib.dsv4_gpu_register_weights(a.ctypes.data, a.nbytes) == 0
+        sec, n = cpu_loop(fn, 1.0, max_calls=20000)
+        r["registered_ms"] = round(sec * 1e3, 4)
+        fn()
+        outs[name] = (y8.copy(),) if name == "fp8_q" else (y0.copy(), y1.copy())
+        for a in wts[name]:
+            lib.dsv4_gpu_forget_weights(C.c_void_p(a.ctypes.data))
+        res[name] = r
+    if cpu_seconds and cpu_available():
+        threads, _ = host_cores()
+        set_omp_threads(threads)
+        ref = cpu_ref()
+        yr = ref.gemv_fp8_q(qx, qs, W8, S8, cols, rows)
+        res["fp8_q"]["bit_exact_vs_reference"] = bool(
+            np.array_equal(yr.view(np.uint32), outs["fp8_q"][0].view(np.uint32)))
+        sec, _ = cpu_loop(lambda: ref.gemv_fp8_q(qx, qs, W8, S8, cols, rows), cpu_seconds / 4)
+        res["fp8_q"]["reference_cpu_ms"] = round(sec * 1e3, 4)
+        r0, r1 = ref.gemv_fp4_pair_q(qx, qs, W0, S0, W1, S1, cols, rows)
+        res["fp4_pair_q"]["bit_exact_vs_reference"] = bool(
+            np.array_equal(r0.view(np.uint32), outs["fp4_pair_q"][0].view(np.uint32)) and
+            np.array_equal(r1.view(np.uint32), outs["fp4_pair_q"][1].view(np.uint32)))
+        sec, _ = cpu_loop(lambda: ref.gemv_fp4_pair_q(qx, qs, W0, S0, W1, S1, cols, rows),
+                          cpu_seconds / 4)
+        res["fp4_pair_q"]["reference_cpu_ms"] = round(sec * 1e3, 4)
+        res["reference_cpu"] = (f"the reference kernels (oracle/_ref, OMP_NUM_THREADS={threads}) "
+                                f"on the same host buffers")
+    return res
+
+
+def synth_tokens(n, hidden, seed):
+    import synth
+    return synth.bf16_tokens(n, hidden, seed=seed, device="cuda")
+
+
 def bench_checkpoint_load(lib, layer):
     """Checkpoint to HBM (dsv4g_load_moe_layer): 16 full-size routed experts of
     one layer, its FP8 shared expert, gate and bias, written as three
@@ -843,6 +944,9 @@ def main():
     if wl == "head":
         print(json.dumps({"vocab_head": bench_vocab_head(lib, cpu_s)}))
         return
+    if wl == "dropin":
+        print(json.dumps({"dropin": bench_dropin(cpu_s)}))
+        return
     nl = args.layers if wl in ("all", "decode") else 1
     t0 = time.perf_counter()
     layers = [synth.device_layer(seed=100 + l, device=dev) for l in range(nl)]
@@ -856,6 +960,7 @@ def main():
         kernels["ffn_step_1_token"] = bench_ffn_step(lib, layers, cpu_s)
         kernels["attention_projections"] = bench_attn_proj(lib, cpu_s)
         kernels["vocab_head"] = bench_vocab_head(lib, cpu_s)
+        kernels["dropin_host_buffers"] = bench_dropin(cpu_s)
         kernels["checkpoint_load"] = bench_checkpoint_load(lib, layers[0])
         if wl == "kernels":
             print(json.dumps(kernels))

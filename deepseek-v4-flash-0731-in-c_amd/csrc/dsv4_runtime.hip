@@ -45,6 +45,22 @@ int dsv4g_free(void *ptr) {
   return 0;
 }
 
+int dsv4g_host_malloc(void **ptr, size_t bytes) {
+  *ptr = NULL;
+  DSV4G_HIP(hipHostMalloc(ptr, bytes ? bytes : 1, hipHostMallocDefault));
+  return 0;
+}
+
+int dsv4g_host_free(void *ptr) {
+  if (ptr) DSV4G_HIP(hipHostFree(ptr));
+  return 0;
+}
+
+int dsv4g_memcpy_d2h_async(void *dst, const void *src, size_t bytes, void *stream) {
+  DSV4G_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, (hipStream_t)stream));
+  return 0;
+}
+
 int dsv4g_memcpy_h2d(void *dst, const void *src, size_t bytes, void *stream) {
   DSV4G_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, (hipStream_t)stream));
   return 0;

@@ -157,16 +157,33 @@ void dsv4_gpu_forget_all_weights(void)
 
 /* ---------------------------------------------------- per-call staging ---- */
 /* One grow-only device arena for activations and outputs (caller holds the
- * lock, so a single arena suffices). */
+ * lock, so a single arena suffices), mirrored by a page-locked host arena of
+ * the same size: up() copies the caller's input into the mirror and queues
+ * an asynchronous upload from it; down() queues an asynchronous download into
+ * the mirror and records where the caller wants it; finish() waits once for
+ * the stream and copies every recorded output out. So a call costs one
+ * synchronisation, not one per output, and no copy goes through pageable
+ * memory. */
 static void *g_arena;
+static unsigned char *g_pin;
 static size_t g_arena_bytes;
+
+#define DSV4_HOST_MAXDOWN 80
+typedef struct { void *host; size_t off, bytes; } PendingDown;
+static PendingDown g_down[DSV4_HOST_MAXDOWN];
+static int g_ndown;
 
 static void *arena(size_t bytes)
 {
     if (bytes > g_arena_bytes) {
         if (g_arena) dsv4g_free(g_arena);
+        if (g_pin) dsv4g_host_free(g_pin);
+        g_arena = NULL;
+        g_pin = NULL;
+        g_arena_bytes = 0;
         size_t want = bytes + bytes / 2 + 4096;
         check(dsv4g_malloc(&g_arena, want), "staging allocation");
+        check(dsv4g_host_malloc((void **)&g_pin, want), "staging allocation");
         g_arena_bytes = want;
     }
     return g_arena;
@@ -182,14 +199,37 @@ static void *carve(Carver *c, size_t bytes)
     return p;
 }
 
+static size_t arena_off(const void *dev)
+{
+    return (size_t)((const unsigned char *)dev - (const unsigned char *)g_arena);
+}
+
 static void up(void *dev, const void *host, size_t bytes)
 {
-    check(dsv4g_memcpy_h2d(dev, host, bytes, NULL), "copy to device");
+    unsigned char *m = g_pin + arena_off(dev);
+    memcpy(m, host, bytes);
+    check(dsv4g_memcpy_h2d(dev, m, bytes, NULL), "copy to device");
 }
+
+static void finish(void);
 
 static void down(void *host, const void *dev, size_t bytes)
 {
-    check(dsv4g_memcpy_d2h(host, dev, bytes, NULL), "copy to host");
+    if (g_ndown == DSV4_HOST_MAXDOWN) finish(); /* a list full of outputs: deliver them */
+    const size_t off = arena_off(dev);
+    check(dsv4g_memcpy_d2h_async(g_pin + off, dev, bytes, NULL), "copy to host");
+    g_down[g_ndown].host = host;
+    g_down[g_ndown].off = off;
+    g_down[g_ndown].bytes = bytes;
+    g_ndown++;
+}
+
+static void finish(void)
+{
+    check(dsv4g_stream_sync(NULL), "copy to host");
+    for (int i = 0; i < g_ndown; i++)
+        memcpy(g_down[i].host, g_pin + g_down[i].off, g_down[i].bytes);
+    g_ndown = 0;
 }
 
 /* ------------------------------------------------------- scalar decode ---- */
@@ -265,6 +305,7 @@ static void quant_act(float *qx, float *qscale, const float *x, int n)
     check(dsv4g_quant_fp8_act(dq, ds, dx, n, 1, NULL), "quant_fp8");
     down(qx, dq, (size_t)n * 4);
     down(qscale, ds, nb * 4);
+    finish();
     pthread_mutex_unlock(&g_lock);
 }
 
@@ -321,6 +362,7 @@ void dsv4_gemv_fp4_batch_q(float *const *y, const float *const *qx,
     up_rows(ds, qscale, batch, qn);
     check(dsv4g_gemv_fp4_batch_q(dy, dq, ds, batch, dW, dS, in, rows, NULL), "gemv_fp4");
     down_rows(y, dy, batch, (size_t)rows);
+    finish();
     pthread_mutex_unlock(&g_lock);
 }
 
@@ -350,6 +392,7 @@ void dsv4_gemv_fp4_pair_q(float *y0, float *y1, const float *qx, const float *qs
           "gemv_fp4_pair");
     down(y0, d0, (size_t)rows * 4);
     down(y1, d1, (size_t)rows * 4);
+    finish();
     pthread_mutex_unlock(&g_lock);
 }
 
@@ -371,6 +414,7 @@ void dsv4_gemv_fp8_batch_q(float *const *y, const float *const *qx,
     check(dsv4g_gemv_fp8_batch_q(dy, dq, ds, batch, dW, dS, in, out, round_out, NULL),
           "gemv_fp8");
     down_rows(y, dy, batch, (size_t)out);
+    finish();
     pthread_mutex_unlock(&g_lock);
 }
 
@@ -400,6 +444,7 @@ void dsv4_gemv_fp8_pair_q(float *y0, float *y1, const float *qx, const float *qs
           "gemv_fp8_pair");
     down(y0, d0, (size_t)out * 4);
     down(y1, d1, (size_t)out * 4);
+    finish();
     pthread_mutex_unlock(&g_lock);
 }
 
@@ -415,6 +460,7 @@ void dsv4_gemv_bf16_batch(float *const *y, const float *const *x, int batch,
     up_rows(dx, x, batch, (size_t)in);
     check(dsv4g_gemv_bf16(dy, dx, dW, in, out, round_out, batch, NULL), "gemv_bf16");
     down_rows(y, dy, batch, (size_t)out);
+    finish();
     pthread_mutex_unlock(&g_lock);
 }
 
@@ -437,6 +483,7 @@ static void gemv_fp8_float(float *y, const float *x, const uint8_t *W, const flo
     up(dx, x, (size_t)in * 4);
     check(dsv4g_gemv_fp8_float(dy, dx, dW, dS, in, rows, block, mode, NULL), "gemv_fp8");
     down(y, dy, (size_t)rows * 4);
+    finish();
     pthread_mutex_unlock(&g_lock);
 }
 
@@ -468,6 +515,7 @@ void dsv4_gemv_fp4(float *y, const float *qx, const float *qscale, const uint8_t
     up(ds, qscale, qn * 4);
     check(dsv4g_gemv_fp4_float(dy, dq, ds, dW, dS, in, rows, group, NULL), "gemv_fp4");
     down(y, dy, (size_t)rows * 4);
+    finish();
     pthread_mutex_unlock(&g_lock);
 }
 
@@ -503,5 +551,6 @@ void dsv4_router(int *idx, float *wt, const float *x, const float *gate, const f
           "router");
     down(idx, didx, (size_t)topk * 4);
     down(wt, dwt, (size_t)topk * 4);
+    finish();
     pthread_mutex_unlock(&g_lock);
 }

@@ -78,6 +78,12 @@ int dsv4g_malloc(void **ptr, size_t bytes);
 int dsv4g_free(void *ptr);
 int dsv4g_memcpy_h2d(void *dst, const void *src, size_t bytes, void *stream);
 int dsv4g_memcpy_d2h(void *dst, const void *src, size_t bytes, void *stream); /* syncs */
+/* Page-locked host memory (the drop-in layer stages activations and outputs
+ * through it, so that its copies are asynchronous), and a device-to-host copy
+ * that does not synchronise (dst page-locked for it to be asynchronous). */
+int dsv4g_host_malloc(void **ptr, size_t bytes);
+int dsv4g_host_free(void *ptr);
+int dsv4g_memcpy_d2h_async(void *dst, const void *src, size_t bytes, void *stream);
 int dsv4g_stream_sync(void *stream);
 
 /* ----------------------------------------------- device-pointer kernels */
