@@ -110,9 +110,15 @@ __device__ __forceinline__ float hc_sigmoid(float x) {
 
 // dsv4_hc_split on the lanes of one wave (call from a whole wave): lane
 // i < m gets pre[i], post[i]; lane a*m + b < m*m gets comb[a][b]. mixes: LDS.
-__device__ void hc_split_wave(float *pre, float *post, float *comb, const float *mixes,
-                              const float *scale3, const float *base, int m, int iters,
-                              float eps) {
+// M: m when known at compile time (the model's 4), else 0. With M the row and
+// column sums of the Sinkhorn passes fetch their M terms with independent
+// shuffles (one LDS round trip per pass instead of M dependent ones) and add
+// them in index order.
+template <int M>
+__device__ void hc_split_wave_t(float *pre, float *post, float *comb, const float *mixes,
+                                const float *scale3, const float *base, int m_rt, int iters,
+                                float eps) {
+  const int m = M ? M : m_rt;
   const int lane = threadIdx.x & 63;
   if (lane < m) {
     pre[lane] = hc_sigmoid(mixes[lane] * scale3[0] + base[lane]) + eps;
@@ -136,10 +142,27 @@ __device__ void hc_split_wave(float *pre, float *post, float *comb, const float 
   for (int pass = 0; pass < 2 * iters - 1; pass++) {
     const bool by_col = (pass & 1) == 0;
     s = 0.0f;
-    for (int j = 0; j < m; j++) s += __shfl(v, by_col ? j * m + b : a * m + j);
+    if (M) {
+      float t[M ? M : 1];
+#pragma unroll
+      for (int j = 0; j < M; j++) t[j] = __shfl(v, by_col ? j * M + b : a * M + j);
+#pragma unroll
+      for (int j = 0; j < M; j++) s += t[j];
+    } else {
+      for (int j = 0; j < m; j++) s += __shfl(v, by_col ? j * m + b : a * m + j);
+    }
     v = v / (s + eps);
   }
   if (lane < mm) comb[lane] = v;
+}
+
+__device__ void hc_split_wave(float *pre, float *post, float *comb, const float *mixes,
+                              const float *scale3, const float *base, int m, int iters,
+                              float eps) {
+  if (m == 4)
+    hc_split_wave_t<4>(pre, post, comb, mixes, scale3, base, m, iters, eps);
+  else
+    hc_split_wave_t<0>(pre, post, comb, mixes, scale3, base, m, iters, eps);
 }
 
 // 16 columns of a chain's row and of the state from a staged chunk.
@@ -224,12 +247,18 @@ __device__ __forceinline__ void hc_store_chunk(const float4 *v, const HcLane<PER
   if ((threadIdx.x & 63) == 0) st_flag_relaxed(flag, c + 1);
 }
 
-// One workgroup per token: wave 0 runs the chains, waves 1..NPROD stage
-// chunks into the ring of a.ring slots, wave NPROD + 1 sums the state's
-// squares. PER: float4 registers per producer lane,
+// One workgroup of NW waves (4 or 8) per token. The waves of a workgroup sit
+// on the CU's four SIMDs in turn (wave w on SIMD w % 4), and the chain wave
+// issues an instruction for every step of its 24 chains, so SIMD 0 is left
+// to it: wave 0 runs the chains (at raised priority), wave SQW sums the
+// state's squares (wave 4 of 8: briefly, then it waits at the barrier; wave
+// 3 of 4), and the other waves (NPROD of them) stage chunks into the ring of
+// a.ring slots. PER: float4 registers per producer lane,
 // ceil((mix_n + 1) * HC_C / 4 / 64).
-template <int PER, int NPROD>
-__global__ void __launch_bounds__(64 * (2 + NPROD)) k_hc_pre(HcArgs a) {
+template <int PER, int NW>
+__global__ void __launch_bounds__(64 * NW) k_hc_pre(HcArgs a) {
+  static_assert(NW == 4 || NW == 8, "4 or 8 waves");
+  constexpr int SQW = NW == 8 ? 4 : 3, NPROD = NW == 8 ? 6 : 2;
   extern __shared__ __align__(16) float lds[];
   __shared__ int s_full[HC_MAX_RING], s_done[HC_MAX_RING];
   __shared__ float s_mix[64], s_pre[8], s_post[8], s_comb[64];
@@ -248,6 +277,7 @@ __global__ void __launch_bounds__(64 * (2 + NPROD)) k_hc_pre(HcArgs a) {
   __syncthreads();
 
   if (wave == 0) {
+    __builtin_amdgcn_s_setprio(3);
     // ---- the chains: lane j < mix_n owns mixes[j]. A chunk is HC_C / 16
     // groups of 16 columns, zero-filled past K by the producers (fmaf(0, 0, acc)
     // returns acc, which is never -0: it starts at +0 and a sum rounding to
@@ -299,10 +329,11 @@ __global__ void __launch_bounds__(64 * (2 + NPROD)) k_hc_pre(HcArgs a) {
 #undef HC_TIE
     }
     if (lane < mix_n) s_mix[lane] = acc;
-  } else if (wave <= NPROD) {
+    __builtin_amdgcn_s_setprio(0);
+  } else if (wave != SQW) {
     // ---- producer p (of NPROD) stages chunks p, p + NPROD, ... into slot
     // c % D once the slot's previous chunk has been consumed (ticket s_done)
-    const int p = wave - 1;
+    const int p = wave - 1 - wave / 4;
     HcLane<PER> L;
     hc_lane_init<PER>(L, a.fn, state, K, mix_n, p, NPROD);
     float4 v[PER];
@@ -313,7 +344,7 @@ __global__ void __launch_bounds__(64 * (2 + NPROD)) k_hc_pre(HcArgs a) {
       hc_store_chunk<PER>(v, L, lds + slot * slot_fl, &s_full[slot], c);
     }
   } else {
-    // ---- the last wave: the state's sum of squares (exact terms, any order)
+    // ---- the state's sum of squares (exact terms, any order)
     double ss = 0.0;
     for (int i = 4 * lane; i < K; i += 256) {
       const float4 x = *(const float4 *)(state + i);
@@ -518,14 +549,14 @@ int dsv4g_hc_pre(float *bin, float *post, float *comb, const float *state, const
   const size_t lds = std::max(ring, (size_t)hidden * sizeof(float));
   if (lds > HC_LDS_BUDGET)
     return dsv4g_fail(DSV4G_EINVAL, "hc_pre: hidden %d too large", hidden);
-  // mult <= 4: 6 producer waves (19 float4 each); larger mult: 2 producers
-  // (48 float4 each)
+  // mult <= 4: 8 waves, 6 of them producers (19 float4 each); larger mult:
+  // 4 waves, 2 producers (48 float4 each)
   const int rows = (2 + mult) * mult + 1;
   if (rows * (HC_C / 4) <= 64 * 19)
-    hipLaunchKernelGGL((k_hc_pre<19, 6>), dim3(n_tokens), dim3(64 * 8), lds,
+    hipLaunchKernelGGL((k_hc_pre<19, 8>), dim3(n_tokens), dim3(64 * 8), lds,
                        (hipStream_t)stream, a);
   else
-    hipLaunchKernelGGL((k_hc_pre<48, 2>), dim3(n_tokens), dim3(64 * 4), lds,
+    hipLaunchKernelGGL((k_hc_pre<48, 4>), dim3(n_tokens), dim3(64 * 4), lds,
                        (hipStream_t)stream, a);
   return dsv4g_check_launch("hc_pre");
 }
