@@ -506,18 +506,63 @@ __global__ __launch_bounds__(64) void k_rowchain(RowChainArgs a) {
 // unrolled, so every read is one instruction with an immediate offset and
 // the lane's instruction stream holds nothing but reads and the dependent
 // adds (in a single wave every other instruction delays the chain by its
-// issue time); the compiler places the reads ahead within its register
-// budget.
+// issue time). The reads run PC_LA float4 ahead of the adds in a register
+// ring; an empty asm on acc after each float4's adds pins that order (left
+// to itself the compiler keeps only one or two reads in flight).
+#define PC_LA 7
 template <int N4>
 __device__ __forceinline__ float pc_chain_fixed(const float4 *p4, float acc) {
+  constexpr int LA = N4 < PC_LA ? N4 : PC_LA, R = LA + 1;
+  float4 v[R];
+#pragma unroll
+  for (int j = 0; j < LA; ++j) v[j] = p4[j];
 #pragma unroll
   for (int j = 0; j < N4; ++j) {
-    const float4 v = p4[j];
-    acc = acc + v.x;
-    acc = acc + v.y;
-    acc = acc + v.z;
-    acc = acc + v.w;
+    if (j + LA < N4) v[(j + LA) % R] = p4[j + LA];
+    const float4 c = v[j % R];
+    acc = acc + c.x;
+    acc = acc + c.y;
+    acc = acc + c.z;
+    acc = acc + c.w;
+    asm volatile("" : "+v"(acc)::"memory");
   }
+  return acc;
+}
+
+// The whole row's chain in one unrolled ring (no block boundaries, where the
+// ring would restart), one 384-column load at a time (96 float4, unrolled
+// within the compiler's limit; the loads chained by template recursion):
+// wait(c) returns once the products of columns < c are in LDS, and is called
+// before the first read of each load.
+template <int J0, int N4, typename Wait>
+__device__ __forceinline__ void pc_chain_seg(const float4 *p4, float &acc,
+                                             float4 (&v)[PC_LA + 1], Wait &wait) {
+  constexpr int LA = PC_LA, R = LA + 1;
+#pragma unroll
+  for (int jj = 0; jj < 96; ++jj) {
+    const int j = J0 + jj;
+    if (j >= N4) break;
+    if (j + LA < N4) {
+      if ((j + LA) % 96 == 0) wait(4 * (j + LA) + 4);
+      v[(j + LA) % R] = p4[j + LA];
+    }
+    const float4 c = v[j % R];
+    acc = acc + c.x;
+    acc = acc + c.y;
+    acc = acc + c.z;
+    acc = acc + c.w;
+    asm volatile("" : "+v"(acc)::"memory");
+  }
+  if constexpr (J0 + 96 < N4) pc_chain_seg<J0 + 96, N4>(p4, acc, v, wait);
+}
+
+template <int N4, typename Wait>
+__device__ __forceinline__ float pc_chain_row(const float4 *p4, float acc, Wait &wait) {
+  float4 v[PC_LA + 1];
+  wait(4 * PC_LA);
+#pragma unroll
+  for (int j = 0; j < PC_LA; ++j) v[j] = p4[j];
+  pc_chain_seg<0, N4>(p4, acc, v, wait);
   return acc;
 }
 
@@ -544,12 +589,17 @@ __device__ __forceinline__ void pc_products(const uint4 w, int r, int c, const f
   }
 }
 
-// Two halves of the columns: every thread loads and forms pieces of the first
-// half; waves 1-3 alone load the second half. After the first half's
-// products (a barrier), wave 0's chain lanes add it while waves 1-3 form the
-// second half's products and then raise an LDS flag, which the chain lanes
-// wait for at the half's boundary; so the chain starts once half the weights
-// have landed.
+// x is loaded first (its loads would otherwise wait behind every weight load:
+// the memory counter is in order), staged as x or x * s, then waves 1-3 form
+// every product as their weight loads land, in column order: load k of a
+// producer lane is piece (tid - 64) + 192 k, that is row i % PC_ROWS of the
+// 16-column chunk i / PC_ROWS, so load k covers columns [384 k, 384 k + 384)
+// of all rows; after its products of load k a producer wave counts itself in
+// s_cnt[k]. Wave 0's chain lanes start as soon as the first 384 columns are
+// counted and check a count only when the chain reaches a load not yet seen
+// complete; so the chain starts after one load round trip, not half the row.
+#define PC_LOADS ((PC_ROWS * PC_MAXIN / 16 + 191) / 192)  // weight loads per producer lane
+#define PC_XQ (PC_MAXIN / 4 / 256)                         // x float4 per thread
 template <int MODE>
 __global__ __launch_bounds__(256) void k_fp8_prodchain(float *__restrict__ y,
                                                        const float *__restrict__ x,
@@ -557,80 +607,96 @@ __global__ __launch_bounds__(256) void k_fp8_prodchain(float *__restrict__ y,
                                                        const float *__restrict__ wscale, int in,
                                                        int rows, int block) {
   extern __shared__ __align__(16) float lds[];
-  __shared__ int s_half;
-  const int tid = threadIdx.x, r0 = blockIdx.x * PC_ROWS;
+  __shared__ int s_cnt[PC_LOADS];
+  const int tid = threadIdx.x, wave = tid >> 6, r0 = blockIdx.x * PC_ROWS;
   const int cblocks = (in + block - 1) / block;
   const int ps = in + 4;             // product row stride (floats)
   float *xs = lds;                   // [in] x (MODE 1) or x * s (MODE 0)
   float *pr = lds + in;              // [PC_ROWS][ps] products
+  float *ss = pr + PC_ROWS * ps;     // [cblocks] the row block's scales
   const float *srow = wscale + (size_t)(r0 / block) * cblocks;
-  const int hp = in / 32;            // 16-byte pieces per half row
+  const int npiece = PC_ROWS * (in / 16);
   const int nrow = min(PC_ROWS, rows - r0);
-  // first half: piece i of PC_ROWS * hp (row i / hp, columns 16 (i % hp) ..),
-  // two per thread at most; second half: PC_ROWS * hp pieces over the 192
-  // threads of waves 1-3, six per thread at most (in <= PC_MAXIN)
-  constexpr int P0 = PC_ROWS * PC_MAXIN / 32 / 256, P1 = (PC_ROWS * PC_MAXIN / 32 + 191) / 192;
+  // the scales and x are loaded before the weights: a wait for them then
+  // leaves the weight loads in flight (the memory counter is in order)
+  const float sv = tid < cblocks ? srow[tid] : 0.0f;
+  float4 xv[PC_XQ];
+#pragma unroll
+  for (int q = 0; q < PC_XQ; ++q) {
+    const int i = tid + 256 * q;
+    xv[q] = i < in / 4 ? reinterpret_cast<const float4 *>(x)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
   const BufRsrc rw = buf_rsrc(W + (size_t)r0 * in, (uint32_t)(nrow * in));
-  auto off = [&](int i, int half) {  // byte offset of piece i of a half
-    return i < PC_ROWS * hp
-               ? (uint32_t)(i / hp) * (uint32_t)in + 16u * (uint32_t)(half * hp + i % hp)
-               : 0xFFFFFFF0u;
-  };
-  uint4 w0[P0], w1[P1];
+  // every wave issues the same loads (wave 0's out of range: zeros, no
+  // memory access), so the wait for x below counts exactly PC_LOADS later
+  // loads on every path instead of draining them all
+  uint4 w[PC_LOADS];
 #pragma unroll
-  for (int k = 0; k < P0; ++k) w0[k] = buf_load16(rw, off(tid + 256 * k, 0));
-  if (tid >= 64) {
-#pragma unroll
-    for (int k = 0; k < P1; ++k) w1[k] = buf_load16(rw, off(tid - 64 + 192 * k, 1));
+  for (int k = 0; k < PC_LOADS; ++k) {
+    const int i = tid - 64 + 192 * k;
+    w[k] = buf_load16(rw, wave > 0 && i < npiece ? (uint32_t)(i % PC_ROWS) * (uint32_t)in +
+                                                       16u * (uint32_t)(i / PC_ROWS)
+                                                 : 0xFFFFFFF0u);
   }
-  if (tid == 0) s_half = 0;
-  for (int i = tid; i < in / 4; i += 256) {
-    float4 v = reinterpret_cast<const float4 *>(x)[i];
-    if (MODE == 0) {  // xs = x * s of the row block (the 4 columns share a column block)
-      const float sc = srow[(4 * i) / block];
-      v = make_float4(v.x * sc, v.y * sc, v.z * sc, v.w * sc);
+  if (tid < PC_LOADS) s_cnt[tid] = 0;
+  if (tid < cblocks) ss[tid] = sv;
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < PC_XQ; ++q) {
+    const int i = tid + 256 * q;
+    if (i < in / 4) {
+      float4 v = xv[q];
+      if (MODE == 0) {  // xs = x * s of the row block (the 4 columns share a column block)
+        const float sc = ss[(4 * i) / block];
+        v = make_float4(v.x * sc, v.y * sc, v.z * sc, v.w * sc);
+      }
+      reinterpret_cast<float4 *>(xs)[i] = v;
     }
-    reinterpret_cast<float4 *>(xs)[i] = v;
   }
   __syncthreads();
+  if (wave > 0) {
 #pragma unroll
-  for (int k = 0; k < P0; ++k) {
-    const int i = tid + 256 * k;
-    if (i < PC_ROWS * hp) pc_products<MODE>(w0[k], i / hp, 16 * (i % hp), xs, srow, block, ps, pr);
-  }
-  __syncthreads();
-  if (tid >= 64) {
-#pragma unroll
-    for (int k = 0; k < P1; ++k) {
+    for (int k = 0; k < PC_LOADS; ++k) {
       const int i = tid - 64 + 192 * k;
-      if (i < PC_ROWS * hp)
-        pc_products<MODE>(w1[k], i / hp, 16 * (hp + i % hp), xs, srow, block, ps, pr);
+      if (192 * k >= npiece) break;  // uniform
+      if (i < npiece) pc_products<MODE>(w[k], i % PC_ROWS, 16 * (i / PC_ROWS), xs, ss, block, ps, pr);
+      // this wave's product stores of load k are issued before the count (the
+      // empty asm keeps the compiler from moving them past it; LDS runs a
+      // wave's operations in order, so they land first): count the wave in
+      asm volatile("" ::: "memory");
+      if ((tid & 63) == 0) atomicAdd(&s_cnt[k], 1);
     }
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's product stores done
-    if (tid % 64 == 0) atomicAdd(&s_half, 1);
     return;
   }
   if (tid >= PC_ROWS || tid >= nrow) return;
   const float4 *p4 = reinterpret_cast<const float4 *>(pr + (size_t)tid * ps);
-  const int n4 = in / 4, h4 = n4 / 2;  // a multiple of 4 each
+  const int n4 = in / 4;  // a multiple of 8
   float acc = 0.0f;
-  auto chain = [&](int b0, int b1) {
-    if (h4 == 512) {  // the model's width: 8 fixed blocks of 64 float4 a half
-#pragma unroll 1
-      for (int b = b0; b < b1; b += 64) acc = pc_chain_fixed<64>(p4 + b, acc);
-    } else {
-      int b = b0;
-      for (; b + 16 <= b1; b += 16) acc = pc_chain_fixed<16>(p4 + b, acc);
-      for (; b < b1; ++b) acc = pc_chain_fixed<1>(p4 + b, acc);
-    }
+  int ready = -1;  // loads known to be counted by all three producer waves
+  auto wait_cols = [&](int cend) {  // products of columns < cend are in LDS
+    const int need = (cend - 1) / 384;
+    if (need <= ready) return;
+    // (an LDS pointer: a generic one would make the read a FLAT one)
+    const volatile __attribute__((address_space(3))) int *cnt =
+        (const volatile __attribute__((address_space(3))) int *)&s_cnt[need];
+    for (unsigned it = 0; *cnt < 3 && it < (1u << 24); ++it) __builtin_amdgcn_s_sleep(1);
+    asm volatile("" ::: "memory");  // the product reads stay after the count's
+    ready = need;
   };
-  chain(0, h4);
-  // the second half's products: every wave of 1-3 has raised the flag (a
-  // bounded wait: they finish their products long before the first half's
-  // chain ends; volatile reads of the LDS counter)
-  for (unsigned it = 0; *(volatile int *)&s_half < 3 && it < (1u << 24); ++it)
-    __builtin_amdgcn_s_sleep(1);
-  chain(h4, n4);
+  if (n4 == 1024) {  // the model's width: one ring over the whole row
+    acc = pc_chain_row<1024>(p4, acc, wait_cols);
+  } else {
+    int b = 0;
+#pragma unroll 1
+    for (; b + 64 <= n4; b += 64) {
+      wait_cols(4 * (b + 64));
+      acc = pc_chain_fixed<64>(p4 + b, acc);
+    }
+    for (; b + 8 <= n4; b += 8) {
+      wait_cols(4 * (b + 8));
+      acc = pc_chain_fixed<8>(p4 + b, acc);
+    }
+  }
   y[r0 + tid] = acc;
 }
 
@@ -1306,11 +1372,12 @@ int dsv4g_gemv_fp8_float(float *y, const float *x, const uint8_t *W, const float
   if (in <= 0 || rows <= 0 || block <= 0)
     return dsv4g_fail(DSV4G_EINVAL, "gemv_fp8_float: bad size");
   if (in % 32 == 0 && in <= PC_MAXIN && block % 16 == 0 && ((uintptr_t)x & 15) == 0) {
-    const size_t lds = ((size_t)in + (size_t)PC_ROWS * (in + 4)) * 4;
+    const size_t lds = ((size_t)in + (size_t)PC_ROWS * (in + 4) + (in + block - 1) / block) * 4;
     const void *fn = mode == 0 ? (const void *)k_fp8_prodchain<0> : (const void *)k_fp8_prodchain<1>;
     // more than the default 64 KB of LDS (a host-side setting of the kernel)
-    DSV4G_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  (int)(((size_t)PC_MAXIN + (size_t)PC_ROWS * (PC_MAXIN + 4)) * 4)));
+    DSV4G_HIP(hipFuncSetAttribute(
+        fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+        (int)(((size_t)PC_MAXIN + (size_t)PC_ROWS * (PC_MAXIN + 4) + PC_MAXIN / 16) * 4)));
     const dim3 grid((unsigned)((rows + PC_ROWS - 1) / PC_ROWS));
     if (mode == 0)
       hipLaunchKernelGGL(k_fp8_prodchain<0>, grid, dim3(256), lds, (hipStream_t)stream, y, x, W,
