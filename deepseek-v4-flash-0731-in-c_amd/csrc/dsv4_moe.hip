@@ -266,6 +266,7 @@ __global__ __launch_bounds__(64) void k_swiglu_quant(float *__restrict__ qy,
 // grid values and scales into LDS while the rows stream; then each lane's
 // sequential fmaf partial and one lane per row chains the groups in order;
 // out[r] = bf16(acc). inter <= 4096, a multiple of 128.
+template <int RPW>  // output rows per workgroup: 8 or 16
 __global__ __launch_bounds__(256) void k_expert_down(float *__restrict__ out,
                                                      const float *__restrict__ y,
                                                      const uint8_t *__restrict__ W2,
@@ -273,8 +274,8 @@ __global__ __launch_bounds__(256) void k_expert_down(float *__restrict__ out,
                                                      int I) {
   __shared__ __align__(16) float xq[4096];
   __shared__ float xs[32];
-  __shared__ __align__(16) float2 ps[8 * 130];
-  const int tid = threadIdx.x, r0 = blockIdx.x * 8;
+  __shared__ __align__(16) float2 ps[RPW * 130];
+  const int tid = threadIdx.x, r0 = blockIdx.x * RPW;
   const int G = I / 32;
   int GP = 1;
   while (GP < G) GP <<= 1;
@@ -289,7 +290,7 @@ __global__ __launch_bounds__(256) void k_expert_down(float *__restrict__ out,
     yv[b][1] = buf_load16(ry, 4u * base + 16u);
   }
   __builtin_amdgcn_sched_barrier(0);  // y ahead of the rows (loads return in order)
-  const int nrow = max(0, min(8, H - r0));
+  const int nrow = max(0, min(RPW, H - r0));
   const BufRsrc rw = buf_rsrc(W2 + (size_t)r0 * (I / 2), (uint32_t)nrow * (uint32_t)(I / 2));
   const BufRsrc rs = buf_rsrc(S2 + (size_t)r0 * G, (uint32_t)nrow * (uint32_t)G);
   uint4 w[4];
@@ -297,7 +298,7 @@ __global__ __launch_bounds__(256) void k_expert_down(float *__restrict__ out,
 #pragma unroll
   for (int h = 0; h < 4; ++h) {
     const int lr = h * rpp + rsub;
-    const bool in = lr < 8 && g < G;
+    const bool in = lr < RPW && g < G;
     w[h] = buf_load16(rw, in ? (uint32_t)lr * (uint32_t)(I / 2) + 16u * g : 0xFFFFFFF0u);
     code[h] = __builtin_amdgcn_raw_buffer_load_b8(rs, in ? (uint32_t)(lr * G + g) : 0xFFFFFFF0u,
                                                   0, 0);
@@ -326,7 +327,7 @@ __global__ __launch_bounds__(256) void k_expert_down(float *__restrict__ out,
 #pragma unroll
   for (int h = 0; h < 4; ++h) {
     const int lr = h * rpp + rsub;
-    if (lr < 8 && g < G) {
+    if (lr < RPW && g < G) {
       float part = fp4_group_partial(w[h], xq + 32 * g);
       float s = xs[g / 4] * e8m0(code[h]);
       if (code[h] == 255u) {  // NaN scale: the reference skips the group
@@ -443,8 +444,14 @@ int dsv4g_expert_forward(float *out, const float *qx, const float *qscale, const
     a.np = 4;  // 4 rows of each matrix per tile: 512 tiles (measured: 14.0 us at the model's
                // shape, against 14.9 with 1024 tiles of 2 rows and 14.2 with 256 of 8)
     DSV4G_TRY(dsv4g_launch_gemv_fp4(&a, 1, 2, stream));
-    hipLaunchKernelGGL(k_expert_down, dim3((unsigned)((hidden + 7) / 8)), dim3(256), 0,
-                       (hipStream_t)stream, out, ws, w2, s2, hidden, inter);
+    // 16 rows per workgroup where a thread's four pieces cover them (inter <=
+    // 2048): half the workgroups reading y
+    if (inter <= 2048)
+      hipLaunchKernelGGL(k_expert_down<16>, dim3((unsigned)((hidden + 15) / 16)), dim3(256), 0,
+                         (hipStream_t)stream, out, ws, w2, s2, hidden, inter);
+    else
+      hipLaunchKernelGGL(k_expert_down<8>, dim3((unsigned)((hidden + 7) / 8)), dim3(256), 0,
+                         (hipStream_t)stream, out, ws, w2, s2, hidden, inter);
     return dsv4g_check_launch("expert_down");
   }
   DSV4G_TRY(dsv4g_gemv_fp4_pair_q(gate, up, qx, qscale, w1, s1, w3, s3, hidden, inter, stream));
