@@ -122,7 +122,9 @@ int dsv4g_gemv_fp8_batch_q(float *y, const float *qx, const float *qscale, int b
                            const uint8_t *W, const uint8_t *S, int in, int out,
                            int round_out, void *stream);
 /* dsv4_gemv_bf16 / _batch (src/dsv4/dsv4_internal.h:256-259); x [batch][in]
- * (16-byte aligned for the streaming kernel). The vocabulary head
+ * (16-byte aligned for the streaming kernels), any batch: in runs of 64, 32,
+ * 16, 8 or 4 tokens and a remainder of 1-3 when in is a multiple of 64, each
+ * run one launch that reads W once. The vocabulary head
  * (head_logits / head_logits_batch, src/dsv4/dsv4_model.c:7314-7445: the same
  * per-row fmaf chain, logits unrounded) is this call with in = hidden,
  * out = vocab, round_out = 0. */
@@ -159,7 +161,9 @@ int dsv4g_router_public(int *idx, float *wt, const float *x, const uint16_t *gat
  * expert in the checkpoint layout (scales [s1|s2|s3], then scale_run bytes on
  * the weights [w1|w2|w3]); weight: device pointer to the route weight, NULL
  * for 1. workspace: dsv4g_expert_workspace_bytes(inter) bytes, 256-aligned.
- * Three launches on the stream. */
+ * Two launches on the stream up to inter 4096 and hidden 8192 (the paired
+ * GEMV with the SwiGLU epilogue, then the down GEMV with the requant folded
+ * in), three beyond. */
 size_t dsv4g_expert_workspace_bytes(int inter);
 int dsv4g_expert_forward(float *out, const float *qx, const float *qscale, const uint8_t *slot,
                          size_t scale_run, int hidden, int inter, float swiglu_limit,
