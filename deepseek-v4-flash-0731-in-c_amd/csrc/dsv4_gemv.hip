@@ -62,19 +62,6 @@ __global__ void k_dequant_fp8(float *__restrict__ out, const uint8_t *__restrict
   }
 }
 
-// Hardware-convert probes: the GEMVs decode with the gfx950 MX/OCP converts;
-// these write their results for every code so the tests can pin them to the
-// reference decode.
-__global__ void k_probe_converts(float *__restrict__ fp4_out, float *__restrict__ fp8_out) {
-  const uint32_t t = threadIdx.x;  // 0..255
-  const uint32_t word = t | (t << 8) | (t << 16) | (t << 24);
-  const float2 a = fp4x2<0>(word);
-  fp4_out[2 * t] = a.x;
-  fp4_out[2 * t + 1] = a.y;
-  const float2 b = fp8x2<false>(word);
-  fp8_out[t] = b.x;
-}
-
 // The FP4 GEMVs (dsv4_gemv_fp4_q / _pair_q / _batch_q,
 // src/dsv4/dsv4_model.c:967-1380) on the decode layer's register tiles
 // (dsv4_tiles.h): one (row, 32-column group) partial per lane as a sequential
@@ -1137,12 +1124,6 @@ int dsv4g_dequant_fp8(float *out, const uint8_t *W, const uint8_t *S, int rows, 
   hipLaunchKernelGGL(k_dequant_fp8, dim3(1024), dim3(256), 0, (hipStream_t)stream, out, W,
                      S, rows, cols);
   return dsv4g_check_launch("dequant_fp8");
-}
-
-int dsv4g_probe_converts(float *fp4_out, float *fp8_out, void *stream) {
-  hipLaunchKernelGGL(k_probe_converts, dim3(1), dim3(256), 0, (hipStream_t)stream, fp4_out,
-                     fp8_out);
-  return dsv4g_check_launch("probe_converts");
 }
 
 static int fp4_shape_ok(int in, const char *who) {

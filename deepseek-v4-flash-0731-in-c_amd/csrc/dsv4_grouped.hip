@@ -65,48 +65,11 @@ __device__ __forceinline__ v4f mx_mfma(v8i a, v8i b, v4f c, int sa, int sb) {
 __device__ __forceinline__ uint32_t scale_code(float s) { return (f2u(s) >> 23) & 0xFFu; }
 
 // Operand layouts of V_MFMA_SCALE_F32_16X16X128_F8F6F4 (measured on gfx950 with
-// dsv4g_probe_mfma): lane l serves row/column l%16; with g = l/16,
+// the test library's probe, probe/dsv4_probe.hip): lane l serves row/column l%16; with g = l/16,
 //   4-bit operand: nibbles 0..31 (4 VGPRs) = K 32g .. 32g+31, low nibble first;
 //   8-bit operand: bytes 0..15 = K 16g .. 16g+15, bytes 16..31 = K 64+16g ..;
 //   scale byte of lane l = E8M0 scale of K block g (K 32g .. 32g+31);
 //   result: lane l holds D[4g + v][l%16], v = 0..3.
-
-// ------------------------------------------------------------ probes ----
-// One 16x16 MFMA tile from row-major operands, for layout validation.
-// A: [16][K] bytes (FP8) or [16][K/2] packed FP4; B: [16][K] FP8 (one row per
-// output column); scales [16][4] E8M0 codes. D: [16][16] row-major.
-__global__ void k_probe_mx(float *D, const uint8_t *A, const uint8_t *B, const uint8_t *sa,
-                           const uint8_t *sb, int afmt) {
-  const int l = threadIdx.x, i = l % 16, kb = l / 16;
-  uint4 a0, a1 = make_uint4(0, 0, 0, 0);
-  if (afmt == MX_FP4) {
-    a0 = *reinterpret_cast<const uint4 *>(A + i * 64 + kb * 16);
-  } else {
-    a0 = *reinterpret_cast<const uint4 *>(A + i * 128 + kb * 16);
-    a1 = *reinterpret_cast<const uint4 *>(A + i * 128 + 64 + kb * 16);
-  }
-  const uint4 b0 = *reinterpret_cast<const uint4 *>(B + i * 128 + kb * 16);
-  const uint4 b1 = *reinterpret_cast<const uint4 *>(B + i * 128 + 64 + kb * 16);
-  v4f acc = {0.f, 0.f, 0.f, 0.f};
-  if (afmt == MX_FP4)
-    acc = mx_mfma<MX_FP4>(u4x2_to_v8i(a0, a1), u4x2_to_v8i(b0, b1), acc, sa[i * 4 + kb],
-                          sb[i * 4 + kb]);
-  else
-    acc = mx_mfma<MX_FP8>(u4x2_to_v8i(a0, a1), u4x2_to_v8i(b0, b1), acc, sa[i * 4 + kb],
-                          sb[i * 4 + kb]);
-  for (int v = 0; v < 4; ++v) D[(4 * kb + v) * 16 + i] = acc[v];
-}
-
-// BF16 16x16x32: A [16][32], B [16][32] bf16 bits.
-__global__ void k_probe_bf16(float *D, const uint16_t *A, const uint16_t *B) {
-  const int l = threadIdx.x, i = l % 16, kb = l / 16;
-  const uint4 a = *reinterpret_cast<const uint4 *>(A + i * 32 + kb * 8);
-  const uint4 b = *reinterpret_cast<const uint4 *>(B + i * 32 + kb * 8);
-  v4f acc = {0.f, 0.f, 0.f, 0.f};
-  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
-                                                __builtin_bit_cast(bf16x8, b), acc, 0, 0, 0);
-  for (int v = 0; v < 4; ++v) D[(4 * kb + v) * 16 + i] = acc[v];
-}
 
 // ------------------------------------------------------- batch quant ----
 // The reference activation quant per (token, 128-group), stored as the
@@ -2105,18 +2068,6 @@ BatchWs batch_ws_layout(const DSV4GLayer *L, int T, void *base) {
 }  // namespace
 
 extern "C" {
-
-int dsv4g_probe_mfma(int kind, float *D, const void *A, const void *B, const uint8_t *sa,
-                     const uint8_t *sb, void *stream) {
-  hipStream_t st = (hipStream_t)stream;
-  if (kind == 2)
-    hipLaunchKernelGGL(k_probe_bf16, dim3(1), dim3(64), 0, st, D, (const uint16_t *)A,
-                       (const uint16_t *)B);
-  else
-    hipLaunchKernelGGL(k_probe_mx, dim3(1), dim3(64), 0, st, D, (const uint8_t *)A,
-                       (const uint8_t *)B, sa, sb, kind == 0 ? MX_FP4 : MX_FP8);
-  return dsv4g_check_launch("probe_mfma");
-}
 
 size_t dsv4g_moe_batch_workspace_bytes(const DSV4GLayer *L, int n_tokens) {
   return batch_ws_layout(L, n_tokens, nullptr).bytes;

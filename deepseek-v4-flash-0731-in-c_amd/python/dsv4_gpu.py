@@ -38,7 +38,6 @@ _SIGS = {
     "dsv4g_quant_fp8_act": [_vp, _vp, _vp, _I, _I, _vp],
     "dsv4g_dequant_fp4": [_vp, _vp, _vp, _I, _I, _vp],
     "dsv4g_dequant_fp8": [_vp, _vp, _vp, _I, _I, _vp],
-    "dsv4g_probe_converts": [_vp, _vp, _vp],
     "dsv4g_gemv_fp4_q": [_vp, _vp, _vp, _vp, _vp, _I, _I, _vp],
     "dsv4g_gemv_fp4_pair_q": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _I, _I, _vp],
     "dsv4g_gemv_fp4_batch_q": [_vp, _vp, _vp, _I, _vp, _vp, _I, _I, _vp],
@@ -68,7 +67,6 @@ _SIGS = {
                                 _vp],
     "dsv4g_moe_forward_batch_routes": [_vp, _vp, C.POINTER(DSV4GLayer), _vp, _I, _vp, _Z, _vp,
                                        _vp, _vp, _vp],
-    "dsv4g_probe_mfma": [_I, _vp, _vp, _vp, _vp, _vp, _vp],
     "dsv4g_quant_fp4_rows": [_vp, _vp, _vp, _I, _I, _vp],
     "dsv4g_quant_fp8_blocks": [_vp, _vp, _vp, _I, _I, _I, _vp],
     "dsv4g_rmsnorm_bf16": [_vp, _vp, _vp, _I, _F, _I, _I, _vp],
@@ -137,13 +135,6 @@ class GpuLib:
         out = torch.empty(rows, cols, dtype=torch.float32, device=W.device)
         self._call("dsv4g_dequant_fp8", _ptr(out), _ptr(W), _ptr(S), rows, cols, self._stream())
         return out
-
-    def probe_converts(self, device):
-        import torch
-        a = torch.empty(512, dtype=torch.float32, device=device)
-        b = torch.empty(256, dtype=torch.float32, device=device)
-        self._call("dsv4g_probe_converts", _ptr(a), _ptr(b), self._stream())
-        return a, b
 
     def gemv_fp4_q(self, qx, qs, W, S, in_, rows, y=None):
         import torch
@@ -375,13 +366,6 @@ class GpuLib:
                        _ptr(token_ids), n, _ptr(workspace), workspace.numel(), _ptr(idx),
                        _ptr(wt), _ptr(route_out), self._stream())
         return out, idx, wt
-
-    def probe_mfma(self, kind, A, B, sa=None, sb=None):
-        import torch
-        D = torch.empty(16, 16, dtype=torch.float32, device=A.device)
-        self._call("dsv4g_probe_mfma", kind, _ptr(D), _ptr(A), _ptr(B), _ptr(sa), _ptr(sb),
-                   self._stream())
-        return D
 
     def moe_decode_phase(self, phase, layer, x, out, workspace, token_ids=None):
         self._call("dsv4g_moe_decode_phase", phase, _ptr(out), _ptr(x), C.byref(layer.struct),

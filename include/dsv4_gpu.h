@@ -96,9 +96,6 @@ int dsv4g_dequant_fp4(float *out, const uint8_t *W, const uint8_t *S, int rows, 
                       void *stream);
 int dsv4g_dequant_fp8(float *out, const uint8_t *W, const uint8_t *S, int rows, int cols,
                       void *stream);
-/* Writes the hardware FP4 (512 floats: both nibbles of bytes 0..255) and FP8
- * (256 floats) conversions the GEMVs use, for validation. */
-int dsv4g_probe_converts(float *fp4_out, float *fp8_out, void *stream);
 
 /* dsv4_gemv_fp4_q / _pair_q / _batch_q (src/dsv4/dsv4_internal.h:274-286).
  * Batched arrays are contiguous: y [batch][rows], qx [batch][in],
@@ -285,11 +282,6 @@ int dsv4g_moe_forward_batch_routes(float *out, const float *x, const DSV4GLayer 
                                    const int *token_ids, int n_tokens, void *workspace,
                                    size_t workspace_bytes, int *idx_out, float *wt_out,
                                    float *route_out, void *stream);
-/* One 16x16 tile of the MFMA forms the batch path uses, from row-major
- * operands (kind 0: FP4 x FP8 block-scaled, 1: FP8 x FP8 block-scaled,
- * 2: BF16), for validating operand layouts. D: 16x16 fp32 row-major. */
-int dsv4g_probe_mfma(int kind, float *D, const void *A, const void *B, const uint8_t *sa,
-                     const uint8_t *sb, void *stream);
 
 /* Synthetic-checkpoint quantisers (the reference ships none in C):
  * FP4 rows with per-32 E8M0 scales; FP8 128x128 blocks with E8M0 codes

@@ -132,3 +132,59 @@ def bf16_ulp(v):
 
 # ------------------------------------------------------------ safetensors
 from st_writer import ST_ITEMSIZE, moe_layer_tensors, write_checkpoint, write_safetensors  # noqa: E402,F401
+
+
+PROBE_LIB = os.path.join(ROOT, "tests", "hip", "libdsv4_probe.so")
+
+
+class ProbeLib:
+    """The test-only ISA probes (tests/hip/dsv4_probe.hip): one tile of each
+    MFMA form the grouped kernels use, and the hardware FP4/FP8 converts over
+    every code. Not part of the product library."""
+
+    def __init__(self, path=PROBE_LIB):
+        import ctypes as C
+        if not os.path.exists(path):
+            raise RuntimeError(f"{path} is missing: build it with `make -C tests/hip` "
+                               f"(or __graft_entry__.build())")
+        self.C, self.lib = C, C.CDLL(path)
+        vp = C.c_void_p
+        self.lib.dsv4p_probe_converts.argtypes = [vp, vp, vp]
+        self.lib.dsv4p_probe_mfma.argtypes = [C.c_int, vp, vp, vp, vp, vp, vp]
+        for f in (self.lib.dsv4p_probe_converts, self.lib.dsv4p_probe_mfma):
+            f.restype = C.c_int
+
+    def _p(self, t):
+        return None if t is None else self.C.c_void_p(t.data_ptr())
+
+    def _stream(self):
+        import torch
+        return self.C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def converts(self, device):
+        """(fp4 [512]: both nibbles of bytes 0..255, fp8 [256]) as fp32."""
+        import torch
+        a = torch.empty(512, dtype=torch.float32, device=device)
+        b = torch.empty(256, dtype=torch.float32, device=device)
+        assert self.lib.dsv4p_probe_converts(self._p(a), self._p(b), self._stream()) == 0
+        return a, b
+
+    def mfma(self, kind, A, B, sa=None, sb=None):
+        """One 16x16 tile, row-major operands (kind 0: FP4 x FP8 block-scaled,
+        1: FP8 x FP8 block-scaled, 2: BF16); D [16][16] fp32 row-major."""
+        import torch
+        D = torch.empty(16, 16, dtype=torch.float32, device=A.device)
+        rc = self.lib.dsv4p_probe_mfma(kind, self._p(D), self._p(A), self._p(B), self._p(sa),
+                                       self._p(sb), self._stream())
+        assert rc == 0, rc
+        return D
+
+
+_PROBE = None
+
+
+def probe_lib() -> ProbeLib:
+    global _PROBE
+    if _PROBE is None:
+        _PROBE = ProbeLib()
+    return _PROBE

@@ -13,7 +13,7 @@ printed."""
 import numpy as np
 import pytest
 
-from common import bf16_input, make_layer, max_rel_err, pyoracle, same_bits
+from common import bf16_input, make_layer, max_rel_err, probe_lib, pyoracle, same_bits
 
 pytestmark = pytest.mark.gpu
 
@@ -36,7 +36,7 @@ def T(env, a):
 def test_mfma_layouts(env):
     """The kernels' operand and result layouts for the block-scaled FP4/FP8
     MFMA and the BF16 MFMA, against a float64 matmul."""
-    orc, lib = env["orc"], env["lib"]
+    orc, probe = env["orc"], probe_lib()
     rng = np.random.default_rng(0)
     t4, t8 = orc.fp4_table().astype(np.float64), orc.fp8_table().astype(np.float64)
     B8 = rng.integers(0, 126, (16, 128), dtype=np.uint8)
@@ -52,17 +52,17 @@ def test_mfma_layouts(env):
     def mx_ok(D, Ad, Bd):
         big = np.max(np.abs(Ad[:, None, :] * Bd[None, :, :]), axis=2)
         return np.all(np.abs(D - Ad @ Bd.T) <= 2.0 ** -10 * big)
-    D = lib.probe_mfma(0, T(env, A4), T(env, B8), T(env, sa), T(env, sb)).cpu().numpy()
+    D = probe.mfma(0, T(env, A4), T(env, B8), T(env, sa), T(env, sb)).cpu().numpy()
     assert mx_ok(D, A4d, Bd)
     A8 = rng.integers(0, 126, (16, 128), dtype=np.uint8)
     A8d = t8[A8] * np.repeat(np.ldexp(1.0, sa.astype(int) - 127), 32, axis=1)
-    D = lib.probe_mfma(1, T(env, A8), T(env, B8), T(env, sa), T(env, sb)).cpu().numpy()
+    D = probe.mfma(1, T(env, A8), T(env, B8), T(env, sa), T(env, sb)).cpu().numpy()
     assert mx_ok(D, A8d, Bd)
     from common import bf16_bits
     Ab = bf16_bits(rng.standard_normal((16, 32), dtype=np.float32))
     Bb = bf16_bits(rng.standard_normal((16, 32), dtype=np.float32))
     f = lambda u: (u.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
-    D = lib.probe_mfma(2, T(env, Ab), T(env, Bb)).cpu().numpy()
+    D = probe.mfma(2, T(env, Ab), T(env, Bb)).cpu().numpy()
     assert np.allclose(D, f(Ab) @ f(Bb).T, rtol=1e-5, atol=1e-5)
 
 

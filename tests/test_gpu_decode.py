@@ -12,8 +12,8 @@ import os
 import numpy as np
 import pytest
 
-from common import (ROOT, bf16_bits, bf16_input, expert_slot, make_layer, pyoracle, same_bits,
-                    max_rel_err)
+from common import (ROOT, bf16_bits, bf16_input, expert_slot, make_layer, probe_lib, pyoracle,
+                    same_bits, max_rel_err)
 
 pytestmark = pytest.mark.gpu
 
@@ -42,7 +42,7 @@ def H(t):
 
 
 def test_hw_converts_match_reference_decode(env):
-    fp4, fp8 = env["lib"].probe_converts(env["dev"])
+    fp4, fp8 = probe_lib().converts(env["dev"])
     fp4, fp8 = H(fp4), H(fp8)
     orc = env["orc"]
     t4 = orc.fp4_table()

@@ -5,8 +5,8 @@ One full-size routed expert (hidden 4096, inter 2048, FP4 weights with per-32
 E8M0 scales) on 16 tokens: gate/up GEMMs, the reference SwiGLU + FP8 requant
 (the oracle's swiglu_quant), the down GEMM, BF16 output - the reference's
 expert_forward_l1/l2 (src/dsv4/dsv4_model.c:6289-6345) with its three GEMMs
-done on the GPU tile by tile through dsv4g_probe_mfma, window sums added in
-fp32 in window order:
+done on the GPU tile by tile through the test library's MFMA probe
+(tests/hip/dsv4_probe.hip), window sums added in fp32 in window order:
   * block-scaled path: one 16x16x128 tile per 128-K window (FP4 weights and
     E4M3 activation codes with their E8M0 scales in the instruction);
   * BF16 path (what the grouped kernels do): the same operands converted
@@ -20,7 +20,7 @@ its largest product.
 import numpy as np
 import pytest
 
-from common import bf16_input, pyoracle
+from common import bf16_input, probe_lib, pyoracle
 
 pytestmark = pytest.mark.gpu
 
@@ -31,7 +31,8 @@ H, I, NT = 4096, 2048, 16
 def env():
     import torch
     import dsv4_gpu
-    return dict(torch=torch, lib=dsv4_gpu.lib(), orc=pyoracle.Oracle(), dev=torch.device("cuda:0"))
+    return dict(torch=torch, lib=dsv4_gpu.lib(), probe=probe_lib(), orc=pyoracle.Oracle(),
+                dev=torch.device("cuda:0"))
 
 
 def bf16r(a):
@@ -69,7 +70,7 @@ class Operands:
 
 
 def gemm_block_scaled(env, op):
-    torch, lib, dev = env["torch"], env["lib"], env["dev"]
+    torch, probe, dev = env["torch"], env["probe"], env["dev"]
     nw, rb_n = op.K // 128, op.rows // 16
     A = torch.from_numpy(np.ascontiguousarray(
         op.w4.reshape(rb_n, 16, nw, 64).transpose(0, 2, 1, 3))).to(dev)
@@ -82,13 +83,13 @@ def gemm_block_scaled(env, op):
     for rb in range(rb_n):
         acc = torch.zeros(16, NT, dtype=torch.float32, device=dev)
         for w in range(nw):
-            acc = acc + lib.probe_mfma(0, A[rb, w], B[w], SA[rb, w], SB[w])
+            acc = acc + probe.mfma(0, A[rb, w], B[w], SA[rb, w], SB[w])
         out[rb] = acc
     return out.reshape(op.rows, NT).cpu().numpy()
 
 
 def gemm_bf16(env, op):
-    torch, lib, dev = env["torch"], env["lib"], env["dev"]
+    torch, probe, dev = env["torch"], env["probe"], env["dev"]
     from common import bf16_bits
     nk, rb_n = op.K // 32, op.rows // 16
     wb = bf16_bits(op.wdq.astype(np.float32))  # exact: <= 4 significant bits x 2^e
@@ -101,7 +102,7 @@ def gemm_bf16(env, op):
     for rb in range(rb_n):
         acc = torch.zeros(16, NT, dtype=torch.float32, device=dev)
         for k in range(nk):
-            acc = acc + lib.probe_mfma(2, A[rb, k], B[k])
+            acc = acc + probe.mfma(2, A[rb, k], B[k])
         out[rb] = acc
     return out.reshape(op.rows, NT).cpu().numpy()
 

@@ -419,6 +419,18 @@ def test_library_exports_every_declared_symbol():
 
 
 @pytest.mark.skipif(not os.path.exists(LIB), reason="library not built")
+def test_probes_live_in_the_test_library_only():
+    """The ISA probes the layout tests use are exported by tests/hip's
+    library, not by the product library."""
+    from common import PROBE_LIB
+    assert not hasattr(C.CDLL(LIB), "dsv4g_probe_mfma")
+    assert not hasattr(C.CDLL(LIB), "dsv4g_probe_converts")
+    if os.path.exists(PROBE_LIB):
+        probe = C.CDLL(PROBE_LIB)
+        assert hasattr(probe, "dsv4p_probe_mfma") and hasattr(probe, "dsv4p_probe_converts")
+
+
+@pytest.mark.skipif(not os.path.exists(LIB), reason="library not built")
 def test_library_scalar_entry_points(orc):
     """The drop-in scalar helpers (host-side pure functions)."""
     lib = C.CDLL(LIB)
