@@ -82,7 +82,9 @@ __global__ __launch_bounds__(256) void k_gemv_fp4_t(GemvArgs a, int pair) {
   const float *qx = a.qx + (size_t)b * a.qx_stride;
   const float *qs = a.qscale + (size_t)b * a.qs_stride;
   // this thread's activation values (16 at 16 tid, and 4096 further for
-  // in > 4096), loaded before the weights
+  // in > 4096) and per-128 scale (thread i < in / 128: scale i), loaded
+  // before the weights (loads complete in order: issued after the weights,
+  // they would wait for every weight to land)
   const BufRsrc rx = buf_rsrc(qx, 4u * (uint32_t)in);
   uint4 xv[8];
 #pragma unroll
@@ -90,6 +92,7 @@ __global__ __launch_bounds__(256) void k_gemv_fp4_t(GemvArgs a, int pair) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       xv[4 * k + i] = buf_load16(rx, 4u * (uint32_t)(16 * tid + 4096 * k) + 16u * i);
+  const float qsv = buf_loadf(buf_rsrc(qs, 4u * (uint32_t)((in + 127) / 128)), 4u * (uint32_t)tid);
   Fp4RegsT<NP> R;
   const int half = q.tr / 2;
   const int r0 = pair ? blockIdx.x * half : blockIdx.x * q.tr;
@@ -114,7 +117,7 @@ __global__ __launch_bounds__(256) void k_gemv_fp4_t(GemvArgs a, int pair) {
       *reinterpret_cast<uint4 *>(x8 + base) = make_uint4(c[0], c[1], c[2], c[3]);
     }
   }
-  for (int i = tid; i < (in + 127) / 128; i += 256) xs[i] = qs[i];
+  if (tid < (in + 127) / 128) xs[tid] = qsv;  // in <= 8192: at most 64 scales
   __syncthreads();
   fp4_tile_x_lds(R, x8, xs, q);
   float2 *ps = reinterpret_cast<float2 *>(lds);
