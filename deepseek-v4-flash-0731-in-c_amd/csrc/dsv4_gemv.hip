@@ -163,8 +163,36 @@ __global__ __launch_bounds__(256) void k_fp8_proj(GemvArgs a, int nvec, int gpw,
   float *xs = lds;                                   // [G][CB][132]
   float *qs = xs + (size_t)G * CB * 132;             // [G][CB]
   float2 *ps = reinterpret_cast<float2 *>(qs + ((G * CB + 3) & ~3));  // [G][TR][stride]
+  // per wave: the exchange of its rows' weights (64 chunks of 128 B, 144 B
+  // apart), over the space of xs, qs and ps before they are written
+  uint8_t *xch = reinterpret_cast<uint8_t *>(lds) + (t / 64) * 9216;
 
-  // the lane's weights and block-scale codes (zeros past the matrix)
+  // this workgroup's token groups: gpw groups of G from blockIdx.y * gpw
+  const int tbeg = blockIdx.y * gpw * G, tend = min(nvec, tbeg + gpw * G);
+  // the first group's activations (up to 8192 values) are loaded ahead of the
+  // weights: loads complete in order, so behind the weights they would wait
+  // for every weight to land
+  const bool xpre = vec4 && G * in <= 8192;  // then also G CB <= 256 scales
+  float4 xr[8];
+  float qr = 0.0f;
+  if (xpre) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int i = 4 * t + 1024 * k;
+      const int g = i / in, c = i % in;
+      xr[k] = i < G * in && tbeg + g < nvec
+                  ? *reinterpret_cast<const float4 *>(a.qx + (size_t)(tbeg + g) * a.qx_stride + c)
+                  : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    if (t < G * CB && tbeg + t / CB < nvec)
+      qr = a.qscale[(size_t)(tbeg + t / CB) * a.qs_stride + t % CB];
+  }
+
+  // the weights (zeros past the matrix): round j covers the row's columns
+  // [128 SL j, 128 SL (j + 1)); load i of the SL lanes of a row reads 16 SL
+  // contiguous bytes (chunk i SL + slot of the round), so every load
+  // instruction covers whole lines; the chunks then go through the wave's
+  // LDS region to the lane that owns their block (block slot + SL j)
   const uint32_t nrow = (uint32_t)max(0, min(TR, rows - r0));
   const BufRsrc rw = buf_rsrc(a.W[m] + (size_t)r0 * in, nrow * (uint32_t)in);
   const BufRsrc rs = buf_rsrc(a.S[m], (uint32_t)((rows + 127) / 128) * CB);
@@ -175,21 +203,54 @@ __global__ __launch_bounds__(256) void k_fp8_proj(GemvArgs a, int nvec, int gpw,
     const uint32_t cb = (uint32_t)(slot + SL * j);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const uint32_t c = cb * 128u + 16u * i;
-      w[8 * j + i] = buf_load16(rw, cb < (uint32_t)CB && c < (uint32_t)in
-                                        ? (uint32_t)lr * (uint32_t)in + c
-                                        : 0xFFFFFFF0u);
+      const uint32_t c = (uint32_t)(SL * 128 * j + 16 * (SL * i + slot));
+      w[8 * j + i] = buf_load16(rw, c < (uint32_t)in ? (uint32_t)lr * (uint32_t)in + c
+                                                     : 0xFFFFFFF0u);
     }
     sc[j] = __builtin_amdgcn_raw_buffer_load_b8(
         rs, cb < (uint32_t)CB && (uint32_t)lr < nrow ? (uint32_t)((r0 + lr) / 128) * CB + cb
                                                       : 0xFFFFFFF0u, 0, 0);
   }
+  {
+    // the exchange: chunk q = SL i + slot of round j lies in block q / 8 at
+    // piece q % 8; the wave's rows (lr % (64 / SL)) are SL 144 B apart
+    const int wr = lr % (64 / SL);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      if (SL * 128 * j >= in) break;  // a round wholly past the row (uniform)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int q = SL * i + slot;
+        *reinterpret_cast<uint4 *>(xch + (wr * SL + q / 8) * 144 + (q % 8) * 16) = w[8 * j + i];
+      }
+      __builtin_amdgcn_wave_barrier();
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        w[8 * j + i] = *reinterpret_cast<const uint4 *>(xch + (wr * SL + slot) * 144 + 16 * i);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_wave_barrier();
+    }
+  }
+  __syncthreads();  // every wave's exchange read before xs, qs and ps take the space
+  if (xpre) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int i = 4 * t + 1024 * k;
+      const int g = i / in, c = i % in;
+      if (i < G * in)
+        *reinterpret_cast<float4 *>(xs + (size_t)g * CB * 132 + (c / 128) * 132 + (c % 128)) =
+            xr[k];
+    }
+    if (t < G * CB) qs[t] = qr;
+  }
 
-  // this workgroup's token groups: gpw groups of G from blockIdx.y * gpw
-  const int tbeg = blockIdx.y * gpw * G, tend = min(nvec, tbeg + gpw * G);
   for (int t0 = tbeg; t0 < tend; t0 += G) {
     // the group's activations and scales into LDS (zeros past the last token)
-    if (vec4) {
+    if (xpre && t0 == tbeg) {
+      // loaded ahead of the weights
+    } else if (vec4) {
       for (int i = 4 * t; i < G * in; i += 1024) {
         const int g = i / in, c = i % in;
         const float4 v = t0 + g < nvec
@@ -205,10 +266,11 @@ __global__ __launch_bounds__(256) void k_fp8_proj(GemvArgs a, int nvec, int gpw,
             t0 + g < nvec ? a.qx[(size_t)(t0 + g) * a.qx_stride + c] : 0.0f;
       }
     }
-    for (int i = t; i < G * CB; i += 256) {
-      const int g = i / CB;
-      qs[i] = t0 + g < nvec ? a.qscale[(size_t)(t0 + g) * a.qs_stride + i % CB] : 0.0f;
-    }
+    if (!(xpre && t0 == tbeg))
+      for (int i = t; i < G * CB; i += 256) {
+        const int g = i / CB;
+        qs[i] = t0 + g < nvec ? a.qscale[(size_t)(t0 + g) * a.qs_stride + i % CB] : 0.0f;
+      }
     __syncthreads();
     if (r0 + lr < rows) {
 #pragma unroll
@@ -276,12 +338,16 @@ __global__ __launch_bounds__(256) void k_fp8_proj(GemvArgs a, int nvec, int gpw,
 // 1024 or more workgroups (each weight read from HBM once); otherwise the
 // groups are spread so the launch still has about that many (a small
 // matrix's re-reads come from the caches).
+static size_t max_size(size_t a, size_t b) { return a > b ? a : b; }
+
 template <int SL, int G>
 static void launch_fp8_proj(const GemvArgs *a, int nvec, int nmat, hipStream_t st) {
   constexpr int TR = 256 / SL;
   const int CB = (a->in + 127) / 128;
-  const size_t lds = ((size_t)G * CB * 132 + ((G * CB + 3) & ~3)) * 4 +
-                     (size_t)G * TR * pair_stride(CB) * 8;
+  // xs, qs and ps, or the four waves' weight exchanges before them
+  const size_t lds = max_size(((size_t)G * CB * 132 + ((G * CB + 3) & ~3)) * 4 +
+                                  (size_t)G * TR * pair_stride(CB) * 8,
+                              (size_t)4 * 9216);
   const int tiles = (a->rows + TR - 1) / TR * nmat, groups = (nvec + G - 1) / G;
   const int split = min(groups, max(1, 1024 / tiles));
   const int gpw = (groups + split - 1) / split;
@@ -1173,19 +1239,24 @@ int dsv4g_launch_gemv_fp8(const GemvArgs *a, int nvec, int nmat, void *stream) {
   if (fp8_shape_ok(a->in, "gemv_fp8")) return DSV4G_EINVAL;
   if (a->rows <= 0 || nvec <= 0) return dsv4g_fail(DSV4G_EINVAL, "gemv_fp8: bad size");
   hipStream_t st = (hipStream_t)stream;
-  // lanes per row: every lane at most two 128-column blocks
+  // lanes per row: one 128-column block per lane up to 32 blocks (more
+  // workgroups, so more weight loads in flight: 4096-wide rows 6.3 -> 5.4 us
+  // at 1024 and 512 rows), two beyond (8192-wide rows: one block per lane
+  // measured no faster at one token and slower at five), at least 8 lanes
+  // per row (shorter rows: a lane per block, the rest idle)
   // tokens four at a time only when the row tiles alone fill the GPU (a
   // smaller matrix runs one token per workgroup, all tokens in parallel)
   const int CB = (a->in + 127) / 128;
-  const int sl = CB <= 16 ? 8 : CB <= 32 ? 16 : 32;
-  const bool many = nvec > 1 && (long)(a->rows + 256 / sl - 1) / (256 / sl) * nmat >= 1024;
+  const int sl = CB <= 8 ? 8 : CB <= 16 ? 16 : 32;
+  // (and the four tokens' activations fit LDS beside the rest: in <= 2048)
+  const bool many = nvec > 1 && a->in <= 2048 &&
+                    (long)(a->rows + 256 / sl - 1) / (256 / sl) * nmat >= 1024;
   switch (sl * (many ? 10 : 1)) {
     case 8: launch_fp8_proj<8, 1>(a, nvec, nmat, st); break;
     case 16: launch_fp8_proj<16, 1>(a, nvec, nmat, st); break;
-    case 32: launch_fp8_proj<32, 1>(a, nvec, nmat, st); break;
     case 80: launch_fp8_proj<8, 4>(a, nvec, nmat, st); break;
     case 160: launch_fp8_proj<16, 4>(a, nvec, nmat, st); break;
-    default: launch_fp8_proj<32, 4>(a, nvec, nmat, st); break;
+    default: launch_fp8_proj<32, 1>(a, nvec, nmat, st); break;
   }
   return dsv4g_check_launch("gemv_fp8");
 }
