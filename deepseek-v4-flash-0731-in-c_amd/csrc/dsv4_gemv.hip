@@ -154,7 +154,8 @@ __global__ __launch_bounds__(256) void k_gemv_fp4_t(GemvArgs a, int pair) {
 // once. LDS: the G tokens' activations (padded to 132 floats per block) and
 // their scales, and the (partial, scale) pairs of the block chains.
 template <int SL, int G>
-__global__ __launch_bounds__(256) void k_fp8_proj(GemvArgs a, int nvec, int gpw, int vec4) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(G == 4 ? 4 : 1))) void k_fp8_proj(
+    GemvArgs a, int nvec, int gpw, int vec4) {
   constexpr int TR = 256 / SL;
   extern __shared__ __align__(16) float lds[];
   const int m = blockIdx.z, t = threadIdx.x, lr = t / SL, slot = t % SL;
